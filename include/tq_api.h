@@ -1,0 +1,187 @@
+/*
+ * tq_api.h -- C ABI of the MI355X (gfx950) TurboQuant KV-compression library.
+ *
+ * Every entry point takes plain device pointers, element counts and strides,
+ * plus the HIP stream to launch on (passed as `void*`, i.e. a hipStream_t;
+ * NULL is the default stream).  Calls are asynchronous on that stream, allocate
+ * no device memory, and return TQ_OK (0) or a negative error code; the message
+ * for the last failure on the calling thread is returned by tq_last_error().
+ *
+ * Conventions shared by all entry points
+ *   - "f16" buffers hold IEEE binary16 bit patterns (uint16_t), "bf16" buffers
+ *     bfloat16 bit patterns.  Norm planes (rn, vn) are always f16, as in the
+ *     reference's packed format.
+ *   - Packed code rows use the reference bit layout: code i of a row occupies
+ *     global bits [i*b, i*b+b) of the row, least-significant bit first; bit k
+ *     lives in byte k/8 at bit position k%8.  A row of d b-bit codes takes
+ *     ceil(d*b/8) bytes (tq_out_cols).
+ *   - A compressed key record (one row = one (batch, kv-head, position)) is the
+ *     four planes  codes u8[ceil(d*(bits-1)/8)], signs u8[d/8], rn f16, vn f16;
+ *     a value record is codes u8[ceil(d*bits/8)], vn f16.  Planes are stored
+ *     structure-of-arrays, rows contiguous in (batch, head, position) order.
+ *   - A "split" d x d matrix W is f16 [2][d][d] row-major: hi = f16(64*W),
+ *     lo = f16(64*W - hi).  The kernels run d x d products on f16 MFMA and
+ *     recover f32 accuracy from the (hi, lo) pair.
+ *
+ * Reference: SrzStephen/transformers-turboquant, Python package
+ * src/turboquant_pytorch (file:line citations below are relative to it).
+ */
+#ifndef TQ_API_H
+#define TQ_API_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types of caller-provided activations */
+enum tq_dtype { TQ_F32 = 0, TQ_F16 = 1, TQ_BF16 = 2 };
+
+/* status codes */
+enum tq_status {
+  TQ_OK = 0,
+  TQ_EINVAL = -1,      /* bad argument (shape, bits, alignment, null pointer) */
+  TQ_EUNSUPPORTED = -2,/* valid but not built (e.g. head_dim outside 32/64/128/256) */
+  TQ_EHIP = -3         /* HIP runtime error at launch */
+};
+
+/* Library version (major*10000 + minor*100 + patch). */
+int tq_version(void);
+
+/* Message for the most recent failing call on this thread ("" if none). */
+const char* tq_last_error(void);
+
+/* Bytes needed for d codes of b bits: ceil(d*b/8).
+ * Replaces kernels/bit_ops.py:162-164 (_out_cols). */
+int64_t tq_out_cols(int64_t d, int32_t b);
+
+/* Pack int32 codes idx[n, d] (row stride ld_idx elements) into out[n, ld_out]
+ * bytes; each code is masked to b bits (1 <= b <= 8).  Writes exactly
+ * tq_out_cols(d, b) bytes per row.
+ * Replaces kernels/bit_ops.py:173-204 (pack_bits; Triton kernel :56-109,
+ * fallback :243-286). */
+int tq_pack_bits(const int32_t* idx, int64_t n, int32_t d, int64_t ld_idx,
+                 int32_t b, uint8_t* out, int64_t ld_out, void* stream);
+
+/* Inverse of tq_pack_bits: packed[n, ld_in] -> int32 out[n, ld_out] (d codes).
+ * Replaces kernels/bit_ops.py:206-235 (unpack_bits; kernel :111-155,
+ * fallback :288-326). */
+int tq_unpack_bits(const uint8_t* packed, int64_t n, int32_t d, int64_t ld_in,
+                   int32_t b, int32_t* out, int64_t ld_out, void* stream);
+
+/* Lloyd-Max quantize + pack: code = #{ j : bounds[j] < y } (torch.searchsorted,
+ * side='left') against the 2^b_eff - 1 sorted f32 boundaries, packed with
+ * b_eff bits.  y is f32 [n, ld_y].
+ * Replaces kernels/quantize.py:201-247 (lloyd_max_quantize; fallback
+ * :299-339). */
+int tq_quantize_pack(const float* y, int64_t n, int32_t d, int64_t ld_y,
+                     const float* bounds, int32_t b_eff, uint8_t* out,
+                     int64_t ld_out, void* stream);
+
+/* Unpack b-bit codes and look them up in f16 centroids[2^b] -> f16 out[n, ld_out].
+ * Replaces kernels/quantize.py:249-290 (lloyd_max_dequantize; fallback
+ * :341-369). */
+int tq_dequantize(const uint8_t* packed, int64_t n, int32_t d, int64_t ld_in,
+                  const uint16_t* centroids_f16, int32_t b, uint16_t* out_f16,
+                  int64_t ld_out, void* stream);
+
+/* Fused key compression of the n = B*H*S rows of x[B, H, S, d] (element
+ * strides sxb, sxh, sxs; unit stride on d; dtype tq_dtype), rows taken in
+ * (b, h, s) order:
+ *   vn = ||x||, y = (x / (vn + 1e-8)) Pi^T, codes = searchsorted(bounds, y),
+ *   k_mse = (f16(C)[codes] Pi) * vn, r = x - k_mse, rn = ||r||,
+ *   proj = r S^T, signs = (proj >= 0),
+ * writing codes u8[n, ceil(d*b_eff/8)], signs u8[n, d/8], rn f16[n], vn f16[n].
+ * pi_split / s_split: the rotation Pi[d,d] and QJL matrix S[d,d] (row-major)
+ * as split matrices, pit_split the split of Pi^T; centroids/bounds are f32 [2^b_eff], [2^b_eff - 1].
+ * y_out / proj_out (nullable) receive the f32 rotated rows and projections the
+ * codes and signs were taken from.
+ * Replaces compressors.py:99-138 (TurboQuantCompressorV2.compress, packed
+ * branch; k_mse uses f16-rounded centroids as at :120-122). */
+int tq_compress_keys(const void* x, int32_t dtype, int32_t B, int32_t H,
+                     int32_t S, int32_t d, int64_t sxb, int64_t sxh, int64_t sxs,
+                     const uint16_t* pi_split,
+                     const uint16_t* pit_split, const uint16_t* s_split,
+                     const float* centroids, const float* bounds, int32_t b_eff,
+                     uint8_t* codes, uint8_t* signs, uint16_t* rn, uint16_t* vn,
+                     float* y_out, float* proj_out, void* stream);
+
+/* Fused value compression of x[B, H, S, d] (strides as tq_compress_keys):
+ * vn = ||x||, y = (x/(vn+1e-8)) Pi^T,
+ * codes = searchsorted(bounds, y) packed with b bits, vn f16.
+ * Replaces compressors.py:271-287 (TurboQuantCompressorMSE.compress, packed
+ * branch). */
+int tq_compress_values(const void* x, int32_t dtype, int32_t B, int32_t H,
+                       int32_t S, int32_t d, int64_t sxb, int64_t sxh, int64_t sxs,
+                       const uint16_t* pi_split,
+                       const float* bounds, int32_t b, uint8_t* codes,
+                       uint16_t* vn, float* y_out, void* stream);
+
+/* Value decompression out[n, d] (dtype tq_dtype, row stride ld_out) =
+ * (centroids[codes] Pi) * vn with f32 centroids.  pit_split is Pi^T split
+ * as in tq_compress_keys.
+ * Replaces compressors.py:297-317 (TurboQuantCompressorMSE.decompress; the
+ * reference's packed branch multiplies an f16 tensor by an f32 Pi and raises,
+ * so this follows its f32 branch :311-317 on packed codes). */
+int tq_decompress_values(const uint8_t* codes, const uint16_t* vn, int64_t n,
+                         int32_t d, const uint16_t* pit_split,
+                         const float* centroids, int32_t b, void* out,
+                         int32_t out_dtype, int64_t ld_out, void* stream);
+
+/* Query preparation for compressed-domain scoring of q[B, Hq, Sq, d]
+ * (element strides sqb, sqh, sqs; unit stride on d):
+ *   q_rot  = f16(q Pi^T)                      -> f16 [B, Hq, Sq, d] contiguous
+ *   q_proj = f16(q_rot S_eff^T), S_eff f16[m=d, d] -> f16 [B, Hq, Sq, d]
+ * (q_proj accumulates in f32 from the f16 operands and is rounded once).
+ * Replaces compressors.py:186-189 (q_rot, S_eff) and the per-query projection
+ * of kernels/attention.py:155-167. */
+int tq_query_prep(const void* q, int32_t dtype, int32_t B, int32_t Hq,
+                  int32_t Sq, int32_t d, int64_t sqb, int64_t sqh, int64_t sqs,
+                  const uint16_t* pi_split, const uint16_t* s_eff_f16,
+                  uint16_t* q_rot, uint16_t* q_proj, void* stream);
+
+/* Materialised asymmetric scores out f32 [B, Hq, Sq, Sk] (contiguous):
+ *   out = vn * <q_rot, C[codes]> + coeff * rn * <q_proj, 2*sign - 1>
+ * from q_rot / q_proj f16 [B, Hq, Sq, d] (tq_query_prep) and key planes of
+ * [B, Hkv, Sk] rows; query head h reads kv head h / (Hq / Hkv).
+ * centroids_f16 holds the 2^(bits-1) key centroids.  bits is the total key
+ * bit budget (codes use bits-1 bits), as in the reference.
+ * Replaces kernels/attention.py:274-372 (asymmetric_attention_scores; fallback
+ * :380-461) and compressors.py:178-200. */
+int tq_attention_scores(const uint16_t* q_rot, const uint16_t* q_proj,
+                        const uint8_t* key_codes, const uint8_t* key_signs,
+                        const uint16_t* key_rn, const uint16_t* key_vn,
+                        const uint16_t* centroids_f16, int32_t B, int32_t Hq,
+                        int32_t Hkv, int32_t Sq, int32_t Sk, int32_t d,
+                        int32_t bits, float coeff, float* out, void* stream);
+
+/* Fused compressed-domain attention (one attention layer's tail):
+ *   s   = (vn*<q_rot,Ck[codes]> + coeff*rn*<q_proj, 2*sign-1>) * scale
+ *         (+ mask[b, h, i, j] if mask != NULL) (causal: key j > i + Sk - Sq dropped)
+ *   p   = softmax_j(s)                    (f32, online)
+ *   o   = (sum_j p_j * vnv_j * Cv[vcodes_j]) Pi_v
+ * out[b, i, h, :] in out_dtype with element strides (sob, soh, sos).
+ * mask: f32 additive, element strides (smb, smh, smq, smk) (0 = broadcast).
+ * val_pi_split: the value compressor's Pi^T split as in tq_compress_keys.
+ * Replaces the family forward tail families/qwen2.py:105-117 (same in
+ * llama.py:222-233, deepseek.py, gpt2.py:90-110): compress -> scores -> /sqrt(d)
+ * -> +mask -> softmax -> decompress(V) -> P V. */
+int tq_attention_fwd(const uint16_t* q_rot, const uint16_t* q_proj,
+                     const uint8_t* key_codes, const uint8_t* key_signs,
+                     const uint16_t* key_rn, const uint16_t* key_vn,
+                     const uint16_t* key_centroids_f16, int32_t bits,
+                     const uint8_t* val_codes, const uint16_t* val_vn,
+                     const uint16_t* val_centroids_f16, int32_t val_bits,
+                     const uint16_t* val_pit_split, int32_t B, int32_t Hq,
+                     int32_t Hkv, int32_t Sq, int32_t Sk, int32_t d,
+                     float coeff, float scale, int32_t causal,
+                     const float* mask, int64_t smb, int64_t smh, int64_t smq,
+                     int64_t smk, void* out, int32_t out_dtype, int64_t sob,
+                     int64_t soh, int64_t sos, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TQ_API_H */

@@ -1,0 +1,77 @@
+"""End-to-end model forwards on the GPU path against the CPU path.
+
+The CPU path reproduces the reference's GPT-2 logits bit for bit
+(tests/test_api_cpu.py); here the same random-init models run through the
+gfx950 kernels and are compared with it.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tq_oracle as O
+from transformers_turboquant import apply_turboquant
+
+pytestmark = pytest.mark.gpu
+
+
+def _gpt2(impl, n_layer=12):
+    from transformers import GPT2Config, GPT2LMHeadModel
+
+    torch.manual_seed(0)
+    cfg = GPT2Config(n_layer=n_layer)
+    cfg._attn_implementation = impl
+    return GPT2LMHeadModel(cfg).eval()
+
+
+@pytest.mark.parametrize("impl", ["eager", "sdpa"])
+def test_gpt2_small_gpu_matches_cpu(impl):
+    print("case: gpt2", impl, flush=True)
+    ids = torch.randint(0, 50257, (1, 512), generator=torch.Generator().manual_seed(0))
+    cpu = apply_turboquant(_gpt2(impl), bits=3, seed=42)
+    gpu = apply_turboquant(_gpt2(impl), bits=3, seed=42).to("cuda")
+    with torch.no_grad():
+        lc = cpu(input_ids=ids).logits[0].numpy()
+        lg = gpu(input_ids=ids.cuda()).logits[0].float().cpu().numpy()
+    assert np.isfinite(lg).all()
+    assert O.cosine(lg, lc) > 0.9999
+    assert (lg.argmax(-1) == lc.argmax(-1)).mean() > 0.97
+
+
+def test_gpt2_output_attentions_path():
+    print("case: gpt2 output_attentions", flush=True)
+    m = apply_turboquant(_gpt2("eager", n_layer=2), bits=3).to("cuda")
+    ids = torch.randint(0, 50257, (1, 40)).cuda()
+    with torch.no_grad():
+        a = m(input_ids=ids).logits
+        b = m(input_ids=ids, output_attentions=True)
+    assert b.attentions[0].shape == (1, 12, 40, 40)
+    assert O.cosine(a.float().cpu().numpy(), b.logits.float().cpu().numpy()) > 0.9999
+
+
+@pytest.mark.parametrize("model_type", ["llama", "qwen2"])
+def test_llama_like_bf16_gpu_matches_cpu(model_type):
+    print("case:", model_type, flush=True)
+    from transformers import LlamaConfig, LlamaForCausalLM, Qwen2Config, Qwen2ForCausalLM
+
+    def make():
+        torch.manual_seed(0)
+        kw = dict(vocab_size=1000, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                  num_attention_heads=8, num_key_value_heads=2)
+        if model_type == "qwen2":
+            return Qwen2ForCausalLM(Qwen2Config(**kw)).eval()
+        return LlamaForCausalLM(LlamaConfig(**kw)).eval()
+
+    ids = torch.randint(0, 1000, (2, 96))
+    cpu = apply_turboquant(make(), bits=3)
+    gpu = apply_turboquant(make(), bits=3).to("cuda")
+    with torch.no_grad():
+        lc = cpu(input_ids=ids).logits.numpy()
+        lg = gpu(input_ids=ids.cuda()).logits.float().cpu().numpy()
+        out = gpu.generate(ids[:1].cuda(), max_new_tokens=4, do_sample=False)
+    assert O.cosine(lg, lc) > 0.9999
+    assert out.shape == (1, 100)
+    gpu16 = apply_turboquant(make(), bits=3).to("cuda", torch.bfloat16)
+    with torch.no_grad():
+        lb = gpu16(input_ids=ids.cuda()).logits.float().cpu().numpy()
+    assert O.cosine(lb, lc) > 0.999

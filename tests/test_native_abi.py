@@ -1,0 +1,50 @@
+"""The C-ABI library loads and exports every entry point declared in include/tq_api.h.
+
+No kernel is launched here: only argument validation, which returns before any
+HIP call.
+"""
+
+import os
+import re
+import subprocess
+
+import pytest
+
+from turboquant_pytorch import _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    text = open(os.path.join(ROOT, "include", "tq_api.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(tq_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declarations_are_bound():
+    assert _declared() == sorted(_native.EXPORTED)
+
+
+def test_library_exports_every_symbol():
+    path = _native.library_path()
+    assert os.path.exists(path), "build the library first (__graft_entry__.build())"
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r" T (tq_\w+)", out))
+    missing = set(_declared()) - exported
+    assert not missing, missing
+
+
+def test_argument_validation_without_gpu():
+    lib = _native.lib()
+    assert lib.tq_version() >= 100
+    assert lib.tq_out_cols(128, 3) == 48 and lib.tq_out_cols(7, 3) == 3
+    assert lib.tq_pack_bits(None, 4, 128, 128, 9, None, 144, None) == -1
+    assert b"between 1 and 8" in lib.tq_last_error()
+    assert lib.tq_compress_keys(None, 0, 1, 1, 1, 96, 0, 0, 0, None, None, None, None, None, 2,
+                                None, None, None, None, None, None, None) == -2
+    assert b"head_dim 96" in lib.tq_last_error()
+    assert lib.tq_attention_fwd(*([None] * 7), 5, None, None, None, 3, None, 1, 8, 8, 1, 1, 128, 0.0, 1.0, 0,
+                                None, 0, 0, 0, 0, None, 0, 0, 0, 0, None) == -1
+    assert b"key bits" in lib.tq_last_error()
+    with pytest.raises(RuntimeError, match="group size|multiple"):
+        _native.check(lib.tq_attention_scores(*([None] * 7), 1, 6, 4, 1, 1, 128, 3, 0.0, None, None),
+                      "scores")

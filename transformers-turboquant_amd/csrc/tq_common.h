@@ -1,0 +1,95 @@
+// Shared device/host helpers for the gfx950 TurboQuant kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tq_api.h"
+
+namespace tq {
+
+// ---------------------------------------------------------------- errors
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+int launch_status(const char* what);  // TQ_OK or TQ_EHIP after a launch
+
+#define TQ_REQUIRE(cond, ...)           \
+  do {                                  \
+    if (!(cond)) {                      \
+      ::tq::set_error(__VA_ARGS__);     \
+      return TQ_EINVAL;                 \
+    }                                   \
+  } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int64_t out_cols(int64_t d, int b) { return (d * b + 7) / 8; }
+
+inline bool supported_dim(int d) { return d == 32 || d == 64 || d == 128 || d == 256; }
+
+// ---------------------------------------------------------------- vector types
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- conversions
+__device__ __forceinline__ float bf16_to_f32(uint16_t v) {
+  return __uint_as_float(static_cast<uint32_t>(v) << 16);
+}
+// round-to-nearest-even f32 -> bf16 (NaN kept quiet)
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+__device__ __forceinline__ float h2f(uint16_t v) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, v));
+}
+__device__ __forceinline__ uint16_t f2h(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+template <int DT>
+__device__ __forceinline__ float load_act(const void* p, int64_t i) {
+  if constexpr (DT == TQ_F32) return static_cast<const float*>(p)[i];
+  else if constexpr (DT == TQ_F16) return h2f(static_cast<const uint16_t*>(p)[i]);
+  else return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+template <int DT>
+__device__ __forceinline__ void store_act(void* p, int64_t i, float v) {
+  if constexpr (DT == TQ_F32) static_cast<float*>(p)[i] = v;
+  else if constexpr (DT == TQ_F16) static_cast<uint16_t*>(p)[i] = f2h(v);
+  else static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+}
+
+// ---------------------------------------------------------------- MFMA
+// v_mfma_f32_16x16x32_f16 (gfx950).  Lane l holds A[m = l%16][k = 8*(l/16) + 0..7],
+// B[k = 8*(l/16) + 0..7][n = l%16]; the accumulator holds D[m = 4*(l/16) + 0..3][n = l%16].
+__device__ __forceinline__ float4v mfma16x16x32(half8 a, half8 b, float4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Split a value that was pre-scaled by 64 into f16 hi + lo parts.
+__device__ __forceinline__ void split_f16(float v, _Float16& hi, _Float16& lo) {
+  hi = static_cast<_Float16>(v);
+  lo = static_cast<_Float16>(v - static_cast<float>(hi));
+}
+
+// ---------------------------------------------------------------- bits
+// Code i of a packed row: bits [i*b, i*b + b), LSB first.
+__device__ __forceinline__ uint32_t read_code(const uint8_t* row, int i, int b) {
+  const int bit = i * b;
+  const int byte = bit >> 3, off = bit & 7;
+  uint32_t v = row[byte] >> off;
+  if (off + b > 8) v |= static_cast<uint32_t>(row[byte + 1]) << (8 - off);
+  return v & ((1u << b) - 1u);
+}
+
+// Number of boundaries strictly below y (torch.searchsorted, side='left').
+__device__ __forceinline__ uint32_t searchsorted_left(float y, const float* bounds, int nb) {
+  uint32_t c = 0;
+  for (int j = 0; j < nb; ++j) c += (bounds[j] < y) ? 1u : 0u;
+  return c;
+}
+
+}  // namespace tq
