@@ -19,8 +19,8 @@
  *     four planes  codes u8[ceil(d*(bits-1)/8)], signs u8[d/8], rn f16, vn f16;
  *     a value record is codes u8[ceil(d*bits/8)], vn f16.  Planes are stored
  *     structure-of-arrays, rows contiguous in (batch, head, position) order.
- *   - A "split" d x d matrix W is f16 [2][d][d] row-major: hi = f16(64*W),
- *     lo = f16(64*W - hi).  The kernels run d x d products on f16 MFMA and
+ *   - A "split" d x d matrix W is f16 [2][d][d] row-major: hi = f16(1024*W),
+ *     lo = f16(1024*W - hi).  The kernels run d x d products on f16 MFMA and
  *     recover f32 accuracy from the (hi, lo) pair.
  *
  * Reference: SrzStephen/transformers-turboquant, Python package
@@ -160,7 +160,7 @@ int tq_attention_scores(const uint16_t* q_rot, const uint16_t* q_proj,
  *   s   = (vn*<q_rot,Ck[codes]> + coeff*rn*<q_proj, 2*sign-1>) * scale
  *         (+ mask[b, h, i, j] if mask != NULL) (causal: key j > i + Sk - Sq dropped)
  *   p   = softmax_j(s)                    (f32, online)
- *   o   = (sum_j p_j * vnv_j * Cv[vcodes_j]) Pi_v
+ *   o   = (sum_j p_j * vnv_j * Cv[vcodes_j]) Pi_v    (Cv: f32 value centroids)
  * out[b, i, h, :] in out_dtype with element strides (sob, soh, sos).
  * mask: f32 additive, element strides (smb, smh, smq, smk) (0 = broadcast).
  * val_pi_split: the value compressor's Pi^T split as in tq_compress_keys.
@@ -172,7 +172,7 @@ int tq_attention_fwd(const uint16_t* q_rot, const uint16_t* q_proj,
                      const uint16_t* key_rn, const uint16_t* key_vn,
                      const uint16_t* key_centroids_f16, int32_t bits,
                      const uint8_t* val_codes, const uint16_t* val_vn,
-                     const uint16_t* val_centroids_f16, int32_t val_bits,
+                     const float* val_centroids, int32_t val_bits,
                      const uint16_t* val_pit_split, int32_t B, int32_t Hq,
                      int32_t Hkv, int32_t Sq, int32_t Sk, int32_t d,
                      float coeff, float scale, int32_t causal,

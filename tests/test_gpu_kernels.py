@@ -104,7 +104,7 @@ def test_compress_keys(d, bits, dt):
     own = O.rotate(xs, kc.Pi.cpu().numpy())[2]
     assert np.max(np.abs(y_dev - own)) < 2e-6
     assert O.rel_err(p_dev, ref["proj"]) < 1e-5
-    assert np.mean(O.quantize_searchsorted(own, kc.boundaries.numpy()) != ref["codes"]) < 1e-3
+    assert np.mean(O.quantize_searchsorted(own, kc.boundaries.cpu().numpy()) != ref["codes"]) < 1e-3
     assert _f16_ulps(_np(ck["vec_norms"]).reshape(-1), ref["vec_norms"]).max() <= 1
     assert _f16_ulps(_np(ck["residual_norm"]).reshape(-1), ref["residual_norm"]).max() <= 1
     assert ck["residual_norm"].shape == (2, 3, 37) and ck["packed_qjl_signs"].shape == (n, d // 8)
@@ -195,8 +195,20 @@ def test_query_prep_matches_oracle():
     kc = TurboQuantCompressorV2(128, 3, seed=42, device=DEV)
     q_rot, q_proj = kc.prepare_queries(q)
     rot_ref, _ = O.query_prep(q.float().cpu().numpy(), kc.Pi.cpu().numpy(), kc._dev_tables.s_eff16.cpu().numpy())
-    ulps = _f16_ulps(_np(q_rot).reshape(-1, 128), rot_ref)
-    assert ulps.max() <= 1 and (ulps > 0).mean() < 0.01
+    exact = q.float().cpu().numpy().reshape(-1, 128).astype(np.float64) @ kc.Pi.cpu().numpy().astype(np.float64).T
+    got = _np(q_rot).reshape(-1, 128).astype(np.float64)
+    # f16 rounding of an f32-grade dot product: each element lies within half an
+    # f16 ulp plus the standard dot-product bound 2^-17 * sum_j |q_j Pi_ij|
+    # (n * u for n = 128, u = 2^-24) of the exact value, and rounds like the
+    # oracle's f32 GEMM almost everywhere
+    absum = np.abs(q.float().cpu().numpy().reshape(-1, 128).astype(np.float64)) @ np.abs(kc.Pi.cpu().numpy().astype(np.float64)).T
+    half_ulp = 2.0 ** -11 * np.abs(exact) + 2.0 ** -25  # f16 rounding bound u|x| (+ subnormal step)
+    excess = (np.abs(got - exact) - half_ulp) / absum
+    print(f"q_rot: rel-err {O.rel_err(got, exact):.2e}, worst excess/absum {excess.max():.2e}, "
+          f"mismatch vs oracle {(got != rot_ref).mean():.2e}")
+    assert O.rel_err(got, exact) < 5e-4
+    assert excess.max() <= 2.0 ** -17
+    assert (got != rot_ref).mean() < 0.01
     proj_ref = _np(q_rot).reshape(-1, 128).astype(np.float64) @ _np(kc._dev_tables.s_eff16).astype(np.float64).T
     assert _f16_ulps(_np(q_proj).reshape(-1, 128), proj_ref.astype(np.float16)).max() <= 1
 
@@ -304,7 +316,7 @@ def test_attention_full_size_slice():
         kv = h // 4
         r = slice(kv * S, (kv + 1) * S)
         sc = O.scores_packed(q_rot[h], q_proj[h], codes[r], signs[r], rn[r], vn[r],
-                             kc.centroids.numpy().astype(np.float16), O.COEFF(d))
+                             kc.centroids.cpu().numpy().astype(np.float16), O.COEFF(d))
         for t, i in enumerate(rows):
             ref = O.attention(sc[t:t + 1, : i + 1], vals[r][: i + 1], 1 / math.sqrt(d))
             assert O.rel_err(_np(out[0, i, h]), ref[0]) < REL, (h, i)

@@ -5,45 +5,71 @@
 // compressors.py:178-200):
 //   s(q, k) = vn_k * <q_rot, Ck[codes_k]> + coeff * rn_k * <q_proj, 2*sign_k - 1>
 // with q_rot = f16(q Pi^T) and q_proj = f16(q_rot S_eff^T) from tq_query_prep.
-// Both inner products run as v_mfma_f32_16x16x32_f16 with the decoded key
-// operands (f16 centroids, +-1 signs) exact in f16, so term 1 is exactly the
-// reference's f32 accumulation of f16 products.
+// Both inner products run as v_mfma_f32_16x16x32_f16 chains with exact f16
+// key operands (f16 centroids, +-1), so term 1 is exactly the reference's f32
+// accumulation of f16 products; the per-key factors vn and coeff * rn are
+// applied in f32 to the two accumulators.
 //
 // Work decomposition: a block of 4 wave64 owns one (batch, kv head) and BR
-// (query row, query head) pairs -- all G = Hq/Hkv heads of the group share each
-// decoded key tile (the reference expands K/V with repeat_interleave instead,
-// families/qwen2.py:101-102).  Per key tile of KT keys the block stages the
-// packed planes in LDS with dword loads, decodes keys once into f16 tiles
-// (K^, sign, V^T), and each wave computes S^T = K^ Q^T for its 16..32 columns.
-// S^T's accumulator layout (4 consecutive keys of one column per lane) is
-// exactly the B-operand layout P^T needs for O^T += V^T P^T, so P never leaves
-// registers.  Values stay in the rotated domain: O = (sum_j p_j vn_j Cv[c_j]) Pi_v,
-// with the final Pi_v applied once per query row (f16 hi/lo split MFMA).
+// (query row, query head) columns -- all G = Hq/Hkv heads of the group share
+// each key tile (the reference expands K/V with repeat_interleave instead,
+// families/qwen2.py:101-102).  Key tiles of KT keys are streamed through LDS
+// as raw packed planes (software pipelined: the next tile's planes are loaded
+// into registers while the current tile computes).  Key and sign MFMA operands
+// are fetched straight from byte -> 8 x f16 lookup tables indexed by the packed
+// bytes (no decode pass); 3-bit keys and the values are decoded once per tile
+// into LDS.  S^T's accumulator layout (4 consecutive keys of one column per
+// lane) is the B-operand layout P^T needs for O^T += V^T P^T, so P stays in
+// registers.  Values stay in the rotated domain:
+// O = (sum_j p_j vn_j Cv[c_j]) Pi_v, with Pi_v applied once per output row.
+// P enters the P.V product as an f16 (hi, lo) pair, so the only f16 rounding
+// on the value side is that of the decoded V^ = f16(Cv * vn).
 #include "tq_common.h"
 
 namespace tq {
 
+#ifndef TQ_ATTN_WAVES
+#define TQ_ATTN_WAVES 4
+#endif
+#ifndef TQ_ATTN_NBW
+#define TQ_ATTN_NBW 2
+#endif
+#ifndef TQ_ATTN_KT
+#define TQ_ATTN_KT 32
+#endif
+#ifndef TQ_ATTN_MINBLK
+#define TQ_ATTN_MINBLK 2
+#endif
+#ifndef TQ_ATTN_TAU
+#define TQ_ATTN_TAU 8.0f
+#endif
+
 template <int D>
 struct ATile {
-  static constexpr int KT = (D == 256) ? 32 : 64;   // keys per tile
-  static constexpr int NBW = (D == 256) ? 1 : 2;    // 16-column blocks per wave
-  static constexpr int BR = 4 * 16 * NBW;           // (query, head) rows per block
+  static constexpr int NW = TQ_ATTN_WAVES;          // waves per block
+  static constexpr int NT = 64 * NW;                // threads per block
+  static constexpr int KT = TQ_ATTN_KT;             // keys per tile
+  static constexpr int NBW = (D == 256) ? 1 : TQ_ATTN_NBW;
+  static constexpr int BR = NW * 16 * NBW;          // (query, head) columns per block
   static constexpr int KS = D / 32;                 // k-steps of the score MFMAs
   static constexpr int MBK = KT / 16;               // 16-key blocks per tile
   static constexpr int DB = D / 16;                 // 16-dim blocks
-  static constexpr int LDK = D + 8;                 // padded f16 row stride of K^ / sign tiles
-  static constexpr int LDV = KT + 8;                // padded f16 row stride of V^T tile
-  static constexpr int KC_MAX = D * 3 / 8;          // key code bytes/row (bits <= 4)
-  static constexpr int VC_MAX = D * 4 / 8;          // value code bytes/row (bits <= 4)
+  static constexpr int LDK = D + 8;                 // f16 row stride of decoded key / sign tiles
+  static constexpr int LDV = KT + 8;                // f16 row stride of the V^T tile
+  static constexpr int SCP = D / 8 + 4;             // padded raw sign row (bytes)
+  static constexpr int VCP_MAX = D * 4 / 8 + 4;     // padded raw value-code row, <= 4 bits
+  static constexpr int KREG = (KT * D * 3 / 32 + NT - 1) / NT;  // per-thread dwords of a tile
+  static constexpr int SREG = (KT * D / 32 + NT - 1) / NT;
+  static constexpr int VREG = (KT * D * 4 / 32 + NT - 1) / NT;
 };
 
 struct AttnArgs {
   const uint16_t *q_rot, *q_proj;
   const uint8_t *kcodes, *ksigns;
   const uint16_t *krn, *kvn, *kcent;
-  int kb;
   const uint8_t* vcodes;
-  const uint16_t *vvn, *vcent, *vpit;
+  const uint16_t *vvn, *vpit;
+  const float* vcent32;
   int vb;
   int B, Hq, Hkv, Sq, Sk, G, QT, nqb;
   float coeff, scale;
@@ -51,6 +77,7 @@ struct AttnArgs {
   const float* mask;
   int64_t smb, smh, smq, smk;
   void* out;
+  int out_dtype;
   int64_t sob, soh, sos;
   float* scores;  // scores-only mode output f32 [B, Hq, Sq, Sk]
 };
@@ -59,38 +86,70 @@ __device__ __forceinline__ half8 cat8(half4 a, half4 b) {
   return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
-// 8 codes of `bits` bits starting at a byte boundary (little endian bytes).
-__device__ __forceinline__ uint64_t load_group(const uint8_t* p, int bits) {
-  uint64_t w = 0;
-  for (int i = 0; i < bits; ++i) w |= static_cast<uint64_t>(p[i]) << (8 * i);
-  return w;
+// 32 bits of a packed row starting at byte `off` (row base 4-byte aligned, one
+// readable dword past the last code byte).
+__device__ __forceinline__ uint32_t bits32_at(const uint8_t* row, int off) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(row + (off & ~3));
+  const int sh = off & 3;
+  if (sh == 0) return w[0];
+  return __builtin_amdgcn_alignbyte(w[1], w[0], sh);
 }
 
-template <int D, int DT, bool SCORES>
-__global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
+template <int DT>
+__device__ __forceinline__ void store4(void* out, int64_t o, float4v v) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) store_act<DT>(out, o + e, v[e]);
+}
+
+template <int D, int KB, bool SCORES, bool MASK>
+__global__ void __launch_bounds__(64 * TQ_ATTN_WAVES, TQ_ATTN_MINBLK) attn_kernel(AttnArgs a) {
   using T = ATile<D>;
-  constexpr int KT = T::KT, NBW = T::NBW, KS = T::KS, MBK = T::MBK, DB = T::DB;
-  __shared__ _Float16 sK[KT * T::LDK];
-  __shared__ _Float16 sS[KT * T::LDK];
-  __shared__ _Float16 sVt[SCORES ? 1 : D * T::LDV];
-  __shared__ uint32_t rawK[KT * T::KC_MAX / 4];
-  __shared__ uint32_t rawS[KT * D / 32];
-  __shared__ uint32_t rawV[SCORES ? 1 : KT * T::VC_MAX / 4];
-  __shared__ _Float16 lutK[8], lutV[16];
-  __shared__ float skv[KT], skr[KT], svv[KT];
+  constexpr int KT = T::KT, NBW = T::NBW, KS = T::KS, MBK = T::MBK, DB = T::DB, NT = T::NT;
+  constexpr int KC = D * KB / 8;          // key code bytes per row
+  constexpr int KCP = KC + 4;             // padded
+  constexpr int SC = D / 8;
+  constexpr int LUTK_W = (KB == 1) ? 8 : 4;  // f16 values per key-LUT entry (KB <= 2)
+  constexpr int KITEMS = KT * (D / 8);       // (key, 8-dim group) decode items
+  constexpr int VITEMS = (D / 8) * (KT / 4);  // (8-dim group, 4-key quad) decode items
+
+  // double-buffered raw planes, decoded tiles, lookup tables
+  __shared__ __attribute__((aligned(16))) uint8_t rawK[2][KT * KCP];
+  __shared__ __attribute__((aligned(16))) uint8_t rawS[2][KT * T::SCP];
+  __shared__ __attribute__((aligned(16))) uint8_t rawV[SCORES ? 1 : 2][SCORES ? 4 : KT * T::VCP_MAX];
+  __shared__ __attribute__((aligned(16))) float skA[2][KT];      // vn * scale * log2(e)
+  __shared__ __attribute__((aligned(16))) float skB[2][KT];      // coeff * rn * scale * log2(e)
+  __shared__ __attribute__((aligned(16))) float svv[2][KT];      // value norms
+  __shared__ __attribute__((aligned(16))) _Float16 sK[KT * T::LDK];
+  __shared__ __attribute__((aligned(16))) _Float16 sS[KT * T::LDK];
+  __shared__ __attribute__((aligned(16))) _Float16 sVt[SCORES ? 8 : D * T::LDV];
+  __shared__ __attribute__((aligned(16))) _Float16 lutS[256 * 8];
+  __shared__ __attribute__((aligned(16))) _Float16 lutK[(KB == 3) ? 8 : 256 * LUTK_W];
+  __shared__ float lutV[16];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
   const int qblk = a.nqb - 1 - static_cast<int>(blockIdx.x);  // heavy causal blocks first
   const int hkv = blockIdx.y, b = blockIdx.z;
   const int q0 = qblk * a.QT;
-  const int kc = D * a.kb / 8, vc = D * a.vb / 8;
+  const int vc = D * a.vb / 8, vcp = vc + 4;
   const int64_t bh_kv = static_cast<int64_t>(b) * a.Hkv + hkv;
 
-  if (tid < (1 << a.kb)) lutK[tid] = __builtin_bit_cast(_Float16, a.kcent[tid]);
-  if (!SCORES && tid < (1 << a.vb)) lutV[tid] = __builtin_bit_cast(_Float16, a.vcent[tid]);
+  // ---- lookup tables: byte -> 8 x (+-1); byte -> key centroids; value centroids (f32)
+  {
+    const _Float16 one = static_cast<_Float16>(1.f), mone = static_cast<_Float16>(-1.f);
+    for (int i = tid; i < 256 * 8; i += NT) lutS[i] = ((i >> 3) >> (i & 7)) & 1 ? one : mone;
+    if constexpr (KB == 3) {
+      if (tid < 8) lutK[tid] = __builtin_bit_cast(_Float16, a.kcent[tid]);
+    } else {
+      for (int i = tid; i < 256 * LUTK_W; i += NT) {
+        const int byte = i / LUTK_W, e = i % LUTK_W;
+        lutK[i] = __builtin_bit_cast(_Float16, a.kcent[(byte >> (e * KB)) & ((1 << KB) - 1)]);
+      }
+    }
+    if (!SCORES && tid < (1 << a.vb)) lutV[tid] = a.vcent32[tid];
+  }
 
-  // ---- this lane's columns: (query position, head) and its q fragments
+  // ---- this lane's columns and their q fragments (B operands)
   int col_i[NBW], col_h[NBW];
   bool col_ok[NBW];
   half8 qr[KS][NBW], qp[KS][NBW];
@@ -105,22 +164,90 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int d0 = ks * 32 + lg * 8;
-      if (col_ok[nb]) {
-        qr[ks][nb] = *reinterpret_cast<const half8*>(a.q_rot + qrow + d0);
-        qp[ks][nb] = *reinterpret_cast<const half8*>(a.q_proj + qrow + d0);
-      } else {
-        qr[ks][nb] = half8{};
-        qp[ks][nb] = half8{};
-      }
+      qr[ks][nb] = col_ok[nb] ? *reinterpret_cast<const half8*>(a.q_rot + qrow + d0) : half8{};
+      qp[ks][nb] = col_ok[nb] ? *reinterpret_cast<const half8*>(a.q_proj + qrow + d0) : half8{};
     }
   }
 
-  // key range this block needs
+  // key range this block needs; tiles past `kfull` need per-element masking
   int kend = a.Sk;
+  int kfull = a.Sk;
   if (a.causal) {
     const int imax = min(q0 + a.QT - 1, a.Sq - 1);
     kend = min(a.Sk, imax + (a.Sk - a.Sq) + 1);
+    kfull = min(kfull, q0 + (a.Sk - a.Sq) + 1);
   }
+  constexpr float LOG2E = 1.4426950408889634f;
+  const float fa = SCORES ? 1.f : a.scale * LOG2E;  // scores kept in log2 units
+
+  // ---- register staging of one tile's planes
+  uint32_t rk[T::KREG], rs[T::SREG], rv[SCORES ? 1 : T::VREG];
+  float r_a = 0.f, r_b = 0.f, r_v = 0.f;
+  auto fetch = [&](int k0) {
+    const int nk = min(KT, a.Sk - k0);
+    const uint32_t* gk = reinterpret_cast<const uint32_t*>(a.kcodes + (bh_kv * a.Sk + k0) * KC);
+    const uint32_t* gs = reinterpret_cast<const uint32_t*>(a.ksigns + (bh_kv * a.Sk + k0) * SC);
+#pragma unroll
+    for (int j = 0; j < T::KREG; ++j) {
+      const int w = tid + j * NT;
+      rk[j] = (w < nk * KC / 4) ? gk[w] : 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < T::SREG; ++j) {
+      const int w = tid + j * NT;
+      rs[j] = (w < nk * SC / 4) ? gs[w] : 0u;
+    }
+    if constexpr (!SCORES) {
+      const uint32_t* gv = reinterpret_cast<const uint32_t*>(a.vcodes + (bh_kv * a.Sk + k0) * vc);
+#pragma unroll
+      for (int j = 0; j < T::VREG; ++j) {
+        const int w = tid + j * NT;
+        rv[j] = (w < nk * vc / 4) ? gv[w] : 0u;
+      }
+    }
+    if (tid < KT) {
+      const int64_t kr = bh_kv * a.Sk + k0 + tid;
+      const bool ok = tid < nk;
+      const float vn = ok ? h2f(a.kvn[kr]) : 0.f;
+      const float rn = ok ? h2f(a.krn[kr]) : 0.f;
+      r_a = fa * vn;
+      r_b = fa * a.coeff * rn;
+      if constexpr (!SCORES) r_v = ok ? h2f(a.vvn[kr]) : 0.f;
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < T::KREG; ++j) {
+      const int w = tid + j * NT;
+      if (w < KT * KC / 4) {
+        const int row = w / (KC / 4), col = w % (KC / 4);
+        *reinterpret_cast<uint32_t*>(&rawK[buf][row * KCP + col * 4]) = rk[j];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < T::SREG; ++j) {
+      const int w = tid + j * NT;
+      if (w < KT * SC / 4) {
+        const int row = w / (SC / 4), col = w % (SC / 4);
+        *reinterpret_cast<uint32_t*>(&rawS[buf][row * T::SCP + col * 4]) = rs[j];
+      }
+    }
+    if constexpr (!SCORES) {
+#pragma unroll
+      for (int j = 0; j < T::VREG; ++j) {
+        const int w = tid + j * NT;
+        if (w < KT * vc / 4) {
+          const int row = w / (vc / 4), col = w % (vc / 4);
+          *reinterpret_cast<uint32_t*>(&rawV[buf][row * vcp + col * 4]) = rv[j];
+        }
+      }
+    }
+    if (tid < KT) {
+      skA[buf][tid] = r_a;
+      skB[buf][tid] = r_b;
+      if constexpr (!SCORES) svv[buf][tid] = r_v;
+    }
+  };
 
   float m_run[NBW], l_run[NBW];
   float4v oacc[SCORES ? 1 : DB][NBW];
@@ -133,85 +260,72 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
       for (int db = 0; db < DB; ++db) oacc[db][nb] = float4v{0.f, 0.f, 0.f, 0.f};
     }
   }
-  constexpr float LOG2E = 1.4426950408889634f;
 
+  if (kend > 0) {
+    fetch(0);
+    stash(0);
+  }
+  int cur = 0;
   for (int k0 = 0; k0 < kend; k0 += KT) {
-    const int nk = min(KT, a.Sk - k0);
-    __syncthreads();  // previous tile fully consumed
-    // ---- stage packed planes (dword loads; rows are 4-byte aligned)
-    {
-      const uint32_t* gk = reinterpret_cast<const uint32_t*>(a.kcodes + (bh_kv * a.Sk + k0) * kc);
-      for (int w = tid; w < nk * kc / 4; w += 256) rawK[w] = gk[w];
-      const uint32_t* gs = reinterpret_cast<const uint32_t*>(a.ksigns + (bh_kv * a.Sk + k0) * (D / 8));
-      for (int w = tid; w < nk * D / 32; w += 256) rawS[w] = gs[w];
-      if constexpr (!SCORES) {
-        const uint32_t* gv = reinterpret_cast<const uint32_t*>(a.vcodes + (bh_kv * a.Sk + k0) * vc);
-        for (int w = tid; w < nk * vc / 4; w += 256) rawV[w] = gv[w];
-      }
-      if (tid < KT) {
-        const int64_t kr = bh_kv * a.Sk + k0 + tid;
-        const bool ok = tid < nk;
-        skv[tid] = ok ? h2f(a.kvn[kr]) : 0.f;
-        skr[tid] = ok ? a.coeff * h2f(a.krn[kr]) : 0.f;
-        if constexpr (!SCORES) svv[tid] = ok ? h2f(a.vvn[kr]) : 0.f;
-      }
-    }
-    __syncthreads();
-    // ---- decode K^ and signs: one 8-dim group per item
-    {
-      const uint8_t* rk = reinterpret_cast<const uint8_t*>(rawK);
-      const uint8_t* rs = reinterpret_cast<const uint8_t*>(rawS);
-      for (int it = tid; it < KT * (D / 8); it += 256) {
-        const int key = it / (D / 8), dg = it % (D / 8);
-        half8 kv, sv;
-        if (key < nk) {
-          const uint64_t w = load_group(rk + key * kc + dg * a.kb, a.kb);
-          const uint32_t sb = rs[key * (D / 8) + dg];
-          const uint32_t mk = (1u << a.kb) - 1u;
+    __syncthreads();  // tile k0 staged in buffer `cur`; previous tile's decoded tiles consumed
+    // ---- decode this tile once per block: K^ and sign tiles [key][dim], V^T [dim][key]
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            kv[e] = lutK[static_cast<uint32_t>(w >> (e * a.kb)) & mk];
-            sv[e] = ((sb >> e) & 1u) ? static_cast<_Float16>(1.0f) : static_cast<_Float16>(-1.0f);
-          }
+    for (int j = 0; j < (KITEMS + NT - 1) / NT; ++j) {
+      const int it = tid + j * NT;
+      if (KITEMS % NT == 0 || it < KITEMS) {
+        const int key = it / (D / 8), dg = it % (D / 8);
+        half8 kv;
+        if constexpr (KB == 1) {
+          kv = *reinterpret_cast<const half8*>(&lutK[rawK[cur][key * KCP + dg] * 8]);
+        } else if constexpr (KB == 2) {
+          const uint32_t two = *reinterpret_cast<const uint16_t*>(&rawK[cur][key * KCP + dg * 2]);
+          kv = cat8(*reinterpret_cast<const half4*>(&lutK[(two & 0xffu) * 4]),
+                    *reinterpret_cast<const half4*>(&lutK[(two >> 8) * 4]));
         } else {
-          kv = half8{};
-          sv = half8{};
+          const uint32_t w = bits32_at(&rawK[cur][key * KCP], dg * 3);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) kv[e] = lutK[(w >> (e * 3)) & 7u];
         }
         *reinterpret_cast<half8*>(&sK[key * T::LDK + dg * 8]) = kv;
-        *reinterpret_cast<half8*>(&sS[key * T::LDK + dg * 8]) = sv;
+        *reinterpret_cast<half8*>(&sS[key * T::LDK + dg * 8]) =
+            *reinterpret_cast<const half8*>(&lutS[rawS[cur][key * T::SCP + dg] * 8]);
       }
-      if constexpr (!SCORES) {
-        // V^T: item = (8-dim group, 4-key quad)
-        const uint8_t* rv = reinterpret_cast<const uint8_t*>(rawV);
-        const uint32_t mv = (1u << a.vb) - 1u;
-        for (int it = tid; it < (D / 8) * (KT / 4); it += 256) {
-          const int dg = it % (D / 8), kq = it / (D / 8);
+    }
+    if constexpr (!SCORES) {
+      // V^ = f16(Cv[code] * vn_v); item = (8-dim group dg, 4-key quad kq)
+      const uint32_t mv = (1u << a.vb) - 1u;
+#pragma unroll
+      for (int j = 0; j < (VITEMS + NT - 1) / NT; ++j) {
+        const int it = tid + j * NT;
+        if (VITEMS % NT == 0 || it < VITEMS) {
+          const int kq = it % (KT / 4), dg = it / (KT / 4);
+          const float4v vn4 = *reinterpret_cast<const float4v*>(&svv[cur][kq * 4]);
           half4 col[8];
 #pragma unroll
           for (int kk = 0; kk < 4; ++kk) {
-            const int key = kq * 4 + kk;
-            uint64_t w = 0;
-            if (key < nk) w = load_group(rv + key * vc + dg * a.vb, a.vb);
+            const uint32_t w = bits32_at(&rawV[cur][(kq * 4 + kk) * vcp], dg * a.vb);
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-              col[e][kk] = (key < nk) ? lutV[static_cast<uint32_t>(w >> (e * a.vb)) & mv]
-                                      : static_cast<_Float16>(0.f);
+              col[e][kk] = static_cast<_Float16>(lutV[(w >> (e * a.vb)) & mv] * vn4[kk]);
           }
 #pragma unroll
-          for (int e = 0; e < 8; ++e) *reinterpret_cast<half4*>(&sVt[(dg * 8 + e) * T::LDV + kq * 4]) = col[e];
+          for (int e = 0; e < 8; ++e)
+            *reinterpret_cast<half4*>(&sVt[(dg * 8 + e) * T::LDV + kq * 4]) = col[e];
         }
       }
     }
+    const bool more = k0 + KT < kend;
+    if (more) fetch(k0 + KT);  // global loads in flight during this tile's math
     __syncthreads();
 
-    // ---- S^T = K^ Q^T (term 1) and Sign Q_proj^T (term 2)
-    float4v s1[MBK][NBW], s2[MBK][NBW];
+    // ---- S^T = K^ Q_rot^T (term 1) and Sign Q_proj^T (term 2)
+    float4v sacc[MBK][NBW], tacc[MBK][NBW];
 #pragma unroll
     for (int mb = 0; mb < MBK; ++mb)
 #pragma unroll
       for (int nb = 0; nb < NBW; ++nb) {
-        s1[mb][nb] = float4v{0.f, 0.f, 0.f, 0.f};
-        s2[mb][nb] = float4v{0.f, 0.f, 0.f, 0.f};
+        sacc[mb][nb] = float4v{0.f, 0.f, 0.f, 0.f};
+        tacc[mb][nb] = float4v{0.f, 0.f, 0.f, 0.f};
       }
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -222,23 +336,10 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
         const half8 sa = *reinterpret_cast<const half8*>(&sS[off]);
 #pragma unroll
         for (int nb = 0; nb < NBW; ++nb) {
-          s1[mb][nb] = mfma16x16x32(ka, qr[ks][nb], s1[mb][nb]);
-          s2[mb][nb] = mfma16x16x32(sa, qp[ks][nb], s2[mb][nb]);
+          sacc[mb][nb] = mfma16x16x32(ka, qr[ks][nb], sacc[mb][nb]);
+          tacc[mb][nb] = mfma16x16x32(sa, qp[ks][nb], tacc[mb][nb]);
         }
       }
-    }
-
-    // ---- combine: s = vn * t1 + coeff * rn * t2
-    float sc[MBK][NBW][4];
-#pragma unroll
-    for (int mb = 0; mb < MBK; ++mb) {
-      const int kk = mb * 16 + lg * 4;
-      const float4v kv = *reinterpret_cast<const float4v*>(&skv[kk]);
-      const float4v kr = *reinterpret_cast<const float4v*>(&skr[kk]);
-#pragma unroll
-      for (int nb = 0; nb < NBW; ++nb)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sc[mb][nb][e] = s1[mb][nb][e] * kv[e] + s2[mb][nb][e] * kr[e];
     }
 
     if constexpr (SCORES) {
@@ -247,56 +348,72 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
         if (!col_ok[nb]) continue;
         float* orow = a.scores + ((static_cast<int64_t>(b) * a.Hq + col_h[nb]) * a.Sq + col_i[nb]) * a.Sk;
 #pragma unroll
-        for (int mb = 0; mb < MBK; ++mb)
+        for (int mb = 0; mb < MBK; ++mb) {
+          const int kk = mb * 16 + lg * 4;
+          const float4v ka4 = *reinterpret_cast<const float4v*>(&skA[cur][kk]);
+          const float4v kb4 = *reinterpret_cast<const float4v*>(&skB[cur][kk]);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int key = k0 + mb * 16 + lg * 4 + e;
-            if (key < a.Sk) orow[key] = sc[mb][nb][e];
+            const int key = k0 + kk + e;
+            if (key < a.Sk) orow[key] = sacc[mb][nb][e] * ka4[e] + tacc[mb][nb][e] * kb4[e];
           }
+        }
       }
     } else {
-      // ---- online softmax (natural-log units; exp via exp2)
-      half8 pb[MBK / 2][NBW];
+      // ---- online softmax in log2 units, lazily rescaled: a column's reference
+      // maximum only moves when its running maximum grows by more than TAU, so
+      // p <= 2^TAU and the accumulator is rescaled on few tiles
+      const bool edge = (k0 + KT > kfull);
+      half8 pb[MBK / 2][NBW], pl[MBK / 2][NBW];  // P = hi + lo (f16 pair, 2^-22 accurate)
 #pragma unroll
       for (int nb = 0; nb < NBW; ++nb) {
-        const int qi = col_i[nb];
-        const int lim = qi + (a.Sk - a.Sq);  // causal: keys <= lim
-        const float* mrow = a.mask ? a.mask + b * a.smb + col_h[nb] * a.smh + static_cast<int64_t>(qi) * a.smq
-                                   : nullptr;
+        float sc[MBK][4];
         float tmax = -INFINITY;
-#pragma unroll
-        for (int mb = 0; mb < MBK; ++mb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int key = k0 + mb * 16 + lg * 4 + e;
-            float v = sc[mb][nb][e] * a.scale;
-            if (mrow && key < a.Sk && col_ok[nb]) v += mrow[key * a.smk];
-            const bool dead = key >= a.Sk || (a.causal && key > lim) || !col_ok[nb];
-            v = dead ? -INFINITY : v;
-            sc[mb][nb][e] = v;
-            tmax = fmaxf(tmax, v);
-          }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float m_new = fmaxf(m_run[nb], tmax);
-        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-        const float alpha = (m_run[nb] == -INFINITY) ? 0.f : exp2f((m_run[nb] - m_use) * LOG2E);
-        m_run[nb] = m_new;
-        float psum = 0.f;
+        const int lim = col_i[nb] + (a.Sk - a.Sq);
 #pragma unroll
         for (int mb = 0; mb < MBK; ++mb) {
           const int kk = mb * 16 + lg * 4;
-          const float4v vv = *reinterpret_cast<const float4v*>(&svv[kk]);
+          const float4v ka4 = *reinterpret_cast<const float4v*>(&skA[cur][kk]);
+          const float4v kb4 = *reinterpret_cast<const float4v*>(&skB[cur][kk]);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float p = exp2f((sc[mb][nb][e] - m_use) * LOG2E);
-            psum += p;
-            pb[mb / 2][nb][(mb & 1) * 4 + e] = static_cast<_Float16>(p * vv[e]);
+            float v = sacc[mb][nb][e] * ka4[e] + tacc[mb][nb][e] * kb4[e];
+            const int key = k0 + kk + e;
+            if constexpr (MASK) {
+              if (col_ok[nb] && key < a.Sk)
+                v += fmaxf(a.mask[b * a.smb + col_h[nb] * a.smh + static_cast<int64_t>(col_i[nb]) * a.smq +
+                                  static_cast<int64_t>(key) * a.smk] * LOG2E,
+                           -3.0e38f);
+            }
+            if (edge && (key >= a.Sk || (a.causal && key > lim))) v = -INFINITY;
+            sc[mb][e] = v;
+            tmax = fmaxf(tmax, v);
           }
         }
-        l_run[nb] = l_run[nb] * alpha + psum;
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const bool grow = tmax > m_run[nb] + TQ_ATTN_TAU;
+        if (__any(grow)) {
+          const float m_new = grow ? tmax : m_run[nb];
+          const float alpha = (m_run[nb] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[nb] - m_new);
+          m_run[nb] = m_new;
+          l_run[nb] *= alpha;
 #pragma unroll
-        for (int db = 0; db < DB; ++db) oacc[db][nb] *= alpha;
+          for (int db = 0; db < DB; ++db) oacc[db][nb] *= alpha;
+        }
+        const float m_use = (m_run[nb] == -INFINITY) ? 0.f : m_run[nb];
+        float psum = 0.f;
+#pragma unroll
+        for (int mb = 0; mb < MBK; ++mb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float p = __builtin_amdgcn_exp2f(sc[mb][e] - m_use);
+            psum += p;
+            const _Float16 ph = static_cast<_Float16>(p);
+            pb[mb / 2][nb][(mb & 1) * 4 + e] = ph;
+            pl[mb / 2][nb][(mb & 1) * 4 + e] = static_cast<_Float16>(p - static_cast<float>(ph));
+          }
+        l_run[nb] += psum;
       }
       // ---- O^T += V^T P^T ; k-slots 8*lg+0..3 <-> keys 32c+4lg+0..3, 8*lg+4..7 <-> 32c+16+4lg+0..3
 #pragma unroll
@@ -307,10 +424,15 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
           const half8 va = cat8(*reinterpret_cast<const half4*>(&sVt[row]),
                                 *reinterpret_cast<const half4*>(&sVt[row + 16]));
 #pragma unroll
-          for (int nb = 0; nb < NBW; ++nb) oacc[db][nb] = mfma16x16x32(va, pb[c][nb], oacc[db][nb]);
+          for (int nb = 0; nb < NBW; ++nb) {
+            oacc[db][nb] = mfma16x16x32(va, pb[c][nb], oacc[db][nb]);
+            oacc[db][nb] = mfma16x16x32(va, pl[c][nb], oacc[db][nb]);
+          }
         }
       }
     }
+    if (more) stash(cur ^ 1);  // other buffer: last read before this tile's first barrier
+    cur ^= 1;
   }
 
   if constexpr (!SCORES) {
@@ -334,8 +456,7 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       int ex;
       frexpf(mx, &ex);
-      const float up = ldexpf(64.f, -ex), down = ldexpf(1.f / 4096.f, ex);
-      // B operand chunks (hi/lo) of O_rot^T
+      const float up = ldexpf(kSplit, -ex), down = ldexpf(kUnsplit2, ex);
       half8 bh[DB / 2], bl[DB / 2];
 #pragma unroll
       for (int c = 0; c < DB / 2; ++c)
@@ -350,7 +471,7 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
           bl[c][4 + e] = lo;
         }
       const int qi = col_i[nb], h = col_h[nb];
-#pragma unroll
+#pragma unroll 1
       for (int ib = 0; ib < DB; ++ib) {
         float4v f = float4v{0.f, 0.f, 0.f, 0.f};
         const int i = ib * 16 + l16;
@@ -366,36 +487,37 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
         if (col_ok[nb]) {
           const int64_t o = static_cast<int64_t>(b) * a.sob + static_cast<int64_t>(h) * a.soh +
                             static_cast<int64_t>(qi) * a.sos + ib * 16 + lg * 4;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) store_act<DT>(a.out, o + e, f[e] * down);
+          const float4v fo = f * down;
+          if (a.out_dtype == TQ_BF16) store4<TQ_BF16>(a.out, o, fo);
+          else if (a.out_dtype == TQ_F16) store4<TQ_F16>(a.out, o, fo);
+          else store4<TQ_F32>(a.out, o, fo);
         }
       }
     }
   }
 }
 
-template <int D, int DT, bool SCORES>
-static void launch_attn(AttnArgs a, hipStream_t s) {
+template <int D, int KB, bool SCORES>
+static void launch_attn(const AttnArgs& a, hipStream_t s) {
   dim3 grid(a.nqb, a.Hkv, a.B);
-  attn_kernel<D, DT, SCORES><<<grid, 256, 0, s>>>(a);
+  if (!SCORES && a.mask) attn_kernel<D, KB, SCORES, !SCORES><<<grid, ATile<D>::NT, 0, s>>>(a);
+  else attn_kernel<D, KB, SCORES, false><<<grid, ATile<D>::NT, 0, s>>>(a);
 }
 
-#define TQ_ATTN_SWITCH(d, dt, SC, a, s)                                \
-  switch ((d) * 4 + (dt)) {                                            \
-    case 32 * 4 + TQ_F32: launch_attn<32, TQ_F32, SC>(a, s); break;    \
-    case 32 * 4 + TQ_F16: launch_attn<32, TQ_F16, SC>(a, s); break;    \
-    case 32 * 4 + TQ_BF16: launch_attn<32, TQ_BF16, SC>(a, s); break;  \
-    case 64 * 4 + TQ_F32: launch_attn<64, TQ_F32, SC>(a, s); break;    \
-    case 64 * 4 + TQ_F16: launch_attn<64, TQ_F16, SC>(a, s); break;    \
-    case 64 * 4 + TQ_BF16: launch_attn<64, TQ_BF16, SC>(a, s); break;  \
-    case 128 * 4 + TQ_F32: launch_attn<128, TQ_F32, SC>(a, s); break;  \
-    case 128 * 4 + TQ_F16: launch_attn<128, TQ_F16, SC>(a, s); break;  \
-    case 128 * 4 + TQ_BF16: launch_attn<128, TQ_BF16, SC>(a, s); break;\
-    case 256 * 4 + TQ_F32: launch_attn<256, TQ_F32, SC>(a, s); break;  \
-    case 256 * 4 + TQ_F16: launch_attn<256, TQ_F16, SC>(a, s); break;  \
-    case 256 * 4 + TQ_BF16: launch_attn<256, TQ_BF16, SC>(a, s); break;\
-    default: break;                                                    \
+template <bool SCORES>
+static void dispatch_attn(int d, int kb, const AttnArgs& a, hipStream_t s) {
+#define TQ_KB_CASES(DD)                                 \
+  if (kb == 1) launch_attn<DD, 1, SCORES>(a, s);        \
+  else if (kb == 2) launch_attn<DD, 2, SCORES>(a, s);   \
+  else launch_attn<DD, 3, SCORES>(a, s);
+  switch (d) {
+    case 32: TQ_KB_CASES(32) break;
+    case 64: TQ_KB_CASES(64) break;
+    case 128: TQ_KB_CASES(128) break;
+    default: TQ_KB_CASES(256) break;
   }
+#undef TQ_KB_CASES
+}
 
 static int block_rows(int d) {
   switch (d) {
@@ -424,6 +546,17 @@ static int check_common(const char* what, int32_t B, int32_t Hq, int32_t Hkv, in
   return TQ_OK;
 }
 
+static void fill_common(AttnArgs& a, int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq, int32_t Sk, int32_t d) {
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.Sq = Sq;
+  a.Sk = Sk;
+  a.G = Hq / Hkv;
+  a.QT = block_rows(d) / a.G;
+  a.nqb = (Sq + a.QT - 1) / a.QT;
+}
+
 extern "C" {
 
 int tq_attention_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* key_codes,
@@ -443,27 +576,19 @@ int tq_attention_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uin
   a.krn = key_rn;
   a.kvn = key_vn;
   a.kcent = centroids_f16;
-  a.kb = bits - 1;
   a.vb = 1;
-  a.B = B;
-  a.Hq = Hq;
-  a.Hkv = Hkv;
-  a.Sq = Sq;
-  a.Sk = Sk;
-  a.G = Hq / Hkv;
-  a.QT = block_rows(d) / a.G;
-  a.nqb = (Sq + a.QT - 1) / a.QT;
+  fill_common(a, B, Hq, Hkv, Sq, Sk, d);
   a.coeff = coeff;
   a.scale = 1.f;
   a.scores = out;
-  TQ_ATTN_SWITCH(d, TQ_F32, true, a, as_stream(stream));
+  dispatch_attn<true>(d, bits - 1, a, as_stream(stream));
   return launch_status("tq_attention_scores");
 }
 
 int tq_attention_fwd(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* key_codes,
                      const uint8_t* key_signs, const uint16_t* key_rn, const uint16_t* key_vn,
                      const uint16_t* key_centroids_f16, int32_t bits, const uint8_t* val_codes,
-                     const uint16_t* val_vn, const uint16_t* val_centroids_f16, int32_t val_bits,
+                     const uint16_t* val_vn, const float* val_centroids, int32_t val_bits,
                      const uint16_t* val_pit_split, int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq,
                      int32_t Sk, int32_t d, float coeff, float scale, int32_t causal,
                      const float* mask, int64_t smb, int64_t smh, int64_t smq, int64_t smk,
@@ -477,7 +602,7 @@ int tq_attention_fwd(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_
              "tq_attention_fwd: unknown out dtype %d", (int)out_dtype);
   TQ_REQUIRE(!causal || Sk >= Sq, "tq_attention_fwd: causal needs Sk >= Sq");
   if (static_cast<int64_t>(B) * Hq * Sq == 0) return TQ_OK;
-  TQ_REQUIRE(q_rot && q_proj && val_pit_split && out && key_centroids_f16 && val_centroids_f16,
+  TQ_REQUIRE(q_rot && q_proj && val_pit_split && out && key_centroids_f16 && val_centroids,
              "tq_attention_fwd: null pointer");
   TQ_REQUIRE(Sk == 0 || (key_codes && key_signs && key_rn && key_vn && val_codes && val_vn),
              "tq_attention_fwd: null key/value plane");
@@ -489,20 +614,12 @@ int tq_attention_fwd(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_
   a.krn = key_rn;
   a.kvn = key_vn;
   a.kcent = key_centroids_f16;
-  a.kb = bits - 1;
   a.vcodes = val_codes;
   a.vvn = val_vn;
-  a.vcent = val_centroids_f16;
+  a.vcent32 = val_centroids;
   a.vpit = val_pit_split;
   a.vb = val_bits;
-  a.B = B;
-  a.Hq = Hq;
-  a.Hkv = Hkv;
-  a.Sq = Sq;
-  a.Sk = Sk;
-  a.G = Hq / Hkv;
-  a.QT = block_rows(d) / a.G;
-  a.nqb = (Sq + a.QT - 1) / a.QT;
+  fill_common(a, B, Hq, Hkv, Sq, Sk, d);
   a.coeff = coeff;
   a.scale = scale;
   a.causal = causal;
@@ -512,10 +629,11 @@ int tq_attention_fwd(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_
   a.smq = smq;
   a.smk = smk;
   a.out = out;
+  a.out_dtype = out_dtype;
   a.sob = sob;
   a.soh = soh;
   a.sos = sos;
-  TQ_ATTN_SWITCH(d, out_dtype, false, a, as_stream(stream));
+  dispatch_attn<false>(d, bits - 1, a, as_stream(stream));
   return launch_status("tq_attention_fwd");
 }
 

@@ -69,7 +69,14 @@ __device__ __forceinline__ float4v mfma16x16x32(half8 a, half8 b, float4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// Split a value that was pre-scaled by 64 into f16 hi + lo parts.
+// f32 operands of f16 MFMA products are split into hi + lo f16 parts after a
+// power-of-two scale (kSplit) that keeps both parts in the normal f16 range for
+// entries down to ~1e-4 of the row scale; split matrices are stored pre-scaled
+// by kSplit, so a product carries kSplit^2, removed exactly by kUnsplit2.
+constexpr float kSplit = 1024.f;
+constexpr float kUnsplit2 = 1.f / (1024.f * 1024.f);
+
+// Split a value (already scaled by kSplit) into f16 hi + lo parts.
 __device__ __forceinline__ void split_f16(float v, _Float16& hi, _Float16& lo) {
   hi = static_cast<_Float16>(v);
   lo = static_cast<_Float16>(v - static_cast<float>(hi));

@@ -4,9 +4,9 @@
 // (v_mfma_f32_16x16x32_f16) with f32 accumulation.  To keep f32 accuracy the
 // f32 operands are split into f16 hi + lo parts (x = hi + lo, |lo| <= 2^-11 |x|)
 // and three products hi*hi + lo*hi + hi*lo are accumulated; the dropped lo*lo
-// term is below 2^-22 relative.  Operands are scaled by 64 before splitting so
-// that the lo parts stay in the normal f16 range; the 4096 factor is removed
-// exactly afterwards.  Operands that are already f16 values (f16 centroids,
+// term is below 2^-22 relative.  Operands are scaled by kSplit = 2^10 before
+// splitting so that the lo parts stay in the normal f16 range; the 2^20 factor
+// is removed exactly afterwards.  Operands that are already f16 values (f16 centroids,
 // q_rot, S_eff) skip the lo part and give exactly the f32 accumulation of f16
 // products that the reference performs.
 //
@@ -30,9 +30,9 @@ struct CTile {
 };
 
 // Z[row][j] = sum_i X[row][i] * W[j][i] for the R x D tile X (LDS, f32).
-// wsplit: f16 bits, [2][D][D] = (hi, lo) of 64*W.  xscale[row] multiplies the
-// row before it is split (it must include the factor 64).  Result left in acc
-// (times 4096 * xscale/64); tile t of this wave covers columns
+// wsplit: f16 bits, [2][D][D] = (hi, lo) of kSplit*W.  xscale[row] multiplies
+// the row before it is split (it includes the factor kSplit).  Result left in
+// acc (times kSplit * xscale); tile t of this wave covers columns
 // j = mb*16 + 4*(lane/16) + 0..3 of row nb*16 + lane%16.
 template <int D, bool X_SPLIT, bool W_SPLIT>
 __device__ __forceinline__ void stage_gemm(const float* __restrict__ X, const float* __restrict__ xscale,
@@ -147,7 +147,7 @@ __global__ void __launch_bounds__(256) compress_keys_kernel(KeyArgs a) {
   __shared__ float A[T::R * T::LDA];   // x
   __shared__ float Bm[T::R * T::LDA];  // stage data
   __shared__ uint8_t idx[T::R * D];
-  __shared__ float s_vn[T::R], s_sc64[T::R], s_rsc[T::R], s_cent16[256], s_bnd[255];
+  __shared__ float s_vn[T::R], s_sc[T::R], s_rsc[T::R], s_cent16[256], s_bnd[255];
 
   const int nb = (1 << a.b) - 1;
   for (int j = threadIdx.x; j <= nb; j += T::NT) {
@@ -157,7 +157,7 @@ __global__ void __launch_bounds__(256) compress_keys_kernel(KeyArgs a) {
   }
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * T::R;
   load_rows<D, DT>(A, a.x, row0, a.n, a.rows);
-  if (threadIdx.x < T::R) s_sc64[threadIdx.x] = 64.f;
+  if (threadIdx.x < T::R) s_sc[threadIdx.x] = kSplit;
   __syncthreads();
 
   // vn = ||x||; xn = x / (vn + 1e-8)   (compressors.py:108-109)
@@ -181,14 +181,14 @@ __global__ void __launch_bounds__(256) compress_keys_kernel(KeyArgs a) {
   const int l16 = lane & 15, g = lane >> 4;
 
   // stage 1: y = xn Pi^T (compressors.py:112)
-  stage_gemm<D, true, true>(Bm, s_sc64, a.pi, acc);
+  stage_gemm<D, true, true>(Bm, s_sc, a.pi, acc);
   __syncthreads();
 #pragma unroll
   for (int t = 0; t < T::TPW; ++t) {
     const int tile = wave * T::TPW + t;
     const int row = (tile % T::NB) * 16 + l16, col = (tile / T::NB) * 16 + 4 * g;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) Bm[row * T::LDA + col + e] = acc[t][e] * (1.f / 4096.f);
+    for (int e = 0; e < 4; ++e) Bm[row * T::LDA + col + e] = acc[t][e] * kUnsplit2;
   }
   __syncthreads();
 
@@ -205,7 +205,7 @@ __global__ void __launch_bounds__(256) compress_keys_kernel(KeyArgs a) {
   __syncthreads();
 
   // stage 2: k_mse = (yhat Pi) * vn; r = x - k_mse   (compressors.py:120-126)
-  stage_gemm<D, false, true>(Bm, s_sc64, a.pit, acc);
+  stage_gemm<D, false, true>(Bm, s_sc, a.pit, acc);
   __syncthreads();
 #pragma unroll
   for (int t = 0; t < T::TPW; ++t) {
@@ -214,7 +214,7 @@ __global__ void __launch_bounds__(256) compress_keys_kernel(KeyArgs a) {
     const float vn = s_vn[row];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float kmse = (acc[t][e] * (1.f / 4096.f)) * vn;
+      const float kmse = (acc[t][e] * kUnsplit2) * vn;
       Bm[row * T::LDA + col + e] = A[row * T::LDA + col + e] - kmse;
     }
   }
@@ -227,7 +227,7 @@ __global__ void __launch_bounds__(256) compress_keys_kernel(KeyArgs a) {
       int e2;
       frexpf(rn, &e2);  // rn = m * 2^e2, m in [0.5, 1)
       s_rsc[r] = ldexpf(1.f, e2);
-      s_sc64[r] = ldexpf(64.f, -e2);  // residual scaled to norm in [0.5, 1)
+      s_sc[r] = ldexpf(kSplit, -e2);  // residual scaled to norm in [0.5, 1)
       const int64_t gr = row0 + r;
       if (gr < a.n) {
         a.rn[gr] = f2h(rn);
@@ -238,7 +238,7 @@ __global__ void __launch_bounds__(256) compress_keys_kernel(KeyArgs a) {
   __syncthreads();
 
   // stage 3: proj = r S^T; sign bit = proj >= 0   (compressors.py:128-130)
-  stage_gemm<D, true, true>(Bm, s_sc64, a.s, acc);
+  stage_gemm<D, true, true>(Bm, s_sc, a.s, acc);
   __syncthreads();
 #pragma unroll
   for (int t = 0; t < T::TPW; ++t) {
@@ -246,7 +246,7 @@ __global__ void __launch_bounds__(256) compress_keys_kernel(KeyArgs a) {
     const int row = (tile % T::NB) * 16 + l16, col = (tile / T::NB) * 16 + 4 * g;
     const float rs = s_rsc[row];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) Bm[row * T::LDA + col + e] = (acc[t][e] * (1.f / 4096.f)) * rs;
+    for (int e = 0; e < 4; ++e) Bm[row * T::LDA + col + e] = (acc[t][e] * kUnsplit2) * rs;
   }
   __syncthreads();
 
@@ -291,12 +291,12 @@ __global__ void __launch_bounds__(256) compress_values_kernel(ValArgs a) {
   using T = CTile<D>;
   __shared__ float A[T::R * T::LDA];
   __shared__ uint8_t idx[T::R * D];
-  __shared__ float s_sc64[T::R], s_bnd[255];
+  __shared__ float s_sc[T::R], s_bnd[255];
   const int nb = (1 << a.b) - 1;
   for (int j = threadIdx.x; j < nb; j += T::NT) s_bnd[j] = a.bounds[j];
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * T::R;
   load_rows<D, DT>(A, a.x, row0, a.n, a.rows);
-  if (threadIdx.x < T::R) s_sc64[threadIdx.x] = 64.f;
+  if (threadIdx.x < T::R) s_sc[threadIdx.x] = kSplit;
   __syncthreads();
   {
     const float ss = row_sum<D>(A, [](float v) { return v * v; });
@@ -312,7 +312,7 @@ __global__ void __launch_bounds__(256) compress_values_kernel(ValArgs a) {
   }
   __syncthreads();
   float4v acc[T::TPW];
-  stage_gemm<D, true, true>(A, s_sc64, a.pi, acc);
+  stage_gemm<D, true, true>(A, s_sc, a.pi, acc);
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g = lane >> 4;
@@ -322,7 +322,7 @@ __global__ void __launch_bounds__(256) compress_values_kernel(ValArgs a) {
     const int row = (tile % T::NB) * 16 + l16, col = (tile / T::NB) * 16 + 4 * g;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float y = acc[t][e] * (1.f / 4096.f);
+      const float y = acc[t][e] * kUnsplit2;
       idx[row * D + col + e] = static_cast<uint8_t>(searchsorted_left(y, s_bnd, nb));
       const int64_t gr = row0 + row;
       if (a.y_out && gr < a.n) a.y_out[gr * D + col + e] = y;
@@ -353,9 +353,9 @@ template <int D, int DT>
 __global__ void __launch_bounds__(256) decompress_values_kernel(DecArgs a) {
   using T = CTile<D>;
   __shared__ float A[T::R * T::LDA];
-  __shared__ float s_sc64[T::R], s_cent[256];
+  __shared__ float s_sc[T::R], s_cent[256];
   for (int j = threadIdx.x; j < (1 << a.b); j += T::NT) s_cent[j] = a.cent[j];
-  if (threadIdx.x < T::R) s_sc64[threadIdx.x] = 64.f;
+  if (threadIdx.x < T::R) s_sc[threadIdx.x] = kSplit;
   __syncthreads();
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * T::R;
   const int kc = D * a.b / 8;
@@ -366,7 +366,7 @@ __global__ void __launch_bounds__(256) decompress_values_kernel(DecArgs a) {
   }
   __syncthreads();
   float4v acc[T::TPW];
-  stage_gemm<D, true, true>(A, s_sc64, a.pit, acc);
+  stage_gemm<D, true, true>(A, s_sc, a.pit, acc);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g = lane >> 4;
 #pragma unroll
@@ -377,7 +377,7 @@ __global__ void __launch_bounds__(256) decompress_values_kernel(DecArgs a) {
     if (gr >= a.n) continue;
     const float vn = h2f(a.vn[gr]);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) store_act<DT>(a.out, gr * a.ld_out + col + e, (acc[t][e] * (1.f / 4096.f)) * vn);
+    for (int e = 0; e < 4; ++e) store_act<DT>(a.out, gr * a.ld_out + col + e, (acc[t][e] * kUnsplit2) * vn);
   }
 }
 
@@ -419,8 +419,8 @@ __global__ void __launch_bounds__(256) query_prep_kernel(PrepArgs a) {
     if (part == 0) {
       int e2;
       frexpf(m, &e2);
-      s_sc[r] = ldexpf(64.f, -e2);
-      s_inv[r] = ldexpf(1.f / 4096.f, e2);
+      s_sc[r] = ldexpf(kSplit, -e2);
+      s_inv[r] = ldexpf(kUnsplit2, e2);
     }
   }
   __syncthreads();

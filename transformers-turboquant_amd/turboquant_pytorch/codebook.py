@@ -85,8 +85,8 @@ def gaussian_matrix(d: int, seed: int) -> torch.Tensor:
 
 
 def split_f16(w: torch.Tensor) -> torch.Tensor:
-    """f16 [2, d, d] (hi, lo) split of 64*W, the layout the HIP kernels take."""
-    w64 = w.detach().to("cpu", torch.float32) * 64.0
+    """f16 [2, d, d] (hi, lo) split of 1024*W, the layout the HIP kernels take."""
+    w64 = w.detach().to("cpu", torch.float32) * 1024.0
     hi = w64.to(torch.float16)
     lo = (w64 - hi.float()).to(torch.float16)
     return torch.stack([hi, lo]).contiguous()

@@ -77,7 +77,7 @@ def attention_from_prepared(q_rot: torch.Tensor, q_proj: torch.Tensor,
         compressed_k["residual_norm"].data_ptr(), compressed_k["vec_norms"].data_ptr(),
         tk.cent16.data_ptr(), key_compressor.mse_bits + 1,
         compressed_v["packed_indices"].data_ptr(), compressed_v["vec_norms"].data_ptr(),
-        tv.cent16.data_ptr(), val_compressor.bits, tv.pit_split.data_ptr(),
+        tv.cent32.data_ptr(), val_compressor.bits, tv.pit_split.data_ptr(),
         B, Hq, Hkv, Sq, Sk, D, float(coeff), float(scale), int(bool(causal)),
         mptr, ms[0], ms[1], ms[2], ms[3],
         out.data_ptr(), _native.dtype_code(out_dtype), out.stride(0), out.stride(2), out.stride(1),
