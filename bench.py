@@ -39,6 +39,19 @@ def val_rec_bytes(bits: int, d: int) -> int:
     return math.ceil(d * bits / 8) + 2
 
 
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes (profiles/traffic_config2.json), scaled by the copy-kernel
+    calibration recorded there; None if no such measurement is committed."""
+    path = os.path.join(ROOT, "profiles", "traffic_config2.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+        return rec["kernels"][kernel]["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline(seconds_budget: float) -> dict:
     """The oracle (numpy restatement of the reference's PyTorch branch) on a bounded
     slice of the same workload: one KV head group (4 query heads), the first S_cpu
@@ -103,6 +116,8 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=30.0)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="run one device-to-device copy of MIB MiB first (PMC byte-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -124,6 +139,15 @@ def main() -> None:
     v = torch.randn(B, HKV, S, D, generator=gen).to(dev, torch.bfloat16)
     kc = TurboQuantCompressorV2(D, BITS, seed=42, device=dev)
     vc = TurboQuantCompressorMSE(D, BITS, seed=10042, device=dev)
+
+    if args.calibrate_copy:
+        n = args.calibrate_copy * (1 << 20) // 4
+        src = torch.ones(n, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
     marks = []
@@ -185,13 +209,13 @@ def main() -> None:
         "query_prep_ms": prep_ms,
         "attention_ms": attn_ms,
         "roofline": {
-            "kernel": "tq::attn_kernel<128, bf16, attention>",
+            "kernel": "tq::attn_kernel<128, 2, false, false> (fused scores + softmax + P.V)",
             "bound": "mfma",
             "achieved": achieved_tflops,
             "peak": MFMA_F16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved_tflops / MFMA_F16_PEAK_TFLOPS,
-            "traffic": None,
+            "traffic": measured_traffic("attn_kernel"),
         },
     }
     if not args.no_cpu_baseline:
