@@ -162,6 +162,8 @@ int tq_attention_scores(const uint16_t* q_rot, const uint16_t* q_proj,
  *   p   = softmax_j(s)                    (f32, online)
  *   o   = (sum_j p_j * vnv_j * Cv[vcodes_j]) Pi_v    (Cv: f32 value centroids)
  * out[b, i, h, :] in out_dtype with element strides (sob, soh, sos).
+ * workspace / workspace_bytes: scratch of at least tq_attention_workspace_size
+ * bytes enables the split-K decode kernels for few-query shapes.
  * mask: f32 additive, element strides (smb, smh, smq, smk) (0 = broadcast).
  * val_pi_split: the value compressor's Pi^T split as in tq_compress_keys.
  * Replaces the family forward tail families/qwen2.py:105-117 (same in
@@ -178,7 +180,18 @@ int tq_attention_fwd(const uint16_t* q_rot, const uint16_t* q_proj,
                      float coeff, float scale, int32_t causal,
                      const float* mask, int64_t smb, int64_t smh, int64_t smq,
                      int64_t smk, void* out, int32_t out_dtype, int64_t sob,
-                     int64_t soh, int64_t sos, void* stream);
+                     int64_t soh, int64_t sos, void* workspace,
+                     int64_t workspace_bytes, void* stream);
+
+/* Bytes of caller-provided device workspace tq_attention_fwd uses for the
+ * split-K decode path at this shape (head_dim 128, bits 2-4, at most 16
+ * (query row, query head) pairs per kv head, value bits == key bits); 0 when
+ * that path does not apply.  With a smaller or NULL workspace
+ * tq_attention_fwd runs its tiled path instead.  No counterpart in the
+ * reference, whose attention is never split over keys. */
+int64_t tq_attention_workspace_size(int32_t B, int32_t Hq, int32_t Hkv,
+                                    int32_t Sq, int32_t Sk, int32_t d,
+                                    int32_t bits);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,134 @@
+"""GPU parity of the split-K decode kernels (head_dim 128, at most 16 query
+(row, head) columns per kv head) against the CPU oracle and the tiled kernel.
+
+Same bars as the other kernel tests: scores and attention outputs within
+rel-err 1e-3 and cosine >= 0.9999 of the float64 oracle estimator evaluated on
+the device's packed planes.  Every case asserts first that the shape really
+takes the decode path (non-zero workspace size).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tq_oracle as O
+from test_gpu_kernels import _np, _oracle_attention, _oracle_scores, _planes
+from turboquant_pytorch import _native, compressed_attention
+from turboquant_pytorch.compressors import TurboQuantCompressorMSE, TurboQuantCompressorV2
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+REL = 1e-3
+
+
+def _case(**kw):
+    print("case:", kw, flush=True)
+
+
+def _on_decode_path(B, hq, hkv, sq, sk, bits, d=128):
+    return _native.lib().tq_attention_workspace_size(B, hq, hkv, sq, sk, d, bits) > 0
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("hq,hkv,sq,sk", [
+    (32, 8, 1, 4097), (8, 8, 1, 300), (16, 2, 2, 1000), (4, 1, 4, 65), (32, 8, 1, 1),
+])
+def test_decode_scores_match_oracle(bits, hq, hkv, sq, sk):
+    _case(bits=bits, hq=hq, hkv=hkv, sq=sq, sk=sk)
+    B, d = 2, 128
+    assert _on_decode_path(B, hq, hkv, sq, sk, bits)
+    torch.manual_seed(bits * 1000 + sk)
+    k = torch.randn(B, hkv, sk, d, device=DEV, dtype=torch.bfloat16)
+    q = torch.randn(B, hq, sq, d, device=DEV, dtype=torch.bfloat16)
+    kc = TurboQuantCompressorV2(d, bits, seed=42, device=DEV)
+    ck = kc.compress(k)
+    got = _np(kc.asymmetric_attention_scores(q, ck))
+    ref = _oracle_scores(kc, q, ck, hq, hkv)
+    assert got.shape == ref.shape
+    assert O.rel_err(got, ref) < REL
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("hq,hkv,sq,sk,causal,qmul,vmul", [
+    (32, 8, 1, 5000, False, 1.0, 1.0),
+    (8, 2, 4, 1025, True, 1.0, 1.0),     # last split holds one key: fully masked for rows 0-2
+    (4, 4, 1, 1, False, 1.0, 1.0),
+    (16, 1, 1, 700, True, 8.0, 1.0),     # sharp softmax, 16 heads per kv head
+    (2, 1, 8, 3000, True, 1.0, 3000.0),  # value norms ~3e4: near the f16 range
+])
+def test_decode_attention_matches_oracle_and_tiled(bits, hq, hkv, sq, sk, causal, qmul, vmul):
+    _case(bits=bits, hq=hq, hkv=hkv, sq=sq, sk=sk, causal=causal, qmul=qmul, vmul=vmul)
+    B, d = 2, 128
+    assert _on_decode_path(B, hq, hkv, sq, sk, bits)
+    torch.manual_seed(bits + 3 * sk)
+    q = torch.randn(B, hq, sq, d, device=DEV, dtype=torch.bfloat16) * qmul
+    k = torch.randn(B, hkv, sk, d, device=DEV, dtype=torch.bfloat16)
+    v = torch.randn(B, hkv, sk, d, device=DEV, dtype=torch.bfloat16) * vmul
+    kc = TurboQuantCompressorV2(d, bits, seed=42, device=DEV)
+    vc = TurboQuantCompressorMSE(d, bits, seed=10042, device=DEV)
+    ck, cv = kc.compress(k), vc.compress(v)
+    got = _np(compressed_attention(q, kc, vc, ck, cv, causal=causal, out_dtype=torch.float32))
+    tiled = _np(compressed_attention(q, kc, vc, ck, cv, causal=causal, out_dtype=torch.float32, split_k=False))
+    ref = _oracle_attention(kc, vc, q, ck, cv, hq, hkv, causal=causal)
+    assert np.isfinite(got).all()
+    print(f"decode rel-err {O.rel_err(got, ref):.2e}, tiled rel-err {O.rel_err(tiled, ref):.2e}")
+    assert O.rel_err(got, ref) < REL and O.cosine(got, ref) > 0.9999
+    assert O.rel_err(tiled, ref) < REL
+
+
+def test_decode_attention_mask_and_dtypes():
+    _case(what="decode mask")
+    torch.manual_seed(12)
+    B, hq, hkv, sq, sk, d = 2, 8, 2, 2, 600, 128
+    assert _on_decode_path(B, hq, hkv, sq, sk, 3)
+    q = torch.randn(B, hq, sq, d, device=DEV)
+    k = torch.randn(B, hkv, sk, d, device=DEV)
+    v = torch.randn(B, hkv, sk, d, device=DEV)
+    kc = TurboQuantCompressorV2(d, 3, seed=42, device=DEV)
+    vc = TurboQuantCompressorMSE(d, 3, seed=10042, device=DEV)
+    ck, cv = kc.compress(k), vc.compress(v)
+    mask = torch.zeros(B, 1, sq, sk)
+    mask[0, 0, :, 400:] = torch.finfo(torch.float32).min  # padding on batch 0
+    mask[1, 0, 1, :37] = -5.0
+    ref = _oracle_attention(kc, vc, q, ck, cv, hq, hkv, mask=mask.numpy())
+    for dt in (torch.float32, torch.bfloat16, torch.float16):
+        got = compressed_attention(q.to(dt), kc, vc, ck, cv, attention_mask=mask.to(DEV), out_dtype=dt)
+        tol = REL if dt == torch.float32 else 8e-3
+        assert O.rel_err(_np(got.float()), ref) < tol
+
+
+def test_decode_long_context_slice():
+    """Decode at the headline shape (4 sequences x 32k keys, 8 kv / 32 q heads, bits=3);
+    oracle on a few (sequence, head) pairs."""
+    _case(what="decode 32k")
+    torch.manual_seed(1)
+    B, hq, hkv, sk, d = 4, 32, 8, 32768, 128
+    assert _on_decode_path(B, hq, hkv, 1, sk, 3)
+    q = torch.randn(B, hq, 1, d, device=DEV, dtype=torch.bfloat16)
+    k = torch.randn(B, hkv, sk, d, device=DEV, dtype=torch.bfloat16)
+    v = torch.randn(B, hkv, sk, d, device=DEV, dtype=torch.bfloat16)
+    k[..., :4] *= 20
+    kc = TurboQuantCompressorV2(d, 3, seed=42, device=DEV)
+    vc = TurboQuantCompressorMSE(d, 3, seed=10042, device=DEV)
+    ck, cv = kc.compress(k), vc.compress(v)
+    out = compressed_attention(q, kc, vc, ck, cv, causal=True, out_dtype=torch.float32)
+    tiled = compressed_attention(q, kc, vc, ck, cv, causal=True, out_dtype=torch.float32, split_k=False)
+    assert torch.isfinite(out).all()
+    codes, signs, rn, vn = _planes(ck, d, kc.mse_bits)
+    codes_v = O.unpack_bits(_np(cv["packed_indices"]), 3, d)
+    q_rot, q_proj = O.query_prep(q.float().cpu().numpy(), kc.Pi.cpu().numpy(), kc._dev_tables.s_eff16.cpu().numpy())
+    q_rot = q_rot.reshape(B, hq, d)
+    q_proj = q_proj.reshape(B, hq, d)
+    cent16 = kc.centroids.cpu().numpy().astype(np.float16)
+    for b, h in ((0, 0), (1, 13), (3, 31)):
+        kv = b * hkv + h // 4
+        r = slice(kv * sk, (kv + 1) * sk)
+        sc = O.scores_packed(q_rot[b, h][None], q_proj[b, h][None], codes[r], signs[r], rn[r], vn[r],
+                             cent16, O.COEFF(d))
+        vals = O.value_decompress(codes_v[r], _np(cv["vec_norms"]).reshape(-1)[r], vc.Pi.cpu().numpy(),
+                                  vc.centroids.cpu().numpy())
+        ref = O.attention(sc, vals, 1 / math.sqrt(d))[0]
+        assert O.rel_err(_np(out[b, 0, h]), ref) < REL, (b, h)
+        assert O.rel_err(_np(tiled[b, 0, h]), ref) < REL, (b, h)

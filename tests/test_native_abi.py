@@ -43,8 +43,12 @@ def test_argument_validation_without_gpu():
                                 None, None, None, None, None, None, None) == -2
     assert b"head_dim 96" in lib.tq_last_error()
     assert lib.tq_attention_fwd(*([None] * 7), 5, None, None, None, 3, None, 1, 8, 8, 1, 1, 128, 0.0, 1.0, 0,
-                                None, 0, 0, 0, 0, None, 0, 0, 0, 0, None) == -1
+                                None, 0, 0, 0, 0, None, 0, 0, 0, 0, None, 0, None) == -1
     assert b"key bits" in lib.tq_last_error()
+    # decode-path workspace: only for head_dim 128, bits 2-4, <= 16 columns per kv head
+    assert lib.tq_attention_workspace_size(4, 32, 8, 1, 32768, 128, 3) > 0
+    assert lib.tq_attention_workspace_size(4, 32, 8, 8, 32768, 128, 3) == 0
+    assert lib.tq_attention_workspace_size(4, 32, 8, 1, 32768, 64, 3) == 0
     with pytest.raises(RuntimeError, match="group size|multiple"):
         _native.check(lib.tq_attention_scores(*([None] * 7), 1, 6, 4, 1, 1, 128, 3, 0.0, None, None),
                       "scores")

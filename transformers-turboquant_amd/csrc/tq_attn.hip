@@ -532,6 +532,22 @@ static int block_rows(int d) {
 
 using namespace tq;
 
+namespace tq {
+int64_t decode_workspace_bytes(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits);
+bool decode_applies(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits);
+int decode_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
+                  const uint8_t* ksigns, const uint16_t* krn, const uint16_t* kvn, const uint16_t* kcent,
+                  int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits, float coeff, float* out,
+                  hipStream_t s);
+int decode_attention(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
+                     const uint8_t* ksigns, const uint16_t* krn, const uint16_t* kvn, const uint16_t* kcent,
+                     int bits, const uint8_t* vcodes, const uint16_t* vvn, const float* vcent32,
+                     const uint16_t* vpit, int B, int Hq, int Hkv, int Sq, int Sk, int d, float coeff,
+                     float scale, int causal, const float* mask, int64_t smb, int64_t smh, int64_t smq,
+                     int64_t smk, void* out, int out_dtype, int64_t sob, int64_t soh, int64_t sos,
+                     void* workspace, hipStream_t s);
+}  // namespace tq
+
 static int check_common(const char* what, int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq, int32_t Sk,
                         int32_t d, int32_t bits) {
   if (!supported_dim(d)) {
@@ -559,6 +575,11 @@ static void fill_common(AttnArgs& a, int32_t B, int32_t Hq, int32_t Hkv, int32_t
 
 extern "C" {
 
+int64_t tq_attention_workspace_size(int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq, int32_t Sk, int32_t d,
+                                    int32_t bits) {
+  return decode_workspace_bytes(B, Hq, Hkv, Sq, Sk, d, bits);
+}
+
 int tq_attention_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* key_codes,
                         const uint8_t* key_signs, const uint16_t* key_rn, const uint16_t* key_vn,
                         const uint16_t* centroids_f16, int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq,
@@ -568,6 +589,9 @@ int tq_attention_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uin
   if (static_cast<int64_t>(B) * Hq * Sq * Sk == 0) return TQ_OK;
   TQ_REQUIRE(q_rot && q_proj && key_codes && key_signs && key_rn && key_vn && centroids_f16 && out,
              "tq_attention_scores: null pointer");
+  if (decode_applies(B, Hq, Hkv, Sq, Sk, d, bits))
+    return decode_scores(q_rot, q_proj, key_codes, key_signs, key_rn, key_vn, centroids_f16, B, Hq, Hkv,
+                         Sq, Sk, d, bits, coeff, out, as_stream(stream));
   AttnArgs a{};
   a.q_rot = q_rot;
   a.q_proj = q_proj;
@@ -593,7 +617,7 @@ int tq_attention_fwd(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_
                      int32_t Sk, int32_t d, float coeff, float scale, int32_t causal,
                      const float* mask, int64_t smb, int64_t smh, int64_t smq, int64_t smk,
                      void* out, int32_t out_dtype, int64_t sob, int64_t soh, int64_t sos,
-                     void* stream) {
+                     void* workspace, int64_t workspace_bytes, void* stream) {
   int st = check_common("tq_attention_fwd", B, Hq, Hkv, Sq, Sk, d, bits);
   if (st != TQ_OK) return st;
   TQ_REQUIRE(val_bits >= 1 && val_bits <= 4, "tq_attention_fwd: value bits must be in [1, 4], got %d",
@@ -606,6 +630,12 @@ int tq_attention_fwd(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_
              "tq_attention_fwd: null pointer");
   TQ_REQUIRE(Sk == 0 || (key_codes && key_signs && key_rn && key_vn && val_codes && val_vn),
              "tq_attention_fwd: null key/value plane");
+  const int64_t need = decode_workspace_bytes(B, Hq, Hkv, Sq, Sk, d, bits);
+  if (need > 0 && val_bits == bits && workspace && workspace_bytes >= need)
+    return decode_attention(q_rot, q_proj, key_codes, key_signs, key_rn, key_vn, key_centroids_f16, bits,
+                            val_codes, val_vn, val_centroids, val_pit_split, B, Hq, Hkv, Sq, Sk, d, coeff,
+                            scale, causal, mask, smb, smh, smq, smk, out, out_dtype, sob, soh, sos,
+                            workspace, as_stream(stream));
   AttnArgs a{};
   a.q_rot = q_rot;
   a.q_proj = q_proj;

@@ -12,6 +12,8 @@ Here the scores never reach memory: tq_attention_fwd streams the packed key and
 value planes once per block of query rows, runs an online softmax in f32, and
 accumulates P.V in the value compressor's rotated domain, applying Pi_v once
 per output row.  Grouped-query attention is served without expanding K/V.
+Few-query (decode) shapes take a split-K path whose partial results live in a
+workspace allocated here from torch (tq_attention_workspace_size bytes).
 """
 
 from __future__ import annotations
@@ -30,20 +32,21 @@ def compressed_attention(queries: torch.Tensor, key_compressor: TurboQuantCompre
                          val_compressor: TurboQuantCompressorMSE, compressed_k: dict,
                          compressed_v: dict, attention_mask: torch.Tensor | None = None,
                          causal: bool = False, scale: float | None = None,
-                         out_dtype: torch.dtype | None = None) -> torch.Tensor:
+                         out_dtype: torch.dtype | None = None, split_k: bool = True) -> torch.Tensor:
     """Attention output [B, S_q, Hq, D] (heads already interleaved for o_proj).
 
     queries [B, Hq, S_q, D] (any strides with unit stride on D) on the GPU;
     compressed_k / compressed_v the packed dicts of [B, Hkv, S_k, D] keys and
     values; attention_mask an additive mask broadcastable to [B, Hq, S_q, S_k];
-    causal drops keys j > i + S_k - S_q inside the kernel.
+    causal drops keys j > i + S_k - S_q inside the kernel; split_k=False keeps
+    few-query shapes on the tiled kernel instead of the split-K decode kernels.
     """
     if "packed_key_indices" not in compressed_k or "packed_indices" not in compressed_v:
         raise ValueError("compressed_attention needs the packed (GPU) formats")
     q_rot, q_proj = key_compressor.prepare_queries(queries)
     out_dtype = out_dtype or queries.dtype
     return attention_from_prepared(q_rot, q_proj, key_compressor, val_compressor, compressed_k,
-                                   compressed_v, attention_mask, causal, scale, out_dtype)
+                                   compressed_v, attention_mask, causal, scale, out_dtype, split_k)
 
 
 def attention_from_prepared(q_rot: torch.Tensor, q_proj: torch.Tensor,
@@ -51,7 +54,7 @@ def attention_from_prepared(q_rot: torch.Tensor, q_proj: torch.Tensor,
                             val_compressor: TurboQuantCompressorMSE, compressed_k: dict,
                             compressed_v: dict, attention_mask: torch.Tensor | None = None,
                             causal: bool = False, scale: float | None = None,
-                            out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+                            out_dtype: torch.dtype = torch.float32, split_k: bool = True) -> torch.Tensor:
     """The tq_attention_fwd launch on queries already prepared by prepare_queries()."""
     B, Hq, Sq, D = q_rot.shape
     _, Hkv, Sk, _ = compressed_k["shape"]
@@ -64,6 +67,12 @@ def attention_from_prepared(q_rot: torch.Tensor, q_proj: torch.Tensor,
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     coeff = math.sqrt(math.pi / 2) / key_compressor.S.shape[0]
+    lib = _native.lib()
+    bits = key_compressor.mse_bits + 1
+    ws_bytes = 0
+    if split_k and val_compressor.bits == bits:
+        ws_bytes = lib.tq_attention_workspace_size(B, Hq, Hkv, Sq, Sk, D, bits)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
     mptr, ms, mask = 0, (0, 0, 0, 0), None
     if attention_mask is not None:
         mask = attention_mask.to(dev, torch.float32)
@@ -71,15 +80,15 @@ def attention_from_prepared(q_rot: torch.Tensor, q_proj: torch.Tensor,
             mask = mask.unsqueeze(0)
         mask = mask.expand(B, Hq, Sq, Sk)
         mptr, ms = mask.data_ptr(), tuple(mask.stride())
-    _native.check(_native.lib().tq_attention_fwd(
+    _native.check(lib.tq_attention_fwd(
         q_rot.data_ptr(), q_proj.data_ptr(),
         compressed_k["packed_key_indices"].data_ptr(), compressed_k["packed_qjl_signs"].data_ptr(),
         compressed_k["residual_norm"].data_ptr(), compressed_k["vec_norms"].data_ptr(),
-        tk.cent16.data_ptr(), key_compressor.mse_bits + 1,
+        tk.cent16.data_ptr(), bits,
         compressed_v["packed_indices"].data_ptr(), compressed_v["vec_norms"].data_ptr(),
         tv.cent32.data_ptr(), val_compressor.bits, tv.pit_split.data_ptr(),
         B, Hq, Hkv, Sq, Sk, D, float(coeff), float(scale), int(bool(causal)),
         mptr, ms[0], ms[1], ms[2], ms[3],
         out.data_ptr(), _native.dtype_code(out_dtype), out.stride(0), out.stride(2), out.stride(1),
-        _native.stream_of(out)), "compressed_attention")
+        _native.ptr(workspace), ws_bytes, _native.stream_of(out)), "compressed_attention")
     return out
