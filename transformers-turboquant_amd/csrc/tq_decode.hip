@@ -19,12 +19,73 @@
 // In scores mode each block writes its keys' f32 scores directly.
 #include "tq_common.h"
 
+// Tuning knobs: scores use NB 16-key blocks per wave slab with R slabs in flight;
+// attention uses ANB / AR likewise; grids target about *_BLOCKS blocks.
+#ifndef TQ_DEC_NB
+#define TQ_DEC_NB 2
+#endif
+#ifndef TQ_DEC_R
+#define TQ_DEC_R 3
+#endif
+#ifndef TQ_DEC_ATTN_BLOCKS
+#define TQ_DEC_ATTN_BLOCKS 2048
+#endif
+#ifndef TQ_DEC_SCORE_BLOCKS
+#define TQ_DEC_SCORE_BLOCKS 2048
+#endif
+#ifndef TQ_DEC_ANB
+#define TQ_DEC_ANB 1
+#endif
+#ifndef TQ_DEC_AR
+#define TQ_DEC_AR 2
+#endif
+#ifndef TQ_DEC_PLO
+#define TQ_DEC_PLO 1
+#endif
+
 namespace tq {
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float4v mfma16x16x16(half4 a, half4 b, float4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+// Raw buffer loads: each 16-key block of a plane is read through a resource
+// whose base is the block's first row and whose record count ends at the
+// split's last key, so lanes past it read zero (the range check covers the
+// per-lane offset only, hence the per-block base).  Lanes carry constant offsets;
+// the base and count are wave-uniform scalar arithmetic.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x3 __attribute__((ext_vector_type(3)));
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+// resource over rows [kb, kend) of a plane with `rb`-byte rows
+__device__ __forceinline__ rsrc_t rows_rsrc(const void* plane, int rb, int kb, int kend) {
+  return make_rsrc(static_cast<const uint8_t*>(plane) + static_cast<int64_t>(kb) * rb,
+                   static_cast<uint32_t>(kend - kb) * rb);
+}
+constexpr uint32_t kOutOfRange = 0x80000000u;  // lane offset that every resource here rejects
+// Streamed planes are read once per step: loads carry the non-temporal hint.
+constexpr int kStream = 2;
+template <int N>
+__device__ __forceinline__ void bload(rsrc_t r, uint32_t voff, uint32_t soff, uint32_t (&out)[N]) {
+  if constexpr (N == 1) {
+    out[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, kStream);
+  } else if constexpr (N == 2) {
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, kStream);
+    out[0] = v[0]; out[1] = v[1];
+  } else {
+    static_assert(N == 3, "1-3 dwords");
+    const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(r, voff, soff, kStream);
+    out[0] = v[0]; out[1] = v[1]; out[2] = v[2];
+  }
+}
+__device__ __forceinline__ uint32_t bload16(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, kStream);
 }
 
 struct DecodeArgs {
@@ -44,62 +105,151 @@ struct DecodeArgs {
   float *part_o, *part_ml;       // attention mode partials
 };
 
+
+// ---------------------------------------------------------------- small tables
+// Lookup tables of at most 32 dwords give every entry its own LDS bank, so the
+// data-dependent lookups of a wave never conflict (64-entry tables share a bank
+// between two entries).  Entries are indexed by nibbles / 6-bit fields of the
+// packed rows:
+//   sign table   16 x half4: 4 sign bits -> 4 x (+-1)
+//   key table    KB=1: 16 x half4 (4 codes) | KB=2: 16 x half2 (2 codes) | KB=3: 64 x half2
+//   value table  VB=2: 16 x half2 | VB=3: 64 x half2 | VB=4: 256 x half2
 template <int BITS>
-struct DecodeLuts {
+struct SmallLuts {
   static constexpr int KB = BITS - 1, VB = BITS;
-  // key table: KB=1 byte -> 8 values, KB=2 byte -> 4 values, KB=3 12 bits -> 4 values
-  static constexpr int KENT = (KB == 3) ? 4096 : 256;
-  static constexpr int KW = (KB == 1) ? 8 : 4;
-  // value table: VB=2 byte -> 4, VB=3 12 bits -> 4, VB=4 byte -> 2
-  static constexpr int VENT = (VB == 3) ? 4096 : 256;
-  static constexpr int VW = (VB == 4) ? 2 : 4;
-  static constexpr int HALVES = 256 * 8 + KENT * KW + VENT * VW;
+  static constexpr int SGN_BYTES = 16 * 8;
+  static constexpr int KEY_BYTES = (KB == 1) ? 16 * 8 : (KB == 2 ? 16 * 4 : 64 * 4);
+  static constexpr int VAL_BYTES = (VB == 2) ? 16 * 4 : (VB == 3 ? 64 * 4 : 256 * 4);
+  static constexpr int SGN_OFF = 0, KEY_OFF = SGN_BYTES, VAL_OFF = SGN_BYTES + KEY_BYTES;
+  static constexpr int BYTES = VAL_OFF + VAL_BYTES;
 };
 
-template <int D, int BITS, bool SCORES>
-__global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
+template <int BITS, bool VALUES>
+__device__ __forceinline__ void build_small_luts(const DecodeArgs& a, uint8_t* t, int tid) {
+  using L = SmallLuts<BITS>;
+  constexpr int KB = L::KB, VB = L::VB;
+  if (tid < 16) {
+    half4 v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = ((tid >> j) & 1) ? static_cast<_Float16>(1.f) : static_cast<_Float16>(-1.f);
+    *reinterpret_cast<half4*>(t + L::SGN_OFF + tid * 8) = v;
+  }
+  auto kc = [&](int i) { return __builtin_bit_cast(_Float16, a.kcent[i]); };
+  if constexpr (KB == 1) {
+    if (tid < 16) {
+      half4 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = kc((tid >> j) & 1);
+      *reinterpret_cast<half4*>(t + L::KEY_OFF + tid * 8) = v;
+    }
+  } else {
+    constexpr int N = (KB == 2) ? 16 : 64;
+    if (tid < N) {
+      half2v v;
+      v[0] = kc(tid & ((1 << KB) - 1));
+      v[1] = kc(tid >> KB);
+      *reinterpret_cast<half2v*>(t + L::KEY_OFF + tid * 4) = v;
+    }
+  }
+  if constexpr (VALUES) {
+    constexpr int N = (VB == 2) ? 16 : (VB == 3 ? 64 : 256);
+    if (tid < N) {
+      half2v v;
+      v[0] = static_cast<_Float16>(a.vcent[tid & ((1 << VB) - 1)]);
+      v[1] = static_cast<_Float16>(a.vcent[tid >> VB]);
+      *reinterpret_cast<half2v*>(t + L::VAL_OFF + tid * 4) = v;
+    }
+  }
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t lds32(const uint8_t* t, uint32_t off) {
+  return *reinterpret_cast<const uint32_t*>(t + off);
+}
+__device__ __forceinline__ u32x2 lds64(const uint8_t* t, uint32_t off) {
+  return *reinterpret_cast<const u32x2*>(t + off);
+}
+// 8 halves from two half4 entries indexed by the two nibbles of byte b
+__device__ __forceinline__ half8 nib2x4(const uint8_t* t, uint32_t b) {
+  const u32x2 lo = lds64(t, (b << 3) & 0x78u), hi = lds64(t, (b >> 1) & 0x78u);
+  return __builtin_bit_cast(half8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+}
+// 8 halves from four half2 entries indexed by the four nibbles of the low 16 bits of w
+__device__ __forceinline__ half8 nib4x2(const uint8_t* t, uint32_t w) {
+  return __builtin_bit_cast(half8, u32x4{lds32(t, (w << 2) & 0x3Cu), lds32(t, (w >> 2) & 0x3Cu),
+                                         lds32(t, (w >> 6) & 0x3Cu), lds32(t, (w >> 10) & 0x3Cu)});
+}
+// 8 halves from four half2 entries indexed by the four 6-bit fields of the low 24 bits of f
+__device__ __forceinline__ half8 six4x2(const uint8_t* t, uint32_t f) {
+  return __builtin_bit_cast(half8, u32x4{lds32(t, (f << 2) & 0xFCu), lds32(t, (f >> 4) & 0xFCu),
+                                         lds32(t, (f >> 10) & 0xFCu), lds32(t, (f >> 16) & 0xFCu)});
+}
+// 8 halves from four half2 entries indexed by the four bytes of w
+__device__ __forceinline__ half8 byte4x2(const uint8_t* t, uint32_t w) {
+  return __builtin_bit_cast(half8, u32x4{lds32(t, (w << 2) & 0x3FCu), lds32(t, (w >> 6) & 0x3FCu),
+                                         lds32(t, (w >> 14) & 0x3FCu), lds32(t, (w >> 22) & 0x3FCu)});
+}
+
+// Key operand of k-step ks: dims ks*8 .. ks*8+7 of the lane's 32-dim field
+template <int KB, int KW32>
+__device__ __forceinline__ half8 key_operand(const uint8_t* t, const uint32_t (&k)[KW32], int ks) {
+  if constexpr (KB == 1) {
+    return nib2x4(t, k[0] >> (8 * ks));
+  } else if constexpr (KB == 2) {
+    return nib4x2(t, k[ks >> 1] >> (16 * (ks & 1)));
+  } else {
+    const int bit = 24 * ks, wi = bit >> 5, sh = bit & 31;
+    const uint32_t lo32 = k[wi];
+    const uint32_t hi32 = (wi + 1 < KW32) ? k[wi + 1] : 0u;
+    return six4x2(t, sh ? __builtin_amdgcn_alignbit(hi32, lo32, sh) : lo32);
+  }
+}
+// Value operand: the 8 dims of one value field (VB bits each, LSB first)
+template <int VB>
+__device__ __forceinline__ half8 value_operand(const uint8_t* t, uint32_t w) {
+  if constexpr (VB == 2) return nib4x2(t, w);
+  else if constexpr (VB == 3) return six4x2(t, w);
+  else return byte4x2(t, w);
+}
+
+
+
+// Fused decode attention.  Lane (column l16, group lg) ends each 16-key block
+// with the scores of keys 4*lg + e for its own column, which is the P^T operand
+// layout of the value MFMA, so P never leaves registers.  Each wave owns
+// 16*NB consecutive keys per slab and keeps R slabs of raw records in flight.
+template <int D, int BITS, int NB, int R, bool PLO>
+__global__ void __launch_bounds__(256) decode_attn_kernel(DecodeArgs a) {
   static_assert(D == 128, "decode kernel is built for head_dim 128");
-  using L = DecodeLuts<BITS>;
+  using L = SmallLuts<BITS>;
   constexpr int KB = L::KB, VB = L::VB;
   constexpr int KS = D / 32;           // score k-steps
   constexpr int DB = D / 16;           // value row blocks
   constexpr int KC = D * KB / 8, SC = D / 8, VC = D * VB / 8;  // bytes per packed row
   constexpr int KLANE = KC / 4;        // key-code bytes per lane (4 lanes share a key row)
+  constexpr int KW32 = KLANE / 4;
+  constexpr int VW32 = (VB == 3) ? 2 : 1;  // dwords holding a lane's value field
+  constexpr int SLAB = 4 * 16 * NB;
   constexpr float LOG2E = 1.4426950408889634f;
+  constexpr float TAU = 8.0f;          // lazy-rescale headroom (log2 units)
 
-  // LUTs, reused as the wave-merge area once every wave is done
-  constexpr int MERGE_FLOATS = 4 * 16 * (D + 2);
-  constexpr int LDS_BYTES = (L::HALVES * 2 > MERGE_FLOATS * 4) ? L::HALVES * 2 : MERGE_FLOATS * 4;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
-  _Float16* lutS = reinterpret_cast<_Float16*>(lds);
-  _Float16* lutK = lutS + 256 * 8;
-  _Float16* lutV = lutK + L::KENT * L::KW;
+  __shared__ __attribute__((aligned(16))) uint8_t luts[L::BYTES];
+  __shared__ __attribute__((aligned(16))) float mrg[4 * 16 * (D + 2)];  // wave merge [wave][col][D + 2]
+  const uint8_t* tS = luts + L::SGN_OFF;
+  const uint8_t* tK = luts + L::KEY_OFF;
+  const uint8_t* tV = luts + L::VAL_OFF;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lg = lane >> 4;
   const int split = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
   const int64_t bh = static_cast<int64_t>(b) * a.Hkv + hkv;
 
-  // ---- tables
-  {
-    const _Float16 one = static_cast<_Float16>(1.f), mone = static_cast<_Float16>(-1.f);
-    for (int i = tid; i < 256 * 8; i += 256) lutS[i] = ((i >> 3) >> (i & 7)) & 1 ? one : mone;
-    for (int i = tid; i < L::KENT * L::KW; i += 256) {
-      const int idx = i / L::KW, e = i % L::KW;
-      lutK[i] = __builtin_bit_cast(_Float16, a.kcent[(idx >> (e * KB)) & ((1 << KB) - 1)]);
-    }
-    if constexpr (!SCORES) {
-      for (int i = tid; i < L::VENT * L::VW; i += 256) {
-        const int idx = i / L::VW, e = i % L::VW;
-        lutV[i] = static_cast<_Float16>(a.vcent[(idx >> (e * VB)) & ((1 << VB) - 1)]);
-      }
-    }
-  }
+  build_small_luts<BITS, true>(a, luts, tid);
 
-  // ---- this lane's column (query row i, head h) and q fragments (permuted k-slots)
-  const int col = l16;
-  const bool col_ok = col < a.C;
-  const int qi = col_ok ? col / a.G : 0, h = hkv * a.G + (col_ok ? col % a.G : 0);
+  // this lane's column (query row qi, head h) and its q fragments (permuted k-slots)
+  const bool col_ok = l16 < a.C;
+  const int qi = col_ok ? l16 / a.G : 0, h = hkv * a.G + (col_ok ? l16 % a.G : 0);
   half8 qr[KS], qp[KS];
   {
     const int64_t qrow = ((static_cast<int64_t>(b) * a.Hq + h) * a.Sq + qi) * D;
@@ -112,53 +262,59 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
   }
   __syncthreads();
 
-  const float fa = SCORES ? 1.f : a.scale * LOG2E;
+  const float fa = a.scale * LOG2E;
   const float fb = a.coeff * fa;
-  const int lim = qi + (a.Sk - a.Sq);  // causal: keys <= lim
+  const int lim = a.causal ? qi + (a.Sk - a.Sq) : 0x7fffffff;  // keys <= lim are visible
+  const int causal_from = a.causal ? a.Sk - a.Sq : 0x7fffffff;  // smallest lim of any column
   const int kbeg = split * a.chunk;
   const int kend = min(a.Sk, kbeg + a.chunk);
 
-  // per-lane registers of one 16-key block
+  // this lane's value field: dims l16*8 .. l16*8+7 of a value row, VB bytes at voff
+  const int voff = l16 * VB;
+  const int vbase = (VB == 3) ? min(voff & ~3, VC - 8) : (voff & ~3);
+  const int vsh = 8 * (voff - vbase);
+
   struct Raw {
-    uint32_t k[KLANE / 4];  // key-code bytes of (key m, group g)
-    uint32_t s;             // sign bytes of (key m, group g)
-    uint32_t v[4];          // value-code field (VB bytes) of keys 4g+kk at dims m*8..m*8+7
-    float kn[4], rn[4], vv[4];
+    uint32_t k[KW32];          // key-code bytes of (key l16, group lg)
+    uint32_t s;                // sign bytes of (key l16, group lg)
+    uint32_t nk[2], nr[2], nv[2];  // f16 norms of keys 4lg .. 4lg+3
+    uint32_t v[4][VW32];       // value-field dwords of keys 4lg + kk
   };
-  auto load = [&](int k0, Raw& r) {
-    const int key = k0 + l16;  // row of this lane's key / sign operand
-    if (key < kend) {
-      const uint32_t* kp = reinterpret_cast<const uint32_t*>(a.kcodes + (bh * a.Sk + key) * KC + lg * KLANE);
-#pragma unroll
-      for (int j = 0; j < KLANE / 4; ++j) r.k[j] = kp[j];
-      r.s = *reinterpret_cast<const uint32_t*>(a.ksigns + (bh * a.Sk + key) * SC + lg * (SC / 4));
+  // this (b, kv head)'s planes; each block reads rows [kb, kend) through its own resource
+  const int64_t g0 = bh * a.Sk;
+  const uint8_t* pk = a.kcodes + g0 * KC;
+  const uint8_t* ps = a.ksigns + g0 * SC;
+  const uint16_t* pkn = a.kvn + g0;
+  const uint16_t* prn = a.krn + g0;
+  const uint16_t* pvn = a.vvn + g0;
+  const uint8_t* pv = a.vcodes + g0 * VC;
+  const bool norms_aligned = ((reinterpret_cast<uintptr_t>(pkn) | reinterpret_cast<uintptr_t>(prn) |
+                               reinterpret_cast<uintptr_t>(pvn)) & 7) == 0;
+  const uint32_t ok_off = l16 * KC + lg * KLANE, os_off = l16 * SC + lg * 4, on_off = 8 * lg;
+  const uint32_t ov_off = 4 * lg * VC + vbase;
+
+  auto load = [&](int kb, Raw& r) {
+    bload(rows_rsrc(pk, KC, kb, kend), ok_off, 0, r.k);
+    r.s = __builtin_amdgcn_raw_buffer_load_b32(rows_rsrc(ps, SC, kb, kend), os_off, 0, kStream);
+    const rsrc_t rkn = rows_rsrc(pkn, 2, kb, kend), rrn = rows_rsrc(prn, 2, kb, kend),
+                 rvn = rows_rsrc(pvn, 2, kb, kend);
+    if (kb + 16 <= kend && norms_aligned && (kb & 3) == 0) {
+      uint32_t t[2];
+      bload(rkn, on_off, 0, t); r.nk[0] = t[0]; r.nk[1] = t[1];
+      bload(rrn, on_off, 0, t); r.nr[0] = t[0]; r.nr[1] = t[1];
+      bload(rvn, on_off, 0, t); r.nv[0] = t[0]; r.nv[1] = t[1];
     } else {
 #pragma unroll
-      for (int j = 0; j < KLANE / 4; ++j) r.k[j] = 0u;
-      r.s = 0u;
-    }
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int vk = k0 + lg * 4 + kk;  // key of this lane's score rows / value k-slots
-      const bool ok = vk < kend;
-      const int64_t row = bh * a.Sk + vk;
-      r.kn[kk] = ok ? h2f(a.kvn[row]) : 0.f;
-      r.rn[kk] = ok ? h2f(a.krn[row]) : 0.f;
-      if constexpr (!SCORES) {
-        r.vv[kk] = ok ? h2f(a.vvn[row]) : 0.f;
-        uint32_t w = 0u;
-        if (ok) {
-          const uint8_t* vp = a.vcodes + row * VC;
-          const int off = l16 * VB;  // byte offset of dims l16*8 .. +7
-          const uint32_t* wp = reinterpret_cast<const uint32_t*>(vp + (off & ~3));
-          const int sh = off & 3;
-          w = wp[0];
-          if (sh + VB > 4) w = __builtin_amdgcn_alignbyte(wp[1], w, sh);
-          else if (sh) w >>= 8 * sh;
-        }
-        r.v[kk] = w;
+      for (int i = 0; i < 2; ++i) {
+        const uint32_t o0 = on_off + 4 * i, o1 = o0 + 2;
+        r.nk[i] = bload16(rkn, o0, 0) | (bload16(rkn, o1, 0) << 16);
+        r.nr[i] = bload16(rrn, o0, 0) | (bload16(rrn, o1, 0) << 16);
+        r.nv[i] = bload16(rvn, o0, 0) | (bload16(rvn, o1, 0) << 16);
       }
     }
+    const rsrc_t rv = rows_rsrc(pv, VC, kb, kend);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) bload(rv, ov_off + kk * VC, 0, r.v[kk]);
   };
 
   float m_run = -INFINITY, l_run = 0.f;
@@ -166,159 +322,251 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
 #pragma unroll
   for (int db = 0; db < DB; ++db) oacc[db] = float4v{0.f, 0.f, 0.f, 0.f};
 
-  Raw cur, nxt;
-  int k0 = kbeg + wave * 16;
-  if (k0 < kend) load(k0, cur);
-  for (; k0 < kend; k0 += 64) {
-    const bool more = k0 + 64 < kend;
-    if (more) load(k0 + 64, nxt);
-
-    // ---- scores: two accumulators over KS k-steps
+  auto block = [&](int kb, const Raw& r) {
+    // ---- scores S^T = K^ Q^T (term 1) and Sign Q_proj^T (term 2)
     float4v s1 = float4v{0.f, 0.f, 0.f, 0.f}, s2 = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      half8 ka;
-      if constexpr (KB == 1) {
-        const uint32_t byte = (cur.k[0] >> (8 * ks)) & 0xffu;
-        ka = *reinterpret_cast<const half8*>(&lutK[byte * 8]);
-      } else if constexpr (KB == 2) {
-        const uint32_t two = (cur.k[ks >> 1] >> (16 * (ks & 1))) & 0xffffu;
-        const half4 lo = *reinterpret_cast<const half4*>(&lutK[(two & 0xffu) * 4]);
-        const half4 hi = *reinterpret_cast<const half4*>(&lutK[(two >> 8) * 4]);
-        ka = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      } else {
-        // 24 bits of k-step ks start at bit 24*ks of the lane's 96-bit field
-        const int bit = 24 * ks, wi = bit >> 5, sh = bit & 31;
-        const uint32_t lo32 = cur.k[wi];
-        const uint32_t hi32 = (wi + 1 < KLANE / 4) ? cur.k[wi + 1] : 0u;
-        const uint32_t f = sh ? __builtin_amdgcn_alignbit(hi32, lo32, sh) : lo32;
-        const half4 lo = *reinterpret_cast<const half4*>(&lutK[(f & 0xfffu) * 4]);
-        const half4 hi = *reinterpret_cast<const half4*>(&lutK[((f >> 12) & 0xfffu) * 4]);
-        ka = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      }
-      const half8 sa = *reinterpret_cast<const half8*>(&lutS[((cur.s >> (8 * ks)) & 0xffu) * 8]);
-      s1 = mfma16x16x32(ka, qr[ks], s1);
-      s2 = mfma16x16x32(sa, qp[ks], s2);
+      s1 = mfma16x16x32(key_operand<KB, KW32>(tK, r.k, ks), qr[ks], s1);
+      s2 = mfma16x16x32(nib2x4(tS, r.s >> (8 * ks)), qp[ks], s2);
     }
-
-    if constexpr (SCORES) {
-      if (col_ok) {
-        float* orow = a.scores + ((static_cast<int64_t>(b) * a.Hq + h) * a.Sq + qi) * a.Sk;
+    // ---- log2-domain scores of keys 4lg + e for this column
+    float sc[4], vv[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int key = k0 + lg * 4 + e;
-          if (key < kend) orow[key] = s1[e] * (fa * cur.kn[e]) + s2[e] * (fb * cur.rn[e]);
-        }
-      }
-    } else {
-      // ---- online softmax (log2 units, lazily rescaled)
-      float sc[4];
-      float tmax = -INFINITY;
+    for (int e = 0; e < 4; ++e) {
+      const int w = e >> 1, t = 16 * (e & 1);
+      const float kn = h2f(static_cast<uint16_t>(r.nk[w] >> t));
+      const float rn = h2f(static_cast<uint16_t>(r.nr[w] >> t));
+      vv[e] = h2f(static_cast<uint16_t>(r.nv[w] >> t));
+      sc[e] = s1[e] * (fa * kn) + s2[e] * (fb * rn);
+    }
+    if (kb + 16 > kend || kb + 15 > causal_from || a.mask) {  // wave-uniform edge test
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int key = k0 + lg * 4 + e;
-        float v = s1[e] * (fa * cur.kn[e]) + s2[e] * (fb * cur.rn[e]);
+        const int key = kb + 4 * lg + e;
         if (a.mask && col_ok && key < kend)
-          v += fmaxf(a.mask[b * a.smb + h * a.smh + static_cast<int64_t>(qi) * a.smq +
-                            static_cast<int64_t>(key) * a.smk] * LOG2E,
-                     -3.0e38f);
-        if (key >= kend || (a.causal && key > lim)) v = -INFINITY;
-        sc[e] = v;
-        tmax = fmaxf(tmax, v);
+          sc[e] += fmaxf(a.mask[b * a.smb + h * a.smh + static_cast<int64_t>(qi) * a.smq +
+                                static_cast<int64_t>(key) * a.smk] * LOG2E,
+                         -3.0e38f);
+        if (key >= kend || key > lim) sc[e] = -INFINITY;
       }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const bool grow = tmax > m_run + 8.0f;
-      if (__any(grow)) {
-        const float m_new = grow ? tmax : m_run;
-        const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
-        m_run = m_new;
+    }
+    // ---- lazy online softmax: the column reference m_run moves only when a score
+    // exceeds it by more than TAU; p = 2^(s - m_run - TAU) <= 1
+    const float lmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    if (__any(lmax > m_run + TAU)) {
+      float t = lmax;
+      t = fmaxf(t, __shfl_xor(t, 16, 64));
+      t = fmaxf(t, __shfl_xor(t, 32, 64));
+      if (t > m_run + TAU) {
+        const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - t);
+        m_run = t;
         l_run *= alpha;
 #pragma unroll
         for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
       }
-      // p = 2^(s - m_run - TAU) <= 1, so P * vn stays inside f16 range for any f16 norm;
-      // (m_run + TAU) is the reference the partial's (O, l) are scaled to
-      const float m_use = (m_run == -INFINITY) ? 0.f : m_run + 8.0f;
-      half4 ph, pl;
+    }
+    const float m_use = (m_run == -INFINITY) ? 0.f : m_run + TAU;
+    half4 ph, pl;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float p = __builtin_amdgcn_exp2f(sc[e] - m_use);
-        l_run += p;
-        const float pv = p * cur.vv[e];
-        const _Float16 hh = static_cast<_Float16>(pv);
-        ph[e] = hh;
-        pl[e] = static_cast<_Float16>(pv - static_cast<float>(hh));
-      }
-      // ---- value operands: per key kk the 8 values of dims l16*8 + db, db = 0..7
-      half8 vals[4];
+    for (int e = 0; e < 4; ++e) {
+      const float p = __builtin_amdgcn_exp2f(sc[e] - m_use);
+      l_run += p;
+      const float pv = p * vv[e];
+      const _Float16 hh = static_cast<_Float16>(pv);
+      ph[e] = hh;
+      if constexpr (PLO) pl[e] = static_cast<_Float16>(pv - static_cast<float>(hh));
+    }
+    // ---- value operands: per key kk the 8 values of dims l16*8 + db
+    half8 vals[4];
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const uint32_t w = cur.v[kk];
-        if constexpr (VB == 2) {
-          const half4 lo = *reinterpret_cast<const half4*>(&lutV[(w & 0xffu) * 4]);
-          const half4 hi = *reinterpret_cast<const half4*>(&lutV[((w >> 8) & 0xffu) * 4]);
-          vals[kk] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        } else if constexpr (VB == 3) {
-          const half4 lo = *reinterpret_cast<const half4*>(&lutV[(w & 0xfffu) * 4]);
-          const half4 hi = *reinterpret_cast<const half4*>(&lutV[((w >> 12) & 0xfffu) * 4]);
-          vals[kk] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        } else {
-          half8 v8;
+    for (int kk = 0; kk < 4; ++kk) {
+      uint32_t w;
+      if constexpr (VB == 3)
+        w = static_cast<uint32_t>(((static_cast<uint64_t>(r.v[kk][1]) << 32) | r.v[kk][0]) >> vsh);
+      else
+        w = r.v[kk][0] >> vsh;
+      vals[kk] = value_operand<VB>(tV, w);
+    }
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const half2v t = *reinterpret_cast<const half2v*>(&lutV[((w >> (8 * q)) & 0xffu) * 2]);
-            v8[2 * q] = t[0];
-            v8[2 * q + 1] = t[1];
-          }
-          vals[kk] = v8;
+    for (int db = 0; db < DB; ++db) {
+      const half4 va = half4{vals[0][db], vals[1][db], vals[2][db], vals[3][db]};
+      oacc[db] = mfma16x16x16(va, ph, oacc[db]);
+      if constexpr (PLO) oacc[db] = mfma16x16x16(va, pl, oacc[db]);
+    }
+  };
+
+  Raw ring[R][NB];
+  const int k0w = kbeg + wave * 16 * NB;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+      if (k0w + r * SLAB + 16 * j < kend) load(k0w + r * SLAB + 16 * j, ring[r][j]);
+  for (int k0 = k0w; k0 < kend; k0 += R * SLAB) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const int kb = k0 + r * SLAB + 16 * j;
+        if (kb < kend) {
+          block(kb, ring[r][j]);
+          if (kb + R * SLAB < kend) load(kb + R * SLAB, ring[r][j]);
         }
       }
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const half4 va = half4{vals[0][db], vals[1][db], vals[2][db], vals[3][db]};
-        oacc[db] = mfma16x16x16(va, ph, oacc[db]);
-        oacc[db] = mfma16x16x16(va, pl, oacc[db]);
-      }
     }
-    if (more) cur = nxt;
   }
 
-  if constexpr (!SCORES) {
-    // ---- merge the 4 waves of the block in LDS, write one partial per block
-    __syncthreads();  // all waves done with the tables
-    float* mrg = reinterpret_cast<float*>(lds);  // [wave][col][D + 2]
-    float l = l_run;
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
-    float* mine = mrg + (wave * 16 + col) * (D + 2);
+  // ---- merge the 4 waves of the block in LDS, write one partial per block
+  float l = l_run;
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  float* mine = mrg + (wave * 16 + l16) * (D + 2);
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+  for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) mine[(lg * 4 + e) * (D / 16) + db] = oacc[db][e];
-    if (lg == 0) {
-      mine[D] = (m_run == -INFINITY) ? m_run : m_run + 8.0f;
-      mine[D + 1] = l;
+    for (int e = 0; e < 4; ++e) mine[(lg * 4 + e) * (D / 16) + db] = oacc[db][e];
+  if (lg == 0) {
+    mine[D] = (m_run == -INFINITY) ? m_run : m_run + TAU;
+    mine[D + 1] = l;
+  }
+  __syncthreads();
+  const int64_t pbase = (bh * a.nsplit + split) * a.C;
+  for (int it = tid; it < a.C * D; it += 256) {
+    const int c = it / D, d = it % D;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, mrg[(w * 16 + c) * (D + 2) + D]);
+    float o = 0.f, ls = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float* src = mrg + (w * 16 + c) * (D + 2);
+      const float sc = (src[D] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(src[D] - mx);
+      o += sc * src[d];
+      ls += sc * src[D + 1];
     }
-    __syncthreads();
-    const int64_t pbase = (bh * a.nsplit + split) * a.C;
-    for (int it = tid; it < a.C * D; it += 256) {
-      const int c = it / D, d = it % D;
-      float mx = -INFINITY;
+    a.part_o[(pbase + c) * D + d] = o;
+    if (d == 0) {
+      a.part_ml[(pbase + c) * 2] = mx;
+      a.part_ml[(pbase + c) * 2 + 1] = ls;
+    }
+  }
+}
+
+// Scores only: S = Q K^T with the keys on the MFMA's n side, so that lane
+// (key l16, group lg) ends with the scores of columns 4*lg + e for its own key:
+// one norm pair per lane, and each column's 16 scores leave as one 64-byte run.
+// Each wave owns 16*NB consecutive keys per slab and keeps two slabs of raw
+// records in flight (ring of 2) while it scores the oldest.
+template <int D, int BITS, int NB>
+__global__ void __launch_bounds__(256) decode_scores_kernel(DecodeArgs a) {
+  static_assert(D == 128, "decode kernel is built for head_dim 128");
+  using L = SmallLuts<BITS>;
+  constexpr int KB = L::KB;
+  constexpr int KS = D / 32;
+  constexpr int KC = D * KB / 8, SC = D / 8;
+  constexpr int KLANE = KC / 4;
+  constexpr int KW32 = KLANE / 4;
+  constexpr int SLAB = 4 * 16 * NB;  // keys per block iteration
+  constexpr int R = TQ_DEC_R;        // slabs in flight per wave
+
+  __shared__ __attribute__((aligned(16))) uint8_t luts[L::BYTES];
+  const uint8_t* tS = luts + L::SGN_OFF;
+  const uint8_t* tK = luts + L::KEY_OFF;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int split = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
+  const int64_t bh = static_cast<int64_t>(b) * a.Hkv + hkv;
+
+  build_small_luts<BITS, false>(a, luts, tid);
+
+  // A operand: query column l16 (row i, head h), dims lg*D/4 + ks*8 + 0..7
+  half8 qr[KS], qp[KS];
+  {
+    const bool ok = l16 < a.C;
+    const int qi = ok ? l16 / a.G : 0, h = hkv * a.G + (ok ? l16 % a.G : 0);
+    const int64_t qrow = ((static_cast<int64_t>(b) * a.Hq + h) * a.Sq + qi) * D;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) mx = fmaxf(mx, mrg[(w * 16 + c) * (D + 2) + D]);
-      float o = 0.f, ls = 0.f;
+    for (int ks = 0; ks < KS; ++ks) {
+      const int d0 = lg * (D / 4) + ks * 8;
+      qr[ks] = ok ? *reinterpret_cast<const half8*>(a.q_rot + qrow + d0) : half8{};
+      qp[ks] = ok ? *reinterpret_cast<const half8*>(a.q_proj + qrow + d0) : half8{};
+    }
+  }
+  __syncthreads();
+
+  const int kbeg = split * a.chunk;
+  const int kend = min(a.Sk, kbeg + a.chunk);
+  const float fb = a.coeff;
+
+  // output: the C score rows of this (b, kv head) are contiguous [C][Sk] f32
+  // (head h = hkv*G + c%G, query row c/G); invalid columns aim past the end and
+  // are dropped by the store's range check
+  const float* pout = a.scores + (static_cast<int64_t>(b) * a.Hq + hkv * a.G) * a.Sq * a.Sk;
+  const uint32_t out_bytes = static_cast<uint32_t>(a.C) * a.Sk * 4;
+  uint32_t oo[4];
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float* src = mrg + (w * 16 + c) * (D + 2);
-        const float sc = (src[D] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(src[D] - mx);
-        o += sc * src[d];
-        ls += sc * src[D + 1];
+  for (int e = 0; e < 4; ++e) {
+    const int c = 4 * lg + e;
+    oo[e] = c < a.C ? static_cast<uint32_t>((c % a.G) * a.Sq + c / a.G) * a.Sk * 4 + 4 * l16 : kOutOfRange;
+  }
+
+  struct Raw {
+    uint32_t k[KW32];
+    uint32_t s;
+    uint32_t kn, rn;
+  };
+  // this (b, kv head)'s planes; each block reads rows [kb, kend) through its own resource
+  const int64_t g0 = bh * a.Sk;
+  const uint8_t* pk = a.kcodes + g0 * KC;
+  const uint8_t* ps = a.ksigns + g0 * SC;
+  const uint16_t* pkn = a.kvn + g0;
+  const uint16_t* prn = a.krn + g0;
+  const uint32_t ok_off = l16 * KC + lg * KLANE, os_off = l16 * SC + lg * 4, on_off = 2 * l16;
+  auto load = [&](int k0, Raw (&r)[NB]) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int kb = k0 + 16 * j;
+      bload(rows_rsrc(pk, KC, kb, kend), ok_off, 0, r[j].k);
+      r[j].s = __builtin_amdgcn_raw_buffer_load_b32(rows_rsrc(ps, SC, kb, kend), os_off, 0, kStream);
+      r[j].kn = bload16(rows_rsrc(pkn, 2, kb, kend), on_off, 0);
+      r[j].rn = bload16(rows_rsrc(prn, 2, kb, kend), on_off, 0);
+    }
+  };
+  auto score = [&](int k0, const Raw (&r)[NB]) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      float4v s1 = float4v{0.f, 0.f, 0.f, 0.f}, s2 = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        s1 = mfma16x16x32(qr[ks], key_operand<KB, KW32>(tK, r[j].k, ks), s1);
+        s2 = mfma16x16x32(qp[ks], nib2x4(tS, r[j].s >> (8 * ks)), s2);
       }
-      a.part_o[(pbase + c) * D + d] = o;
-      if (d == 0) {
-        a.part_ml[(pbase + c) * 2] = mx;
-        a.part_ml[(pbase + c) * 2 + 1] = ls;
+      const int kb = k0 + 16 * j;
+      const float kn = h2f(static_cast<uint16_t>(r[j].kn)), rn = fb * h2f(static_cast<uint16_t>(r[j].rn));
+      const rsrc_t ro = make_rsrc(pout + kb, out_bytes - static_cast<uint32_t>(kb) * 4);
+      if (kb + 16 <= kend || kb + l16 < kend) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, s1[e] * kn + s2[e] * rn), ro, oo[e], 0,
+                                                2);
+      }
+    }
+  };
+
+  Raw ring[R][NB];
+  const int k0w = kbeg + wave * 16 * NB;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (k0w + r * SLAB < kend) load(k0w + r * SLAB, ring[r]);
+  for (int k0 = k0w; k0 < kend; k0 += R * SLAB) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int kb = k0 + r * SLAB;
+      if (kb < kend) {
+        score(kb, ring[r]);
+        if (kb + R * SLAB < kend) load(kb + R * SLAB, ring[r]);
       }
     }
   }
@@ -446,25 +694,44 @@ struct DecodePlan {
   int64_t ws_bytes;
 };
 
-static DecodePlan plan_decode(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
-  DecodePlan p{false, 0, 0, 0};
-  if (d != 128 || bits < 2 || bits > 4 || Hkv <= 0 || Hq % Hkv) return p;
-  const int C = (Hq / Hkv) * Sq;
-  if (C > 16 || Sk < 1) return p;
+
+// Split S_k so that about `target` blocks cover the (batch, kv head) groups, each
+// split a multiple of `quantum` keys and no shorter than `min_chunk`.
+static DecodePlan plan_split(int B, int Hkv, int Sk, int target, int quantum, int min_chunk) {
+  DecodePlan p{true, 0, 0, 0};
   const int64_t groups = static_cast<int64_t>(B) * Hkv;
-  int nsplit = static_cast<int>((1024 + groups - 1) / groups);
-  const int max_split = (Sk + 255) / 256;
+  int nsplit = static_cast<int>((target + groups - 1) / groups);
+  const int max_split = (Sk + min_chunk - 1) / min_chunk;
   if (nsplit > max_split) nsplit = max_split;
   if (nsplit > 1024) nsplit = 1024;
   if (nsplit < 1) nsplit = 1;
   int chunk = (Sk + nsplit - 1) / nsplit;
-  chunk = (chunk + 63) / 64 * 64;
-  nsplit = (Sk + chunk - 1) / chunk;
-  p.use = true;
-  p.nsplit = nsplit;
+  chunk = (chunk + quantum - 1) / quantum * quantum;
+  p.nsplit = (Sk + chunk - 1) / chunk;
   p.chunk = chunk;
-  p.ws_bytes = groups * nsplit * C * static_cast<int64_t>(d + 2) * 4;
   return p;
+}
+
+// head_dim 128, bits 2-4, at most 16 query columns per kv head; S_k below 2^24
+// keeps every per-group byte offset of the planes and score rows under 2^31
+static bool decode_shape(int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
+  if (d != 128 || bits < 2 || bits > 4 || Hkv <= 0 || Hq % Hkv) return false;
+  return (Hq / Hkv) * Sq <= 16 && Sk >= 1 && Sk < (1 << 24);
+}
+
+static DecodePlan plan_decode(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
+  if (!decode_shape(Hq, Hkv, Sq, Sk, d, bits)) return DecodePlan{false, 0, 0, 0};
+  constexpr int slab = 64 * TQ_DEC_ANB;
+  DecodePlan p = plan_split(B, Hkv, Sk, TQ_DEC_ATTN_BLOCKS, slab, 2 * slab);
+  const int C = (Hq / Hkv) * Sq;
+  p.ws_bytes = static_cast<int64_t>(B) * Hkv * p.nsplit * C * static_cast<int64_t>(d + 2) * 4;
+  return p;
+}
+
+static DecodePlan plan_scores(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
+  if (!decode_shape(Hq, Hkv, Sq, Sk, d, bits)) return DecodePlan{false, 0, 0, 0};
+  constexpr int slab = 64 * TQ_DEC_NB;
+  return plan_split(B, Hkv, Sk, TQ_DEC_SCORE_BLOCKS, slab, 2 * slab);
 }
 
 }  // namespace tq
@@ -483,17 +750,17 @@ bool decode_applies(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
   return plan_decode(B, Hq, Hkv, Sq, Sk, d, bits).use;
 }
 
-template <int BITS, bool SCORES>
-static void launch_decode(const DecodeArgs& a, hipStream_t s) {
+template <int BITS>
+static void launch_decode_attn(const DecodeArgs& a, hipStream_t s) {
   dim3 grid(a.nsplit, a.Hkv, a.B);
-  decode_kernel<128, BITS, SCORES><<<grid, 256, 0, s>>>(a);
+  decode_attn_kernel<128, BITS, TQ_DEC_ANB, TQ_DEC_AR, TQ_DEC_PLO != 0><<<grid, 256, 0, s>>>(a);
 }
 
 int decode_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
                   const uint8_t* ksigns, const uint16_t* krn, const uint16_t* kvn, const uint16_t* kcent,
                   int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits, float coeff, float* out,
                   hipStream_t s) {
-  const DecodePlan p = plan_decode(B, Hq, Hkv, Sq, Sk, d, bits);
+  const DecodePlan p = plan_scores(B, Hq, Hkv, Sq, Sk, d, bits);
   DecodeArgs a{};
   a.q_rot = q_rot;
   a.q_proj = q_proj;
@@ -514,9 +781,10 @@ int decode_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* 
   a.coeff = coeff;
   a.scale = 1.f;
   a.scores = out;
-  if (bits == 2) launch_decode<2, true>(a, s);
-  else if (bits == 3) launch_decode<3, true>(a, s);
-  else launch_decode<4, true>(a, s);
+  dim3 grid(a.nsplit, a.Hkv, a.B);
+  if (bits == 2) decode_scores_kernel<128, 2, TQ_DEC_NB><<<grid, 256, 0, s>>>(a);
+  else if (bits == 3) decode_scores_kernel<128, 3, TQ_DEC_NB><<<grid, 256, 0, s>>>(a);
+  else decode_scores_kernel<128, 4, TQ_DEC_NB><<<grid, 256, 0, s>>>(a);
   return launch_status("tq_attention_scores (decode)");
 }
 
@@ -560,9 +828,9 @@ int decode_attention(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_
   const int64_t n_part = static_cast<int64_t>(B) * Hkv * p.nsplit * a.C;
   a.part_o = ws;
   a.part_ml = ws + n_part * d;
-  if (bits == 2) launch_decode<2, false>(a, s);
-  else if (bits == 3) launch_decode<3, false>(a, s);
-  else launch_decode<4, false>(a, s);
+  if (bits == 2) launch_decode_attn<2>(a, s);
+  else if (bits == 3) launch_decode_attn<3>(a, s);
+  else launch_decode_attn<4>(a, s);
   int st = launch_status("tq_attention_fwd (decode)");
   if (st != TQ_OK) return st;
   MergeArgs m{};
