@@ -28,19 +28,22 @@
 #define TQ_DEC_R 3
 #endif
 #ifndef TQ_DEC_ATTN_BLOCKS
-#define TQ_DEC_ATTN_BLOCKS 2048
+#define TQ_DEC_ATTN_BLOCKS 768
 #endif
 #ifndef TQ_DEC_SCORE_BLOCKS
 #define TQ_DEC_SCORE_BLOCKS 2048
 #endif
 #ifndef TQ_DEC_ANB
-#define TQ_DEC_ANB 1
+#define TQ_DEC_ANB 2
 #endif
 #ifndef TQ_DEC_AR
-#define TQ_DEC_AR 2
+#define TQ_DEC_AR 3
 #endif
 #ifndef TQ_DEC_PLO
 #define TQ_DEC_PLO 1
+#endif
+#ifndef TQ_DEC_ATTN_LDS
+#define TQ_DEC_ATTN_LDS 1
 #endif
 
 namespace tq {
@@ -87,6 +90,43 @@ __device__ __forceinline__ void bload(rsrc_t r, uint32_t voff, uint32_t soff, ui
 __device__ __forceinline__ uint32_t bload16(rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, kStream);
 }
+// Direct-to-LDS copies (buffer_load ... lds): every lane moves 16 bytes (or one
+// u16, zero-extended to a dword) from its resource offset into LDS at
+// M0 + lane*16 (lane*4).  They are issued through inline asm so that the compiler
+// does not serialise them against LDS reads of other ring slots; the kernel waits
+// for a slot itself with wait_vm<N>() (vmcnt completes in issue order, so DMAs the
+// compiler does not count only make its own waits stronger).  The kernel keeps
+// no value of its own in M0.
+typedef __attribute__((address_space(3))) void* lds_void_t;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t)(const_cast<void*>(p))));
+}
+__device__ __forceinline__ i32x4 rows_desc(const void* plane, int rb, int kb, int kend) {
+  const uint64_t base = reinterpret_cast<uint64_t>(static_cast<const uint8_t*>(plane) + static_cast<int64_t>(kb) * rb);
+  return i32x4{static_cast<int>(static_cast<uint32_t>(base)), static_cast<int>(static_cast<uint32_t>(base >> 32) & 0xffffu),
+               static_cast<int>(static_cast<uint32_t>(kend - kb) * rb), 0x00020000};
+}
+// descriptor and LDS address are wave-uniform; readfirstlane lets the compiler
+// prove it where the call sits under a lane-dependent branch
+__device__ __forceinline__ i32x4 uniform4(i32x4 r) {
+  return i32x4{__builtin_amdgcn_readfirstlane(r[0]), __builtin_amdgcn_readfirstlane(r[1]),
+               __builtin_amdgcn_readfirstlane(r[2]), __builtin_amdgcn_readfirstlane(r[3])};
+}
+__device__ __forceinline__ void dma16(i32x4 r, uint32_t lds, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(uniform4(r)) : "memory", "m0");
+}
+__device__ __forceinline__ void dma_u16(i32x4 r, uint32_t lds, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_ushort %1, %2, 0 offen nt lds"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(uniform4(r)) : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 struct DecodeArgs {
   const uint16_t *q_rot, *q_proj;
@@ -453,6 +493,287 @@ __global__ void __launch_bounds__(256) decode_attn_kernel(DecodeArgs a) {
   }
 }
 
+// Fused decode attention, LDS-staged.  Each wave streams 64-key slabs of the key
+// codes, sign bits, value codes and the three norm planes straight into its own
+// LDS ring (R slots) with direct-to-LDS buffer loads, so many KB per wave are in
+// flight without holding registers; lanes then gather their MFMA operands from
+// the slot.  Lane (column l16, group lg) ends each 16-key block with the scores
+// of keys 4*lg + e for its own column, which is the P^T operand layout of the
+// value MFMA, so P never leaves registers.
+template <int D, int BITS, int NBS, int R, bool PLO>
+__global__ void __launch_bounds__(256) decode_attn_lds_kernel(DecodeArgs a) {
+  static_assert(D == 128, "decode kernel is built for head_dim 128");
+  using L = SmallLuts<BITS>;
+  constexpr int KB = L::KB, VB = L::VB;
+  constexpr int KS = D / 32;           // score k-steps
+  constexpr int DB = D / 16;           // value row blocks
+  constexpr int KC = D * KB / 8, SC = D / 8, VC = D * VB / 8;  // bytes per packed row
+  constexpr int KLANE = KC / 4;        // key-code bytes per lane (4 lanes share a key row)
+  constexpr int KW32 = KLANE / 4;
+  constexpr int VW32 = (VB == 3) ? 2 : 1;  // dwords holding a lane's value field
+  constexpr int NK = 16 * NBS;         // keys per wave slab
+  constexpr int SLAB = 4 * NK;         // keys per block slab
+  constexpr int OFF_K = 0, OFF_S = NK * KC, OFF_V = OFF_S + NK * SC, OFF_N = OFF_V + NK * VC;
+  constexpr int NRM = NK * 4;          // one norm plane: a dword per key
+  constexpr int SLOT = OFF_N + 3 * NRM;
+  constexpr int STAGE = 4 * R * SLOT;
+  constexpr int MERGE = 4 * 16 * (D + 2) * 4;
+  static_assert(NBS == 2 || NBS == 4, "slabs of 32 or 64 keys");
+  constexpr float LOG2E = 1.4426950408889634f;
+  constexpr float TAU = 8.0f;          // lazy-rescale headroom (log2 units)
+
+  __shared__ __attribute__((aligned(16))) uint8_t luts[L::BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t stage[STAGE > MERGE ? STAGE : MERGE];
+  const uint8_t* tS = luts + L::SGN_OFF;
+  const uint8_t* tK = luts + L::KEY_OFF;
+  const uint8_t* tV = luts + L::VAL_OFF;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int split = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
+  const int64_t bh = static_cast<int64_t>(b) * a.Hkv + hkv;
+
+  build_small_luts<BITS, true>(a, luts, tid);
+
+  const bool col_ok = l16 < a.C;
+  const int qi = col_ok ? l16 / a.G : 0, h = hkv * a.G + (col_ok ? l16 % a.G : 0);
+  half8 qr[KS], qp[KS];
+  {
+    const int64_t qrow = ((static_cast<int64_t>(b) * a.Hq + h) * a.Sq + qi) * D;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int d0 = lg * (D / 4) + ks * 8;
+      qr[ks] = col_ok ? *reinterpret_cast<const half8*>(a.q_rot + qrow + d0) : half8{};
+      qp[ks] = col_ok ? *reinterpret_cast<const half8*>(a.q_proj + qrow + d0) : half8{};
+    }
+  }
+
+  const float fa = a.scale * LOG2E;
+  const float fb = a.coeff * fa;
+  const int lim = a.causal ? qi + (a.Sk - a.Sq) : 0x7fffffff;  // keys <= lim are visible
+  const int causal_from = a.causal ? a.Sk - a.Sq : 0x7fffffff;  // smallest lim of any column
+  const int kbeg = split * a.chunk;
+  const int kend = min(a.Sk, kbeg + a.chunk);
+
+  const int voff = l16 * VB;
+  const int vbase = (VB == 3) ? min(voff & ~3, VC - 8) : (voff & ~3);
+  const int vsh = 8 * (voff - vbase);
+
+  const int64_t g0 = bh * a.Sk;
+  const uint8_t* pk = a.kcodes + g0 * KC;
+  const uint8_t* ps = a.ksigns + g0 * SC;
+  const uint16_t* pkn = a.kvn + g0;
+  const uint16_t* prn = a.krn + g0;
+  const uint16_t* pvn = a.vvn + g0;
+  const uint8_t* pv = a.vcodes + g0 * VC;
+
+  uint8_t* mine = stage + wave * (R * SLOT);
+  const uint32_t mine_lds = lds_offset(mine);
+  constexpr int NKD = (NK * KC + 1023) / 1024, NSD = (NK * SC + 1023) / 1024, NVD = (NK * VC + 1023) / 1024;
+  constexpr int NDMA = NKD + NSD + NVD + 3;  // DMA instructions per slot
+  // a plane of `bytes` (a multiple of 512) moves in 1 KB rounds of 64 lanes x 16 B;
+  // a final half round uses lanes 0-31 only
+  auto copy_plane = [&](const i32x4& r, uint32_t dst, int bytes, int nrounds) {
+    const uint32_t lo = lane * 16;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (c >= nrounds) break;
+      if ((c + 1) * 1024 <= bytes || lane < 32) dma16(r, dst + c * 1024, lo + c * 1024);
+    }
+  };
+  // DMA the wave's slab of keys [kb, kb + NK) into ring slot `slot`; rows past kend read zero
+  auto issue = [&](int kb, int slot) {
+    const uint32_t dst = mine_lds + slot * SLOT;
+    wait_lds();  // earlier reads of this slot have landed
+    copy_plane(rows_desc(pk, KC, kb, kend), dst + OFF_K, NK * KC, NKD);
+    copy_plane(rows_desc(ps, SC, kb, kend), dst + OFF_S, NK * SC, NSD);
+    copy_plane(rows_desc(pv, VC, kb, kend), dst + OFF_V, NK * VC, NVD);
+    if (NK == 64 || lane < 32) {
+      dma_u16(rows_desc(pkn, 2, kb, kend), dst + OFF_N, lane * 2);
+      dma_u16(rows_desc(prn, 2, kb, kend), dst + OFF_N + NRM, lane * 2);
+      dma_u16(rows_desc(pvn, 2, kb, kend), dst + OFF_N + 2 * NRM, lane * 2);
+    }
+  };
+  // wait until the slot issued `later` slots ago has landed
+  auto wait_slot = [&](int later) {
+    static_assert(R <= 3, "ring of at most 3 slots");
+    if (later >= 2) wait_vm<(R >= 3 ? 2 * NDMA : 0)>();
+    else if (later == 1) wait_vm<NDMA>();
+    else wait_vm<0>();
+  };
+
+  float m_run = -INFINITY, l_run = 0.f;
+  float4v oacc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) oacc[db] = float4v{0.f, 0.f, 0.f, 0.f};
+
+  // one NK-key slab in four phases (scores of all 4 blocks, scaling and edge
+  // masking, one lazy-softmax step, values), giving the scheduler long
+  // branch-free stretches; rows 16j .. 16j+15 of the slot are keys ks0 + 16j ..
+  auto slab = [&](const uint8_t* src, int ks0) {
+    // ---- scores S^T = K^ Q^T (term 1) and Sign Q_proj^T (term 2), 4 blocks
+    float4v s1[NBS], s2[NBS];
+#pragma unroll
+    for (int j = 0; j < NBS; ++j) {
+      uint32_t kw[KW32];
+      const uint8_t* kp = src + OFF_K + (16 * j + l16) * KC + lg * KLANE;
+      if constexpr (KW32 == 2) {
+        const u32x2 t = *reinterpret_cast<const u32x2*>(kp);
+        kw[0] = t[0];
+        kw[1] = t[1];
+      } else {
+#pragma unroll
+        for (int w = 0; w < KW32; ++w) kw[w] = reinterpret_cast<const uint32_t*>(kp)[w];
+      }
+      const uint32_t sw = *reinterpret_cast<const uint32_t*>(src + OFF_S + (16 * j + l16) * SC + lg * 4);
+      s1[j] = float4v{0.f, 0.f, 0.f, 0.f};
+      s2[j] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        s1[j] = mfma16x16x32(key_operand<KB, KW32>(tK, kw, ks), qr[ks], s1[j]);
+        s2[j] = mfma16x16x32(nib2x4(tS, sw >> (8 * ks)), qp[ks], s2[j]);
+      }
+    }
+    // ---- log2-domain scores of keys ks0 + 16j + 4lg + e for this column
+    float sc[NBS][4];
+#pragma unroll
+    for (int j = 0; j < NBS; ++j) {
+      const u32x4 nk = *reinterpret_cast<const u32x4*>(src + OFF_N + (16 * j + 4 * lg) * 4);
+      const u32x4 nr = *reinterpret_cast<const u32x4*>(src + OFF_N + NRM + (16 * j + 4 * lg) * 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float kn = h2f(static_cast<uint16_t>(nk[e]));
+        const float rn = h2f(static_cast<uint16_t>(nr[e]));
+        sc[j][e] = fmaf(s2[j][e], fb * rn, s1[j][e] * (fa * kn));
+      }
+    }
+    if (ks0 + NK > kend || ks0 + NK - 1 > causal_from || a.mask) {  // wave-uniform edge test
+#pragma unroll
+      for (int j = 0; j < NBS; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int key = ks0 + 16 * j + 4 * lg + e;
+          if (a.mask && col_ok && key < kend)
+            sc[j][e] += fmaxf(a.mask[b * a.smb + h * a.smh + static_cast<int64_t>(qi) * a.smq +
+                                     static_cast<int64_t>(key) * a.smk] * LOG2E,
+                              -3.0e38f);
+          if (key >= kend || key > lim) sc[j][e] = -INFINITY;
+        }
+    }
+    // ---- lazy online softmax over the slab: the column reference m_run moves only
+    // when a score exceeds it by more than TAU; p = 2^(s - m_run - TAU) <= 1
+    float lmax = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NBS; ++j) lmax = fmaxf(lmax, fmaxf(fmaxf(sc[j][0], sc[j][1]), fmaxf(sc[j][2], sc[j][3])));
+    if (__any(lmax > m_run + TAU)) {
+      float t = lmax;
+      t = fmaxf(t, __shfl_xor(t, 16, 64));
+      t = fmaxf(t, __shfl_xor(t, 32, 64));
+      if (t > m_run + TAU) {
+        const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - t);
+        m_run = t;
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
+      }
+    }
+    const float m_use = (m_run == -INFINITY) ? 0.f : m_run + TAU;
+    // ---- values: O^T += V^T (P * vn)^T per block
+#pragma unroll
+    for (int j = 0; j < NBS; ++j) {
+      const u32x4 nv = *reinterpret_cast<const u32x4*>(src + OFF_N + 2 * NRM + (16 * j + 4 * lg) * 4);
+      half4 ph, pl;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float p = __builtin_amdgcn_exp2f(sc[j][e] - m_use);
+        l_run += p;
+        const float pvv = p * h2f(static_cast<uint16_t>(nv[e]));
+        const _Float16 hh = static_cast<_Float16>(pvv);
+        ph[e] = hh;
+        if constexpr (PLO) pl[e] = static_cast<_Float16>(pvv - static_cast<float>(hh));
+      }
+      half8 vals[4];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const uint32_t* vp = reinterpret_cast<const uint32_t*>(src + OFF_V + (16 * j + 4 * lg + kk) * VC + vbase);
+        uint32_t w;
+        if constexpr (VW32 == 2)
+          w = static_cast<uint32_t>(((static_cast<uint64_t>(vp[1]) << 32) | vp[0]) >> vsh);
+        else
+          w = vp[0] >> vsh;
+        vals[kk] = value_operand<VB>(tV, w);
+      }
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const half4 va = half4{vals[0][db], vals[1][db], vals[2][db], vals[3][db]};
+        oacc[db] = mfma16x16x16(va, ph, oacc[db]);
+        if constexpr (PLO) oacc[db] = mfma16x16x16(va, pl, oacc[db]);
+      }
+    }
+  };
+
+  // the q fragments (the compiler's only outstanding loads) land before the ring
+  // starts, so none of its own waits inside the loop reach back past a DMA
+  __builtin_amdgcn_s_waitcnt(0);
+  const int k0w = kbeg + wave * NK;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (k0w + r * SLAB < kend) issue(k0w + r * SLAB, r);
+  __syncthreads();  // tables built
+  for (int k0 = k0w; k0 < kend; k0 += R * SLAB) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int ks0 = k0 + r * SLAB;
+      if (ks0 < kend) {
+        // slots issued after this one: those of the next R-1 slabs that exist
+        int later = 0;
+#pragma unroll
+        for (int q = 1; q < R; ++q) later += (ks0 + q * SLAB < kend) ? 1 : 0;
+        wait_slot(later);
+        slab(mine + r * SLOT, ks0);
+        if (ks0 + R * SLAB < kend) issue(ks0 + R * SLAB, r);
+      }
+    }
+  }
+
+  // ---- merge the 4 waves of the block in LDS (reusing the staging area)
+  __syncthreads();
+  float* mrg = reinterpret_cast<float*>(stage);  // [wave][col][D + 2]
+  float l = l_run;
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  float* my = mrg + (wave * 16 + l16) * (D + 2);
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) my[(lg * 4 + e) * (D / 16) + db] = oacc[db][e];
+  if (lg == 0) {
+    my[D] = (m_run == -INFINITY) ? m_run : m_run + TAU;
+    my[D + 1] = l;
+  }
+  __syncthreads();
+  const int64_t pbase = (bh * a.nsplit + split) * a.C;
+  for (int it = tid; it < a.C * D; it += 256) {
+    const int c = it / D, d = it % D;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, mrg[(w * 16 + c) * (D + 2) + D]);
+    float o = 0.f, ls = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float* srcm = mrg + (w * 16 + c) * (D + 2);
+      const float scw = (srcm[D] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(srcm[D] - mx);
+      o += scw * srcm[d];
+      ls += scw * srcm[D + 1];
+    }
+    a.part_o[(pbase + c) * D + d] = o;
+    if (d == 0) {
+      a.part_ml[(pbase + c) * 2] = mx;
+      a.part_ml[(pbase + c) * 2 + 1] = ls;
+    }
+  }
+}
+
 // Scores only: S = Q K^T with the keys on the MFMA's n side, so that lane
 // (key l16, group lg) ends with the scores of columns 4*lg + e for its own key:
 // one norm pair per lane, and each column's 16 scores leave as one 64-byte run.
@@ -753,7 +1074,11 @@ bool decode_applies(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
 template <int BITS>
 static void launch_decode_attn(const DecodeArgs& a, hipStream_t s) {
   dim3 grid(a.nsplit, a.Hkv, a.B);
+#if TQ_DEC_ATTN_LDS
+  decode_attn_lds_kernel<128, BITS, TQ_DEC_ANB, TQ_DEC_AR, TQ_DEC_PLO != 0><<<grid, 256, 0, s>>>(a);
+#else
   decode_attn_kernel<128, BITS, TQ_DEC_ANB, TQ_DEC_AR, TQ_DEC_PLO != 0><<<grid, 256, 0, s>>>(a);
+#endif
 }
 
 int decode_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
