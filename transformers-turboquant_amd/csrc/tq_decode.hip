@@ -113,6 +113,9 @@ __device__ __forceinline__ i32x4 uniform4(i32x4 r) {
   return i32x4{__builtin_amdgcn_readfirstlane(r[0]), __builtin_amdgcn_readfirstlane(r[1]),
                __builtin_amdgcn_readfirstlane(r[2]), __builtin_amdgcn_readfirstlane(r[3])};
 }
+// M0 is written here only; the compiler keeps nothing of its own in it in these kernels
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(i32x4 r, uint32_t lds, uint32_t voff) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
                :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(uniform4(r)) : "memory", "m0");
@@ -121,6 +124,7 @@ __device__ __forceinline__ void dma_u16(i32x4 r, uint32_t lds, uint32_t voff) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_ushort %1, %2, 0 offen nt lds"
                :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(uniform4(r)) : "memory", "m0");
 }
+#pragma clang diagnostic pop
 template <int N>
 __device__ __forceinline__ void wait_vm() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
