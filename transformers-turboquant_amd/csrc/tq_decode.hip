@@ -906,21 +906,25 @@ struct MergeArgs {
   int64_t sob, soh, sos;
 };
 
-// One block per (batch, kv head): combine the splits of its C columns, normalise,
-// rotate back with Pi_v (read once per block) and store.
+// One block per (batch, kv head): combine the splits of its C columns with
+// log-sum-exp weights into o[c][:] (LDS), then out^T = Pi_v^T o^T on MFMA with
+// Pi_v^T as the split-f16 A operand (rows i = output dim) and o^T as split-f16 B
+// operand (columns c, scaled per column by a power of two), hi.hi + lo.hi + hi.lo.
 template <int D>
 __global__ void __launch_bounds__(256) decode_merge_kernel(MergeArgs a) {
+  static_assert(D == 128, "merge is built for head_dim 128");
   constexpr int SW = 64;  // splits per weight batch
-  __shared__ float o_rot[16 * D];
+  __shared__ float o_s[16 * D];
   __shared__ float s_w[16 * SW];
   __shared__ float s_red[16 * 16];
-  __shared__ float s_mx[16], s_l[16];
+  __shared__ float s_mx[16], s_l[16], s_up[16];
   const int hkv = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6, l16 = lane & 15, lg = lane >> 4;
   const int C = a.C, ns = a.nsplit;
   const int64_t base = (static_cast<int64_t>(b) * a.Hkv + hkv) * ns;  // first split record
   auto ml = [&](int s, int c, int k) { return a.part_ml[((base + s) * C + c) * 2 + k]; };
 
-  // column maxima: thread (c, r) scans splits r, r + 16, ...
+  // ---- column maxima: thread (c, r) scans splits r, r + 16, ...
   {
     const int c = tid & 15, r = tid >> 4;
     float mx = -INFINITY;
@@ -937,7 +941,7 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeArgs a) {
     __syncthreads();
   }
 
-  // weighted sum of the splits; thread owns outputs it, it + 256, ... of the C x D tile
+  // ---- weighted sum of the splits; thread owns outputs it, it + 256, ... of the 16 x D tile
   constexpr int PER = 16 * D / 256;
   float acc[PER];
 #pragma unroll
@@ -971,43 +975,71 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeArgs a) {
     }
     __syncthreads();
   }
+  // normalised o in LDS (columns >= C are zero) and per-column max |o|
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
     const int it = tid + 256 * k, c = it / D, j = it % D;
-    if (c < C) o_rot[c * D + j] = (s_l[c] > 0.f) ? acc[k] / s_l[c] : 0.f;
+    o_s[c * D + j] = (c < C && s_l[c] > 0.f) ? acc[k] / s_l[c] : 0.f;
   }
   __syncthreads();
-
-  // out[c][j] = sum_i o_rot[c][i] * Pi_v[i][j] = sum_i o_rot[c][i] * Pi_v^T[j][i], Pi_v^T = (hi + lo) / 1024
-  const int j = tid % D, c0 = tid / D;
-  const _Float16* ph = reinterpret_cast<const _Float16*>(a.vpit) + j * D;
-  const _Float16* pl = ph + D * D;
-  constexpr int CS = 256 / D;  // columns handled per pass
-  for (int cb = 0; cb < C; cb += 4 * CS) {
-    float r[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int i = 0; i < D; i += 8) {
-      const half8 h = *reinterpret_cast<const half8*>(ph + i);
-      const half8 l = *reinterpret_cast<const half8*>(pl + i);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float w = (static_cast<float>(h[e]) + static_cast<float>(l[e])) * (1.f / kSplit);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int c = cb + c0 + q * CS;
-          if (c < C) r[q] += o_rot[c * D + i + e] * w;
-        }
-      }
+  {
+    // 16 lanes per column: lane r of column c scans dims r, r + 16, ...
+    const int c = tid >> 4, r = tid & 15;
+    float mx = 0.f;
+    for (int j = r; j < D; j += 16) mx = fmaxf(mx, fabsf(o_s[c * D + j]));
+    s_red[c * 16 + r] = mx;
+    __syncthreads();
+    if (tid < 16) {
+      float m = 0.f;
+      for (int i = 0; i < 16; ++i) m = fmaxf(m, s_red[tid * 16 + i]);
+      int ex;
+      frexpf(m, &ex);
+      s_up[tid] = ldexpf(kSplit, -ex);  // scaled |o| < kSplit
     }
+    __syncthreads();
+  }
+
+  // ---- out^T[i][c] = sum_j Pi_v^T[i][j] o[c][j]; wave w owns output rows 32w .. 32w+31
+  const float up = s_up[l16];
+  half8 bh[D / 32], bl[D / 32];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int c = cb + c0 + q * CS;
-      if (c >= C) continue;
-      const int qi = c / a.G, h = hkv * a.G + c % a.G;
+  for (int ks = 0; ks < D / 32; ++ks) {
+    const float* src = o_s + l16 * D + ks * 32 + lg * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      _Float16 h, lo;
+      split_f16(src[e] * up, h, lo);
+      bh[ks][e] = h;
+      bl[ks][e] = lo;
+    }
+  }
+  const _Float16* Ph = reinterpret_cast<const _Float16*>(a.vpit);
+  const _Float16* Pl = Ph + D * D;
+  const bool col_ok = l16 < C;
+  const int qi = col_ok ? l16 / a.G : 0, h = hkv * a.G + (col_ok ? l16 % a.G : 0);
+  const float down = kUnsplit2 / up;  // 1/(kSplit * up) * (1/kSplit) for Pi_v^T's scale
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const int i = wave * 32 + rb * 16 + l16;  // A-operand row (output dim)
+    float4v f = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) {
+      const half8 ah = *reinterpret_cast<const half8*>(Ph + i * D + ks * 32 + lg * 8);
+      const half8 al = *reinterpret_cast<const half8*>(Pl + i * D + ks * 32 + lg * 8);
+      f = mfma16x16x32(ah, bh[ks], f);
+      f = mfma16x16x32(al, bh[ks], f);
+      f = mfma16x16x32(ah, bl[ks], f);
+    }
+    if (col_ok) {
       const int64_t off = static_cast<int64_t>(b) * a.sob + static_cast<int64_t>(h) * a.soh +
-                          static_cast<int64_t>(qi) * a.sos + j;
-      if (a.out_dtype == TQ_BF16) store_act<TQ_BF16>(a.out, off, r[q]);
-      else if (a.out_dtype == TQ_F16) store_act<TQ_F16>(a.out, off, r[q]);
-      else store_act<TQ_F32>(a.out, off, r[q]);
+                          static_cast<int64_t>(qi) * a.sos + wave * 32 + rb * 16 + lg * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float v = f[e] * (down * kSplit);
+        if (a.out_dtype == TQ_BF16) store_act<TQ_BF16>(a.out, off + e, v);
+        else if (a.out_dtype == TQ_F16) store_act<TQ_F16>(a.out, off + e, v);
+        else store_act<TQ_F32>(a.out, off + e, v);
+      }
     }
   }
 }
