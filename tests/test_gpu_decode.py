@@ -73,7 +73,7 @@ def test_decode_attention_matches_oracle_and_tiled(bits, hq, hkv, sq, sk, causal
     tiled = _np(compressed_attention(q, kc, vc, ck, cv, causal=causal, out_dtype=torch.float32, split_k=False))
     ref = _oracle_attention(kc, vc, q, ck, cv, hq, hkv, causal=causal)
     assert np.isfinite(got).all()
-    print(f"decode rel-err {O.rel_err(got, ref):.2e}, tiled rel-err {O.rel_err(tiled, ref):.2e}")
+    print(f"ERR decode {O.rel_err(got, ref):.2e} cos {1 - O.cosine(got, ref):.1e} tiled {O.rel_err(tiled, ref):.2e}")
     assert O.rel_err(got, ref) < REL and O.cosine(got, ref) > 0.9999
     assert O.rel_err(tiled, ref) < REL
 

@@ -40,7 +40,7 @@
 #define TQ_DEC_AR 3
 #endif
 #ifndef TQ_DEC_PLO
-#define TQ_DEC_PLO 1
+#define TQ_DEC_PLO 0
 #endif
 #ifndef TQ_DEC_ATTN_LDS
 #define TQ_DEC_ATTN_LDS 1
