@@ -19,6 +19,8 @@
 // In scores mode each block writes its keys' f32 scores directly.
 #include "tq_common.h"
 
+#include <type_traits>
+
 // Tuning knobs: scores use NB 16-key blocks per wave slab with R slabs in flight;
 // attention uses ANB / AR likewise; grids target about *_BLOCKS blocks.
 #ifndef TQ_DEC_NB
@@ -42,11 +44,21 @@
 #ifndef TQ_DEC_PLO
 #define TQ_DEC_PLO 0
 #endif
-#ifndef TQ_DEC_ATTN_LDS
-#define TQ_DEC_ATTN_LDS 1
-#endif
 
 namespace tq {
+
+// compile-time loop: f(std::integral_constant<int, I>) for I = 0 .. N-1
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for_impl(F& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for_impl<I + 1, N>(f);
+  }
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl<0, N>(f);
+}
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
@@ -214,36 +226,79 @@ __device__ __forceinline__ uint32_t lds32(const uint8_t* t, uint32_t off) {
 __device__ __forceinline__ u32x2 lds64(const uint8_t* t, uint32_t off) {
   return *reinterpret_cast<const u32x2*>(t + off);
 }
-// 8 halves from two half4 entries indexed by the two nibbles of byte b
-__device__ __forceinline__ half8 nib2x4(const uint8_t* t, uint32_t b) {
-  const u32x2 lo = lds64(t, (b << 3) & 0x78u), hi = lds64(t, (b >> 1) & 0x78u);
+// Table offsets are built with SDWA byte selects: (byte K of x) & mask in one
+// instruction, on copies of the packed word pre-shifted so that each field lands
+// at the entry stride (x4 or x8 bytes) inside a byte.
+template <int K>
+__device__ __forceinline__ uint32_t and_byte(uint32_t mask, uint32_t x) {
+  static_assert(K >= 0 && K < 4, "byte select");
+  uint32_t r;
+  if constexpr (K == 0)
+    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+        : "=v"(r) : "v"(mask), "v"(x));
+  else if constexpr (K == 1)
+    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+        : "=v"(r) : "v"(mask), "v"(x));
+  else if constexpr (K == 2)
+    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+        : "=v"(r) : "v"(mask), "v"(x));
+  else
+    asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+        : "=v"(r) : "v"(mask), "v"(x));
+  return r;
+}
+// (byte K of x) << 2 in one instruction
+template <int K>
+__device__ __forceinline__ uint32_t byte_x4(uint32_t x) {
+  static_assert(K >= 0 && K < 4, "byte select");
+  uint32_t r;
+  if constexpr (K == 0)
+    asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0" : "=v"(r) : "v"(x));
+  else if constexpr (K == 1)
+    asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1" : "=v"(r) : "v"(x));
+  else if constexpr (K == 2)
+    asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2" : "=v"(r) : "v"(x));
+  else
+    asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3" : "=v"(r) : "v"(x));
+  return r;
+}
+
+// 8 halves from two half4 entries (x8 bytes) indexed by the two nibbles of byte K of w
+template <int K>
+__device__ __forceinline__ half8 nib2x4(const uint8_t* t, uint32_t w) {
+  const uint32_t m = 0x78u;
+  const u32x2 lo = lds64(t, and_byte<K>(m, w << 3)), hi = lds64(t, and_byte<K>(m, w >> 1));
   return __builtin_bit_cast(half8, u32x4{lo[0], lo[1], hi[0], hi[1]});
 }
-// 8 halves from four half2 entries indexed by the four nibbles of the low 16 bits of w
+// 8 halves from four half2 entries (x4 bytes) indexed by the nibbles of bytes K, K+1 of w
+template <int K>
 __device__ __forceinline__ half8 nib4x2(const uint8_t* t, uint32_t w) {
-  return __builtin_bit_cast(half8, u32x4{lds32(t, (w << 2) & 0x3Cu), lds32(t, (w >> 2) & 0x3Cu),
-                                         lds32(t, (w >> 6) & 0x3Cu), lds32(t, (w >> 10) & 0x3Cu)});
+  const uint32_t m = 0x3Cu;
+  const uint32_t a = w << 2, b = w >> 2;
+  return __builtin_bit_cast(half8, u32x4{lds32(t, and_byte<K>(m, a)), lds32(t, and_byte<K>(m, b)),
+                                         lds32(t, and_byte<K + 1>(m, a)), lds32(t, and_byte<K + 1>(m, b))});
 }
 // 8 halves from four half2 entries indexed by the four 6-bit fields of the low 24 bits of f
 __device__ __forceinline__ half8 six4x2(const uint8_t* t, uint32_t f) {
-  return __builtin_bit_cast(half8, u32x4{lds32(t, (f << 2) & 0xFCu), lds32(t, (f >> 4) & 0xFCu),
-                                         lds32(t, (f >> 10) & 0xFCu), lds32(t, (f >> 16) & 0xFCu)});
+  const uint32_t m = 0xFCu;
+  return __builtin_bit_cast(half8, u32x4{lds32(t, and_byte<0>(m, f << 2)), lds32(t, and_byte<0>(m, f >> 4)),
+                                         lds32(t, and_byte<1>(m, f >> 2)), lds32(t, and_byte<2>(m, f))});
 }
 // 8 halves from four half2 entries indexed by the four bytes of w
 __device__ __forceinline__ half8 byte4x2(const uint8_t* t, uint32_t w) {
-  return __builtin_bit_cast(half8, u32x4{lds32(t, (w << 2) & 0x3FCu), lds32(t, (w >> 6) & 0x3FCu),
-                                         lds32(t, (w >> 14) & 0x3FCu), lds32(t, (w >> 22) & 0x3FCu)});
+  return __builtin_bit_cast(half8, u32x4{lds32(t, byte_x4<0>(w)), lds32(t, byte_x4<1>(w)),
+                                         lds32(t, byte_x4<2>(w)), lds32(t, byte_x4<3>(w))});
 }
 
-// Key operand of k-step ks: dims ks*8 .. ks*8+7 of the lane's 32-dim field
-template <int KB, int KW32>
-__device__ __forceinline__ half8 key_operand(const uint8_t* t, const uint32_t (&k)[KW32], int ks) {
+// Key operand of k-step KS: dims KS*8 .. KS*8+7 of the lane's 32-dim field
+template <int KB, int KW32, int KS>
+__device__ __forceinline__ half8 key_operand(const uint8_t* t, const uint32_t (&k)[KW32]) {
   if constexpr (KB == 1) {
-    return nib2x4(t, k[0] >> (8 * ks));
+    return nib2x4<KS>(t, k[0]);
   } else if constexpr (KB == 2) {
-    return nib4x2(t, k[ks >> 1] >> (16 * (ks & 1)));
+    return nib4x2<2 * (KS & 1)>(t, k[KS >> 1]);
   } else {
-    const int bit = 24 * ks, wi = bit >> 5, sh = bit & 31;
+    constexpr int bit = 24 * KS, wi = bit >> 5, sh = bit & 31;
     const uint32_t lo32 = k[wi];
     const uint32_t hi32 = (wi + 1 < KW32) ? k[wi + 1] : 0u;
     return six4x2(t, sh ? __builtin_amdgcn_alignbit(hi32, lo32, sh) : lo32);
@@ -252,250 +307,12 @@ __device__ __forceinline__ half8 key_operand(const uint8_t* t, const uint32_t (&
 // Value operand: the 8 dims of one value field (VB bits each, LSB first)
 template <int VB>
 __device__ __forceinline__ half8 value_operand(const uint8_t* t, uint32_t w) {
-  if constexpr (VB == 2) return nib4x2(t, w);
+  if constexpr (VB == 2) return nib4x2<0>(t, w);
   else if constexpr (VB == 3) return six4x2(t, w);
   else return byte4x2(t, w);
 }
 
 
-
-// Fused decode attention.  Lane (column l16, group lg) ends each 16-key block
-// with the scores of keys 4*lg + e for its own column, which is the P^T operand
-// layout of the value MFMA, so P never leaves registers.  Each wave owns
-// 16*NB consecutive keys per slab and keeps R slabs of raw records in flight.
-template <int D, int BITS, int NB, int R, bool PLO>
-__global__ void __launch_bounds__(256) decode_attn_kernel(DecodeArgs a) {
-  static_assert(D == 128, "decode kernel is built for head_dim 128");
-  using L = SmallLuts<BITS>;
-  constexpr int KB = L::KB, VB = L::VB;
-  constexpr int KS = D / 32;           // score k-steps
-  constexpr int DB = D / 16;           // value row blocks
-  constexpr int KC = D * KB / 8, SC = D / 8, VC = D * VB / 8;  // bytes per packed row
-  constexpr int KLANE = KC / 4;        // key-code bytes per lane (4 lanes share a key row)
-  constexpr int KW32 = KLANE / 4;
-  constexpr int VW32 = (VB == 3) ? 2 : 1;  // dwords holding a lane's value field
-  constexpr int SLAB = 4 * 16 * NB;
-  constexpr float LOG2E = 1.4426950408889634f;
-  constexpr float TAU = 8.0f;          // lazy-rescale headroom (log2 units)
-
-  __shared__ __attribute__((aligned(16))) uint8_t luts[L::BYTES];
-  __shared__ __attribute__((aligned(16))) float mrg[4 * 16 * (D + 2)];  // wave merge [wave][col][D + 2]
-  const uint8_t* tS = luts + L::SGN_OFF;
-  const uint8_t* tK = luts + L::KEY_OFF;
-  const uint8_t* tV = luts + L::VAL_OFF;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int l16 = lane & 15, lg = lane >> 4;
-  const int split = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
-  const int64_t bh = static_cast<int64_t>(b) * a.Hkv + hkv;
-
-  build_small_luts<BITS, true>(a, luts, tid);
-
-  // this lane's column (query row qi, head h) and its q fragments (permuted k-slots)
-  const bool col_ok = l16 < a.C;
-  const int qi = col_ok ? l16 / a.G : 0, h = hkv * a.G + (col_ok ? l16 % a.G : 0);
-  half8 qr[KS], qp[KS];
-  {
-    const int64_t qrow = ((static_cast<int64_t>(b) * a.Hq + h) * a.Sq + qi) * D;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int d0 = lg * (D / 4) + ks * 8;
-      qr[ks] = col_ok ? *reinterpret_cast<const half8*>(a.q_rot + qrow + d0) : half8{};
-      qp[ks] = col_ok ? *reinterpret_cast<const half8*>(a.q_proj + qrow + d0) : half8{};
-    }
-  }
-  __syncthreads();
-
-  const float fa = a.scale * LOG2E;
-  const float fb = a.coeff * fa;
-  const int lim = a.causal ? qi + (a.Sk - a.Sq) : 0x7fffffff;  // keys <= lim are visible
-  const int causal_from = a.causal ? a.Sk - a.Sq : 0x7fffffff;  // smallest lim of any column
-  const int kbeg = split * a.chunk;
-  const int kend = min(a.Sk, kbeg + a.chunk);
-
-  // this lane's value field: dims l16*8 .. l16*8+7 of a value row, VB bytes at voff
-  const int voff = l16 * VB;
-  const int vbase = (VB == 3) ? min(voff & ~3, VC - 8) : (voff & ~3);
-  const int vsh = 8 * (voff - vbase);
-
-  struct Raw {
-    uint32_t k[KW32];          // key-code bytes of (key l16, group lg)
-    uint32_t s;                // sign bytes of (key l16, group lg)
-    uint32_t nk[2], nr[2], nv[2];  // f16 norms of keys 4lg .. 4lg+3
-    uint32_t v[4][VW32];       // value-field dwords of keys 4lg + kk
-  };
-  // this (b, kv head)'s planes; each block reads rows [kb, kend) through its own resource
-  const int64_t g0 = bh * a.Sk;
-  const uint8_t* pk = a.kcodes + g0 * KC;
-  const uint8_t* ps = a.ksigns + g0 * SC;
-  const uint16_t* pkn = a.kvn + g0;
-  const uint16_t* prn = a.krn + g0;
-  const uint16_t* pvn = a.vvn + g0;
-  const uint8_t* pv = a.vcodes + g0 * VC;
-  const bool norms_aligned = ((reinterpret_cast<uintptr_t>(pkn) | reinterpret_cast<uintptr_t>(prn) |
-                               reinterpret_cast<uintptr_t>(pvn)) & 7) == 0;
-  const uint32_t ok_off = l16 * KC + lg * KLANE, os_off = l16 * SC + lg * 4, on_off = 8 * lg;
-  const uint32_t ov_off = 4 * lg * VC + vbase;
-
-  auto load = [&](int kb, Raw& r) {
-    bload(rows_rsrc(pk, KC, kb, kend), ok_off, 0, r.k);
-    r.s = __builtin_amdgcn_raw_buffer_load_b32(rows_rsrc(ps, SC, kb, kend), os_off, 0, kStream);
-    const rsrc_t rkn = rows_rsrc(pkn, 2, kb, kend), rrn = rows_rsrc(prn, 2, kb, kend),
-                 rvn = rows_rsrc(pvn, 2, kb, kend);
-    if (kb + 16 <= kend && norms_aligned && (kb & 3) == 0) {
-      uint32_t t[2];
-      bload(rkn, on_off, 0, t); r.nk[0] = t[0]; r.nk[1] = t[1];
-      bload(rrn, on_off, 0, t); r.nr[0] = t[0]; r.nr[1] = t[1];
-      bload(rvn, on_off, 0, t); r.nv[0] = t[0]; r.nv[1] = t[1];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const uint32_t o0 = on_off + 4 * i, o1 = o0 + 2;
-        r.nk[i] = bload16(rkn, o0, 0) | (bload16(rkn, o1, 0) << 16);
-        r.nr[i] = bload16(rrn, o0, 0) | (bload16(rrn, o1, 0) << 16);
-        r.nv[i] = bload16(rvn, o0, 0) | (bload16(rvn, o1, 0) << 16);
-      }
-    }
-    const rsrc_t rv = rows_rsrc(pv, VC, kb, kend);
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) bload(rv, ov_off + kk * VC, 0, r.v[kk]);
-  };
-
-  float m_run = -INFINITY, l_run = 0.f;
-  float4v oacc[DB];
-#pragma unroll
-  for (int db = 0; db < DB; ++db) oacc[db] = float4v{0.f, 0.f, 0.f, 0.f};
-
-  auto block = [&](int kb, const Raw& r) {
-    // ---- scores S^T = K^ Q^T (term 1) and Sign Q_proj^T (term 2)
-    float4v s1 = float4v{0.f, 0.f, 0.f, 0.f}, s2 = float4v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      s1 = mfma16x16x32(key_operand<KB, KW32>(tK, r.k, ks), qr[ks], s1);
-      s2 = mfma16x16x32(nib2x4(tS, r.s >> (8 * ks)), qp[ks], s2);
-    }
-    // ---- log2-domain scores of keys 4lg + e for this column
-    float sc[4], vv[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int w = e >> 1, t = 16 * (e & 1);
-      const float kn = h2f(static_cast<uint16_t>(r.nk[w] >> t));
-      const float rn = h2f(static_cast<uint16_t>(r.nr[w] >> t));
-      vv[e] = h2f(static_cast<uint16_t>(r.nv[w] >> t));
-      sc[e] = s1[e] * (fa * kn) + s2[e] * (fb * rn);
-    }
-    if (kb + 16 > kend || kb + 15 > causal_from || a.mask) {  // wave-uniform edge test
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int key = kb + 4 * lg + e;
-        if (a.mask && col_ok && key < kend)
-          sc[e] += fmaxf(a.mask[b * a.smb + h * a.smh + static_cast<int64_t>(qi) * a.smq +
-                                static_cast<int64_t>(key) * a.smk] * LOG2E,
-                         -3.0e38f);
-        if (key >= kend || key > lim) sc[e] = -INFINITY;
-      }
-    }
-    // ---- lazy online softmax: the column reference m_run moves only when a score
-    // exceeds it by more than TAU; p = 2^(s - m_run - TAU) <= 1
-    const float lmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-    if (__any(lmax > m_run + TAU)) {
-      float t = lmax;
-      t = fmaxf(t, __shfl_xor(t, 16, 64));
-      t = fmaxf(t, __shfl_xor(t, 32, 64));
-      if (t > m_run + TAU) {
-        const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - t);
-        m_run = t;
-        l_run *= alpha;
-#pragma unroll
-        for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
-      }
-    }
-    const float m_use = (m_run == -INFINITY) ? 0.f : m_run + TAU;
-    half4 ph, pl;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float p = __builtin_amdgcn_exp2f(sc[e] - m_use);
-      l_run += p;
-      const float pv = p * vv[e];
-      const _Float16 hh = static_cast<_Float16>(pv);
-      ph[e] = hh;
-      if constexpr (PLO) pl[e] = static_cast<_Float16>(pv - static_cast<float>(hh));
-    }
-    // ---- value operands: per key kk the 8 values of dims l16*8 + db
-    half8 vals[4];
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      uint32_t w;
-      if constexpr (VB == 3)
-        w = static_cast<uint32_t>(((static_cast<uint64_t>(r.v[kk][1]) << 32) | r.v[kk][0]) >> vsh);
-      else
-        w = r.v[kk][0] >> vsh;
-      vals[kk] = value_operand<VB>(tV, w);
-    }
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      const half4 va = half4{vals[0][db], vals[1][db], vals[2][db], vals[3][db]};
-      oacc[db] = mfma16x16x16(va, ph, oacc[db]);
-      if constexpr (PLO) oacc[db] = mfma16x16x16(va, pl, oacc[db]);
-    }
-  };
-
-  Raw ring[R][NB];
-  const int k0w = kbeg + wave * 16 * NB;
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int j = 0; j < NB; ++j)
-      if (k0w + r * SLAB + 16 * j < kend) load(k0w + r * SLAB + 16 * j, ring[r][j]);
-  for (int k0 = k0w; k0 < kend; k0 += R * SLAB) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-#pragma unroll
-      for (int j = 0; j < NB; ++j) {
-        const int kb = k0 + r * SLAB + 16 * j;
-        if (kb < kend) {
-          block(kb, ring[r][j]);
-          if (kb + R * SLAB < kend) load(kb + R * SLAB, ring[r][j]);
-        }
-      }
-    }
-  }
-
-  // ---- merge the 4 waves of the block in LDS, write one partial per block
-  float l = l_run;
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
-  float* mine = mrg + (wave * 16 + l16) * (D + 2);
-#pragma unroll
-  for (int db = 0; db < DB; ++db)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) mine[(lg * 4 + e) * (D / 16) + db] = oacc[db][e];
-  if (lg == 0) {
-    mine[D] = (m_run == -INFINITY) ? m_run : m_run + TAU;
-    mine[D + 1] = l;
-  }
-  __syncthreads();
-  const int64_t pbase = (bh * a.nsplit + split) * a.C;
-  for (int it = tid; it < a.C * D; it += 256) {
-    const int c = it / D, d = it % D;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, mrg[(w * 16 + c) * (D + 2) + D]);
-    float o = 0.f, ls = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float* src = mrg + (w * 16 + c) * (D + 2);
-      const float sc = (src[D] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(src[D] - mx);
-      o += sc * src[d];
-      ls += sc * src[D + 1];
-    }
-    a.part_o[(pbase + c) * D + d] = o;
-    if (d == 0) {
-      a.part_ml[(pbase + c) * 2] = mx;
-      a.part_ml[(pbase + c) * 2 + 1] = ls;
-    }
-  }
-}
 
 // Fused decode attention, LDS-staged.  Each wave streams 64-key slabs of the key
 // codes, sign bits, value codes and the three norm planes straight into its own
@@ -528,6 +345,9 @@ __global__ void __launch_bounds__(256) decode_attn_lds_kernel(DecodeArgs a) {
 
   __shared__ __attribute__((aligned(16))) uint8_t luts[L::BYTES];
   __shared__ __attribute__((aligned(16))) uint8_t stage[STAGE > MERGE ? STAGE : MERGE];
+  // per-wave f32 key factors of the current slab: fa*vn_k, fb*rn_k, vn_v (one pass per key
+  // instead of one per (key, column) lane)
+  __shared__ __attribute__((aligned(16))) float fac[4][3][NK];
   const uint8_t* tS = luts + L::SGN_OFF;
   const uint8_t* tK = luts + L::KEY_OFF;
   const uint8_t* tV = luts + L::VAL_OFF;
@@ -559,9 +379,12 @@ __global__ void __launch_bounds__(256) decode_attn_lds_kernel(DecodeArgs a) {
   const int kbeg = split * a.chunk;
   const int kend = min(a.Sk, kbeg + a.chunk);
 
+  // this lane's value field: dims l16*8 .. l16*8+7 = VB bytes at byte voff of the row,
+  // read as the dword pair at vbase = voff & ~3 (the pair may run past the row end into
+  // the next row or the slot's norm area; those bytes are not used)
   const int voff = l16 * VB;
-  const int vbase = (VB == 3) ? min(voff & ~3, VC - 8) : (voff & ~3);
-  const int vsh = 8 * (voff - vbase);
+  const int vbase = voff & ~3;
+  const int vbyte = voff & 3;
 
   const int64_t g0 = bh * a.Sk;
   const uint8_t* pk = a.kcodes + g0 * KC;
@@ -614,8 +437,18 @@ __global__ void __launch_bounds__(256) decode_attn_lds_kernel(DecodeArgs a) {
   // one NK-key slab in four phases (scores of all 4 blocks, scaling and edge
   // masking, one lazy-softmax step, values), giving the scheduler long
   // branch-free stretches; rows 16j .. 16j+15 of the slot are keys ks0 + 16j ..
+  float (*fw)[NK] = fac[wave];
   auto slab = [&](const uint8_t* src, int ks0) {
-    // ---- scores S^T = K^ Q^T (term 1) and Sign Q_proj^T (term 2), 4 blocks
+    // ---- per-key factors fa*vn_k, fb*rn_k, vn_v: 3*NK values, one per lane and pass
+#pragma unroll
+    for (int i0 = 0; i0 < 3 * NK; i0 += 64) {
+      const int i = i0 + lane, which = i / NK, k = i % NK;
+      if (i < 3 * NK) {
+        const float v = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + which * NRM + k * 4)));
+        fw[which][k] = (which == 0) ? fa * v : (which == 1 ? fb * v : v);
+      }
+    }
+    // ---- scores S^T = K^ Q^T (term 1) and Sign Q_proj^T (term 2), NBS blocks
     float4v s1[NBS], s2[NBS];
 #pragma unroll
     for (int j = 0; j < NBS; ++j) {
@@ -632,24 +465,20 @@ __global__ void __launch_bounds__(256) decode_attn_lds_kernel(DecodeArgs a) {
       const uint32_t sw = *reinterpret_cast<const uint32_t*>(src + OFF_S + (16 * j + l16) * SC + lg * 4);
       s1[j] = float4v{0.f, 0.f, 0.f, 0.f};
       s2[j] = float4v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        s1[j] = mfma16x16x32(key_operand<KB, KW32>(tK, kw, ks), qr[ks], s1[j]);
-        s2[j] = mfma16x16x32(nib2x4(tS, sw >> (8 * ks)), qp[ks], s2[j]);
-      }
+      static_for<KS>([&](auto c) {
+        constexpr int ks = decltype(c)::value;
+        s1[j] = mfma16x16x32(key_operand<KB, KW32, ks>(tK, kw), qr[ks], s1[j]);
+        s2[j] = mfma16x16x32(nib2x4<ks>(tS, sw), qp[ks], s2[j]);
+      });
     }
     // ---- log2-domain scores of keys ks0 + 16j + 4lg + e for this column
     float sc[NBS][4];
 #pragma unroll
     for (int j = 0; j < NBS; ++j) {
-      const u32x4 nk = *reinterpret_cast<const u32x4*>(src + OFF_N + (16 * j + 4 * lg) * 4);
-      const u32x4 nr = *reinterpret_cast<const u32x4*>(src + OFF_N + NRM + (16 * j + 4 * lg) * 4);
+      const float4v ka = *reinterpret_cast<const float4v*>(&fw[0][16 * j + 4 * lg]);
+      const float4v kb2 = *reinterpret_cast<const float4v*>(&fw[1][16 * j + 4 * lg]);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float kn = h2f(static_cast<uint16_t>(nk[e]));
-        const float rn = h2f(static_cast<uint16_t>(nr[e]));
-        sc[j][e] = fmaf(s2[j][e], fb * rn, s1[j][e] * (fa * kn));
-      }
+      for (int e = 0; e < 4; ++e) sc[j][e] = fmaf(s2[j][e], kb2[e], s1[j][e] * ka[e]);
     }
     if (ks0 + NK > kend || ks0 + NK - 1 > causal_from || a.mask) {  // wave-uniform edge test
 #pragma unroll
@@ -685,13 +514,13 @@ __global__ void __launch_bounds__(256) decode_attn_lds_kernel(DecodeArgs a) {
     // ---- values: O^T += V^T (P * vn)^T per block
 #pragma unroll
     for (int j = 0; j < NBS; ++j) {
-      const u32x4 nv = *reinterpret_cast<const u32x4*>(src + OFF_N + 2 * NRM + (16 * j + 4 * lg) * 4);
+      const float4v nv = *reinterpret_cast<const float4v*>(&fw[2][16 * j + 4 * lg]);
       half4 ph, pl;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float p = __builtin_amdgcn_exp2f(sc[j][e] - m_use);
         l_run += p;
-        const float pvv = p * h2f(static_cast<uint16_t>(nv[e]));
+        const float pvv = p * nv[e];
         const _Float16 hh = static_cast<_Float16>(pvv);
         ph[e] = hh;
         if constexpr (PLO) pl[e] = static_cast<_Float16>(pvv - static_cast<float>(hh));
@@ -702,9 +531,9 @@ __global__ void __launch_bounds__(256) decode_attn_lds_kernel(DecodeArgs a) {
         const uint32_t* vp = reinterpret_cast<const uint32_t*>(src + OFF_V + (16 * j + 4 * lg + kk) * VC + vbase);
         uint32_t w;
         if constexpr (VW32 == 2)
-          w = static_cast<uint32_t>(((static_cast<uint64_t>(vp[1]) << 32) | vp[0]) >> vsh);
+          w = __builtin_amdgcn_alignbyte(vp[1], vp[0], vbyte);
         else
-          w = vp[0] >> vsh;
+          w = vp[0] >> (8 * vbyte);
         vals[kk] = value_operand<VB>(tV, w);
       }
 #pragma unroll
@@ -863,11 +692,11 @@ __global__ void __launch_bounds__(256) decode_scores_kernel(DecodeArgs a) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       float4v s1 = float4v{0.f, 0.f, 0.f, 0.f}, s2 = float4v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        s1 = mfma16x16x32(qr[ks], key_operand<KB, KW32>(tK, r[j].k, ks), s1);
-        s2 = mfma16x16x32(qp[ks], nib2x4(tS, r[j].s >> (8 * ks)), s2);
-      }
+      static_for<KS>([&](auto c) {
+        constexpr int ks = decltype(c)::value;
+        s1 = mfma16x16x32(qr[ks], key_operand<KB, KW32, ks>(tK, r[j].k), s1);
+        s2 = mfma16x16x32(qp[ks], nib2x4<ks>(tS, r[j].s), s2);
+      });
       const int kb = k0 + 16 * j;
       const float kn = h2f(static_cast<uint16_t>(r[j].kn)), rn = fb * h2f(static_cast<uint16_t>(r[j].rn));
       const rsrc_t ro = make_rsrc(pout + kb, out_bytes - static_cast<uint32_t>(kb) * 4);
@@ -1110,11 +939,7 @@ bool decode_applies(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
 template <int BITS>
 static void launch_decode_attn(const DecodeArgs& a, hipStream_t s) {
   dim3 grid(a.nsplit, a.Hkv, a.B);
-#if TQ_DEC_ATTN_LDS
   decode_attn_lds_kernel<128, BITS, TQ_DEC_ANB, TQ_DEC_AR, TQ_DEC_PLO != 0><<<grid, 256, 0, s>>>(a);
-#else
-  decode_attn_kernel<128, BITS, TQ_DEC_ANB, TQ_DEC_AR, TQ_DEC_PLO != 0><<<grid, 256, 0, s>>>(a);
-#endif
 }
 
 int decode_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
