@@ -1,39 +1,36 @@
 // Decode-shaped compressed attention: few query rows per head (G * Sq <= 16
 // (query row, query head) columns per kv head) against long compressed
 // caches.  The work is HBM-bound: every key and value record is streamed
-// once per step, so the kernel is organised around the byte stream.
+// once per step, so the kernels are organised around the byte stream.
 //
-// Split-K: a block of 4 wave64 owns a chunk of keys of one (batch, kv head);
-// each wave walks its own 16-key blocks straight from HBM into registers
-// (prefetching the next block while computing the current one) with no LDS
-// staging and no block barriers.  MFMA operands are built from the packed
-// bytes through LDS lookup tables (byte -> f16 values); the k-slot order of
-// each MFMA is permuted so that a lane's operand bytes are contiguous in the
-// packed rows:
-//   scores  S^T = K^ Q_rot^T, Sign Q_proj^T  (16x16x32): lane (key m, group g)
-//           holds dims g*D/4 + ks*8 + 0..7 at k-step ks
-//   values  O^T += V^T P^T (16x16x16): O^T row m of block db is dim m*(D/16)+db,
-//           so a lane's value operand comes from one contiguous code field
-// The (m, l, O) state of the 4 waves is merged in LDS into one partial per
-// block; tq_decode_merge combines the splits, normalises and applies Pi_v.
-// In scores mode each block writes its keys' f32 scores directly.
+// Split-K: a block of 4 wave64 owns a chunk of keys of one (batch, kv head).
+// Each wave streams its own slabs of the packed planes into a private LDS ring
+// with direct-to-LDS buffer loads (16 B per lane, several slabs in flight, no
+// block barriers) and builds MFMA operands from the packed bytes through small
+// LDS lookup tables; the k-slot order of each MFMA is permuted so that a lane's
+// operand bytes are one contiguous field of a packed row:
+//   scores     S = Q K^T (16x16x32), keys on the N side: lane (key n, group g)
+//              supplies dims g*D/4 + ks*8 + 0..7 of its key at k-step ks and
+//              ends with 4 columns of its own key
+//   attention  S^T = K Q^T (16x16x32), keys on the M side, so the accumulator
+//              is the P^T operand of O^T += V^T P^T (16x16x16); O^T row m of
+//              block db is dim m*(D/16)+db, so a lane's value operand comes
+//              from one contiguous code field
+// In attention mode the (m, l, O) state of the 4 waves is merged in LDS into
+// one partial per block; decode_merge_kernel combines the splits, normalises
+// and applies Pi_v.  In scores mode each block writes its keys' f32 scores.
 #include "tq_common.h"
 
 #include <type_traits>
 
-// Tuning knobs: scores use NB 16-key blocks per wave slab with R slabs in flight;
-// attention uses ANB / AR likewise; grids target about *_BLOCKS blocks.
-#ifndef TQ_DEC_NB
-#define TQ_DEC_NB 2
-#endif
-#ifndef TQ_DEC_R
-#define TQ_DEC_R 3
-#endif
+// Tuning knobs: scores use SNK-key wave slabs with SR slots in flight; attention
+// uses ANB 16-key blocks per wave slab with AR slots; grids target about *_BLOCKS
+// blocks (more, shorter blocks balance the last round of blocks better).
 #ifndef TQ_DEC_ATTN_BLOCKS
 #define TQ_DEC_ATTN_BLOCKS 768
 #endif
 #ifndef TQ_DEC_SCORE_BLOCKS
-#define TQ_DEC_SCORE_BLOCKS 2048
+#define TQ_DEC_SCORE_BLOCKS 4096
 #endif
 #ifndef TQ_DEC_ANB
 #define TQ_DEC_ANB 2
@@ -43,6 +40,12 @@
 #endif
 #ifndef TQ_DEC_PLO
 #define TQ_DEC_PLO 0
+#endif
+#ifndef TQ_DEC_SR
+#define TQ_DEC_SR 2
+#endif
+#ifndef TQ_DEC_SNK
+#define TQ_DEC_SNK 64
 #endif
 
 namespace tq {
@@ -117,7 +120,7 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) {
 __device__ __forceinline__ i32x4 rows_desc(const void* plane, int rb, int kb, int kend) {
   const uint64_t base = reinterpret_cast<uint64_t>(static_cast<const uint8_t*>(plane) + static_cast<int64_t>(kb) * rb);
   return i32x4{static_cast<int>(static_cast<uint32_t>(base)), static_cast<int>(static_cast<uint32_t>(base >> 32) & 0xffffu),
-               static_cast<int>(static_cast<uint32_t>(kend - kb) * rb), 0x00020000};
+               static_cast<int>(static_cast<uint32_t>(kend > kb ? kend - kb : 0) * rb), 0x00020000};
 }
 // descriptor and LDS address are wave-uniform; readfirstlane lets the compiler
 // prove it where the call sits under a lane-dependent branch
@@ -311,8 +314,6 @@ __device__ __forceinline__ half8 value_operand(const uint8_t* t, uint32_t w) {
   else if constexpr (VB == 3) return six4x2(t, w);
   else return byte4x2(t, w);
 }
-
-
 
 // Fused decode attention, LDS-staged.  Each wave streams 64-key slabs of the key
 // codes, sign bits, value codes and the three norm planes straight into its own
@@ -607,24 +608,30 @@ __global__ void __launch_bounds__(256) decode_attn_lds_kernel(DecodeArgs a) {
   }
 }
 
-// Scores only: S = Q K^T with the keys on the MFMA's n side, so that lane
-// (key l16, group lg) ends with the scores of columns 4*lg + e for its own key:
-// one norm pair per lane, and each column's 16 scores leave as one 64-byte run.
-// Each wave owns 16*NB consecutive keys per slab and keeps two slabs of raw
-// records in flight (ring of 2) while it scores the oldest.
-template <int D, int BITS, int NB>
+// Scores: each wave DMAs NK-key slabs of the code, sign and norm planes into its
+// own R-slot LDS ring (16 B per lane; nothing is held in registers while in
+// flight) and scores them with the keys on the MFMA's N side, so lane (key l16,
+// group lg) ends with columns 4*lg + e of its own key: the two norms are
+// per-lane scalars and each column's 16 scores leave as one 64-byte run.
+template <int D, int BITS, int R, int NK>
 __global__ void __launch_bounds__(256) decode_scores_kernel(DecodeArgs a) {
   static_assert(D == 128, "decode kernel is built for head_dim 128");
+  static_assert(R >= 2 && R <= 4, "ring of 2 to 4 slots");
+  static_assert(NK == 32 || NK == 64, "slabs of 32 or 64 keys");
   using L = SmallLuts<BITS>;
   constexpr int KB = L::KB;
   constexpr int KS = D / 32;
   constexpr int KC = D * KB / 8, SC = D / 8;
   constexpr int KLANE = KC / 4;
   constexpr int KW32 = KLANE / 4;
-  constexpr int SLAB = 4 * 16 * NB;  // keys per block iteration
-  constexpr int R = TQ_DEC_R;        // slabs in flight per wave
+  constexpr int NBS = NK / 16;
+  constexpr int SLAB = 4 * NK;           // keys per block slab
+  constexpr int OFF_K = 0, OFF_S = NK * KC, OFF_N = OFF_S + NK * SC;
+  constexpr int NRM = NK * 4;            // one norm plane: a dword per key
+  constexpr int SLOT = OFF_N + 2 * NRM;
 
   __shared__ __attribute__((aligned(16))) uint8_t luts[L::BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t stage[4 * R * SLOT];
   const uint8_t* tS = luts + L::SGN_OFF;
   const uint8_t* tK = luts + L::KEY_OFF;
 
@@ -648,7 +655,6 @@ __global__ void __launch_bounds__(256) decode_scores_kernel(DecodeArgs a) {
       qp[ks] = ok ? *reinterpret_cast<const half8*>(a.q_proj + qrow + d0) : half8{};
     }
   }
-  __syncthreads();
 
   const int kbeg = split * a.chunk;
   const int kend = min(a.Sk, kbeg + a.chunk);
@@ -666,41 +672,72 @@ __global__ void __launch_bounds__(256) decode_scores_kernel(DecodeArgs a) {
     oo[e] = c < a.C ? static_cast<uint32_t>((c % a.G) * a.Sq + c / a.G) * a.Sk * 4 + 4 * l16 : kOutOfRange;
   }
 
-  struct Raw {
-    uint32_t k[KW32];
-    uint32_t s;
-    uint32_t kn, rn;
-  };
-  // this (b, kv head)'s planes; each block reads rows [kb, kend) through its own resource
   const int64_t g0 = bh * a.Sk;
   const uint8_t* pk = a.kcodes + g0 * KC;
   const uint8_t* ps = a.ksigns + g0 * SC;
   const uint16_t* pkn = a.kvn + g0;
   const uint16_t* prn = a.krn + g0;
-  const uint32_t ok_off = l16 * KC + lg * KLANE, os_off = l16 * SC + lg * 4, on_off = 2 * l16;
-  auto load = [&](int k0, Raw (&r)[NB]) {
+
+  uint8_t* mine = stage + wave * (R * SLOT);
+  const uint32_t mine_lds = lds_offset(mine);
+  constexpr int NKD = (NK * KC + 1023) / 1024, NSD = (NK * SC + 1023) / 1024;
+  constexpr int NDMA = NKD + NSD + 2;  // DMA instructions per slot
+  // a plane of `bytes` (a multiple of 512) moves in 1 KB rounds of 64 lanes x 16 B;
+  // a final half round uses lanes 0-31 only
+  auto copy_plane = [&](const i32x4& r, uint32_t dst, int bytes, int nrounds) {
+    const uint32_t lo = lane * 16;
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      const int kb = k0 + 16 * j;
-      bload(rows_rsrc(pk, KC, kb, kend), ok_off, 0, r[j].k);
-      r[j].s = __builtin_amdgcn_raw_buffer_load_b32(rows_rsrc(ps, SC, kb, kend), os_off, 0, kStream);
-      r[j].kn = bload16(rows_rsrc(pkn, 2, kb, kend), on_off, 0);
-      r[j].rn = bload16(rows_rsrc(prn, 2, kb, kend), on_off, 0);
+    for (int c = 0; c < 4; ++c) {
+      if (c >= nrounds) break;
+      if ((c + 1) * 1024 <= bytes || lane < 32) dma16(r, dst + c * 1024, lo + c * 1024);
     }
   };
-  auto score = [&](int k0, const Raw (&r)[NB]) {
+  // DMA the wave's slab of keys [kb, kb + NK) into ring slot `slot`; rows past kend read zero
+  auto issue = [&](int kb, int slot) {
+    const uint32_t dst = mine_lds + slot * SLOT;
+    wait_lds();  // earlier reads of this slot have landed
+    copy_plane(rows_desc(pk, KC, kb, kend), dst + OFF_K, NK * KC, NKD);
+    copy_plane(rows_desc(ps, SC, kb, kend), dst + OFF_S, NK * SC, NSD);
+    if (NK == 64 || lane < 32) {
+      dma_u16(rows_desc(pkn, 2, kb, kend), dst + OFF_N, lane * 2);
+      dma_u16(rows_desc(prn, 2, kb, kend), dst + OFF_N + NRM, lane * 2);
+    }
+  };
+  // wait until the slot issued `later` slots ago has landed (score stores issued
+  // in between only make the wait stronger: loads complete in issue order)
+  auto wait_slot = [&](int later) {
+    if (later >= 3) wait_vm<(R >= 4 ? 3 * NDMA : 0)>();
+    else if (later == 2) wait_vm<(R >= 3 ? 2 * NDMA : 0)>();
+    else if (later == 1) wait_vm<NDMA>();
+    else wait_vm<0>();
+  };
+
+  auto slab = [&](const uint8_t* src, int ks0) {
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
+    for (int j = 0; j < NBS; ++j) {
+      uint32_t kw[KW32];
+      const uint8_t* kp = src + OFF_K + (16 * j + l16) * KC + lg * KLANE;
+      if constexpr (KW32 == 2) {
+        const u32x2 t = *reinterpret_cast<const u32x2*>(kp);
+        kw[0] = t[0];
+        kw[1] = t[1];
+      } else {
+#pragma unroll
+        for (int w = 0; w < KW32; ++w) kw[w] = reinterpret_cast<const uint32_t*>(kp)[w];
+      }
+      const uint32_t sw = *reinterpret_cast<const uint32_t*>(src + OFF_S + (16 * j + l16) * SC + lg * 4);
       float4v s1 = float4v{0.f, 0.f, 0.f, 0.f}, s2 = float4v{0.f, 0.f, 0.f, 0.f};
       static_for<KS>([&](auto c) {
         constexpr int ks = decltype(c)::value;
-        s1 = mfma16x16x32(qr[ks], key_operand<KB, KW32, ks>(tK, r[j].k), s1);
-        s2 = mfma16x16x32(qp[ks], nib2x4<ks>(tS, r[j].s), s2);
+        s1 = mfma16x16x32(qr[ks], key_operand<KB, KW32, ks>(tK, kw), s1);
+        s2 = mfma16x16x32(qp[ks], nib2x4<ks>(tS, sw), s2);
       });
-      const int kb = k0 + 16 * j;
-      const float kn = h2f(static_cast<uint16_t>(r[j].kn)), rn = fb * h2f(static_cast<uint16_t>(r[j].rn));
-      const rsrc_t ro = make_rsrc(pout + kb, out_bytes - static_cast<uint32_t>(kb) * 4);
-      if (kb + 16 <= kend || kb + l16 < kend) {
+      const float kn = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + (16 * j + l16) * 4)));
+      const float rn =
+          fb * h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + NRM + (16 * j + l16) * 4)));
+      const int kb = ks0 + 16 * j;
+      if (kb + l16 < kend) {
+        const rsrc_t ro = make_rsrc(pout + kb, out_bytes - static_cast<uint32_t>(kb) * 4);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, s1[e] * kn + s2[e] * rn), ro, oo[e], 0,
@@ -709,18 +746,26 @@ __global__ void __launch_bounds__(256) decode_scores_kernel(DecodeArgs a) {
     }
   };
 
-  Raw ring[R][NB];
-  const int k0w = kbeg + wave * 16 * NB;
+  // the q fragments (the compiler's only outstanding loads) land before the ring
+  // starts, so none of its own waits inside the loop reach back past a DMA
+  __builtin_amdgcn_s_waitcnt(0);
+  const int k0w = kbeg + wave * NK;
 #pragma unroll
   for (int r = 0; r < R; ++r)
-    if (k0w + r * SLAB < kend) load(k0w + r * SLAB, ring[r]);
+    if (k0w + r * SLAB < kend) issue(k0w + r * SLAB, r);
+  __syncthreads();  // tables built
   for (int k0 = k0w; k0 < kend; k0 += R * SLAB) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int kb = k0 + r * SLAB;
-      if (kb < kend) {
-        score(kb, ring[r]);
-        if (kb + R * SLAB < kend) load(kb + R * SLAB, ring[r]);
+      const int ks0 = k0 + r * SLAB;
+      if (ks0 < kend) {
+        // slots issued after this one: those of the next R-1 slabs that exist
+        int later = 0;
+#pragma unroll
+        for (int q = 1; q < R; ++q) later += (ks0 + q * SLAB < kend) ? 1 : 0;
+        wait_slot(later);
+        slab(mine + r * SLOT, ks0);
+        if (ks0 + R * SLAB < kend) issue(ks0 + R * SLAB, r);
       }
     }
   }
@@ -916,7 +961,7 @@ static DecodePlan plan_decode(int B, int Hq, int Hkv, int Sq, int Sk, int d, int
 
 static DecodePlan plan_scores(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
   if (!decode_shape(Hq, Hkv, Sq, Sk, d, bits)) return DecodePlan{false, 0, 0, 0};
-  constexpr int slab = 64 * TQ_DEC_NB;
+  constexpr int slab = 4 * TQ_DEC_SNK;
   return plan_split(B, Hkv, Sk, TQ_DEC_SCORE_BLOCKS, slab, 2 * slab);
 }
 
@@ -968,9 +1013,9 @@ int decode_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* 
   a.scale = 1.f;
   a.scores = out;
   dim3 grid(a.nsplit, a.Hkv, a.B);
-  if (bits == 2) decode_scores_kernel<128, 2, TQ_DEC_NB><<<grid, 256, 0, s>>>(a);
-  else if (bits == 3) decode_scores_kernel<128, 3, TQ_DEC_NB><<<grid, 256, 0, s>>>(a);
-  else decode_scores_kernel<128, 4, TQ_DEC_NB><<<grid, 256, 0, s>>>(a);
+  if (bits == 2) decode_scores_kernel<128, 2, TQ_DEC_SR, TQ_DEC_SNK><<<grid, 256, 0, s>>>(a);
+  else if (bits == 3) decode_scores_kernel<128, 3, TQ_DEC_SR, TQ_DEC_SNK><<<grid, 256, 0, s>>>(a);
+  else decode_scores_kernel<128, 4, TQ_DEC_SR, TQ_DEC_SNK><<<grid, 256, 0, s>>>(a);
   return launch_status("tq_attention_scores (decode)");
 }
 
