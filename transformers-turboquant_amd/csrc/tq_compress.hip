@@ -10,11 +10,15 @@
 // q_rot, S_eff) skip the lo part and give exactly the f32 accumulation of f16
 // products that the reference performs.
 //
-// A block of 256 threads (4 wave64) owns a tile of R rows held in LDS as f32.
-// Each GEMM stage computes Z^T = W X^T so the weight matrix W (row-major,
-// pre-split in global memory, L2 resident) is the MFMA A operand and the LDS
-// row tile is the B operand; the accumulator layout (4 consecutive output
-// columns of one row per lane) is written straight back into the row tile.
+// Two kernel families:
+// * row-owned kernels (head_dim 64 / 128, 1-4 code bits): each wave owns 16
+//   rows end to end with the weights in LDS; see the section comment below.
+// * tile kernels (every head_dim, any bit width; also decompression): a block
+//   of 256 threads owns a tile of R rows held in LDS as f32.  Each GEMM stage
+//   computes Z^T = W X^T so the weight matrix W (row-major, pre-split in global
+//   memory, L2 resident) is the MFMA A operand and the LDS row tile is the B
+//   operand; the accumulator layout (4 consecutive output columns of one row per
+//   lane) is written straight back into the row tile.
 #include "tq_common.h"
 
 namespace tq {
@@ -476,6 +480,566 @@ __global__ void __launch_bounds__(256) query_prep_kernel(PrepArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- row-owned kernels (head_dim 64 / 128)
+// The same products, organised for throughput.  A block of 16 wave64 walks
+// rounds of 256 rows (persistent: the grid is what the device holds at once);
+// wave w owns rows 16w .. 16w+15 of a round and computes every output column of
+// them, so nothing is exchanged between waves inside a product and row norms
+// and maxima are shuffle reductions.  The weights live in LDS for the whole
+// block.  A wave's rows are the MFMA B operand, split into f16 (hi, lo) in
+// registers: lane (row l16, group g) supplies k = 32*ks + 8g + 0..7.  The weight
+// rows (output columns) are stored permuted, so that the accumulator of output
+// block mb = 2*ks + h holds columns 32*ks + 8g + 4h + e in lane (row, g): one
+// product's output is already the next product's B operand, and each lane's
+// outputs are 8 consecutive columns per k-step.
+enum { TM_KEYS = 0, TM_VALUES = 1, TM_QUERY = 2 };
+
+// n / d for n < 2^31 as (n * m) >> sh with m = ceil(2^sh / d), sh = 31 + ceil(log2 d):
+// the rounding error of m adds less than 1/d to n/d, which never crosses an integer.
+struct DivU31 {
+  uint32_t d, m, sh;
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    return static_cast<uint32_t>((static_cast<uint64_t>(n) * m) >> sh);
+  }
+};
+static DivU31 make_div(uint32_t d) {
+  uint32_t l = 0;
+  while ((uint64_t(1) << l) < d) ++l;
+  const uint64_t p = uint64_t(1) << (31 + l);
+  return DivU31{d, static_cast<uint32_t>((p + d - 1) / d), 31 + l};
+}
+
+struct TileArgs {
+  const void* x;
+  int64_t n;
+  DivU31 H, S;          // rows enumerate (batch, head, position)
+  int64_t sb, sh, ss;   // element strides; unit stride along d
+  int vec;              // row starts 16-byte aligned: vector loads
+  const uint16_t *w1, *w2, *w3;  // keys: Pi, Pi^T, S split; values: Pi split; queries: Pi split, S_eff f16
+  const float *cent, *bounds;
+  uint8_t *codes, *signs;
+  uint16_t *rn, *vn;
+  float *y_out, *proj_out;
+  uint16_t *q_rot, *q_proj;
+};
+
+template <int D, int NW_ = 8>
+struct RT {
+  static constexpr int NW = NW_, NT = 64 * NW, R = 16 * NW;  // waves, threads, rows per round
+  static constexpr int KS = D / 32, MB = D / 16, CH = D / 8;  // k-steps, output blocks, 16-byte chunks per row
+};
+
+// Weight plane in LDS: row p holds weight row perm_row(p); its 16-byte chunk c sits
+// at chunk swz(p, c), so the 16 rows of an A fragment read fall in distinct banks.
+__device__ __forceinline__ int perm_row(int p) {
+  const int mb = p >> 4, i = p & 15;
+  return 32 * (mb >> 1) + 8 * (i >> 2) + 4 * (mb & 1) + (i & 3);
+}
+template <int D>
+__device__ __forceinline__ int swz(int p, int c) {
+  return D == 128 ? (c ^ (p & 15)) : (c ^ ((p >> 1) & 7));
+}
+template <int D, int NT>
+__device__ __forceinline__ void load_plane(_Float16* __restrict__ dst, const uint16_t* __restrict__ src) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  for (int q = threadIdx.x; q < D * D / 8; q += NT) {
+    const int p = q / (D / 8), c = q % (D / 8);
+    const u32x4 v = *reinterpret_cast<const u32x4*>(src + perm_row(p) * D + c * 8);
+    *reinterpret_cast<u32x4*>(dst + p * D + swz<D>(p, c) * 8) = v;
+  }
+}
+
+// acc[mb] (output columns 32*(mb>>1) + 8g + 4*(mb&1) + e of row l16) = W . X^T for this
+// wave's 16 rows; B fragments b_hi/b_lo in registers, A from the LDS planes (hi, lo).
+// Passes hi.hi, + lo(W).hi(X) if W_LO, + hi(W).lo(X) if X_LO.
+#ifndef TQ_ROW_WAVES
+#define TQ_ROW_WAVES 8
+#endif
+template <int D, bool W_LO, bool X_LO, bool DBUF = (TQ_ROW_WAVES <= 8)>
+__device__ __forceinline__ void row_gemm(const _Float16* __restrict__ wh, const _Float16* __restrict__ wl,
+                                         const half8 (&b_hi)[D / 32], const half8 (&b_lo)[D / 32],
+                                         float4v (&acc)[D / 16], int l16, int g) {
+  using T = RT<D>;
+#pragma unroll
+  for (int mb = 0; mb < T::MB; ++mb) acc[mb] = float4v{0.f, 0.f, 0.f, 0.f};
+  // groups of 4 output blocks x one k-step; the A fragments of group q + 1 are
+  // read while the MFMAs of group q run (two register slots)
+  constexpr int NG = T::KS * (T::MB / 4);
+  half8 ah[DBUF ? 2 : 1][4], al[DBUF ? 2 : 1][W_LO ? 4 : 1];
+  auto fetch = [&](int q, int slot) {
+    const int ks = q / (T::MB / 4), m0 = (q % (T::MB / 4)) * 4;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int p = (m0 + u) * 16 + l16;
+      const int o = p * D + swz<D>(p, ks * 4 + g) * 8;
+      ah[slot][u] = *reinterpret_cast<const half8*>(wh + o);
+      if constexpr (W_LO) al[slot][u] = *reinterpret_cast<const half8*>(wl + o);
+    }
+  };
+  if constexpr (DBUF) fetch(0, 0);
+#pragma unroll
+  for (int q = 0; q < NG; ++q) {
+    if constexpr (DBUF) {
+      if (q + 1 < NG) fetch(q + 1, (q + 1) & 1);
+    } else {
+      fetch(q, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int ks = q / (T::MB / 4), m0 = (q % (T::MB / 4)) * 4, c = DBUF ? (q & 1) : 0;
+    // passes outermost: consecutive MFMAs write different accumulators
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[m0 + u] = mfma16x16x32(ah[c][u], b_hi[ks], acc[m0 + u]);
+    if constexpr (W_LO) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[m0 + u] = mfma16x16x32(al[c][u], b_hi[ks], acc[m0 + u]);
+    }
+    if constexpr (X_LO) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[m0 + u] = mfma16x16x32(ah[c][u], b_lo[ks], acc[m0 + u]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// value j (0..7) of k-step ks from an accumulator in the permuted layout
+__device__ __forceinline__ float acc_at(const float4v* acc, int ks, int j) { return acc[2 * ks + (j >> 2)][j & 3]; }
+
+// searchsorted-left over the 2^BB - 1 sorted boundaries (quantize.py:334-337):
+// BB <= 3 counts boundaries below y from registers, BB == 4 binary-searches the LDS copy
+template <int BB>
+__device__ __forceinline__ uint32_t code_of(float y, const float (&br)[7], const float* bnd) {
+  if constexpr (BB <= 3) {
+    uint32_t c = 0;
+#pragma unroll
+    for (int j = 0; j < (1 << BB) - 1; ++j) c += br[j] < y ? 1u : 0u;
+    return c;
+  } else {
+    uint32_t idx = 0;
+#pragma unroll
+    for (int step = 1 << (BB - 1); step; step >>= 1)
+      if (bnd[idx + step - 1] < y) idx += step;
+    return idx;
+  }
+}
+
+// waves per block; each holds up to 256 VGPRs and the weights sit in LDS
+#ifndef TQ_ROW_WAVES
+#define TQ_ROW_WAVES 8
+#endif
+constexpr int kRowWaves = TQ_ROW_WAVES;
+// wave-tiles (16 rows) a key wave carries through both phases of a chunk
+#ifndef TQ_KEY_TILES
+#define TQ_KEY_TILES 1
+#endif
+constexpr int kKeyTiles = TQ_KEY_TILES;
+
+template <int D, int DT, int MODE, int BB>
+__global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
+  using T = RT<D, kRowWaves>;
+  constexpr int KS = T::KS, MB = T::MB, NW = T::NW;
+  constexpr int KC = D * BB / 8;                                         // packed code bytes per row
+  constexpr int SC = D / 8;                                              // sign bytes per row
+  constexpr int NPL = MODE == TM_KEYS ? 4 : (MODE == TM_VALUES ? 2 : 3);  // weight planes resident at once
+  constexpr int STG = MODE == TM_QUERY ? 16 : 16 * (KC + (MODE == TM_KEYS ? SC : 0));  // wave staging bytes
+  __shared__ __attribute__((aligned(16))) _Float16 wsm[NPL * D * D];
+  __shared__ __attribute__((aligned(16))) uint8_t stg_all[NW * STG];
+  __shared__ float s_cent[MODE == TM_KEYS ? 16 : 1], s_bnd[MODE == TM_QUERY ? 1 : 16];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, g = lane >> 4;
+  uint8_t* const stg = stg_all + wave * STG;  // this wave's 16 packed rows: codes, then signs
+  const int64_t ntiles = (a.n + 15) / 16;
+  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * NW;
+  const int64_t gw = static_cast<int64_t>(blockIdx.x) * NW + wave;  // this wave's tiles: gw, gw + nwaves, ...
+  float br[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if constexpr (MODE != TM_QUERY) {
+    constexpr int NC = 1 << BB;
+    // keys reconstruct with the f16-rounded centroids (compressors.py:120-122)
+    if (tid < NC) {
+      if constexpr (MODE == TM_KEYS) s_cent[tid] = static_cast<float>(static_cast<_Float16>(a.cent[tid]));
+      if (tid < NC - 1) s_bnd[tid] = a.bounds[tid];
+    }
+    if constexpr (BB <= 3) {
+#pragma unroll
+      for (int j = 0; j < NC - 1; ++j) br[j] = a.bounds[j];
+    }
+  }
+  _Float16* const P0 = wsm;
+  _Float16* const P1 = wsm + D * D;
+  _Float16* const P2 = wsm + (NPL > 2 ? 2 : 0) * D * D;
+  _Float16* const P3 = wsm + (NPL > 3 ? 3 : 0) * D * D;
+
+  // ---- this lane's row of tile t and its elements k = 32*ks + 8g + 0..7, fetched raw
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  constexpr int RW = DT == TQ_F32 ? 2 : 1;  // 16-byte pieces per k-step
+  struct Raw {
+    u32x4 v[KS][RW];
+  };
+  auto fetch_row = [&](int64_t t, Raw& raw) {
+    const int64_t gr = t * 16 + l16;
+    if (t >= ntiles || gr >= a.n) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int q = 0; q < RW; ++q) raw.v[ks][q] = u32x4{0u, 0u, 0u, 0u};
+      return;
+    }
+    const uint32_t r32 = static_cast<uint32_t>(gr);
+    const uint32_t bh = a.S.div(r32), s = r32 - bh * a.S.d;
+    const uint32_t bb = a.H.div(bh), h = bh - bb * a.H.d;
+    const int64_t off = static_cast<int64_t>(bb) * a.sb + static_cast<int64_t>(h) * a.sh +
+                        static_cast<int64_t>(s) * a.ss + 8 * g;
+    constexpr int ES = DT == TQ_F32 ? 4 : 2;
+    const uint8_t* base = static_cast<const uint8_t*>(a.x) + off * ES;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int q = 0; q < RW; ++q) {
+        const uint8_t* p = base + (32 * ks) * ES + 16 * q;
+        if (a.vec) {
+          raw.v[ks][q] = *reinterpret_cast<const u32x4*>(p);
+        } else {
+          u32x4 v;
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            uint32_t x = 0;
+            if constexpr (ES == 4) x = *reinterpret_cast<const uint32_t*>(p + 4 * w);
+            else x = static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(p + 4 * w)) |
+                     (static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(p + 4 * w + 2)) << 16);
+            v[w] = x;
+          }
+          raw.v[ks][q] = v;
+        }
+      }
+  };
+  auto unpack_row = [&](const Raw& raw, float (&xv)[KS][8]) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if constexpr (DT == TQ_F32) {
+          xv[ks][j] = __uint_as_float(raw.v[ks][j >> 2][j & 3]);
+        } else {
+          const uint32_t w = raw.v[ks][0][j >> 1];
+          const uint16_t h = static_cast<uint16_t>((j & 1) ? (w >> 16) : (w & 0xffffu));
+          xv[ks][j] = DT == TQ_F16 ? h2f(h) : bf16_to_f32(h);
+        }
+      }
+  };
+  // sum / max over the 4 lanes of a row (lanes l16, l16+16, l16+32, l16+48)
+  auto row_sum = [&](float v) {
+    v += __shfl_xor(v, 16, 64);
+    return v + __shfl_xor(v, 32, 64);
+  };
+  auto row_max = [&](float v) {
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    return fmaxf(v, __shfl_xor(v, 32, 64));
+  };
+  auto split_row = [&](const float (&v)[KS][8], float sc, half8 (&hi)[KS], half8 (&lo)[KS]) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        _Float16 h, l;
+        split_f16(v[ks][j] * sc, h, l);
+        hi[ks][j] = h;
+        lo[ks][j] = l;
+      }
+  };
+  // wave-private staging is written and read by this wave only: order it within the wave
+  auto wave_sync = [&]() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  // copy `bytes`-byte rows of this wave's 16 staged rows at `src` to out + row0 * bytes
+  auto store_rows = [&](const uint8_t* src, uint8_t* out, int64_t row0, int bytes) {
+    const int64_t nr = a.n - row0 < 16 ? a.n - row0 : 16;
+    const int nd = static_cast<int>(nr) * bytes / 4;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(out + row0 * bytes);
+    for (int i = lane; i < nd; i += 64) dst[i] = reinterpret_cast<const uint32_t*>(src)[i];
+  };
+  // y -> codes of this lane's 8 columns per k-step, staged at the row's packed position
+  auto quantize_stage = [&](const float4v (&acc)[MB], int64_t gr, uint32_t (&cw)[KS]) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      float4v y0, y1;
+      uint32_t v = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float y = acc_at(acc, ks, j) * kUnsplit2;
+        if (j < 4) y0[j] = y;
+        else y1[j - 4] = y;
+        v |= code_of<BB>(y, br, s_bnd) << (BB * j);
+      }
+      cw[ks] = v;
+      if (a.y_out && gr < a.n) {
+        float4v* yo = reinterpret_cast<float4v*>(a.y_out + gr * D + 32 * ks + 8 * g);
+        yo[0] = y0;
+        yo[1] = y1;
+      }
+      uint8_t* dst = stg + l16 * KC + (32 * ks + 8 * g) * BB / 8;
+#pragma unroll
+      for (int k = 0; k < BB; ++k) dst[k] = static_cast<uint8_t>(v >> (8 * k));
+    }
+  };
+
+  half8 bh[KS], bl[KS];
+  float4v acc[MB];
+  float xv[KS][8];
+  Raw raw, nxt;
+
+  if constexpr (MODE == TM_QUERY) {
+    load_plane<D, T::NT>(P0, a.w1);
+    load_plane<D, T::NT>(P1, a.w1 + D * D);
+    load_plane<D, T::NT>(P2, a.w2);
+    fetch_row(gw, raw);
+    __syncthreads();
+    for (int64_t t = gw; t < ntiles; t += nwaves) {
+      const int64_t gr = t * 16 + l16;
+      unpack_row(raw, xv);
+      fetch_row(t + nwaves, nxt);  // next tile's row, in flight during the products
+      // per-row power-of-two scale so the split parts stay in range (|q| * scale < kSplit)
+      float mx = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(xv[ks][j]));
+      int e2;
+      frexpf(row_max(mx), &e2);
+      split_row(xv, ldexpf(kSplit, -e2), bh, bl);
+      // q_rot = f16(q Pi^T)   (compressors.py:186)
+      row_gemm<D, true, true>(P0, P1, bh, bl, acc, l16, g);
+      const float inv = ldexpf(kUnsplit2, e2);
+      mx = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          bh[ks][j] = static_cast<_Float16>(acc_at(acc, ks, j) * inv);
+          mx = fmaxf(mx, fabsf(static_cast<float>(bh[ks][j])));
+        }
+        if (gr < a.n) *reinterpret_cast<half8*>(a.q_rot + gr * D + 32 * ks + 8 * g) = bh[ks];
+      }
+      // q_rot holds f16 values: scaling by 2^(12-e) keeps them exact in f16
+      frexpf(row_max(mx), &e2);
+      const float sc2 = ldexpf(4096.f, -e2), inv2 = ldexpf(1.f / 4096.f, e2);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) bh[ks][j] = static_cast<_Float16>(static_cast<float>(bh[ks][j]) * sc2);
+      // q_proj = f16(q_rot S_eff^T): f32 accumulation of exact f16 products (kernels/attention.py:158-167)
+      row_gemm<D, false, false>(P2, P2, bh, bl, acc, l16, g);
+      if (gr < a.n) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          half8 o;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) o[j] = static_cast<_Float16>(acc_at(acc, ks, j) * inv2);
+          *reinterpret_cast<half8*>(a.q_proj + gr * D + 32 * ks + 8 * g) = o;
+        }
+      }
+      raw = nxt;
+    }
+  } else if constexpr (MODE == TM_VALUES) {
+    load_plane<D, T::NT>(P0, a.w1);
+    load_plane<D, T::NT>(P1, a.w1 + D * D);
+    fetch_row(gw, raw);
+    __syncthreads();
+    for (int64_t t = gw; t < ntiles; t += nwaves) {
+      const int64_t gr = t * 16 + l16;
+      unpack_row(raw, xv);
+      fetch_row(t + nwaves, nxt);  // next tile's row, in flight during the product
+      // ---- vn = ||x||; xn = x / (vn + 1e-8)   (compressors.py:274-275)
+      float ss = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = fmaf(xv[ks][j], xv[ks][j], ss);
+      const float vn = sqrtf(row_sum(ss));
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xv[ks][j] = xv[ks][j] / (vn + 1e-8f);
+      split_row(xv, kSplit, bh, bl);
+      // ---- y = xn Pi^T (compressors.py:276); codes = searchsorted-left, packed LSB first
+      row_gemm<D, true, true>(P0, P1, bh, bl, acc, l16, g);
+      uint32_t cw[KS];
+      quantize_stage(acc, gr, cw);
+      if (g == 0 && gr < a.n) a.vn[gr] = f2h(vn);
+      wave_sync();
+      store_rows(stg, a.codes, t * 16, KC);
+      wave_sync();
+      raw = nxt;
+    }
+  } else {
+    // keys: S stays in P2/P3; P0/P1 hold Pi for phase A and Pi^T for phase B of each chunk
+    load_plane<D, T::NT>(P2, a.w3);
+    load_plane<D, T::NT>(P3, a.w3 + D * D);
+    const int64_t per_wave = (ntiles + nwaves - 1) / nwaves;  // tiles of the busiest wave
+    for (int64_t c0 = 0; c0 < per_wave; c0 += kKeyTiles) {
+      __syncthreads();  // the previous chunk's phase B is done with P0/P1
+      load_plane<D, T::NT>(P0, a.w1);
+      load_plane<D, T::NT>(P1, a.w1 + D * D);
+      __syncthreads();
+      // ---- phase A: vn, y = xn Pi^T, codes   (compressors.py:108-116)
+      uint32_t cws[kKeyTiles][KS];
+      float vns[kKeyTiles];
+      fetch_row(gw + c0 * nwaves, raw);
+#pragma unroll
+      for (int i = 0; i < kKeyTiles; ++i) {
+        const int64_t t = gw + (c0 + i) * nwaves;
+        const int64_t gr = t * 16 + l16;
+        unpack_row(raw, xv);
+        if (i + 1 < kKeyTiles) fetch_row(t + nwaves, nxt);
+        float ss = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) ss = fmaf(xv[ks][j], xv[ks][j], ss);
+        const float vn = sqrtf(row_sum(ss));
+        vns[i] = vn;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) xv[ks][j] = xv[ks][j] / (vn + 1e-8f);
+        split_row(xv, kSplit, bh, bl);
+        row_gemm<D, true, true>(P0, P1, bh, bl, acc, l16, g);
+        if (t < ntiles) {
+          quantize_stage(acc, gr, cws[i]);
+          if (g == 0 && gr < a.n) a.vn[gr] = f2h(vn);
+          wave_sync();
+          store_rows(stg, a.codes, t * 16, KC);
+          wave_sync();
+        }
+        raw = nxt;
+      }
+      __syncthreads();  // every wave is done with Pi
+      load_plane<D, T::NT>(P0, a.w2);
+      load_plane<D, T::NT>(P1, a.w2 + D * D);
+      __syncthreads();
+      // ---- phase B: k_mse = (yhat Pi) vn, r = x - k_mse, rn, proj = r S^T, signs   (compressors.py:120-136)
+      fetch_row(gw + c0 * nwaves, raw);
+#pragma unroll
+      for (int i = 0; i < kKeyTiles; ++i) {
+        const int64_t t = gw + (c0 + i) * nwaves;
+        const int64_t gr = t * 16 + l16;
+        if (i + 1 < kKeyTiles) fetch_row(t + nwaves, nxt);
+        // yhat = f16(C)[code] times 2^10 (exact)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            bh[ks][j] = static_cast<_Float16>(s_cent[(cws[i][ks] >> (BB * j)) & ((1u << BB) - 1u)] * kSplit);
+        row_gemm<D, true, false>(P0, P1, bh, bl, acc, l16, g);
+        unpack_row(raw, xv);
+        const float vn = vns[i];
+        float ss = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float rr = xv[ks][j] - (acc_at(acc, ks, j) * kUnsplit2) * vn;
+            xv[ks][j] = rr;
+            ss = fmaf(rr, rr, ss);
+          }
+        const float rn = sqrtf(row_sum(ss));
+        // split scale from ||x||: |r| <= ~||x||, so r * 2^(10 - e(vn)) keeps both parts in range
+        int e2;
+        frexpf(vn, &e2);
+        split_row(xv, ldexpf(kSplit, -e2), bh, bl);
+        row_gemm<D, true, true>(P2, P3, bh, bl, acc, l16, g);
+        const float inv = ldexpf(kUnsplit2, e2);
+        if (t < ntiles) {
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) {
+            float4v p0, p1;
+            uint32_t bits = 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const float pv = acc_at(acc, ks, j) * inv;
+              if (j < 4) p0[j] = pv;
+              else p1[j - 4] = pv;
+              bits |= (pv >= 0.f ? 1u : 0u) << j;
+            }
+            if (a.proj_out && gr < a.n) {
+              float4v* po = reinterpret_cast<float4v*>(a.proj_out + gr * D + 32 * ks + 8 * g);
+              po[0] = p0;
+              po[1] = p1;
+            }
+            stg[16 * KC + l16 * SC + 4 * ks + g] = static_cast<uint8_t>(bits);
+          }
+          if (g == 0 && gr < a.n) a.rn[gr] = f2h(rn);
+          wave_sync();
+          store_rows(stg + 16 * KC, a.signs, t * 16, SC);
+          wave_sync();
+        }
+        raw = nxt;
+      }
+    }
+  }
+}
+
+// Blocks of `kernel` the device holds at once (occupancy x compute units), per device.
+static int resident_blocks(const void* kernel, int threads, int* cache) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) dev = 0;
+  if (cache[dev] > 0) return cache[dev];
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess || per_cu < 1) per_cu = 1;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 1;
+  cache[dev] = per_cu * cus;
+  return cache[dev];
+}
+
+template <int D, int DT, int MODE, int BB>
+static void launch_tile(const TileArgs& a, hipStream_t s) {
+  static int cache[16] = {};
+  using T = RT<D, kRowWaves>;
+  const int64_t blocks = (a.n + T::R - 1) / T::R;  // one 16-row tile per wave
+  const int64_t res = resident_blocks(reinterpret_cast<const void*>(&rows_kernel<D, DT, MODE, BB>), T::NT, cache);
+  const unsigned grid = static_cast<unsigned>(blocks < res ? blocks : res);
+  rows_kernel<D, DT, MODE, BB><<<grid, T::NT, 0, s>>>(a);
+}
+
+template <int D, int MODE, int BB>
+static void launch_tile_dt(const TileArgs& a, int dtype, hipStream_t s) {
+  if (dtype == TQ_F32) launch_tile<D, TQ_F32, MODE, BB>(a, s);
+  else if (dtype == TQ_F16) launch_tile<D, TQ_F16, MODE, BB>(a, s);
+  else launch_tile<D, TQ_BF16, MODE, BB>(a, s);
+}
+
+// The row-owned kernels take head_dim 64 / 128, 1-4 code bits and fewer than
+// 2^31 rows; packed outputs must be dword aligned.
+static bool tile_applies(int d, int64_t n, int b) {
+  return (d == 64 || d == 128) && b >= 1 && b <= 4 && n < (int64_t(1) << 31);
+}
+// 16-byte vector loads need every row start 16-byte aligned
+static int tile_vec(const void* x, int dtype, int64_t sb, int64_t sh, int64_t ss) {
+  const int64_t es = dtype == TQ_F32 ? 4 : 2;
+  return (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (sb * es) % 16 == 0 && (sh * es) % 16 == 0 &&
+         (ss * es) % 16 == 0;
+}
+
+template <int MODE>
+static void dispatch_tile(const TileArgs& a, int d, int dtype, int b, hipStream_t s) {
+  switch (d * 8 + b) {
+    case 64 * 8 + 1: launch_tile_dt<64, MODE, 1>(a, dtype, s); break;
+    case 64 * 8 + 2: launch_tile_dt<64, MODE, 2>(a, dtype, s); break;
+    case 64 * 8 + 3: launch_tile_dt<64, MODE, 3>(a, dtype, s); break;
+    case 64 * 8 + 4: launch_tile_dt<64, MODE, 4>(a, dtype, s); break;
+    case 128 * 8 + 1: launch_tile_dt<128, MODE, 1>(a, dtype, s); break;
+    case 128 * 8 + 2: launch_tile_dt<128, MODE, 2>(a, dtype, s); break;
+    case 128 * 8 + 3: launch_tile_dt<128, MODE, 3>(a, dtype, s); break;
+    default: launch_tile_dt<128, MODE, 4>(a, dtype, s); break;
+  }
+}
+template <>
+void dispatch_tile<TM_QUERY>(const TileArgs& a, int d, int dtype, int, hipStream_t s) {
+  if (d == 64) launch_tile_dt<64, TM_QUERY, 1>(a, dtype, s);
+  else launch_tile_dt<128, TM_QUERY, 1>(a, dtype, s);
+}
+
 // ---------------------------------------------------------------- dispatch
 #define TQ_DEFINE_LAUNCH(NAME, KERNEL, ARGS)                                                     \
   template <int D, int DT>                                                                      \
@@ -533,6 +1097,17 @@ int tq_compress_keys(const void* x, int32_t dtype, int32_t B, int32_t H, int32_t
   if (n == 0) return TQ_OK;
   TQ_REQUIRE(x && pi_split && pit_split && s_split && centroids && bounds && codes && signs && rn && vn,
              "tq_compress_keys: null pointer");
+  if (tile_applies(d, n, b_eff) && reinterpret_cast<uintptr_t>(codes) % 4 == 0 &&
+      reinterpret_cast<uintptr_t>(signs) % 4 == 0) {
+    TileArgs t{};
+    t.x = x; t.n = n; t.H = make_div(static_cast<uint32_t>(H)); t.S = make_div(static_cast<uint32_t>(S));
+    t.sb = sxb; t.sh = sxh; t.ss = sxs; t.vec = tile_vec(x, dtype, sxb, sxh, sxs);
+    t.w1 = pi_split; t.w2 = pit_split; t.w3 = s_split;
+    t.cent = centroids; t.bounds = bounds;
+    t.codes = codes; t.signs = signs; t.rn = rn; t.vn = vn; t.y_out = y_out; t.proj_out = proj_out;
+    dispatch_tile<TM_KEYS>(t, d, dtype, b_eff, as_stream(stream));
+    return launch_status("tq_compress_keys");
+  }
   KeyArgs a{x, n, Rows4{H, S, sxb, sxh, sxs}, pi_split, pit_split, s_split, centroids, bounds, b_eff, codes, signs, rn, vn,
             y_out, proj_out};
   TQ_SWITCH_DD(launch_keys, d, dtype, a, n, as_stream(stream));
@@ -548,6 +1123,15 @@ int tq_compress_values(const void* x, int32_t dtype, int32_t B, int32_t H, int32
   const int64_t n = static_cast<int64_t>(B) * H * S;
   if (n == 0) return TQ_OK;
   TQ_REQUIRE(x && pi_split && bounds && codes && vn, "tq_compress_values: null pointer");
+  if (tile_applies(d, n, b) && reinterpret_cast<uintptr_t>(codes) % 4 == 0) {
+    TileArgs t{};
+    t.x = x; t.n = n; t.H = make_div(static_cast<uint32_t>(H)); t.S = make_div(static_cast<uint32_t>(S));
+    t.sb = sxb; t.sh = sxh; t.ss = sxs; t.vec = tile_vec(x, dtype, sxb, sxh, sxs);
+    t.w1 = pi_split; t.bounds = bounds;
+    t.codes = codes; t.vn = vn; t.y_out = y_out;
+    dispatch_tile<TM_VALUES>(t, d, dtype, b, as_stream(stream));
+    return launch_status("tq_compress_values");
+  }
   ValArgs a{x, n, Rows4{H, S, sxb, sxh, sxs}, pi_split, bounds, b, codes, vn, y_out};
   TQ_SWITCH_DD(launch_values, d, dtype, a, n, as_stream(stream));
   return launch_status("tq_compress_values");
@@ -574,6 +1158,15 @@ int tq_query_prep(const void* q, int32_t dtype, int32_t B, int32_t Hq, int32_t S
   const int64_t n = static_cast<int64_t>(B) * Hq * Sq;
   if (n == 0) return TQ_OK;
   TQ_REQUIRE(q && pi_split && s_eff_f16 && q_rot && q_proj, "tq_query_prep: null pointer");
+  if (tile_applies(d, n, 1) && reinterpret_cast<uintptr_t>(q_rot) % 8 == 0 &&
+      reinterpret_cast<uintptr_t>(q_proj) % 8 == 0) {
+    TileArgs t{};
+    t.x = q; t.n = n; t.H = make_div(static_cast<uint32_t>(Hq)); t.S = make_div(static_cast<uint32_t>(Sq));
+    t.sb = sqb; t.sh = sqh; t.ss = sqs; t.vec = tile_vec(q, dtype, sqb, sqh, sqs);
+    t.w1 = pi_split; t.w2 = s_eff_f16; t.q_rot = q_rot; t.q_proj = q_proj;
+    dispatch_tile<TM_QUERY>(t, d, dtype, 1, as_stream(stream));
+    return launch_status("tq_query_prep");
+  }
   PrepArgs a{q, B, Hq, Sq, sqb, sqh, sqs, pi_split, s_eff_f16, q_rot, q_proj};
   TQ_SWITCH_DD(launch_prep, d, dtype, a, n, as_stream(stream));
   return launch_status("tq_query_prep");
