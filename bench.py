@@ -46,7 +46,7 @@ def val_rec_bytes(bits: int, d: int) -> int:
     return math.ceil(d * bits / 8) + 2
 
 
-def measured_traffic(kernel: str, record: str = "traffic_config2.json"):
+def measured_traffic(kernel: str, record: str = "traffic_bench.json"):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE passes (profiles/<record>), scaled by the copy-kernel calibration
     recorded there; None if no such measurement is committed."""
@@ -246,14 +246,13 @@ def decode_legs(kc, vc, outliers, steps: int, warmup: int) -> tuple[dict, dict]:
                   + DEC_B * HQ * D * 2)
     gbs_s = score_bytes / (ms_scores * 1e-3) / 1e9
     gbs_a = attn_bytes / (ms_attn * 1e-3) / 1e9
-    rec = "traffic_decode.json"
     scores_leg = {
         "ms_per_launch": ms_scores,
         "key_heads_per_s": key_heads / (ms_scores * 1e-3),
         "roofline": {
             "kernel": "tq::decode_scores_kernel<128, 3, 2, 64> (scores, f32 written)",
             "bound": "hbm", "achieved": gbs_s, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": gbs_s / HBM_PEAK_GBS, "traffic": measured_traffic("decode_scores", rec),
+            "frac": gbs_s / HBM_PEAK_GBS, "traffic": measured_traffic("tq::decode_scores_kernel<128, 3, 2, 64>"),
             "algorithmic_bytes_per_launch": score_bytes,
         },
     }
@@ -262,9 +261,9 @@ def decode_legs(kc, vc, outliers, steps: int, warmup: int) -> tuple[dict, dict]:
         "ms_per_launch": ms_attn,
         "key_heads_per_s": key_heads / (ms_attn * 1e-3),
         "roofline": {
-            "kernel": "tq::decode_attn_lds_kernel<128, 3, 2, 3, true> + tq::decode_merge_kernel<128>",
+            "kernel": "tq::decode_attn_lds_kernel<128, 3, 2, 3, false> + tq::decode_merge_kernel<128>",
             "bound": "hbm", "achieved": gbs_a, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": gbs_a / HBM_PEAK_GBS, "traffic": measured_traffic("decode_attention", rec),
+            "frac": gbs_a / HBM_PEAK_GBS, "traffic": measured_traffic("decode_attention (attention + merge)"),
             "algorithmic_bytes_per_launch": attn_bytes,
         },
     }
@@ -328,7 +327,7 @@ def prefill_leg(kc, vc, q, k, v, steps: int, warmup: int) -> dict:
         "roofline": {
             "kernel": "tq::attn_kernel<128, 2, false, false> (fused scores + softmax + P.V)",
             "bound": "mfma", "achieved": tflops, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": tflops / MFMA_F16_PEAK_TFLOPS, "traffic": measured_traffic("attn_kernel"),
+            "frac": tflops / MFMA_F16_PEAK_TFLOPS, "traffic": measured_traffic("tq::attn_kernel<128, 2, false, false>"),
         },
     }
 
