@@ -183,6 +183,34 @@ int tq_attention_fwd(const uint16_t* q_rot, const uint16_t* q_proj,
                      int64_t soh, int64_t sos, void* workspace,
                      int64_t workspace_bytes, void* stream);
 
+/* tq_attention_scores / tq_attention_fwd over key and value planes whose
+ * (batch, kv head) planes start kv_stride rows apart (kv_stride >= Sk; 0 means
+ * Sk): the first Sk rows of each plane are attended.  This is the layout of a
+ * compressed KV cache that preallocates kv_stride positions per head and
+ * appends tokens in place.  No counterpart in the reference, which disables
+ * the KV cache (patch.py:81); the tensor-level concept is
+ * turboquant.py:199-286 (TurboQuantKVCache). */
+int tq_attention_scores_kv(const uint16_t* q_rot, const uint16_t* q_proj,
+                           const uint8_t* key_codes, const uint8_t* key_signs,
+                           const uint16_t* key_rn, const uint16_t* key_vn,
+                           const uint16_t* centroids_f16, int32_t B, int32_t Hq,
+                           int32_t Hkv, int32_t Sq, int32_t Sk,
+                           int64_t kv_stride, int32_t d, int32_t bits,
+                           float coeff, float* out, void* stream);
+int tq_attention_fwd_kv(const uint16_t* q_rot, const uint16_t* q_proj,
+                        const uint8_t* key_codes, const uint8_t* key_signs,
+                        const uint16_t* key_rn, const uint16_t* key_vn,
+                        const uint16_t* key_centroids_f16, int32_t bits,
+                        const uint8_t* val_codes, const uint16_t* val_vn,
+                        const float* val_centroids, int32_t val_bits,
+                        const uint16_t* val_pit_split, int32_t B, int32_t Hq,
+                        int32_t Hkv, int32_t Sq, int32_t Sk, int64_t kv_stride,
+                        int32_t d, float coeff, float scale, int32_t causal,
+                        const float* mask, int64_t smb, int64_t smh, int64_t smq,
+                        int64_t smk, void* out, int32_t out_dtype, int64_t sob,
+                        int64_t soh, int64_t sos, void* workspace,
+                        int64_t workspace_bytes, void* stream);
+
 /* Bytes of caller-provided device workspace tq_attention_fwd uses for the
  * split-K decode path at this shape (head_dim 128, bits 2-4, at most 16
  * (query row, query head) pairs per kv head, value bits == key bits); 0 when

@@ -1,0 +1,132 @@
+"""The compressed KV cache on the GPU: in-place appends and kv_stride attention.
+
+The cache's planes must equal a one-shot compression of the concatenated
+sequence bit for bit, and attention read through kv_stride from the capacity
+planes must equal attention over compact planes exactly (same kernels, same
+data).  End to end, cached greedy decoding must follow the cache-less
+recomputation the reference performs.
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import tq_oracle as O
+from transformers_turboquant import TurboQuantCache, apply_turboquant
+from turboquant_pytorch import _native
+from turboquant_pytorch.compressors import TurboQuantCompressorMSE, TurboQuantCompressorV2, _tables
+from turboquant_pytorch.fused import compressed_attention
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_cache_planes_and_attention_match_compact(bits):
+    print("case: cache planes bits", bits, flush=True)
+    dev, d, B, Hkv, G = "cuda", 128, 2, 2, 4
+    kc = TurboQuantCompressorV2(d, bits, seed=42, device=dev)
+    vc = TurboQuantCompressorMSE(d, bits, seed=10042, device=dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    total = 100 + 5 + 300
+    k = torch.randn(B, Hkv, total, d, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, total, d, device=dev, generator=g).to(torch.bfloat16)
+    cache = TurboQuantCache()
+    steps = [(0, 100)] + [(100 + i, 101 + i) for i in range(5)] + [(105, total)]
+    for lo, hi in steps:
+        ck, cv = cache.append(0, kc, vc, k[:, :, lo:hi], v[:, :, lo:hi])
+        lay = cache.layer(0)
+        assert ck["shape"] == (B, Hkv, hi, d) and ck["kv_stride"] == lay.capacity >= hi
+        fk, fv = kc.compress(k[:, :, :hi]), vc.compress(v[:, :, :hi])
+        n = B * Hkv * hi
+        got_k, got_v = lay.compact()
+        for name in ("packed_key_indices", "packed_qjl_signs"):
+            assert torch.equal(got_k[name], fk[name]), name
+        assert torch.equal(got_k["residual_norm"], fk["residual_norm"])
+        assert torch.equal(got_k["vec_norms"], fk["vec_norms"])
+        assert torch.equal(got_v["packed_indices"], fv["packed_indices"])
+        assert torch.equal(got_v["vec_norms"], fv["vec_norms"].reshape(n))
+        # one decode row (split-K decode kernels) and 40 causal rows (tiled kernel)
+        for sq in (1, 40) if hi >= 40 else (1,):
+            q = torch.randn(B, Hkv * G, sq, d, device=dev, generator=g).to(torch.bfloat16)
+            a = compressed_attention(q, kc, vc, ck, cv, causal=True, out_dtype=torch.float32)
+            c = compressed_attention(q, kc, vc, fk, fv, causal=True, out_dtype=torch.float32)
+            torch.cuda.synchronize()
+            assert torch.equal(a, c), (hi, sq)
+    assert cache.layer(0).capacity == 512  # 256 -> grown by doubling
+
+
+def test_scores_kv_stride_match_compact():
+    print("case: scores kv_stride", flush=True)
+    dev, d, B, Hkv, G, bits = "cuda", 128, 2, 2, 4, 3
+    kc = TurboQuantCompressorV2(d, bits, seed=7, device=dev)
+    vc = TurboQuantCompressorMSE(d, bits, seed=10007, device=dev)
+    g = torch.Generator(device=dev).manual_seed(1)
+    k = torch.randn(B, Hkv, 333, d, device=dev, generator=g)
+    cache = TurboQuantCache()
+    ck, _ = cache.append(0, kc, vc, k, k)
+    fk = kc.compress(k)
+    lib = _native.lib()
+    t = _tables(kc, dev, with_qjl=True)
+    coeff = math.sqrt(math.pi / 2) / d
+    for sq in (1, 3, 33):
+        q = torch.randn(B, Hkv * G, sq, d, device=dev, generator=g)
+        q_rot, q_proj = kc.prepare_queries(q)
+        outs = []
+        for planes, stride in ((ck, ck["kv_stride"]), (fk, 0)):
+            o = torch.empty(B, Hkv * G, sq, 333, device=dev)
+            _native.check(lib.tq_attention_scores_kv(
+                q_rot.data_ptr(), q_proj.data_ptr(), planes["packed_key_indices"].data_ptr(),
+                planes["packed_qjl_signs"].data_ptr(), planes["residual_norm"].data_ptr(),
+                planes["vec_norms"].data_ptr(), t.cent16.data_ptr(), B, Hkv * G, Hkv, sq, 333, stride, d,
+                bits, coeff, o.data_ptr(), _native.stream_of(o)), "scores_kv")
+            outs.append(o)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], outs[1]), sq
+        # the compressor's method reads kv_stride from the cache dict
+        assert torch.equal(kc.asymmetric_attention_scores(q, ck), kc.asymmetric_attention_scores(q, fk))
+        # and the oracle's estimator on the same packed planes and prepared queries
+        n = B * Hkv * 333
+        codes = O.unpack_bits(fk["packed_key_indices"].reshape(n, -1).cpu().numpy(), bits - 1, d)
+        signs = O.unpack_bits(fk["packed_qjl_signs"].reshape(n, -1).cpu().numpy(), 1, d)
+        rn = fk["residual_norm"].reshape(n).cpu().numpy()
+        vn = fk["vec_norms"].reshape(n).cpu().numpy()
+        qr, qp = q_rot.cpu().numpy(), q_proj.cpu().numpy()
+        cent = t.cent16.cpu().numpy()
+        for b in range(B):
+            for h in range(Hkv * G):
+                r = slice((b * Hkv + h // G) * 333, (b * Hkv + h // G + 1) * 333)
+                ref = O.scores_packed(qr[b, h], qp[b, h], codes[r], signs[r], rn[r], vn[r], cent, coeff)
+                assert O.rel_err(outs[0][b, h].cpu().numpy(), ref) < 1e-5, (sq, b, h)
+    # a stride below Sk is rejected
+    bad = lib.tq_attention_scores_kv(q_rot.data_ptr(), q_proj.data_ptr(), fk["packed_key_indices"].data_ptr(),
+                                     fk["packed_qjl_signs"].data_ptr(), fk["residual_norm"].data_ptr(),
+                                     fk["vec_norms"].data_ptr(), t.cent16.data_ptr(), B, Hkv * G, Hkv, 33, 333,
+                                     100, d, bits, coeff, outs[0].data_ptr(), None)
+    assert bad != 0 and b"kv_stride" in lib.tq_last_error()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_cached_generate_matches_recompute_gpu(dtype):
+    print("case: cached generate", dtype, flush=True)
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    torch.manual_seed(0)
+    cfg = LlamaConfig(vocab_size=1000, hidden_size=1024, intermediate_size=1024, num_hidden_layers=2,
+                      num_attention_heads=8, num_key_value_heads=2)  # head_dim 128, G = 4: decode kernels
+    model = apply_turboquant(LlamaForCausalLM(cfg).eval(), bits=3).to("cuda", dtype)
+    ids = torch.randint(0, 1000, (2, 37), generator=torch.Generator().manual_seed(5)).cuda()
+    kw = dict(max_new_tokens=8, min_new_tokens=8, do_sample=False, output_logits=True,
+              return_dict_in_generate=True, attention_mask=torch.ones_like(ids))
+    with torch.no_grad():
+        ref = model.generate(ids, use_cache=False, **kw)
+        cache = TurboQuantCache()
+        got = model.generate(ids, use_cache=True, past_key_values=cache, **kw)
+    assert cache.get_seq_length() == 37 + 7
+    # the cached path runs the split-K decode kernels, the recomputation the tiled
+    # kernel: the same estimator with different f16 roundings of P.  Raw logits,
+    # since min_new_tokens writes -inf into the processed scores.
+    assert len(got.logits) == len(ref.logits) == 8
+    cos = [O.cosine(a.float().cpu().numpy(), b.float().cpu().numpy()) for a, b in zip(got.logits, ref.logits)]
+    assert min(cos) > (0.9999 if dtype == torch.float32 else 0.999), cos
+    assert (got.sequences == ref.sequences).float().mean() > 0.95

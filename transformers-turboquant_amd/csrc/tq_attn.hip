@@ -72,6 +72,7 @@ struct AttnArgs {
   const float* vcent32;
   int vb;
   int B, Hq, Hkv, Sq, Sk, G, QT, nqb;
+  int64_t ldk;  // rows between consecutive (batch, kv head) planes (>= Sk)
   float coeff, scale;
   int causal;
   const float* mask;
@@ -185,8 +186,8 @@ __global__ void __launch_bounds__(64 * TQ_ATTN_WAVES, TQ_ATTN_MINBLK) attn_kerne
   float r_a = 0.f, r_b = 0.f, r_v = 0.f;
   auto fetch = [&](int k0) {
     const int nk = min(KT, a.Sk - k0);
-    const uint32_t* gk = reinterpret_cast<const uint32_t*>(a.kcodes + (bh_kv * a.Sk + k0) * KC);
-    const uint32_t* gs = reinterpret_cast<const uint32_t*>(a.ksigns + (bh_kv * a.Sk + k0) * SC);
+    const uint32_t* gk = reinterpret_cast<const uint32_t*>(a.kcodes + (bh_kv * a.ldk + k0) * KC);
+    const uint32_t* gs = reinterpret_cast<const uint32_t*>(a.ksigns + (bh_kv * a.ldk + k0) * SC);
 #pragma unroll
     for (int j = 0; j < T::KREG; ++j) {
       const int w = tid + j * NT;
@@ -198,7 +199,7 @@ __global__ void __launch_bounds__(64 * TQ_ATTN_WAVES, TQ_ATTN_MINBLK) attn_kerne
       rs[j] = (w < nk * SC / 4) ? gs[w] : 0u;
     }
     if constexpr (!SCORES) {
-      const uint32_t* gv = reinterpret_cast<const uint32_t*>(a.vcodes + (bh_kv * a.Sk + k0) * vc);
+      const uint32_t* gv = reinterpret_cast<const uint32_t*>(a.vcodes + (bh_kv * a.ldk + k0) * vc);
 #pragma unroll
       for (int j = 0; j < T::VREG; ++j) {
         const int w = tid + j * NT;
@@ -206,7 +207,7 @@ __global__ void __launch_bounds__(64 * TQ_ATTN_WAVES, TQ_ATTN_MINBLK) attn_kerne
       }
     }
     if (tid < KT) {
-      const int64_t kr = bh_kv * a.Sk + k0 + tid;
+      const int64_t kr = bh_kv * a.ldk + k0 + tid;
       const bool ok = tid < nk;
       const float vn = ok ? h2f(a.kvn[kr]) : 0.f;
       const float rn = ok ? h2f(a.krn[kr]) : 0.f;
@@ -535,11 +536,11 @@ using namespace tq;
 namespace tq {
 int64_t decode_workspace_bytes(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits);
 bool decode_applies(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits);
-int decode_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
+int decode_scores(int64_t ldk, const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
                   const uint8_t* ksigns, const uint16_t* krn, const uint16_t* kvn, const uint16_t* kcent,
                   int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits, float coeff, float* out,
                   hipStream_t s);
-int decode_attention(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
+int decode_attention(int64_t ldk, const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
                      const uint8_t* ksigns, const uint16_t* krn, const uint16_t* kvn, const uint16_t* kcent,
                      int bits, const uint8_t* vcodes, const uint16_t* vvn, const float* vcent32,
                      const uint16_t* vpit, int B, int Hq, int Hkv, int Sq, int Sk, int d, float coeff,
@@ -562,12 +563,14 @@ static int check_common(const char* what, int32_t B, int32_t Hq, int32_t Hkv, in
   return TQ_OK;
 }
 
-static void fill_common(AttnArgs& a, int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq, int32_t Sk, int32_t d) {
+static void fill_common(AttnArgs& a, int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq, int32_t Sk, int64_t ldk,
+                        int32_t d) {
   a.B = B;
   a.Hq = Hq;
   a.Hkv = Hkv;
   a.Sq = Sq;
   a.Sk = Sk;
+  a.ldk = ldk;
   a.G = Hq / Hkv;
   a.QT = block_rows(d) / a.G;
   a.nqb = (Sq + a.QT - 1) / a.QT;
@@ -580,17 +583,20 @@ int64_t tq_attention_workspace_size(int32_t B, int32_t Hq, int32_t Hkv, int32_t 
   return decode_workspace_bytes(B, Hq, Hkv, Sq, Sk, d, bits);
 }
 
-int tq_attention_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* key_codes,
-                        const uint8_t* key_signs, const uint16_t* key_rn, const uint16_t* key_vn,
-                        const uint16_t* centroids_f16, int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq,
-                        int32_t Sk, int32_t d, int32_t bits, float coeff, float* out, void* stream) {
+int tq_attention_scores_kv(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* key_codes,
+                           const uint8_t* key_signs, const uint16_t* key_rn, const uint16_t* key_vn,
+                           const uint16_t* centroids_f16, int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq,
+                           int32_t Sk, int64_t kv_stride, int32_t d, int32_t bits, float coeff, float* out,
+                           void* stream) {
   int st = check_common("tq_attention_scores", B, Hq, Hkv, Sq, Sk, d, bits);
   if (st != TQ_OK) return st;
+  const int64_t ldk = kv_stride > 0 ? kv_stride : Sk;
+  TQ_REQUIRE(ldk >= Sk, "tq_attention_scores: kv_stride %lld < Sk %d", (long long)kv_stride, (int)Sk);
   if (static_cast<int64_t>(B) * Hq * Sq * Sk == 0) return TQ_OK;
   TQ_REQUIRE(q_rot && q_proj && key_codes && key_signs && key_rn && key_vn && centroids_f16 && out,
              "tq_attention_scores: null pointer");
   if (decode_applies(B, Hq, Hkv, Sq, Sk, d, bits))
-    return decode_scores(q_rot, q_proj, key_codes, key_signs, key_rn, key_vn, centroids_f16, B, Hq, Hkv,
+    return decode_scores(ldk, q_rot, q_proj, key_codes, key_signs, key_rn, key_vn, centroids_f16, B, Hq, Hkv,
                          Sq, Sk, d, bits, coeff, out, as_stream(stream));
   AttnArgs a{};
   a.q_rot = q_rot;
@@ -601,7 +607,7 @@ int tq_attention_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uin
   a.kvn = key_vn;
   a.kcent = centroids_f16;
   a.vb = 1;
-  fill_common(a, B, Hq, Hkv, Sq, Sk, d);
+  fill_common(a, B, Hq, Hkv, Sq, Sk, ldk, d);
   a.coeff = coeff;
   a.scale = 1.f;
   a.scores = out;
@@ -609,17 +615,19 @@ int tq_attention_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uin
   return launch_status("tq_attention_scores");
 }
 
-int tq_attention_fwd(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* key_codes,
-                     const uint8_t* key_signs, const uint16_t* key_rn, const uint16_t* key_vn,
-                     const uint16_t* key_centroids_f16, int32_t bits, const uint8_t* val_codes,
-                     const uint16_t* val_vn, const float* val_centroids, int32_t val_bits,
-                     const uint16_t* val_pit_split, int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq,
-                     int32_t Sk, int32_t d, float coeff, float scale, int32_t causal,
-                     const float* mask, int64_t smb, int64_t smh, int64_t smq, int64_t smk,
-                     void* out, int32_t out_dtype, int64_t sob, int64_t soh, int64_t sos,
-                     void* workspace, int64_t workspace_bytes, void* stream) {
+int tq_attention_fwd_kv(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* key_codes,
+                        const uint8_t* key_signs, const uint16_t* key_rn, const uint16_t* key_vn,
+                        const uint16_t* key_centroids_f16, int32_t bits, const uint8_t* val_codes,
+                        const uint16_t* val_vn, const float* val_centroids, int32_t val_bits,
+                        const uint16_t* val_pit_split, int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq,
+                        int32_t Sk, int64_t kv_stride, int32_t d, float coeff, float scale, int32_t causal,
+                        const float* mask, int64_t smb, int64_t smh, int64_t smq, int64_t smk,
+                        void* out, int32_t out_dtype, int64_t sob, int64_t soh, int64_t sos,
+                        void* workspace, int64_t workspace_bytes, void* stream) {
   int st = check_common("tq_attention_fwd", B, Hq, Hkv, Sq, Sk, d, bits);
   if (st != TQ_OK) return st;
+  const int64_t ldk = kv_stride > 0 ? kv_stride : Sk;
+  TQ_REQUIRE(ldk >= Sk, "tq_attention_fwd: kv_stride %lld < Sk %d", (long long)kv_stride, (int)Sk);
   TQ_REQUIRE(val_bits >= 1 && val_bits <= 4, "tq_attention_fwd: value bits must be in [1, 4], got %d",
              (int)val_bits);
   TQ_REQUIRE(out_dtype == TQ_F32 || out_dtype == TQ_F16 || out_dtype == TQ_BF16,
@@ -632,7 +640,7 @@ int tq_attention_fwd(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_
              "tq_attention_fwd: null key/value plane");
   const int64_t need = decode_workspace_bytes(B, Hq, Hkv, Sq, Sk, d, bits);
   if (need > 0 && val_bits == bits && workspace && workspace_bytes >= need)
-    return decode_attention(q_rot, q_proj, key_codes, key_signs, key_rn, key_vn, key_centroids_f16, bits,
+    return decode_attention(ldk, q_rot, q_proj, key_codes, key_signs, key_rn, key_vn, key_centroids_f16, bits,
                             val_codes, val_vn, val_centroids, val_pit_split, B, Hq, Hkv, Sq, Sk, d, coeff,
                             scale, causal, mask, smb, smh, smq, smk, out, out_dtype, sob, soh, sos,
                             workspace, as_stream(stream));
@@ -649,7 +657,7 @@ int tq_attention_fwd(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_
   a.vcent32 = val_centroids;
   a.vpit = val_pit_split;
   a.vb = val_bits;
-  fill_common(a, B, Hq, Hkv, Sq, Sk, d);
+  fill_common(a, B, Hq, Hkv, Sq, Sk, ldk, d);
   a.coeff = coeff;
   a.scale = scale;
   a.causal = causal;
@@ -665,6 +673,29 @@ int tq_attention_fwd(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_
   a.sos = sos;
   dispatch_attn<false>(d, bits - 1, a, as_stream(stream));
   return launch_status("tq_attention_fwd");
+}
+
+int tq_attention_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* key_codes,
+                        const uint8_t* key_signs, const uint16_t* key_rn, const uint16_t* key_vn,
+                        const uint16_t* centroids_f16, int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq,
+                        int32_t Sk, int32_t d, int32_t bits, float coeff, float* out, void* stream) {
+  return tq_attention_scores_kv(q_rot, q_proj, key_codes, key_signs, key_rn, key_vn, centroids_f16, B, Hq, Hkv,
+                                Sq, Sk, Sk, d, bits, coeff, out, stream);
+}
+
+int tq_attention_fwd(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* key_codes,
+                     const uint8_t* key_signs, const uint16_t* key_rn, const uint16_t* key_vn,
+                     const uint16_t* key_centroids_f16, int32_t bits, const uint8_t* val_codes,
+                     const uint16_t* val_vn, const float* val_centroids, int32_t val_bits,
+                     const uint16_t* val_pit_split, int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq,
+                     int32_t Sk, int32_t d, float coeff, float scale, int32_t causal,
+                     const float* mask, int64_t smb, int64_t smh, int64_t smq, int64_t smk,
+                     void* out, int32_t out_dtype, int64_t sob, int64_t soh, int64_t sos,
+                     void* workspace, int64_t workspace_bytes, void* stream) {
+  return tq_attention_fwd_kv(q_rot, q_proj, key_codes, key_signs, key_rn, key_vn, key_centroids_f16, bits,
+                             val_codes, val_vn, val_centroids, val_bits, val_pit_split, B, Hq, Hkv, Sq, Sk, Sk, d,
+                             coeff, scale, causal, mask, smb, smh, smq, smk, out, out_dtype, sob, soh, sos,
+                             workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

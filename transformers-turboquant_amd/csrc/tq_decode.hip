@@ -155,6 +155,7 @@ struct DecodeArgs {
   const uint16_t* vvn;
   const float* vcent;            // f32 value centroids (tables hold their f16 values)
   int B, Hq, Hkv, Sq, Sk, G, C;  // C = G * Sq valid columns
+  int64_t ldk;                   // rows between consecutive (batch, kv head) planes (>= Sk)
   int nsplit, chunk;             // keys per block (multiple of 64)
   float coeff, scale;
   int causal;
@@ -387,7 +388,7 @@ __global__ void __launch_bounds__(256) decode_attn_lds_kernel(DecodeArgs a) {
   const int vbase = voff & ~3;
   const int vbyte = voff & 3;
 
-  const int64_t g0 = bh * a.Sk;
+  const int64_t g0 = bh * a.ldk;
   const uint8_t* pk = a.kcodes + g0 * KC;
   const uint8_t* ps = a.ksigns + g0 * SC;
   const uint16_t* pkn = a.kvn + g0;
@@ -672,7 +673,7 @@ __global__ void __launch_bounds__(256) decode_scores_kernel(DecodeArgs a) {
     oo[e] = c < a.C ? static_cast<uint32_t>((c % a.G) * a.Sq + c / a.G) * a.Sk * 4 + 4 * l16 : kOutOfRange;
   }
 
-  const int64_t g0 = bh * a.Sk;
+  const int64_t g0 = bh * a.ldk;
   const uint8_t* pk = a.kcodes + g0 * KC;
   const uint8_t* ps = a.ksigns + g0 * SC;
   const uint16_t* pkn = a.kvn + g0;
@@ -987,7 +988,7 @@ static void launch_decode_attn(const DecodeArgs& a, hipStream_t s) {
   decode_attn_lds_kernel<128, BITS, TQ_DEC_ANB, TQ_DEC_AR, TQ_DEC_PLO != 0><<<grid, 256, 0, s>>>(a);
 }
 
-int decode_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
+int decode_scores(int64_t ldk, const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
                   const uint8_t* ksigns, const uint16_t* krn, const uint16_t* kvn, const uint16_t* kcent,
                   int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits, float coeff, float* out,
                   hipStream_t s) {
@@ -1005,6 +1006,7 @@ int decode_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* 
   a.Hkv = Hkv;
   a.Sq = Sq;
   a.Sk = Sk;
+  a.ldk = ldk;
   a.G = Hq / Hkv;
   a.C = a.G * Sq;
   a.nsplit = p.nsplit;
@@ -1019,7 +1021,7 @@ int decode_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* 
   return launch_status("tq_attention_scores (decode)");
 }
 
-int decode_attention(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
+int decode_attention(int64_t ldk, const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
                      const uint8_t* ksigns, const uint16_t* krn, const uint16_t* kvn, const uint16_t* kcent,
                      int bits, const uint8_t* vcodes, const uint16_t* vvn, const float* vcent32,
                      const uint16_t* vpit, int B, int Hq, int Hkv, int Sq, int Sk, int d, float coeff,
@@ -1043,6 +1045,7 @@ int decode_attention(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_
   a.Hkv = Hkv;
   a.Sq = Sq;
   a.Sk = Sk;
+  a.ldk = ldk;
   a.G = Hq / Hkv;
   a.C = a.G * Sq;
   a.nsplit = p.nsplit;

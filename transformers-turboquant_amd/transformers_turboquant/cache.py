@@ -1,0 +1,265 @@
+"""Compressed KV cache for incremental decoding.
+
+The reference recomputes every forward from the full sequence and disables the
+cache (patch.py:81); a compressed cache exists there only as a tensor-level
+sketch (turboquant.py:199-286, ``TurboQuantKVCache``).  ``TurboQuantCache``
+stores what the patched attention layers compress, so each decoding step
+compresses only its new tokens and attends to everything cached:
+
+* GPU: per layer, the packed planes of ``capacity`` positions per (batch, kv
+  head) — key codes, QJL signs, residual and vector norms, value codes and
+  norms — laid out ``[B, Hkv, capacity, ...]``.  New tokens are compressed and
+  copied into positions ``[length, length + S)``; capacity grows by doubling.
+  Attention reads the first ``length`` rows of each plane in place (the
+  ``kv_stride`` entry of the dicts, see ``tq_attention_fwd_kv``), so the
+  split-K decode kernels stream exactly the cached bytes.
+* CPU: the reference's unpacked formats, concatenated along the sequence.
+
+Pass an instance to ``generate(..., past_key_values=TurboQuantCache(),
+use_cache=True)`` on a model patched by ``apply_turboquant``.
+"""
+
+from __future__ import annotations
+
+import torch
+from transformers.cache_utils import Cache, CacheLayerMixin
+
+__all__ = ["TurboQuantCache", "TurboQuantCacheLayer"]
+
+_KEY_PLANES = ("packed_key_indices", "packed_qjl_signs", "residual_norm", "vec_norms")
+_VAL_PLANES = ("packed_indices", "vec_norms")
+_ROUND = 256  # capacity granularity (positions)
+
+
+class TurboQuantCacheLayer(CacheLayerMixin):
+    """One attention layer's compressed keys and values."""
+
+    is_compileable = False
+    supports_early_init = False
+
+    def __init__(self, **kwargs):
+        super().__init__()
+        self.length = 0
+        self.capacity = 0
+        self.shape: tuple | None = None  # (B, Hkv, D)
+        self.kp: dict[str, torch.Tensor] | None = None  # GPU key planes [B, Hkv, capacity, ...]
+        self.vp: dict[str, torch.Tensor] | None = None  # GPU value planes
+        self.cpu_k: dict | None = None  # CPU unpacked dicts
+        self.cpu_v: dict | None = None
+
+    # ------------------------------------------------------------------ Cache layer API
+    def lazy_initialization(self, key_states, value_states) -> None:
+        return None
+
+    def update(self, key_states, value_states, *args, **kwargs):
+        raise NotImplementedError(
+            "TurboQuantCache holds compressed planes; it is filled by attention modules patched with "
+            "apply_turboquant, not by uncompressed key/value updates")
+
+    def get_seq_length(self) -> int:
+        return self.length
+
+    def get_mask_sizes(self, query_length: int) -> tuple[int, int]:
+        return self.length + query_length, 0
+
+    def get_max_length(self) -> int:
+        return -1
+
+    def reset(self) -> None:
+        self.length = 0
+        self.cpu_k = self.cpu_v = None
+
+    def crop(self, tokens_to_remove: int) -> None:
+        """Drop the last -tokens_to_remove positions (a positive value is the length to keep)."""
+        keep = tokens_to_remove if tokens_to_remove > 0 else self.length + tokens_to_remove
+        keep = max(0, min(self.length, keep))
+        if self.cpu_k is not None:
+            self.cpu_k = _slice_cpu(self.cpu_k, keep)
+            self.cpu_v = _slice_cpu(self.cpu_v, keep)
+        self.length = keep
+
+    def reorder_cache(self, beam_idx: torch.LongTensor) -> None:
+        self._select_batch(beam_idx)
+
+    def batch_select_indices(self, indices: torch.Tensor) -> None:
+        self._select_batch(indices)
+
+    def batch_repeat_interleave(self, repeats: int) -> None:
+        if self.shape is None:
+            return
+        idx = torch.arange(self.shape[0]).repeat_interleave(repeats)
+        self._select_batch(idx)
+
+    # ------------------------------------------------------------------ compressed storage
+    def append(self, key_compressor, val_compressor, k: torch.Tensor, v: torch.Tensor) -> tuple[dict, dict]:
+        """Compress k, v [B, Hkv, S, D], append them, and return dicts covering every cached position."""
+        B, H, S, D = k.shape
+        if self.shape is not None and self.length > 0 and self.shape != (B, H, D):
+            raise ValueError(f"cache holds [B, Hkv, D] = {self.shape}, got {(B, H, D)}")
+        self.shape = (B, H, D)
+        if k.device.type != "cuda":
+            return self._append_cpu(key_compressor, val_compressor, k, v)
+        ck = key_compressor.compress(k)
+        cv = val_compressor.compress(v)
+        need = self.length + S
+        if self.kp is None or need > self.capacity or self.kp["vec_norms"].shape[:2] != (B, H):
+            self._grow(need, ck, cv, B, H, S)
+        lo, hi = self.length, need
+        for name in _KEY_PLANES:
+            src = ck[name]
+            self.kp[name][:, :, lo:hi] = src.reshape(B, H, S, *src.shape[1:]) if src.dim() == 2 else src.reshape(B, H, S)
+        self.vp["packed_indices"][:, :, lo:hi] = cv["packed_indices"].reshape(B, H, S, -1)
+        self.vp["vec_norms"][:, :, lo:hi] = cv["vec_norms"].reshape(B, H, S)
+        self.length = need
+        return self.strided()
+
+    def strided(self) -> tuple[dict, dict]:
+        """GPU dicts over the capacity planes: attend the first `length` rows (kv_stride = capacity)."""
+        B, H, D = self.shape
+        ck = {name: self.kp[name] for name in _KEY_PLANES}
+        cv = {name: self.vp[name] for name in _VAL_PLANES}
+        for c in (ck, cv):
+            c["shape"] = (B, H, self.length, D)
+            c["kv_stride"] = self.capacity
+        return ck, cv
+
+    def compact(self) -> tuple[dict, dict]:
+        """The cached positions in the compressors' own packed format (contiguous copies)."""
+        if self.kp is None:
+            return self.cpu_k, self.cpu_v
+        B, H, D = self.shape
+        L, n = self.length, self.shape[0] * self.shape[1] * self.length
+        k = {name: self.kp[name][:, :, :L].contiguous() for name in _KEY_PLANES}
+        ck = {"packed_key_indices": k["packed_key_indices"].reshape(n, -1),
+              "packed_qjl_signs": k["packed_qjl_signs"].reshape(n, -1),
+              "residual_norm": k["residual_norm"], "vec_norms": k["vec_norms"], "shape": (B, H, L, D)}
+        cv = {"packed_indices": self.vp["packed_indices"][:, :, :L].contiguous().reshape(n, -1),
+              "vec_norms": self.vp["vec_norms"][:, :, :L].contiguous().reshape(n), "shape": (B, H, L, D)}
+        return ck, cv
+
+    def _grow(self, need: int, ck: dict, cv: dict, B: int, H: int, S: int) -> None:
+        cap = max(need, 2 * self.capacity, _ROUND)
+        cap = (cap + _ROUND - 1) // _ROUND * _ROUND
+        dev = ck["vec_norms"].device
+        kp = {
+            "packed_key_indices": torch.zeros(B, H, cap, ck["packed_key_indices"].shape[-1], dtype=torch.uint8, device=dev),
+            "packed_qjl_signs": torch.zeros(B, H, cap, ck["packed_qjl_signs"].shape[-1], dtype=torch.uint8, device=dev),
+            "residual_norm": torch.zeros(B, H, cap, dtype=torch.float16, device=dev),
+            "vec_norms": torch.zeros(B, H, cap, dtype=torch.float16, device=dev),
+        }
+        vp = {
+            "packed_indices": torch.zeros(B, H, cap, cv["packed_indices"].shape[-1], dtype=torch.uint8, device=dev),
+            "vec_norms": torch.zeros(B, H, cap, dtype=torch.float16, device=dev),
+        }
+        if self.kp is not None and self.length > 0:
+            L = self.length
+            for name in _KEY_PLANES:
+                kp[name][:, :, :L] = self.kp[name][:, :, :L]
+            for name in _VAL_PLANES:
+                vp[name][:, :, :L] = self.vp[name][:, :, :L]
+        self.kp, self.vp, self.capacity = kp, vp, cap
+
+    def _append_cpu(self, key_compressor, val_compressor, k, v) -> tuple[dict, dict]:
+        ck = key_compressor.compress(k)
+        cv = val_compressor.compress(v)
+        if self.cpu_k is None or self.length == 0:
+            self.cpu_k, self.cpu_v = ck, cv
+        else:
+            self.cpu_k = _cat_cpu(self.cpu_k, ck)
+            self.cpu_v = _cat_cpu(self.cpu_v, cv)
+        self.length = self.cpu_k["shape"][2]
+        return self.cpu_k, self.cpu_v
+
+    def _select_batch(self, idx: torch.Tensor) -> None:
+        if self.length == 0 or self.shape is None:
+            return
+        if self.kp is not None:
+            i = idx.to(self.kp["vec_norms"].device)
+            self.kp = {name: t.index_select(0, i) for name, t in self.kp.items()}
+            self.vp = {name: t.index_select(0, i) for name, t in self.vp.items()}
+            self.shape = (int(i.numel()),) + self.shape[1:]
+        else:
+            self.cpu_k = _select_cpu(self.cpu_k, idx)
+            self.cpu_v = _select_cpu(self.cpu_v, idx)
+            self.shape = (int(idx.numel()),) + self.shape[1:]
+
+
+def _cat_cpu(a: dict, b: dict) -> dict:
+    """Concatenate two unpacked CPU dicts of one layer along the sequence."""
+    B, H, S1, D = a["shape"]
+    S2 = b["shape"][2]
+    out = {"shape": (B, H, S1 + S2, D)}
+    for name, t in a.items():
+        if name == "shape":
+            continue
+        u = b[name]
+        if t.dim() >= 3:  # [B, H, S, ...]
+            out[name] = torch.cat([t, u], dim=2)
+        else:  # flat rows [B*H*S, ...] (value indices / norms)
+            t4 = t.reshape(B, H, S1, *t.shape[1:])
+            u4 = u.reshape(B, H, S2, *u.shape[1:])
+            out[name] = torch.cat([t4, u4], dim=2).reshape(B * H * (S1 + S2), *t.shape[1:])
+    return out
+
+
+def _slice_cpu(a: dict, keep: int) -> dict:
+    B, H, S, D = a["shape"]
+    out = {"shape": (B, H, keep, D)}
+    for name, t in a.items():
+        if name == "shape":
+            continue
+        if t.dim() >= 3:
+            out[name] = t[:, :, :keep].contiguous()
+        else:
+            out[name] = t.reshape(B, H, S, *t.shape[1:])[:, :, :keep].reshape(B * H * keep, *t.shape[1:])
+    return out
+
+
+def _select_cpu(a: dict, idx: torch.Tensor) -> dict:
+    B, H, S, D = a["shape"]
+    idx = idx.to("cpu")
+    out = {"shape": (int(idx.numel()), H, S, D)}
+    for name, t in a.items():
+        if name == "shape":
+            continue
+        if t.dim() >= 3:
+            out[name] = t.index_select(0, idx)
+        else:
+            t4 = t.reshape(B, H, S, *t.shape[1:]).index_select(0, idx)
+            out[name] = t4.reshape(-1, *t.shape[1:])
+    return out
+
+
+class TurboQuantCache(Cache):
+    """A transformers ``Cache`` whose layers hold TurboQuant-compressed keys and values."""
+
+    def __init__(self, **kwargs):
+        super().__init__(layer_class_to_replicate=TurboQuantCacheLayer)
+
+    def layer(self, layer_idx: int) -> TurboQuantCacheLayer:
+        while len(self.layers) <= layer_idx:
+            self.layers.append(TurboQuantCacheLayer())
+        return self.layers[layer_idx]
+
+    def append(self, layer_idx: int, key_compressor, val_compressor, k: torch.Tensor,
+               v: torch.Tensor) -> tuple[dict, dict]:
+        """Compress and append one layer's new keys/values; return dicts over all cached positions."""
+        if layer_idx is None:
+            raise ValueError("TurboQuantCache needs attention modules with a layer_idx")
+        return self.layer(layer_idx).append(key_compressor, val_compressor, k, v)
+
+    def nbytes(self) -> int:
+        """Bytes of compressed planes currently cached (positions in use only)."""
+        total = 0
+        for lay in self.layers:
+            if lay.length == 0 or lay.shape is None:
+                continue
+            B, H, D = lay.shape
+            if lay.kp is not None:
+                per_pos = sum(t[0, 0, 0].numel() * t.element_size() for t in lay.kp.values())
+                per_pos += sum(t[0, 0, 0].numel() * t.element_size() for t in lay.vp.values())
+                total += per_pos * B * H * lay.length
+            else:
+                for c in (lay.cpu_k, lay.cpu_v):
+                    total += sum(t.numel() * t.element_size() for n, t in c.items() if n != "shape")
+        return total

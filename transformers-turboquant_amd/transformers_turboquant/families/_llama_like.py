@@ -57,5 +57,5 @@ class LlamaLikeAttention(TurboQuantAttentionBase):
         if position_embeddings is not None:
             cos, sin = position_embeddings
             q, k = type(self).apply_rotary(q, k, cos, sin)
-        attn, weights = attention_tail(self, q, k, v, attention_mask, output_attentions)
+        attn, weights = attention_tail(self, q, k, v, attention_mask, output_attentions, cache=past_key_values)
         return self.o_proj(attn), weights

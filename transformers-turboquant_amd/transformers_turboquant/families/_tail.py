@@ -9,6 +9,11 @@ On the GPU the tail is one tq_attention_fwd launch over Hkv compressed heads
 path (HIP scores + HIP decompress, softmax/dropout in torch) is used only when
 attention weights are requested or attention dropout is active.  On the CPU
 the reference's own sequence runs on its unpacked format.
+
+With a ``TurboQuantCache`` as the decoder's cache only the new tokens are
+compressed (appended to the cache) and attention runs over every cached
+position; any other transformers cache keeps the uncompressed K/V (its own
+``update``), which are compressed whole on every step.
 """
 
 from __future__ import annotations
@@ -19,6 +24,8 @@ import torch
 import torch.nn.functional as F
 
 from turboquant_pytorch.fused import compressed_attention
+
+from ..cache import TurboQuantCache
 
 
 def additive_mask(mask: torch.Tensor | None, dtype=torch.float32) -> torch.Tensor | None:
@@ -42,28 +49,43 @@ def want_causal(module, attention_mask) -> bool:
     return attention_mask is None and mode == "auto" and getattr(module, "is_causal", True)
 
 
-def attention_tail(module, q, k, v, attention_mask, output_attentions: bool = False, dropout=None):
-    """q [B, Hq, T, D], k/v [B, Hkv, S, D] -> (attn [B, T, Hq*D] in q.dtype, weights or None)."""
+def attention_tail(module, q, k, v, attention_mask, output_attentions: bool = False, dropout=None, cache=None):
+    """q [B, Hq, T, D], k/v [B, Hkv, T_new, D] -> (attn [B, T, Hq*D] in q.dtype, weights or None).
+
+    cache: the decoder's past_key_values (None without caching)."""
     B, Hq, T, D = q.shape
-    Hkv, S = k.shape[1], k.shape[2]
+    Hkv = k.shape[1]
     group = Hq // Hkv
     mask = additive_mask(attention_mask)
     causal = want_causal(module, attention_mask)
     drop_active = dropout is not None and module.training and dropout.p > 0
     kc, vc = module.key_compressor, module.val_compressor
 
+    cached = None  # (compressed keys, compressed values) of every cached position
+    if isinstance(cache, TurboQuantCache):
+        cached = cache.append(module.layer_idx, kc, vc, k, v)
+        lay = cache.layer(module.layer_idx)
+    elif cache is not None:
+        k, v = cache.update(k, v, module.layer_idx)
+    S = cached[0]["shape"][2] if cached is not None else k.shape[2]
+
     if q.device.type == "cuda" and not output_attentions and not drop_active:
-        ck = kc.compress(k)
-        cv = vc.compress(v)
+        ck, cv = cached if cached is not None else (kc.compress(k), vc.compress(v))
         out = compressed_attention(q, kc, vc, ck, cv, attention_mask=mask, causal=causal,
                                    scale=1.0 / math.sqrt(D), out_dtype=q.dtype)
         return out.reshape(B, T, Hq * D), None
 
     if q.device.type == "cuda":
-        ck = kc.compress(k)
-        cv = vc.compress(v)
+        ck, cv = lay.compact() if cached is not None else (kc.compress(k), vc.compress(v))
         scores = kc.asymmetric_attention_scores(q, ck)
         values = vc.decompress(cv)
+        if group > 1:
+            values = values.repeat_interleave(group, dim=1)
+    elif cached is not None:
+        # unpacked CPU dicts of Hkv heads; per-row compression makes them equal to the
+        # compression of the repeated heads
+        scores = kc.asymmetric_attention_scores(q, cached[0])
+        values = vc.decompress(cached[1])
         if group > 1:
             values = values.repeat_interleave(group, dim=1)
     else:

@@ -41,7 +41,7 @@ class TurboQuantGPT2Attention(TurboQuantAttentionBase):
         move_compressors(self, fn)
         return self
 
-    def forward(self, hidden_states, layer_past=None, attention_mask=None, head_mask=None,
+    def forward(self, hidden_states, past_key_values=None, attention_mask=None, head_mask=None,
                 encoder_hidden_states=None, encoder_attention_mask=None, use_cache=False,
                 output_attentions=False, **kwargs):
         B, T, _ = hidden_states.shape
@@ -50,6 +50,6 @@ class TurboQuantGPT2Attention(TurboQuantAttentionBase):
         k = k.view(B, T, self.num_heads, self.head_dim).transpose(1, 2)
         v = v.view(B, T, self.num_heads, self.head_dim).transpose(1, 2)
         attn, weights = attention_tail(self, q, k, v, attention_mask, output_attentions,
-                                       dropout=self.attn_dropout)
+                                       dropout=self.attn_dropout, cache=past_key_values)
         attn = self.resid_dropout(self.c_proj(attn))
         return attn, weights

@@ -48,6 +48,11 @@ _SIGNATURES = {
     "tq_attention_fwd": [_p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _p, _i32, _p,
                          _i32, _i32, _i32, _i32, _i32, _i32, _f32, _f32, _i32,
                          _p, _i64, _i64, _i64, _i64, _p, _i32, _i64, _i64, _i64, _p, _i64, _p],
+    "tq_attention_scores_kv": [_p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i64, _i32,
+                               _i32, _f32, _p, _p],
+    "tq_attention_fwd_kv": [_p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _p, _i32, _p,
+                            _i32, _i32, _i32, _i32, _i32, _i64, _i32, _f32, _f32, _i32,
+                            _p, _i64, _i64, _i64, _i64, _p, _i32, _i64, _i64, _i64, _p, _i64, _p],
     "tq_attention_workspace_size": [_i32, _i32, _i32, _i32, _i32, _i32, _i32],
 }
 _RESTYPE = {"tq_last_error": ctypes.c_char_p, "tq_out_cols": _i64, "tq_attention_workspace_size": _i64}

@@ -171,7 +171,7 @@ class TurboQuantCompressorV2:
             return scores_from_prepared(
                 q_rot, q_proj, compressed["packed_key_indices"], compressed["packed_qjl_signs"],
                 compressed["residual_norm"], compressed["vec_norms"], t.cent16, self.mse_bits + 1,
-                coeff, Hk)
+                coeff, Hk, Sk, int(compressed.get("kv_stride", Sk)))
         # reference PyTorch branch (compressors.py:201-224)
         k_mse = compressed["k_mse"].float()
         signs = compressed["qjl_signs"].float()

@@ -14,6 +14,10 @@ accumulates P.V in the value compressor's rotated domain, applying Pi_v once
 per output row.  Grouped-query attention is served without expanding K/V.
 Few-query (decode) shapes take a split-K path whose partial results live in a
 workspace allocated here from torch (tq_attention_workspace_size bytes).
+
+A compressed dict may carry ``kv_stride``: its planes then hold ``kv_stride``
+positions per (batch, kv head) of which the first ``shape[2]`` are attended
+(the layout of :class:`transformers_turboquant.cache.TurboQuantCache`).
 """
 
 from __future__ import annotations
@@ -58,6 +62,9 @@ def attention_from_prepared(q_rot: torch.Tensor, q_proj: torch.Tensor,
     """The tq_attention_fwd launch on queries already prepared by prepare_queries()."""
     B, Hq, Sq, D = q_rot.shape
     _, Hkv, Sk, _ = compressed_k["shape"]
+    kv_stride = int(compressed_k.get("kv_stride", Sk))
+    if int(compressed_v.get("kv_stride", Sk)) != kv_stride:
+        raise ValueError("compressed key and value planes must share their kv_stride")
     dev = q_rot.device
     tk = _tables(key_compressor, dev, with_qjl=True)
     tv = _tables(val_compressor, dev, with_qjl=False)
@@ -80,14 +87,14 @@ def attention_from_prepared(q_rot: torch.Tensor, q_proj: torch.Tensor,
             mask = mask.unsqueeze(0)
         mask = mask.expand(B, Hq, Sq, Sk)
         mptr, ms = mask.data_ptr(), tuple(mask.stride())
-    _native.check(lib.tq_attention_fwd(
+    _native.check(lib.tq_attention_fwd_kv(
         q_rot.data_ptr(), q_proj.data_ptr(),
         compressed_k["packed_key_indices"].data_ptr(), compressed_k["packed_qjl_signs"].data_ptr(),
         compressed_k["residual_norm"].data_ptr(), compressed_k["vec_norms"].data_ptr(),
         tk.cent16.data_ptr(), bits,
         compressed_v["packed_indices"].data_ptr(), compressed_v["vec_norms"].data_ptr(),
         tv.cent32.data_ptr(), val_compressor.bits, tv.pit_split.data_ptr(),
-        B, Hq, Hkv, Sq, Sk, D, float(coeff), float(scale), int(bool(causal)),
+        B, Hq, Hkv, Sq, Sk, kv_stride, D, float(coeff), float(scale), int(bool(causal)),
         mptr, ms[0], ms[1], ms[2], ms[3],
         out.data_ptr(), _native.dtype_code(out_dtype), out.stride(0), out.stride(2), out.stride(1),
         _native.ptr(workspace), ws_bytes, _native.stream_of(out)), "compressed_attention")

@@ -42,15 +42,20 @@ def project_queries(q_rot: torch.Tensor, s_eff_f16: torch.Tensor) -> torch.Tenso
 
 def scores_from_prepared(q_rot16: torch.Tensor, q_proj16: torch.Tensor, codes: torch.Tensor,
                          signs: torch.Tensor, rn: torch.Tensor, vn: torch.Tensor,
-                         centroids16: torch.Tensor, bits: int, coeff: float, hkv: int) -> torch.Tensor:
-    """Launch tq_attention_scores; key planes hold B*hkv*Sk rows."""
+                         centroids16: torch.Tensor, bits: int, coeff: float, hkv: int,
+                         sk: int | None = None, kv_stride: int = 0) -> torch.Tensor:
+    """Launch tq_attention_scores_kv.
+
+    The key planes hold B*hkv head sequences of kv_stride rows each (kv_stride
+    0: contiguous, B*hkv*Sk rows); the first sk rows of each are scored.
+    """
     B, Hq, Sq, d = q_rot16.shape
-    Sk = rn.numel() // (B * hkv)
+    Sk = rn.numel() // (B * hkv) if sk is None else int(sk)
     out = torch.empty(B, Hq, Sq, Sk, dtype=torch.float32, device=q_rot16.device)
-    _native.check(_native.lib().tq_attention_scores(
+    _native.check(_native.lib().tq_attention_scores_kv(
         q_rot16.data_ptr(), q_proj16.data_ptr(), codes.data_ptr(), signs.data_ptr(),
-        rn.data_ptr(), vn.data_ptr(), centroids16.data_ptr(), B, Hq, hkv, Sq, Sk, d, bits,
-        float(coeff), out.data_ptr(), _native.stream_of(out)), "asymmetric_attention_scores")
+        rn.data_ptr(), vn.data_ptr(), centroids16.data_ptr(), B, Hq, hkv, Sq, Sk, int(kv_stride), d,
+        bits, float(coeff), out.data_ptr(), _native.stream_of(out)), "asymmetric_attention_scores")
     return out
 
 
