@@ -46,6 +46,7 @@ class TurboQuantCacheLayer(CacheLayerMixin):
         self.vp: dict[str, torch.Tensor] | None = None  # GPU value planes
         self.cpu_k: dict | None = None  # CPU unpacked dicts
         self.cpu_v: dict | None = None
+        self.codec: dict = {}  # key/value bits and seeds of the compressors that filled the layer
 
     # ------------------------------------------------------------------ Cache layer API
     def lazy_initialization(self, key_states, value_states) -> None:
@@ -97,6 +98,9 @@ class TurboQuantCacheLayer(CacheLayerMixin):
         if self.shape is not None and self.length > 0 and self.shape != (B, H, D):
             raise ValueError(f"cache holds [B, Hkv, D] = {self.shape}, got {(B, H, D)}")
         self.shape = (B, H, D)
+        self.codec = {"key_bits": key_compressor.bits, "value_bits": val_compressor.bits,
+                      "key_seed": getattr(key_compressor, "seed", None),
+                      "value_seed": getattr(val_compressor, "seed", None)}
         if k.device.type != "cuda":
             return self._append_cpu(key_compressor, val_compressor, k, v)
         ck = key_compressor.compress(k)
@@ -136,6 +140,33 @@ class TurboQuantCacheLayer(CacheLayerMixin):
         cv = {"packed_indices": self.vp["packed_indices"][:, :, :L].contiguous().reshape(n, -1),
               "vec_norms": self.vp["vec_norms"][:, :, :L].contiguous().reshape(n), "shape": (B, H, L, D)}
         return ck, cv
+
+    def restore(self, keys: dict, values: dict, codec: dict) -> None:
+        """Replace the layer's contents with compressor-format dicts (packed on the GPU,
+        unpacked on the CPU), as `TurboQuantCache.load` reads them."""
+        B, H, S, D = keys["shape"]
+        self.reset()
+        self.kp = self.vp = None
+        self.capacity = 0
+        self.shape = (B, H, D)
+        self.codec = dict(codec)
+        packed = "packed_key_indices" in keys
+        dev = keys["residual_norm"].device
+        if packed != (dev.type == "cuda"):
+            raise ValueError("packed planes are restored onto a GPU device, unpacked dicts onto the CPU")
+        if not packed:
+            self.cpu_k, self.cpu_v = keys, values
+            self.length = S
+            return
+        self._grow(S, keys, values, B, H, S)
+        n = B * H * S
+        for name in _KEY_PLANES:
+            src = keys[name]
+            self.kp[name][:, :, :S] = src.reshape(B, H, S, -1) if src.dim() == 2 and src.shape[0] == n else \
+                src.reshape(B, H, S)
+        self.vp["packed_indices"][:, :, :S] = values["packed_indices"].reshape(B, H, S, -1)
+        self.vp["vec_norms"][:, :, :S] = values["vec_norms"].reshape(B, H, S)
+        self.length = S
 
     def _grow(self, need: int, ck: dict, cv: dict, B: int, H: int, S: int) -> None:
         cap = max(need, 2 * self.capacity, _ROUND)
@@ -247,6 +278,37 @@ class TurboQuantCache(Cache):
         if layer_idx is None:
             raise ValueError("TurboQuantCache needs attention modules with a layer_idx")
         return self.layer(layer_idx).append(key_compressor, val_compressor, k, v)
+
+    def save(self, path, metadata: dict | None = None) -> None:
+        """Write every non-empty layer's cached positions to `path` (format turboquant-kv, one
+        group per layer named ``layer<i>``, with the compressors' bits and seeds)."""
+        from turboquant_pytorch.serialize import save_groups
+
+        groups = []
+        for i, lay in enumerate(self.layers):
+            if lay.length == 0 or lay.shape is None:
+                continue
+            keys, values = lay.compact()
+            groups.append({"name": f"layer{i}", "keys": keys, "values": values, **lay.codec})
+        save_groups(path, groups, metadata)
+
+    @classmethod
+    def load(cls, path, device="cpu") -> "TurboQuantCache":
+        """A cache holding what `save` wrote; packed planes go to a GPU `device`, unpacked
+        dicts to the CPU.  Decoding continues with compressors of the recorded bits and seeds."""
+        from turboquant_pytorch.serialize import FormatError, load_groups
+
+        groups, _ = load_groups(path, device)
+        cache = cls()
+        for g in groups:
+            name = g["name"]
+            if not (name.startswith("layer") and name[5:].isdigit()):
+                raise FormatError(f"cache groups are named layer<i>, found {name!r}")
+            if g["keys"] is None or g["values"] is None:
+                raise FormatError(f"{name}: a cache layer needs keys and values")
+            codec = {k: g[k] for k in ("key_bits", "value_bits", "key_seed", "value_seed")}
+            cache.layer(int(name[5:])).restore(g["keys"], g["values"], codec)
+        return cache
 
     def nbytes(self) -> int:
         """Bytes of compressed planes currently cached (positions in use only)."""

@@ -89,6 +89,7 @@ class TurboQuantCompressorV2:
     def __init__(self, head_dim: int, bits: int, seed: int, device: str = "cpu", use_triton: bool = True):
         self.head_dim = head_dim
         self.bits = bits
+        self.seed = seed
         self.mse_bits = max(bits - 1, 1)
         self.device = device
         self.use_triton = use_triton
@@ -211,6 +212,7 @@ class TurboQuantCompressorMSE:
     def __init__(self, head_dim: int, bits: int, seed: int, device: str = "cpu", use_triton: bool = True):
         self.head_dim = head_dim
         self.bits = bits
+        self.seed = seed
         self.device = device
         self.use_triton = use_triton
         self.Pi = random_rotation(head_dim, seed).to(device)
