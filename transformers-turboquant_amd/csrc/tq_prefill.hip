@@ -1,0 +1,526 @@
+// Fused compressed-domain attention for many query rows (prefill), head_dim 128.
+//
+// Same estimator and output as tq_attn.hip's tiled kernel (scores from packed
+// keys, online softmax, P.V over packed values, Pi_v applied once per output
+// row), organised so that no phase waits on another:
+//
+//  * Raw packed planes of each 32-key tile (codes, signs, value codes, the
+//    three norm planes) are copied straight into an R-slot LDS ring with
+//    direct-to-LDS buffer loads issued R-1 tiles ahead (no register staging).
+//  * Each tile is decoded once per block into f16 tiles: K^ = Ck[codes] and
+//    the +-1 sign tile as [key][dim] rows, and V^T = Cv[codes] as [dim][key]
+//    rows (the value norms are folded into P instead).  Decoding uses small
+//    LDS tables indexed by nibbles / bit fields (conflict-free for <= 32
+//    entries); the value table is indexed by the codes of two keys at one dim,
+//    so each lookup yields the (key, key+1) pair the MFMA operand needs and no
+//    transposition is done.
+//  * The decoded tiles are double-buffered: in one pass between two barriers
+//    every wave decodes its share of tile t+1 and runs the MFMAs and softmax of
+//    tile t, one block barrier per tile.
+//  * A block of 4 wave64 owns 128 (query row, query head) columns of one
+//    (batch, kv head); each wave owns two 16-column blocks.  S^T = K^ Q^T comes
+//    out of v_mfma_f32_16x16x32_f16 with 4 consecutive keys of one column per
+//    lane, the P^T operand layout of O^T += V^T P^T, so P stays in registers.
+//    P' = f16(p * vn_v) (one f16 rounding, the value norm folded in).
+#include "tq_common.h"
+#include "tq_stream.h"
+
+#ifndef TQ_PF_R
+#define TQ_PF_R 3  // raw tiles in the LDS ring (R-1 in flight while one is decoded)
+#endif
+
+namespace tq {
+
+struct PrefillArgs {
+  const uint16_t *q_rot, *q_proj;
+  const uint8_t *kcodes, *ksigns;
+  const uint16_t *krn, *kvn, *kcent;  // f16 key centroids
+  const uint8_t* vcodes;
+  const uint16_t *vvn, *vpit;         // vpit: split Pi_v^T (hi, lo)
+  const float* vcent;                 // f32 value centroids
+  int B, Hq, Hkv, Sq, Sk, G, QT, nqb;
+  int64_t ldk;                        // rows between consecutive (batch, kv head) planes
+  float coeff, scale;
+  int causal;
+  const float* mask;
+  int64_t smb, smh, smq, smk;
+  void* out;
+  int out_dtype;
+  int64_t sob, soh, sos;
+};
+
+template <int BITS>
+struct PfCfg {
+  static constexpr int D = 128, KT = 32, R = TQ_PF_R, NT = 256;
+  static constexpr int KB = BITS - 1, VB = BITS;
+  static constexpr int KC = D * KB / 8, SC = D / 8, VC = D * VB / 8;  // bytes per packed row
+  // raw slot: code planes, sign plane, value codes (+16 so that dword-pair reads of the
+  // last row stay inside the slot), three norm planes of one dword per key
+  static constexpr int OFF_K = 0, OFF_S = OFF_K + KT * KC, OFF_V = OFF_S + KT * SC;
+  static constexpr int OFF_N = OFF_V + KT * VC + 16;
+  static constexpr int NRM = KT * 4;
+  static constexpr int SLOT = OFF_N + 3 * NRM;
+  static constexpr int NKD = (KT * KC + 1023) / 1024, NSD = (KT * SC + 1023) / 1024, NVD = (KT * VC + 1023) / 1024;
+  static constexpr int NDMA = NKD + NSD + NVD + 3;  // DMA instructions per tile (issued by wave 0)
+  static constexpr int LDK = D + 8;   // f16 stride of K^ / sign rows: 8-lane b128 reads hit distinct banks
+  static constexpr int LDV = KT + 4;  // f16 stride of V^T rows: 16-lane b64 reads hit distinct banks
+  // lookup tables: signs 16 x half4; keys KB=1 16 x half4, KB=2 16 x half2, KB=3 64 x half2;
+  // value pairs (C[x], C[y]) indexed by x | y << VB: 16 / 64 / 256 x half2
+  static constexpr int T_SGN = 0, T_KEY = 128;
+  static constexpr int T_VAL = T_KEY + (KB == 1 ? 128 : (KB == 2 ? 64 : 256));
+  static constexpr int T_BYTES = T_VAL + (VB == 2 ? 64 : (VB == 3 ? 256 : 1024));
+  static_assert(KT * SC == 512, "sign plane is half a DMA round");
+};
+
+// 32 bits of a packed row from byte `off` on (reads the dword pair around it)
+__device__ __forceinline__ uint32_t field32(const uint8_t* row, int off) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(row + (off & ~3));
+  return (off & 3) ? __builtin_amdgcn_alignbyte(w[1], w[0], off & 3) : w[0];
+}
+
+__device__ __forceinline__ half8 cat8h(half4 a, half4 b) {
+  return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// odd VB-bit fields of 8 consecutive fields
+template <int VB>
+constexpr uint32_t odd_fields() {
+  return VB == 2 ? 0xCCCCu : (VB == 3 ? 0xE38E38u : 0xF0F0F0F0u);
+}
+
+template <int BITS, bool MASK>
+__global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
+  using C = PfCfg<BITS>;
+  constexpr int D = C::D, KT = C::KT, R = C::R, KB = C::KB, VB = C::VB;
+  constexpr int KC = C::KC, SC = C::SC, VC = C::VC, LDK = C::LDK, LDV = C::LDV;
+  constexpr int KS = D / 32, DB = D / 16, NBW = 2;
+  constexpr float LOG2E = 1.4426950408889634f;
+  constexpr float TAU = 8.0f;  // lazy-rescale headroom (log2 units)
+
+  __shared__ __attribute__((aligned(16))) uint8_t luts[C::T_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t ring[R * C::SLOT];
+  __shared__ __attribute__((aligned(16))) _Float16 sK0[KT * LDK], sK1[KT * LDK];
+  __shared__ __attribute__((aligned(16))) _Float16 sS0[KT * LDK], sS1[KT * LDK];
+  __shared__ __attribute__((aligned(16))) _Float16 sV0[D * LDV], sV1[D * LDV];
+  __shared__ __attribute__((aligned(16))) float fac0[3][KT], fac1[3][KT];  // fa*vn_k, fa*coeff*rn_k, vn_v
+  const uint8_t* tS = luts + C::T_SGN;
+  const uint8_t* tK = luts + C::T_KEY;
+  const uint8_t* tV = luts + C::T_VAL;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int qblk = a.nqb - 1 - static_cast<int>(blockIdx.x);  // heavy causal blocks first
+  const int hkv = blockIdx.y, b = blockIdx.z;
+  const int q0 = qblk * a.QT;
+  const int64_t bh = static_cast<int64_t>(b) * a.Hkv + hkv;
+
+  // ---- lookup tables
+  {
+    auto kc = [&](int i) { return __builtin_bit_cast(_Float16, a.kcent[i]); };
+    auto vc = [&](int i) { return static_cast<_Float16>(a.vcent[i]); };
+    if (tid < 16) {
+      half4 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = ((tid >> j) & 1) ? static_cast<_Float16>(1.f) : static_cast<_Float16>(-1.f);
+      *reinterpret_cast<half4*>(luts + C::T_SGN + tid * 8) = v;
+    }
+    if constexpr (KB == 1) {
+      if (tid < 16) {
+        half4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = kc((tid >> j) & 1);
+        *reinterpret_cast<half4*>(luts + C::T_KEY + tid * 8) = v;
+      }
+    } else {
+      constexpr int N = (KB == 2) ? 16 : 64;
+      if (tid < N) {
+        half2v v;
+        v[0] = kc(tid & ((1 << KB) - 1));
+        v[1] = kc(tid >> KB);
+        *reinterpret_cast<half2v*>(luts + C::T_KEY + tid * 4) = v;
+      }
+    }
+    constexpr int NV = 1 << (2 * VB);
+    if (tid < NV) {
+      half2v v;
+      v[0] = vc(tid & ((1 << VB) - 1));
+      v[1] = vc(tid >> VB);
+      *reinterpret_cast<half2v*>(luts + C::T_VAL + tid * 4) = v;
+    }
+  }
+
+  // ---- this lane's columns and their query fragments (B operands)
+  int col_i[NBW], col_h[NBW];
+  bool col_ok[NBW];
+  half8 qr[KS][NBW], qp[KS][NBW];
+#pragma unroll
+  for (int nb = 0; nb < NBW; ++nb) {
+    const int r = (wave * NBW + nb) * 16 + l16;
+    const int ql = r / a.G, gi = r % a.G;
+    col_i[nb] = q0 + ql;
+    col_h[nb] = hkv * a.G + gi;
+    col_ok[nb] = (ql < a.QT) && (col_i[nb] < a.Sq);
+    const int64_t qrow = ((static_cast<int64_t>(b) * a.Hq + col_h[nb]) * a.Sq + (col_ok[nb] ? col_i[nb] : 0)) * D;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int d0 = ks * 32 + lg * 8;
+      qr[ks][nb] = col_ok[nb] ? *reinterpret_cast<const half8*>(a.q_rot + qrow + d0) : half8{};
+      qp[ks][nb] = col_ok[nb] ? *reinterpret_cast<const half8*>(a.q_proj + qrow + d0) : half8{};
+    }
+  }
+
+  // keys this block needs; tiles past `kfull` need per-element masking
+  int kend = a.Sk, kfull = a.Sk;
+  if (a.causal) {
+    const int imax = min(q0 + a.QT - 1, a.Sq - 1);
+    kend = min(a.Sk, imax + (a.Sk - a.Sq) + 1);
+    kfull = min(kfull, q0 + (a.Sk - a.Sq) + 1);
+  }
+  const int nt = (kend + KT - 1) / KT;
+  const float fa = a.scale * LOG2E;  // scores kept in log2 units
+  const float fb = fa * a.coeff;
+
+  // ---- raw ring: wave 0 copies tile j's planes into slot j % R
+  const int64_t g0 = bh * a.ldk;
+  const uint8_t* pk = a.kcodes + g0 * KC;
+  const uint8_t* ps = a.ksigns + g0 * SC;
+  const uint8_t* pv = a.vcodes + g0 * VC;
+  const uint16_t* pkn = a.kvn + g0;
+  const uint16_t* prn = a.krn + g0;
+  const uint16_t* pvn = a.vvn + g0;
+  const uint32_t ring_lds = lds_offset(ring);
+  auto copy_plane = [&](const i32x4& r, uint32_t dst, int bytes, int nrounds) {
+    const uint32_t lo = lane * 16;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (c >= nrounds) break;
+      if ((c + 1) * 1024 <= bytes || lane < 32) dma16(r, dst + c * 1024, lo + c * 1024);
+    }
+  };
+  auto issue = [&](int j) {  // wave 0 only
+    const int kb = j * KT;
+    const uint32_t dst = ring_lds + (j % R) * C::SLOT;
+    copy_plane(rows_desc(pk, KC, kb, kend), dst + C::OFF_K, KT * KC, C::NKD);
+    copy_plane(rows_desc(ps, SC, kb, kend), dst + C::OFF_S, KT * SC, C::NSD);
+    copy_plane(rows_desc(pv, VC, kb, kend), dst + C::OFF_V, KT * VC, C::NVD);
+    if (lane < 32) {
+      dma_u16(rows_desc(pkn, 2, kb, kend), dst + C::OFF_N, lane * 2);
+      dma_u16(rows_desc(prn, 2, kb, kend), dst + C::OFF_N + C::NRM, lane * 2);
+      dma_u16(rows_desc(pvn, 2, kb, kend), dst + C::OFF_N + 2 * C::NRM, lane * 2);
+    }
+  };
+  // wave 0: wait until tile j has landed, `later` tiles having been issued after it
+  auto wait_tile = [&](int later) {
+    static_assert(R >= 2 && R <= 4, "ring of 2 to 4 tiles");
+    if (later >= 2) wait_vm<(R >= 4 ? 2 * C::NDMA : 0)>();
+    else if (later == 1) wait_vm<(R >= 3 ? C::NDMA : 0)>();
+    else wait_vm<0>();
+  };
+
+  // ---- decode tile j (raw slot j % R) into (dK, dS, dV, dF); every thread one item of each kind
+  auto decode = [&](int j, _Float16* dK, _Float16* dS, _Float16* dV, float (*dF)[KT]) {
+    const uint8_t* raw = ring + (j % R) * C::SLOT;
+    {  // keys and signs: item (key, 16-dim group)
+      const int key = tid >> 3, g = tid & 7;
+      half8 k0, k1;
+      if constexpr (KB == 1) {
+        const uint32_t w = *reinterpret_cast<const uint16_t*>(raw + C::OFF_K + key * KC + 2 * g);
+        k0 = nib2x4<0>(tK, w);
+        k1 = nib2x4<1>(tK, w);
+      } else if constexpr (KB == 2) {
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(raw + C::OFF_K + key * KC + 4 * g);
+        k0 = nib4x2<0>(tK, w);
+        k1 = nib4x2<2>(tK, w);
+      } else {
+        const uint8_t* row = raw + C::OFF_K + key * KC;
+        k0 = six4x2(tK, field32(row, 6 * g));
+        k1 = six4x2(tK, field32(row, 6 * g + 3));
+      }
+      const uint32_t sw = *reinterpret_cast<const uint16_t*>(raw + C::OFF_S + key * SC + 2 * g);
+      const half8 s0 = nib2x4<0>(tS, sw), s1 = nib2x4<1>(tS, sw);
+      // lanes 4-7 of each 8-lane store group write their halves in the other order,
+      // so the group covers all 32 banks
+      const int sw1 = (g >> 2) & 1;
+      _Float16* kr = dK + key * LDK + 16 * g;
+      _Float16* sr = dS + key * LDK + 16 * g;
+      *reinterpret_cast<half8*>(kr + 8 * sw1) = sw1 ? k1 : k0;
+      *reinterpret_cast<half8*>(sr + 8 * sw1) = sw1 ? s1 : s0;
+      *reinterpret_cast<half8*>(kr + 8 * (1 - sw1)) = sw1 ? k0 : k1;
+      *reinterpret_cast<half8*>(sr + 8 * (1 - sw1)) = sw1 ? s0 : s1;
+    }
+    {  // values: item (key pair kp, 8-dim group dg) -> dwords (C[code 2kp], C[code 2kp+1]) per dim
+      const int kp = tid & 15, dg = tid >> 4;
+      const uint8_t* r0 = raw + C::OFF_V + (2 * kp) * VC;
+      const uint32_t w0 = field32(r0, dg * VB), w1 = field32(r0 + VC, dg * VB);
+      constexpr uint32_t M = odd_fields<VB>();
+      const uint32_t te = ((w1 << VB) & M) | (w0 & ~M);  // even dims
+      const uint32_t to = (w1 & M) | ((w0 >> VB) & ~M);                                    // odd dims
+      half8 pe, po;
+      if constexpr (VB == 2) {
+        pe = nib4x2<0>(tV, te);
+        po = nib4x2<0>(tV, to);
+      } else if constexpr (VB == 3) {
+        pe = six4x2(tV, te);
+        po = six4x2(tV, to);
+      } else {
+        pe = byte4x2(tV, te);
+        po = byte4x2(tV, to);
+      }
+      const u32x4 de = __builtin_bit_cast(u32x4, pe), dd = __builtin_bit_cast(u32x4, po);
+      uint32_t* vcol = reinterpret_cast<uint32_t*>(dV + (8 * dg) * LDV + 2 * kp);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vcol[(2 * e) * (LDV / 2)] = de[e];
+        vcol[(2 * e + 1) * (LDV / 2)] = dd[e];
+      }
+    }
+    if (tid < KT) {  // per-key factors (rows past the block's keys read zero)
+      const uint32_t* nrm = reinterpret_cast<const uint32_t*>(raw + C::OFF_N);
+      dF[0][tid] = fa * h2f(static_cast<uint16_t>(nrm[tid]));
+      dF[1][tid] = fb * h2f(static_cast<uint16_t>(nrm[KT + tid]));
+      dF[2][tid] = h2f(static_cast<uint16_t>(nrm[2 * KT + tid]));
+    }
+  };
+
+  float m_run[NBW], l_run[NBW];
+  float4v oacc[DB][NBW];
+#pragma unroll
+  for (int nb = 0; nb < NBW; ++nb) {
+    m_run[nb] = -INFINITY;
+    l_run[nb] = 0.f;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) oacc[db][nb] = float4v{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // ---- scores, online softmax and P.V of tile j from decoded buffers
+  auto compute = [&](int j, const _Float16* cK, const _Float16* cS, const _Float16* cV, const float (*cF)[KT]) {
+    const int k0 = j * KT;
+    float4v sacc[2][NBW], tacc[2][NBW];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NBW; ++nb) {
+        sacc[mb][nb] = float4v{0.f, 0.f, 0.f, 0.f};
+        tacc[mb][nb] = float4v{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const int off = (mb * 16 + l16) * LDK + ks * 32 + lg * 8;
+        const half8 ka = *reinterpret_cast<const half8*>(cK + off);
+        const half8 sa = *reinterpret_cast<const half8*>(cS + off);
+#pragma unroll
+        for (int nb = 0; nb < NBW; ++nb) {
+          sacc[mb][nb] = mfma16x16x32(ka, qr[ks][nb], sacc[mb][nb]);
+          tacc[mb][nb] = mfma16x16x32(sa, qp[ks][nb], tacc[mb][nb]);
+        }
+      }
+    const float4v fA0 = *reinterpret_cast<const float4v*>(&cF[0][4 * lg]);
+    const float4v fA1 = *reinterpret_cast<const float4v*>(&cF[0][16 + 4 * lg]);
+    const float4v fB0 = *reinterpret_cast<const float4v*>(&cF[1][4 * lg]);
+    const float4v fB1 = *reinterpret_cast<const float4v*>(&cF[1][16 + 4 * lg]);
+    const float4v fV0 = *reinterpret_cast<const float4v*>(&cF[2][4 * lg]);
+    const float4v fV1 = *reinterpret_cast<const float4v*>(&cF[2][16 + 4 * lg]);
+    const bool edge = k0 + KT > kfull;
+    half8 pb[NBW];
+#pragma unroll
+    for (int nb = 0; nb < NBW; ++nb) {
+      float sc[2][4];
+      float tmax = -INFINITY;
+      const int lim = col_i[nb] + (a.Sk - a.Sq);
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float v = fmaf(tacc[mb][nb][e], mb ? fB1[e] : fB0[e], sacc[mb][nb][e] * (mb ? fA1[e] : fA0[e]));
+          const int key = k0 + mb * 16 + 4 * lg + e;
+          if constexpr (MASK) {
+            if (col_ok[nb] && key < a.Sk)
+              v += fmaxf(a.mask[b * a.smb + col_h[nb] * a.smh + static_cast<int64_t>(col_i[nb]) * a.smq +
+                                static_cast<int64_t>(key) * a.smk] * LOG2E,
+                         -3.0e38f);
+          }
+          if (edge && (key >= a.Sk || (a.causal && key > lim))) v = -INFINITY;
+          sc[mb][e] = v;
+          tmax = fmaxf(tmax, v);
+        }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const bool grow = tmax > m_run[nb] + TAU;
+      if (__any(grow)) {
+        const float m_new = grow ? tmax : m_run[nb];
+        const float alpha = (m_run[nb] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[nb] - m_new);
+        m_run[nb] = m_new;
+        l_run[nb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) oacc[db][nb] *= alpha;
+      }
+      const float m_use = (m_run[nb] == -INFINITY) ? 0.f : m_run[nb];
+      float psum = 0.f;
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float p = __builtin_amdgcn_exp2f(sc[mb][e] - m_use);
+          psum += p;
+          pb[nb][mb * 4 + e] = static_cast<_Float16>(p * (mb ? fV1[e] : fV0[e]));
+        }
+      l_run[nb] += psum;
+    }
+    // O^T += V^T P'^T: k-slots 8*lg+0..3 <-> keys 4lg+0..3, 8*lg+4..7 <-> keys 16+4lg+0..3
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const _Float16* vrow = cV + (db * 16 + l16) * LDV + 4 * lg;
+      const half8 va = cat8h(*reinterpret_cast<const half4*>(vrow), *reinterpret_cast<const half4*>(vrow + 16));
+#pragma unroll
+      for (int nb = 0; nb < NBW; ++nb) oacc[db][nb] = mfma16x16x32(va, pb[nb], oacc[db][nb]);
+    }
+  };
+
+  // ---- pipeline: tiles 0..R-1 in flight, tile 0 decoded, then one barrier per tile
+  __builtin_amdgcn_s_waitcnt(0);  // q fragments landed: the ring's vmcnt waits count DMAs only
+  if (nt > 0) {
+    if (wave == 0) {
+#pragma unroll
+      for (int j = 0; j < R; ++j)
+        if (j < nt) issue(j);
+      wait_tile(min(nt, R) - 1);
+    }
+    __syncthreads();  // tables and raw tile 0 visible
+    decode(0, sK0, sS0, sV0, fac0);
+  }
+  auto iter = [&](int t, const _Float16* cK, const _Float16* cS, const _Float16* cV, const float (*cF)[KT],
+                  _Float16* nK, _Float16* nS, _Float16* nV, float (*nF)[KT]) {
+    const bool has_next = t + 1 < nt;
+    if (wave == 0 && has_next) wait_tile(max(0, min(nt, t + R) - (t + 2)));
+    __syncthreads();  // tile t decoded by all waves; raw tile t+1 landed; buffers of tile t-1 free
+    if (wave == 0 && t + R < nt) issue(t + R);
+    if (has_next) decode(t + 1, nK, nS, nV, nF);
+    compute(t, cK, cS, cV, cF);
+  };
+  for (int t = 0; t < nt; t += 2) {
+    iter(t, sK0, sS0, sV0, fac0, sK1, sS1, sV1, fac1);
+    if (t + 1 < nt) iter(t + 1, sK1, sS1, sV1, fac1, sK0, sS0, sV0, fac0);
+  }
+
+  // ---- normalise and rotate back: out = (O^T / l)^T Pi_v, Pi_v^T as split-f16 A operand
+  const half4* Ph = reinterpret_cast<const half4*>(a.vpit);
+  const half4* Pl = reinterpret_cast<const half4*>(a.vpit + D * D);
+#pragma unroll
+  for (int nb = 0; nb < NBW; ++nb) {
+    float l = l_run[nb];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    const float inv_l = (l > 0.f) ? 1.f / l : 0.f;
+    float mx = 0.f;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      oacc[db][nb] *= inv_l;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) mx = fmaxf(mx, fabsf(oacc[db][nb][e]));
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    int ex;
+    frexpf(mx, &ex);
+    const float up = ldexpf(kSplit, -ex), down = ldexpf(kUnsplit2, ex);
+    half8 bh[DB / 2], bl[DB / 2];
+#pragma unroll
+    for (int c = 0; c < DB / 2; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        _Float16 h, lo;
+        split_f16(oacc[2 * c][nb][e] * up, h, lo);
+        bh[c][e] = h;
+        bl[c][e] = lo;
+        split_f16(oacc[2 * c + 1][nb][e] * up, h, lo);
+        bh[c][4 + e] = h;
+        bl[c][4 + e] = lo;
+      }
+    const int qi = col_i[nb], h = col_h[nb];
+#pragma unroll 1
+    for (int ib = 0; ib < DB; ++ib) {
+      float4v f = float4v{0.f, 0.f, 0.f, 0.f};
+      const int i = ib * 16 + l16;
+#pragma unroll
+      for (int c = 0; c < DB / 2; ++c) {
+        const int j0 = c * 32 + lg * 4;
+        const half8 ah = cat8h(Ph[(i * D + j0) / 4], Ph[(i * D + j0 + 16) / 4]);
+        const half8 al = cat8h(Pl[(i * D + j0) / 4], Pl[(i * D + j0 + 16) / 4]);
+        f = mfma16x16x32(ah, bh[c], f);
+        f = mfma16x16x32(al, bh[c], f);
+        f = mfma16x16x32(ah, bl[c], f);
+      }
+      if (col_ok[nb]) {
+        const int64_t o = static_cast<int64_t>(b) * a.sob + static_cast<int64_t>(h) * a.soh +
+                          static_cast<int64_t>(qi) * a.sos + ib * 16 + lg * 4;
+        const float4v fo = f * down;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (a.out_dtype == TQ_BF16) store_act<TQ_BF16>(a.out, o + e, fo[e]);
+          else if (a.out_dtype == TQ_F16) store_act<TQ_F16>(a.out, o + e, fo[e]);
+          else store_act<TQ_F32>(a.out, o + e, fo[e]);
+        }
+      }
+    }
+  }
+}
+
+// Used by tq_attn.hip's entry points.
+bool prefill_applies(int Hq, int Hkv, int d, int bits, int val_bits) {
+  return d == 128 && bits >= 2 && bits <= 4 && val_bits == bits && Hq / Hkv <= 128;
+}
+
+int prefill_attention(int64_t ldk, const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
+                      const uint8_t* ksigns, const uint16_t* krn, const uint16_t* kvn, const uint16_t* kcent,
+                      int bits, const uint8_t* vcodes, const uint16_t* vvn, const float* vcent,
+                      const uint16_t* vpit, int B, int Hq, int Hkv, int Sq, int Sk, float coeff, float scale,
+                      int causal, const float* mask, int64_t smb, int64_t smh, int64_t smq, int64_t smk, void* out,
+                      int out_dtype, int64_t sob, int64_t soh, int64_t sos, hipStream_t s) {
+  PrefillArgs a{};
+  a.q_rot = q_rot;
+  a.q_proj = q_proj;
+  a.kcodes = kcodes;
+  a.ksigns = ksigns;
+  a.krn = krn;
+  a.kvn = kvn;
+  a.kcent = kcent;
+  a.vcodes = vcodes;
+  a.vvn = vvn;
+  a.vcent = vcent;
+  a.vpit = vpit;
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.Sq = Sq;
+  a.Sk = Sk;
+  a.G = Hq / Hkv;
+  a.QT = 128 / a.G;
+  a.nqb = (Sq + a.QT - 1) / a.QT;
+  a.ldk = ldk;
+  a.coeff = coeff;
+  a.scale = scale;
+  a.causal = causal;
+  a.mask = mask;
+  a.smb = smb;
+  a.smh = smh;
+  a.smq = smq;
+  a.smk = smk;
+  a.out = out;
+  a.out_dtype = out_dtype;
+  a.sob = sob;
+  a.soh = soh;
+  a.sos = sos;
+  const dim3 grid(a.nqb, Hkv, B);
+#define TQ_PF_LAUNCH(BB)                                                   \
+  if (mask) prefill_kernel<BB, true><<<grid, 256, 0, s>>>(a);             \
+  else prefill_kernel<BB, false><<<grid, 256, 0, s>>>(a);
+  if (bits == 2) { TQ_PF_LAUNCH(2) }
+  else if (bits == 3) { TQ_PF_LAUNCH(3) }
+  else { TQ_PF_LAUNCH(4) }
+#undef TQ_PF_LAUNCH
+  return launch_status("tq_attention_fwd (prefill)");
+}
+
+}  // namespace tq
