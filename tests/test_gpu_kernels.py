@@ -275,10 +275,11 @@ def test_attention_matches_oracle(d, bits, hq, hkv, sq, sk, causal):
     assert O.rel_err(got, ref) < REL and O.cosine(got, ref) > 0.9999
 
 
-def test_attention_additive_mask_and_dtypes():
-    _case(what="mask")
+@pytest.mark.parametrize("d", [64, 128])
+def test_attention_additive_mask_and_dtypes(d):
+    _case(what="mask", d=d)
     torch.manual_seed(11)
-    B, hq, hkv, S, d = 2, 4, 2, 45, 64
+    B, hq, hkv, S = 2, 4, 2, 45
     q = torch.randn(B, hq, S, d, device=DEV)
     k = torch.randn(B, hkv, S, d, device=DEV)
     v = torch.randn(B, hkv, S, d, device=DEV)

@@ -9,7 +9,8 @@
 //    direct-to-LDS buffer loads issued R-1 tiles ahead (no register staging).
 //  * Each tile is decoded once per block into f16 tiles: K^ = Ck[codes] and
 //    the +-1 sign tile as [key][dim] rows, and V^T = Cv[codes] as [dim][key]
-//    rows (the value norms are folded into P instead).  Decoding uses small
+//    rows, V^ = f16(Cv[code] * vn) with the value norm applied by a packed f16
+//    multiply of each (key, key+1) dword.  Decoding uses small
 //    LDS tables indexed by nibbles / bit fields (conflict-free for <= 32
 //    entries); the value table is indexed by the codes of two keys at one dim,
 //    so each lookup yields the (key, key+1) pair the MFMA operand needs and no
@@ -21,12 +22,18 @@
 //    (batch, kv head); each wave owns two 16-column blocks.  S^T = K^ Q^T comes
 //    out of v_mfma_f32_16x16x32_f16 with 4 consecutive keys of one column per
 //    lane, the P^T operand layout of O^T += V^T P^T, so P stays in registers.
-//    P' = f16(p * vn_v) (one f16 rounding, the value norm folded in).
+//    P = f16(2^(s - m)) enters the P.V product (one f16 rounding, P <= 2^TAU).
 #include "tq_common.h"
 #include "tq_stream.h"
 
 #ifndef TQ_PF_R
-#define TQ_PF_R 3  // raw tiles in the LDS ring (R-1 in flight while one is decoded)
+#define TQ_PF_R 2  // raw tiles in the LDS ring (R-1 in flight while one is decoded)
+#endif
+#ifndef TQ_PF_WAVES
+#define TQ_PF_WAVES 4  // waves per block, each with two 16-column blocks (128 or 256 columns)
+#endif
+#ifndef TQ_PF_PRIO
+#define TQ_PF_PRIO 1  // 1: raise the wave priority while it issues MFMAs
 #endif
 
 namespace tq {
@@ -51,7 +58,8 @@ struct PrefillArgs {
 
 template <int BITS>
 struct PfCfg {
-  static constexpr int D = 128, KT = 32, R = TQ_PF_R, NT = 256;
+  static constexpr int D = 128, KT = 32, R = TQ_PF_R, NW = TQ_PF_WAVES, NT = 64 * NW;
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves per block");
   static constexpr int KB = BITS - 1, VB = BITS;
   static constexpr int KC = D * KB / 8, SC = D / 8, VC = D * VB / 8;  // bytes per packed row
   // raw slot: code planes, sign plane, value codes (+16 so that dword-pair reads of the
@@ -72,10 +80,11 @@ struct PfCfg {
   static_assert(KT * SC == 512, "sign plane is half a DMA round");
 };
 
-// 32 bits of a packed row from byte `off` on (reads the dword pair around it)
+// 32 bits of a packed row from byte `off` on: the dword pair around it, byte-aligned
+// without a branch (a shift of 0 returns the low dword)
 __device__ __forceinline__ uint32_t field32(const uint8_t* row, int off) {
   const uint32_t* w = reinterpret_cast<const uint32_t*>(row + (off & ~3));
-  return (off & 3) ? __builtin_amdgcn_alignbyte(w[1], w[0], off & 3) : w[0];
+  return __builtin_amdgcn_alignbyte(w[1], w[0], off & 3);
 }
 
 __device__ __forceinline__ half8 cat8h(half4 a, half4 b) {
@@ -89,11 +98,11 @@ constexpr uint32_t odd_fields() {
 }
 
 template <int BITS, bool MASK>
-__global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
+__global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_per_eu(2))) prefill_kernel(PrefillArgs a) {
   using C = PfCfg<BITS>;
   constexpr int D = C::D, KT = C::KT, R = C::R, KB = C::KB, VB = C::VB;
   constexpr int KC = C::KC, SC = C::SC, VC = C::VC, LDK = C::LDK, LDV = C::LDV;
-  constexpr int KS = D / 32, DB = D / 16, NBW = 2;
+  constexpr int KS = D / 32, DB = D / 16, NT = C::NT, NBW = 2;  // 32 columns per wave
   constexpr float LOG2E = 1.4426950408889634f;
   constexpr float TAU = 8.0f;  // lazy-rescale headroom (log2 units)
 
@@ -102,7 +111,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) _Float16 sK0[KT * LDK], sK1[KT * LDK];
   __shared__ __attribute__((aligned(16))) _Float16 sS0[KT * LDK], sS1[KT * LDK];
   __shared__ __attribute__((aligned(16))) _Float16 sV0[D * LDV], sV1[D * LDV];
-  __shared__ __attribute__((aligned(16))) float fac0[3][KT], fac1[3][KT];  // fa*vn_k, fa*coeff*rn_k, vn_v
+  __shared__ __attribute__((aligned(16))) float fac0[3][KT], fac1[3][KT];  // fa*vn_k, fa*coeff*rn_k, unused
   const uint8_t* tS = luts + C::T_SGN;
   const uint8_t* tK = luts + C::T_KEY;
   const uint8_t* tV = luts + C::T_VAL;
@@ -217,68 +226,57 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
     else wait_vm<0>();
   };
 
-  // ---- decode tile j (raw slot j % R) into (dK, dS, dV, dF); every thread one item of each kind
-  auto decode = [&](int j, _Float16* dK, _Float16* dS, _Float16* dV, float (*dF)[KT]) {
+  // ---- decode tile j (raw slot j % R): every thread one item of each kind, branch-free (a
+  // slot past the last tile decodes stale bytes into a buffer nobody reads)
+  auto decode_ks = [&](int j, _Float16* dK, _Float16* dS) {  // item (key, 8-dim group)
     const uint8_t* raw = ring + (j % R) * C::SLOT;
-    {  // keys and signs: item (key, 16-dim group)
-      const int key = tid >> 3, g = tid & 7;
-      half8 k0, k1;
+#pragma unroll
+    for (int rep = 0; rep < 512 / NT; ++rep) {
+      const int i = tid + rep * NT, key = i >> 4, g = i & 15;
+      half8 kv;
       if constexpr (KB == 1) {
-        const uint32_t w = *reinterpret_cast<const uint16_t*>(raw + C::OFF_K + key * KC + 2 * g);
-        k0 = nib2x4<0>(tK, w);
-        k1 = nib2x4<1>(tK, w);
+        kv = nib2x4<0>(tK, raw[C::OFF_K + key * KC + g]);
       } else if constexpr (KB == 2) {
-        const uint32_t w = *reinterpret_cast<const uint32_t*>(raw + C::OFF_K + key * KC + 4 * g);
-        k0 = nib4x2<0>(tK, w);
-        k1 = nib4x2<2>(tK, w);
+        kv = nib4x2<0>(tK, *reinterpret_cast<const uint16_t*>(raw + C::OFF_K + key * KC + 2 * g));
       } else {
-        const uint8_t* row = raw + C::OFF_K + key * KC;
-        k0 = six4x2(tK, field32(row, 6 * g));
-        k1 = six4x2(tK, field32(row, 6 * g + 3));
+        kv = six4x2(tK, field32(raw + C::OFF_K + key * KC, 3 * g));
       }
-      const uint32_t sw = *reinterpret_cast<const uint16_t*>(raw + C::OFF_S + key * SC + 2 * g);
-      const half8 s0 = nib2x4<0>(tS, sw), s1 = nib2x4<1>(tS, sw);
-      // lanes 4-7 of each 8-lane store group write their halves in the other order,
-      // so the group covers all 32 banks
-      const int sw1 = (g >> 2) & 1;
-      _Float16* kr = dK + key * LDK + 16 * g;
-      _Float16* sr = dS + key * LDK + 16 * g;
-      *reinterpret_cast<half8*>(kr + 8 * sw1) = sw1 ? k1 : k0;
-      *reinterpret_cast<half8*>(sr + 8 * sw1) = sw1 ? s1 : s0;
-      *reinterpret_cast<half8*>(kr + 8 * (1 - sw1)) = sw1 ? k0 : k1;
-      *reinterpret_cast<half8*>(sr + 8 * (1 - sw1)) = sw1 ? s0 : s1;
+      const half8 sv = nib2x4<0>(tS, raw[C::OFF_S + key * SC + g]);
+      *reinterpret_cast<half8*>(dK + key * LDK + 8 * g) = kv;
+      *reinterpret_cast<half8*>(dS + key * LDK + 8 * g) = sv;
     }
-    {  // values: item (key pair kp, 8-dim group dg) -> dwords (C[code 2kp], C[code 2kp+1]) per dim
-      const int kp = tid & 15, dg = tid >> 4;
+  };
+  auto decode_v = [&](int j, _Float16* dV, float (*dF)[KT]) {
+    const uint8_t* raw = ring + (j % R) * C::SLOT;
+#pragma unroll
+    for (int rep = 0; rep < 512 / NT; ++rep) {
+      // values: item (key pair kp, 8-dim group dg, parity par) -> dwords (C[code 2kp], C[code 2kp+1])
+      // of the even (par 0) or odd (par 1) dims of the group
+      const int i = tid + rep * NT, kp = i & 15, dg = (i >> 4) & 15, par = i >> 8;
       const uint8_t* r0 = raw + C::OFF_V + (2 * kp) * VC;
       const uint32_t w0 = field32(r0, dg * VB), w1 = field32(r0 + VC, dg * VB);
       constexpr uint32_t M = odd_fields<VB>();
-      const uint32_t te = ((w1 << VB) & M) | (w0 & ~M);  // even dims
-      const uint32_t to = (w1 & M) | ((w0 >> VB) & ~M);                                    // odd dims
-      half8 pe, po;
-      if constexpr (VB == 2) {
-        pe = nib4x2<0>(tV, te);
-        po = nib4x2<0>(tV, to);
-      } else if constexpr (VB == 3) {
-        pe = six4x2(tV, te);
-        po = six4x2(tV, to);
-      } else {
-        pe = byte4x2(tV, te);
-        po = byte4x2(tV, to);
-      }
-      const u32x4 de = __builtin_bit_cast(u32x4, pe), dd = __builtin_bit_cast(u32x4, po);
-      uint32_t* vcol = reinterpret_cast<uint32_t*>(dV + (8 * dg) * LDV + 2 * kp);
+      const uint32_t x = par ? (w0 >> VB) : w0, y = par ? w1 : (w1 << VB);
+      const uint32_t f = (y & M) | (x & ~M);
+      half8 pv8;
+      if constexpr (VB == 2) pv8 = nib4x2<0>(tV, f);
+      else if constexpr (VB == 3) pv8 = six4x2(tV, f);
+      else pv8 = byte4x2(tV, f);
+      // V^ = f16(Cv[code] * vn): the pair's two value norms scale their halves of each dword
+      const uint32_t* vnr = reinterpret_cast<const uint32_t*>(raw + C::OFF_N + 2 * C::NRM) + 2 * kp;
+      const uint32_t vnw = (vnr[0] & 0xffffu) | (vnr[1] << 16);
+      const half2v vn2 = __builtin_bit_cast(half2v, vnw);
+      half2v* vcol = reinterpret_cast<half2v*>(dV + (8 * dg + par) * LDV + 2 * kp);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        vcol[(2 * e) * (LDV / 2)] = de[e];
-        vcol[(2 * e + 1) * (LDV / 2)] = dd[e];
+        const half2v c2 = half2v{pv8[2 * e], pv8[2 * e + 1]};
+        vcol[(2 * e) * (LDV / 2)] = c2 * vn2;
       }
     }
-    if (tid < KT) {  // per-key factors (rows past the block's keys read zero)
+    {  // per-key score factors from the key norm planes; threads past them write row 2 (unused)
       const uint32_t* nrm = reinterpret_cast<const uint32_t*>(raw + C::OFF_N);
-      dF[0][tid] = fa * h2f(static_cast<uint16_t>(nrm[tid]));
-      dF[1][tid] = fb * h2f(static_cast<uint16_t>(nrm[KT + tid]));
-      dF[2][tid] = h2f(static_cast<uint16_t>(nrm[2 * KT + tid]));
+      const int which = min(tid >> 5, 2), k = tid & 31;
+      dF[which][k] = (which == 0 ? fa : fb) * h2f(static_cast<uint16_t>(nrm[min(which, 1) * KT + k]));
     }
   };
 
@@ -292,10 +290,8 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
     for (int db = 0; db < DB; ++db) oacc[db][nb] = float4v{0.f, 0.f, 0.f, 0.f};
   }
 
-  // ---- scores, online softmax and P.V of tile j from decoded buffers
-  auto compute = [&](int j, const _Float16* cK, const _Float16* cS, const _Float16* cV, const float (*cF)[KT]) {
-    const int k0 = j * KT;
-    float4v sacc[2][NBW], tacc[2][NBW];
+  // ---- scores of tile j: S^T = K^ Q_rot^T (term 1) and Sign Q_proj^T (term 2)
+  auto scores = [&](const _Float16* cK, const _Float16* cS, float4v (&sacc)[2][NBW], float4v (&tacc)[2][NBW]) {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
@@ -316,59 +312,90 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
           tacc[mb][nb] = mfma16x16x32(sa, qp[ks][nb], tacc[mb][nb]);
         }
       }
+  };
+  // ---- log2-domain scores with masking, column maxima, lazy rescale (one rare branch per tile)
+  auto softmax_max = [&](int j, const float (*cF)[KT], const float4v (&sacc)[2][NBW],
+                         const float4v (&tacc)[2][NBW], float (&sc)[NBW][2][4]) {
+    const int k0 = j * KT;
     const float4v fA0 = *reinterpret_cast<const float4v*>(&cF[0][4 * lg]);
     const float4v fA1 = *reinterpret_cast<const float4v*>(&cF[0][16 + 4 * lg]);
     const float4v fB0 = *reinterpret_cast<const float4v*>(&cF[1][4 * lg]);
     const float4v fB1 = *reinterpret_cast<const float4v*>(&cF[1][16 + 4 * lg]);
-    const float4v fV0 = *reinterpret_cast<const float4v*>(&cF[2][4 * lg]);
-    const float4v fV1 = *reinterpret_cast<const float4v*>(&cF[2][16 + 4 * lg]);
     const bool edge = k0 + KT > kfull;
-    half8 pb[NBW];
+    float lmax[NBW];
+    bool grow_any = false;
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb) {
-      float sc[2][4];
-      float tmax = -INFINITY;
-      const int lim = col_i[nb] + (a.Sk - a.Sq);
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           float v = fmaf(tacc[mb][nb][e], mb ? fB1[e] : fB0[e], sacc[mb][nb][e] * (mb ? fA1[e] : fA0[e]));
-          const int key = k0 + mb * 16 + 4 * lg + e;
           if constexpr (MASK) {
+            const int key = k0 + mb * 16 + 4 * lg + e;
             if (col_ok[nb] && key < a.Sk)
               v += fmaxf(a.mask[b * a.smb + col_h[nb] * a.smh + static_cast<int64_t>(col_i[nb]) * a.smq +
                                 static_cast<int64_t>(key) * a.smk] * LOG2E,
                          -3.0e38f);
           }
-          if (edge && (key >= a.Sk || (a.causal && key > lim))) v = -INFINITY;
-          sc[mb][e] = v;
-          tmax = fmaxf(tmax, v);
+          sc[nb][mb][e] = v;
         }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const bool grow = tmax > m_run[nb] + TAU;
-      if (__any(grow)) {
-        const float m_new = grow ? tmax : m_run[nb];
+    }
+    if (edge) {  // wave-uniform: only the block's last tiles reach past the causal edge or Sk
+#pragma unroll
+      for (int nb = 0; nb < NBW; ++nb) {
+        const int lim = a.causal ? col_i[nb] + (a.Sk - a.Sq) : a.Sk - 1;
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int key = k0 + mb * 16 + 4 * lg + e;
+            if (key >= a.Sk || key > lim) sc[nb][mb][e] = -INFINITY;
+          }
+      }
+    }
+    // the reference maximum of a column moves only when one of its scores exceeds it by
+    // more than TAU: each lane tests its own scores, the exact column maxima are formed
+    // (cross-lane) only when some lane triggers
+#pragma unroll
+    for (int nb = 0; nb < NBW; ++nb) {
+      lmax[nb] = fmaxf(fmaxf(fmaxf(sc[nb][0][0], sc[nb][0][1]), fmaxf(sc[nb][0][2], sc[nb][0][3])),
+                       fmaxf(fmaxf(sc[nb][1][0], sc[nb][1][1]), fmaxf(sc[nb][1][2], sc[nb][1][3])));
+      grow_any = grow_any || (lmax[nb] > m_run[nb] + TAU);
+    }
+    if (__any(grow_any)) {
+#pragma unroll
+      for (int nb = 0; nb < NBW; ++nb) {
+        float tmax = lmax[nb];
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float m_new = tmax > m_run[nb] + TAU ? tmax : m_run[nb];
         const float alpha = (m_run[nb] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[nb] - m_new);
         m_run[nb] = m_new;
         l_run[nb] *= alpha;
 #pragma unroll
         for (int db = 0; db < DB; ++db) oacc[db][nb] *= alpha;
       }
+    }
+  };
+  // ---- P = f16(2^(s - m)) (<= 2^TAU), row sums, O^T += V^T P^T
+  auto pv_tile = [&](const _Float16* cV, const float (&sc)[NBW][2][4]) {
+    half8 pb[NBW];
+#pragma unroll
+    for (int nb = 0; nb < NBW; ++nb) {
       const float m_use = (m_run[nb] == -INFINITY) ? 0.f : m_run[nb];
       float psum = 0.f;
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float p = __builtin_amdgcn_exp2f(sc[mb][e] - m_use);
+          const float p = __builtin_amdgcn_exp2f(sc[nb][mb][e] - m_use);
           psum += p;
-          pb[nb][mb * 4 + e] = static_cast<_Float16>(p * (mb ? fV1[e] : fV0[e]));
+          pb[nb][mb * 4 + e] = static_cast<_Float16>(p);
         }
       l_run[nb] += psum;
     }
-    // O^T += V^T P'^T: k-slots 8*lg+0..3 <-> keys 4lg+0..3, 8*lg+4..7 <-> keys 16+4lg+0..3
+    // k-slots 8*lg+0..3 <-> keys 4lg+0..3, 8*lg+4..7 <-> keys 16+4lg+0..3
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
       const _Float16* vrow = cV + (db * 16 + l16) * LDV + 4 * lg;
@@ -388,16 +415,30 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
       wait_tile(min(nt, R) - 1);
     }
     __syncthreads();  // tables and raw tile 0 visible
-    decode(0, sK0, sS0, sV0, fac0);
+    decode_ks(0, sK0, sS0);
+    decode_v(0, sV0, fac0);
   }
   auto iter = [&](int t, const _Float16* cK, const _Float16* cS, const _Float16* cV, const float (*cF)[KT],
                   _Float16* nK, _Float16* nS, _Float16* nV, float (*nF)[KT]) {
-    const bool has_next = t + 1 < nt;
-    if (wave == 0 && has_next) wait_tile(max(0, min(nt, t + R) - (t + 2)));
+    if (wave == 0 && t + 1 < nt) wait_tile(max(0, min(nt, t + R) - (t + 2)));
     __syncthreads();  // tile t decoded by all waves; raw tile t+1 landed; buffers of tile t-1 free
     if (wave == 0 && t + R < nt) issue(t + R);
-    if (has_next) decode(t + 1, nK, nS, nV, nF);
-    compute(t, cK, cS, cV, cF);
+    float4v sacc[2][NBW], tacc[2][NBW];
+    float sc[NBW][2][4];
+    if (TQ_PF_PRIO == 2) __builtin_amdgcn_s_setprio(1);
+    decode_ks(t + 1, nK, nS);  // overlaps the score MFMAs
+    if (TQ_PF_PRIO == 1) __builtin_amdgcn_s_setprio(1);
+    if (TQ_PF_PRIO == 3) __builtin_amdgcn_s_setprio(0);
+    scores(cK, cS, sacc, tacc);
+    if (TQ_PF_PRIO == 1 || TQ_PF_PRIO == 2) __builtin_amdgcn_s_setprio(0);
+    if (TQ_PF_PRIO == 3) __builtin_amdgcn_s_setprio(1);
+    softmax_max(t, cF, sacc, tacc, sc);
+    if (TQ_PF_PRIO == 1 || TQ_PF_PRIO == 2) __builtin_amdgcn_s_setprio(1);
+    if (TQ_PF_PRIO == 3) __builtin_amdgcn_s_setprio(0);
+    pv_tile(cV, sc);
+    if (TQ_PF_PRIO == 1) __builtin_amdgcn_s_setprio(0);
+    decode_v(t + 1, nV, nF);   // overlaps the P.V MFMAs
+    if (TQ_PF_PRIO == 2) __builtin_amdgcn_s_setprio(0);
   };
   for (int t = 0; t < nt; t += 2) {
     iter(t, sK0, sS0, sV0, fac0, sK1, sS1, sV1, fac1);
@@ -469,7 +510,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
 
 // Used by tq_attn.hip's entry points.
 bool prefill_applies(int Hq, int Hkv, int d, int bits, int val_bits) {
-  return d == 128 && bits >= 2 && bits <= 4 && val_bits == bits && Hq / Hkv <= 128;
+  return d == 128 && bits >= 2 && bits <= 4 && val_bits == bits && Hq / Hkv <= TQ_PF_WAVES * 32;
 }
 
 int prefill_attention(int64_t ldk, const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
@@ -496,7 +537,7 @@ int prefill_attention(int64_t ldk, const uint16_t* q_rot, const uint16_t* q_proj
   a.Sq = Sq;
   a.Sk = Sk;
   a.G = Hq / Hkv;
-  a.QT = 128 / a.G;
+  a.QT = PfCfg<3>::NW * 32 / a.G;  // 32 columns per wave
   a.nqb = (Sq + a.QT - 1) / a.QT;
   a.ldk = ldk;
   a.coeff = coeff;
@@ -514,8 +555,8 @@ int prefill_attention(int64_t ldk, const uint16_t* q_rot, const uint16_t* q_proj
   a.sos = sos;
   const dim3 grid(a.nqb, Hkv, B);
 #define TQ_PF_LAUNCH(BB)                                                   \
-  if (mask) prefill_kernel<BB, true><<<grid, 256, 0, s>>>(a);             \
-  else prefill_kernel<BB, false><<<grid, 256, 0, s>>>(a);
+  if (mask) prefill_kernel<BB, true><<<grid, PfCfg<BB>::NT, 0, s>>>(a);  \
+  else prefill_kernel<BB, false><<<grid, PfCfg<BB>::NT, 0, s>>>(a);
   if (bits == 2) { TQ_PF_LAUNCH(2) }
   else if (bits == 3) { TQ_PF_LAUNCH(3) }
   else { TQ_PF_LAUNCH(4) }
