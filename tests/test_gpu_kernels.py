@@ -259,6 +259,10 @@ def _oracle_attention(kc, vc, q, ck, cv, hq, hkv, mask=None, causal=False):
     (128, 3, 32, 8, 70, 70, True), (128, 3, 8, 2, 1, 300, False), (128, 2, 4, 4, 64, 64, True),
     (128, 4, 16, 2, 33, 97, True), (64, 3, 12, 12, 40, 40, False), (32, 3, 4, 2, 20, 20, True),
     (256, 3, 4, 4, 24, 50, True),
+    # head_dim-128 prefill kernel: GQA groups that leave columns of a block unused (G=3) or give
+    # 16 query rows per block (G=8), MHA non-causal with Sk > Sq, several causal blocks at bits 2 and 4
+    (128, 2, 12, 4, 50, 50, True), (128, 3, 32, 4, 20, 300, True), (128, 4, 8, 8, 40, 90, False),
+    (128, 2, 4, 2, 130, 130, True), (128, 4, 8, 2, 97, 160, True),
 ])
 def test_attention_matches_oracle(d, bits, hq, hkv, sq, sk, causal):
     _case(d=d, bits=bits, hq=hq, hkv=hkv, sq=sq, sk=sk, causal=causal)
