@@ -26,6 +26,8 @@
 #include "tq_common.h"
 #include "tq_stream.h"
 
+#include <type_traits>
+
 #ifndef TQ_PF_R
 #define TQ_PF_R 2  // raw tiles in the LDS ring (R-1 in flight while one is decoded)
 #endif
@@ -71,7 +73,7 @@ struct PfCfg {
   static constexpr int NKD = (KT * KC + 1023) / 1024, NSD = (KT * SC + 1023) / 1024, NVD = (KT * VC + 1023) / 1024;
   static constexpr int NDMA = NKD + NSD + NVD + 3;  // DMA instructions per tile (issued by wave 0)
   static constexpr int LDK = D + 8;   // f16 stride of K^ / sign rows: 8-lane b128 reads hit distinct banks
-  static constexpr int LDV = KT + 4;  // f16 stride of V^T rows: 16-lane b64 reads hit distinct banks
+  static constexpr int LDV = KT + 8;  // f16 stride of V^T rows: 8-lane b128 reads hit distinct banks
   // lookup tables: signs 16 x half4; keys KB=1 16 x half4, KB=2 16 x half2, KB=3 64 x half2;
   // value pairs (C[x], C[y]) indexed by x | y << VB: 16 / 64 / 256 x half2
   static constexpr int T_SGN = 0, T_KEY = 128;
@@ -198,7 +200,7 @@ __global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_
   const uint16_t* prn = a.krn + g0;
   const uint16_t* pvn = a.vvn + g0;
   const uint32_t ring_lds = lds_offset(ring);
-  auto copy_plane = [&](const i32x4& r, uint32_t dst, int bytes, int nrounds) {
+  auto copy_plane = [&](const i32x4& r, uint32_t dst, int bytes, int nrounds) __attribute__((always_inline)) {
     const uint32_t lo = lane * 16;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -206,7 +208,7 @@ __global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_
       if ((c + 1) * 1024 <= bytes || lane < 32) dma16(r, dst + c * 1024, lo + c * 1024);
     }
   };
-  auto issue = [&](int j) {  // wave 0 only
+  auto issue = [&](int j) __attribute__((always_inline)) {  // wave 0 only
     const int kb = j * KT;
     const uint32_t dst = ring_lds + (j % R) * C::SLOT;
     copy_plane(rows_desc(pk, KC, kb, kend), dst + C::OFF_K, KT * KC, C::NKD);
@@ -219,7 +221,7 @@ __global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_
     }
   };
   // wave 0: wait until tile j has landed, `later` tiles having been issued after it
-  auto wait_tile = [&](int later) {
+  auto wait_tile = [&](int later) __attribute__((always_inline)) {
     static_assert(R >= 2 && R <= 4, "ring of 2 to 4 tiles");
     if (later >= 2) wait_vm<(R >= 4 ? 2 * C::NDMA : 0)>();
     else if (later == 1) wait_vm<(R >= 3 ? C::NDMA : 0)>();
@@ -228,7 +230,7 @@ __global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_
 
   // ---- decode tile j (raw slot j % R): every thread one item of each kind, branch-free (a
   // slot past the last tile decodes stale bytes into a buffer nobody reads)
-  auto decode_ks = [&](int j, _Float16* dK, _Float16* dS) {  // item (key, 8-dim group)
+  auto decode_ks = [&](int j, _Float16* dK, _Float16* dS) __attribute__((always_inline)) {  // item (key, 8-dim group)
     const uint8_t* raw = ring + (j % R) * C::SLOT;
 #pragma unroll
     for (int rep = 0; rep < 512 / NT; ++rep) {
@@ -246,7 +248,7 @@ __global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_
       *reinterpret_cast<half8*>(dS + key * LDK + 8 * g) = sv;
     }
   };
-  auto decode_v = [&](int j, _Float16* dV, float (*dF)[KT]) {
+  auto decode_v = [&](int j, _Float16* dV, float (*dF)[KT]) __attribute__((always_inline)) {
     const uint8_t* raw = ring + (j % R) * C::SLOT;
 #pragma unroll
     for (int rep = 0; rep < 512 / NT; ++rep) {
@@ -266,7 +268,10 @@ __global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_
       const uint32_t* vnr = reinterpret_cast<const uint32_t*>(raw + C::OFF_N + 2 * C::NRM) + 2 * kp;
       const uint32_t vnw = (vnr[0] & 0xffffu) | (vnr[1] << 16);
       const half2v vn2 = __builtin_bit_cast(half2v, vnw);
-      half2v* vcol = reinterpret_cast<half2v*>(dV + (8 * dg + par) * LDV + 2 * kp);
+      // V^T column order: key 16h + 4g + e sits at position 8g + 4h + e, so the 8 keys of one
+      // P.V k-group (4g..4g+3 and 16+4g..16+4g+3) are one 16-byte run of a row
+      const int pos = 8 * ((kp >> 1) & 3) + 4 * (kp >> 3) + 2 * (kp & 1);
+      half2v* vcol = reinterpret_cast<half2v*>(dV + (8 * dg + par) * LDV + pos);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const half2v c2 = half2v{pv8[2 * e], pv8[2 * e + 1]};
@@ -291,7 +296,7 @@ __global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_
   }
 
   // ---- scores of tile j: S^T = K^ Q_rot^T (term 1) and Sign Q_proj^T (term 2)
-  auto scores = [&](const _Float16* cK, const _Float16* cS, float4v (&sacc)[2][NBW], float4v (&tacc)[2][NBW]) {
+  auto scores = [&](const _Float16* cK, const _Float16* cS, float4v (&sacc)[2][NBW], float4v (&tacc)[2][NBW]) __attribute__((always_inline)) {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
@@ -315,7 +320,7 @@ __global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_
   };
   // ---- log2-domain scores with masking, column maxima, lazy rescale (one rare branch per tile)
   auto softmax_max = [&](int j, const float (*cF)[KT], const float4v (&sacc)[2][NBW],
-                         const float4v (&tacc)[2][NBW], float (&sc)[NBW][2][4]) {
+                         const float4v (&tacc)[2][NBW], float (&sc)[NBW][2][4]) __attribute__((always_inline)) {
     const int k0 = j * KT;
     const float4v fA0 = *reinterpret_cast<const float4v*>(&cF[0][4 * lg]);
     const float4v fA1 = *reinterpret_cast<const float4v*>(&cF[0][16 + 4 * lg]);
@@ -342,6 +347,7 @@ __global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_
         }
     }
     if (edge) {  // wave-uniform: only the block's last tiles reach past the causal edge or Sk
+      asm volatile("; edge");  // a side effect keeps this a branch instead of selects on every tile
 #pragma unroll
       for (int nb = 0; nb < NBW; ++nb) {
         const int lim = a.causal ? col_i[nb] + (a.Sk - a.Sq) : a.Sk - 1;
@@ -364,6 +370,7 @@ __global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_
       grow_any = grow_any || (lmax[nb] > m_run[nb] + TAU);
     }
     if (__any(grow_any)) {
+      asm volatile("; rescale");  // a side effect: the rare rescale stays a branch, never speculated
 #pragma unroll
       for (int nb = 0; nb < NBW; ++nb) {
         float tmax = lmax[nb];
@@ -379,7 +386,7 @@ __global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_
     }
   };
   // ---- P = f16(2^(s - m)) (<= 2^TAU), row sums, O^T += V^T P^T
-  auto pv_tile = [&](const _Float16* cV, const float (&sc)[NBW][2][4]) {
+  auto pv_tile = [&](const _Float16* cV, const float (&sc)[NBW][2][4]) __attribute__((always_inline)) {
     half8 pb[NBW];
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb) {
@@ -395,11 +402,10 @@ __global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_
         }
       l_run[nb] += psum;
     }
-    // k-slots 8*lg+0..3 <-> keys 4lg+0..3, 8*lg+4..7 <-> keys 16+4lg+0..3
+    // k-slots 8*lg+0..3 <-> keys 4lg+0..3, 8*lg+4..7 <-> keys 16+4lg+0..3: positions 8lg..8lg+7
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
-      const _Float16* vrow = cV + (db * 16 + l16) * LDV + 4 * lg;
-      const half8 va = cat8h(*reinterpret_cast<const half4*>(vrow), *reinterpret_cast<const half4*>(vrow + 16));
+      const half8 va = *reinterpret_cast<const half8*>(cV + (db * 16 + l16) * LDV + 8 * lg);
 #pragma unroll
       for (int nb = 0; nb < NBW; ++nb) oacc[db][nb] = mfma16x16x32(va, pb[nb], oacc[db][nb]);
     }
@@ -419,7 +425,7 @@ __global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_
     decode_v(0, sV0, fac0);
   }
   auto iter = [&](int t, const _Float16* cK, const _Float16* cS, const _Float16* cV, const float (*cF)[KT],
-                  _Float16* nK, _Float16* nS, _Float16* nV, float (*nF)[KT]) {
+                  _Float16* nK, _Float16* nS, _Float16* nV, float (*nF)[KT]) __attribute__((always_inline)) {
     if (wave == 0 && t + 1 < nt) wait_tile(max(0, min(nt, t + R) - (t + 2)));
     __syncthreads();  // tile t decoded by all waves; raw tile t+1 landed; buffers of tile t-1 free
     if (wave == 0 && t + R < nt) issue(t + R);
