@@ -24,9 +24,11 @@
 
 // Tuning knobs: scores use SNK-key wave slabs with SR slots in flight; attention
 // uses ANB 16-key blocks per wave slab with AR slots; grids target about *_BLOCKS
-// blocks (more, shorter blocks balance the last round of blocks better).
+// blocks.  Scores run best with many short blocks (dynamic balancing of the last
+// round); attention with one round of resident blocks (4 per CU at 128 VGPRs and
+// a 2-slot ring: 1024 on 256 CUs).
 #ifndef TQ_DEC_ATTN_BLOCKS
-#define TQ_DEC_ATTN_BLOCKS 768
+#define TQ_DEC_ATTN_BLOCKS 1024
 #endif
 #ifndef TQ_DEC_SCORE_BLOCKS
 #define TQ_DEC_SCORE_BLOCKS 4096
@@ -35,7 +37,7 @@
 #define TQ_DEC_ANB 2
 #endif
 #ifndef TQ_DEC_AR
-#define TQ_DEC_AR 3
+#define TQ_DEC_AR 2
 #endif
 #ifndef TQ_DEC_PLO
 #define TQ_DEC_PLO 0
@@ -48,7 +50,7 @@
 #endif
 // minimum waves per SIMD the attention kernel's register budget must allow (0: compiler's choice)
 #ifndef TQ_DEC_AWPE
-#define TQ_DEC_AWPE 0
+#define TQ_DEC_AWPE 4
 #endif
 #if TQ_DEC_AWPE > 0
 #define TQ_DEC_ATTN_ATTR __attribute__((amdgpu_waves_per_eu(TQ_DEC_AWPE)))
