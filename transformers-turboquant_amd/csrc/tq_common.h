@@ -26,6 +26,19 @@ inline int64_t out_cols(int64_t d, int b) { return (d * b + 7) / 8; }
 
 inline bool supported_dim(int d) { return d == 32 || d == 64 || d == 128 || d == 256; }
 
+// Blocks of `kernel` (launched with `threads` threads) resident on the whole current
+// device at once: occupancy per CU x CU count, cached per device in `cache[16]`.
+inline int resident_blocks(const void* kernel, int threads, int* cache) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) dev = 0;
+  if (cache[dev] > 0) return cache[dev];
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess || per_cu < 1) per_cu = 1;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 1;
+  cache[dev] = per_cu * cus;
+  return cache[dev];
+}
+
 // ---------------------------------------------------------------- vector types
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));

@@ -981,17 +981,6 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
 }
 
 // Blocks of `kernel` the device holds at once (occupancy x compute units), per device.
-static int resident_blocks(const void* kernel, int threads, int* cache) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) dev = 0;
-  if (cache[dev] > 0) return cache[dev];
-  int per_cu = 0, cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess || per_cu < 1) per_cu = 1;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 1;
-  cache[dev] = per_cu * cus;
-  return cache[dev];
-}
-
 template <int D, int DT, int MODE, int BB>
 static void launch_tile(const TileArgs& a, hipStream_t s) {
   static int cache[16] = {};

@@ -26,9 +26,9 @@
 // uses ANB 16-key blocks per wave slab with AR slots; grids target about *_BLOCKS
 // blocks.  Scores run best with many short blocks (dynamic balancing of the last
 // round); attention with one round of resident blocks (4 per CU at 128 VGPRs and
-// a 2-slot ring: 1024 on 256 CUs).
+// a 2-slot ring: 1024 on 256 CUs), which TQ_DEC_ATTN_BLOCKS = 0 asks the device for.
 #ifndef TQ_DEC_ATTN_BLOCKS
-#define TQ_DEC_ATTN_BLOCKS 1024
+#define TQ_DEC_ATTN_BLOCKS 0  // 0: the device's resident blocks (one round)
 #endif
 #ifndef TQ_DEC_SCORE_BLOCKS
 #define TQ_DEC_SCORE_BLOCKS 4096
@@ -793,10 +793,20 @@ static bool decode_shape(int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
   return (Hq / Hkv) * Sq <= 16 && Sk >= 1 && Sk < (1 << 24);
 }
 
+// grid target of the fused decode attention: one round of resident blocks
+static int attn_target_blocks(int bits) {
+  if (TQ_DEC_ATTN_BLOCKS > 0) return TQ_DEC_ATTN_BLOCKS;
+  static int cache[3][16] = {};
+  const void* k = bits == 2 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 2, TQ_DEC_ANB, TQ_DEC_AR, TQ_DEC_PLO != 0>)
+                : bits == 3 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 3, TQ_DEC_ANB, TQ_DEC_AR, TQ_DEC_PLO != 0>)
+                            : reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 4, TQ_DEC_ANB, TQ_DEC_AR, TQ_DEC_PLO != 0>);
+  return resident_blocks(k, 256, cache[bits - 2]);
+}
+
 static DecodePlan plan_decode(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
   if (!decode_shape(Hq, Hkv, Sq, Sk, d, bits)) return DecodePlan{false, 0, 0, 0};
   constexpr int slab = 64 * TQ_DEC_ANB;
-  DecodePlan p = plan_split(B, Hkv, Sk, TQ_DEC_ATTN_BLOCKS, slab, 2 * slab);
+  DecodePlan p = plan_split(B, Hkv, Sk, attn_target_blocks(bits), slab, 2 * slab);
   const int C = (Hq / Hkv) * Sq;
   p.ws_bytes = static_cast<int64_t>(B) * Hkv * p.nsplit * C * static_cast<int64_t>(d + 2) * 4;
   return p;
