@@ -170,12 +170,12 @@ __global__ void __launch_bounds__(256) compress_keys_kernel(KeyArgs a) {
     const int r = threadIdx.x / T::TPR;
     const float vn = sqrtf(ss);
     if (threadIdx.x % T::TPR == 0) s_vn[r] = vn;
-    const float den = vn + 1e-8f;
+    const DivBy div(vn + 1e-8f);
     constexpr int PER = D / T::TPR;
     const int part = threadIdx.x % T::TPR;
     for (int i = 0; i < PER; ++i) {
       const int c = part * PER + i;
-      Bm[r * T::LDA + c] = A[r * T::LDA + c] / den;
+      Bm[r * T::LDA + c] = div(A[r * T::LDA + c]);
     }
   }
   __syncthreads();
@@ -308,11 +308,11 @@ __global__ void __launch_bounds__(256) compress_values_kernel(ValArgs a) {
     const float vn = sqrtf(ss);
     const int64_t gr = row0 + r;
     if (threadIdx.x % T::TPR == 0 && gr < a.n) a.vn[gr] = f2h(vn);
-    const float den = vn + 1e-8f;
+    const DivBy div(vn + 1e-8f);
     constexpr int PER = D / T::TPR;
     const int part = threadIdx.x % T::TPR;
     __syncthreads();
-    for (int i = 0; i < PER; ++i) A[r * T::LDA + part * PER + i] /= den;
+    for (int i = 0; i < PER; ++i) A[r * T::LDA + part * PER + i] = div(A[r * T::LDA + part * PER + i]);
   }
   __syncthreads();
   float4v acc[T::TPW];
@@ -857,10 +857,11 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) ss = fmaf(xv[ks][j], xv[ks][j], ss);
       const float vn = sqrtf(row_sum(ss));
+      const DivBy div(vn + 1e-8f);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) xv[ks][j] = xv[ks][j] / (vn + 1e-8f);
+        for (int j = 0; j < 8; ++j) xv[ks][j] = div(xv[ks][j]);
       split_row(xv, kSplit, bh, bl);
       // ---- y = xn Pi^T (compressors.py:276); codes = searchsorted-left, packed LSB first
       row_gemm<D, true, true>(P0, P1, bh, bl, acc, l16, g);
@@ -899,10 +900,11 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
           for (int j = 0; j < 8; ++j) ss = fmaf(xv[ks][j], xv[ks][j], ss);
         const float vn = sqrtf(row_sum(ss));
         vns[i] = vn;
+        const DivBy div(vn + 1e-8f);
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-          for (int j = 0; j < 8; ++j) xv[ks][j] = xv[ks][j] / (vn + 1e-8f);
+          for (int j = 0; j < 8; ++j) xv[ks][j] = div(xv[ks][j]);
         split_row(xv, kSplit, bh, bl);
         row_gemm<D, true, true>(P0, P1, bh, bl, acc, l16, g);
         if (t < ntiles) {
