@@ -20,6 +20,7 @@
 //   operand; the accumulator layout (4 consecutive output columns of one row per
 //   lane) is written straight back into the row tile.
 #include "tq_common.h"
+#include "tq_stream.h"
 
 namespace tq {
 
@@ -539,14 +540,30 @@ template <int D>
 __device__ __forceinline__ int swz(int p, int c) {
   return D == 128 ? (c ^ (p & 15)) : (c ^ ((p >> 1) & 7));
 }
-template <int D, int NT>
-__device__ __forceinline__ void load_plane(_Float16* __restrict__ dst, const uint16_t* __restrict__ src) {
-  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-  for (int q = threadIdx.x; q < D * D / 8; q += NT) {
-    const int p = q / (D / 8), c = q % (D / 8);
-    const u32x4 v = *reinterpret_cast<const u32x4*>(src + perm_row(p) * D + c * 8);
-    *reinterpret_cast<u32x4*>(dst + p * D + swz<D>(p, c) * 8) = v;
-  }
+// Copy NP weight planes src[0 .. NP*D*D) (split (hi, lo) pairs: NP = 2) into dst0 (and
+// dst1) in the permuted, swizzled layout with direct-to-LDS buffer loads: LDS chunk L of a
+// plane (row p = L / (D/8), swizzled chunk L % (D/8)) receives source chunk swz(p, .) of
+// weight row perm_row(p) (swz is an involution).  Every copy is in flight at once and
+// holds no registers; the caller waits with wait_vm<0>() and a block barrier.
+template <int D, int NT, int NP = 2>
+__device__ __forceinline__ void load_planes(_Float16* dst0, _Float16* dst1, const uint16_t* src) {
+  constexpr int CH = D * D / 8;  // 16-byte chunks per plane
+  static_assert(CH % NT == 0 && NT % 64 == 0, "whole 64-chunk rounds per wave");
+  const uint64_t base = reinterpret_cast<uint64_t>(src);
+  const i32x4 desc{static_cast<int>(static_cast<uint32_t>(base)), static_cast<int>(static_cast<uint32_t>(base >> 32) & 0xffffu),
+                   NP * D * D * 2, 0x00020000};
+  int t = static_cast<int>(threadIdx.x);
+  asm volatile("" : "+v"(t));  // recomputed per call: hoisted offsets would hold VGPRs across the tile loop
+  const int w0 = t & ~63;
+#pragma unroll
+  for (int pl = 0; pl < NP; ++pl)
+#pragma unroll
+    for (int i = 0; i < CH / NT; ++i) {
+      const int L = i * NT + t, p = L / (D / 8);
+      const int c = swz<D>(p, L % (D / 8));
+      const uint32_t voff = static_cast<uint32_t>((pl * D * D + perm_row(p) * D + c * 8) * 2);
+      dma16_cached(desc, lds_offset(pl ? dst1 : dst0) + (i * NT + w0) * 16, voff);
+    }
 }
 
 // acc[mb] (output columns 32*(mb>>1) + 8g + 4*(mb&1) + e of row l16) = W . X^T for this
@@ -790,10 +807,10 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
   Raw raw, nxt;
 
   if constexpr (MODE == TM_QUERY) {
-    load_plane<D, T::NT>(P0, a.w1);
-    load_plane<D, T::NT>(P1, a.w1 + D * D);
-    load_plane<D, T::NT>(P2, a.w2);
+    load_planes<D, T::NT>(P0, P1, a.w1);
+    load_planes<D, T::NT, 1>(P2, P2, a.w2);
     fetch_row(gw, raw);
+    wait_vm<0>();
     __syncthreads();
     for (int64_t t = gw; t < ntiles; t += nwaves) {
       const int64_t gr = t * 16 + l16;
@@ -842,9 +859,9 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
       raw = nxt;
     }
   } else if constexpr (MODE == TM_VALUES) {
-    load_plane<D, T::NT>(P0, a.w1);
-    load_plane<D, T::NT>(P1, a.w1 + D * D);
+    load_planes<D, T::NT>(P0, P1, a.w1);
     fetch_row(gw, raw);
+    wait_vm<0>();
     __syncthreads();
     for (int64_t t = gw; t < ntiles; t += nwaves) {
       const int64_t gr = t * 16 + l16;
@@ -875,13 +892,12 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
     }
   } else {
     // keys: S stays in P2/P3; P0/P1 hold Pi for phase A and Pi^T for phase B of each chunk
-    load_plane<D, T::NT>(P2, a.w3);
-    load_plane<D, T::NT>(P3, a.w3 + D * D);
+    load_planes<D, T::NT>(P2, P3, a.w3);
     const int64_t per_wave = (ntiles + nwaves - 1) / nwaves;  // tiles of the busiest wave
     for (int64_t c0 = 0; c0 < per_wave; c0 += kKeyTiles) {
       __syncthreads();  // the previous chunk's phase B is done with P0/P1
-      load_plane<D, T::NT>(P0, a.w1);
-      load_plane<D, T::NT>(P1, a.w1 + D * D);
+      load_planes<D, T::NT>(P0, P1, a.w1);
+      wait_vm<0>();  // this wave's plane copies have landed
       __syncthreads();
       // ---- phase A: vn, y = xn Pi^T, codes   (compressors.py:108-116)
       uint32_t cws[kKeyTiles][KS];
@@ -917,8 +933,8 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
         raw = nxt;
       }
       __syncthreads();  // every wave is done with Pi
-      load_plane<D, T::NT>(P0, a.w2);
-      load_plane<D, T::NT>(P1, a.w2 + D * D);
+      load_planes<D, T::NT>(P0, P1, a.w2);
+      wait_vm<0>();
       __syncthreads();
       // ---- phase B: k_mse = (yhat Pi) vn, r = x - k_mse, rn, proj = r S^T, signs   (compressors.py:120-136)
       fetch_row(gw + c0 * nwaves, raw);
@@ -979,6 +995,7 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
         raw = nxt;
       }
     }
+    wait_vm<0>();  // no plane copy outlives the block, even with no tile to process
   }
 }
 

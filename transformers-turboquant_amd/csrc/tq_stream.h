@@ -94,6 +94,11 @@ __device__ __forceinline__ void dma16(i32x4 r, uint32_t lds, uint32_t voff) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
                :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(uniform4(r)) : "memory", "m0");
 }
+// the same copy without the non-temporal hint, for data that many blocks re-read (weights)
+__device__ __forceinline__ void dma16_cached(i32x4 r, uint32_t lds, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(uniform4(r)) : "memory", "m0");
+}
 __device__ __forceinline__ void dma_u16(i32x4 r, uint32_t lds, uint32_t voff) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_ushort %1, %2, 0 offen nt lds"
                :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(uniform4(r)) : "memory", "m0");
