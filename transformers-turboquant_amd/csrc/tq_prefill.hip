@@ -9,7 +9,8 @@
 //    direct-to-LDS buffer loads issued R-1 tiles ahead (no register staging).
 //  * Each tile is decoded once per block into f16 tiles: K^ = Ck[codes] and
 //    the +-1 sign tile as [key][dim] rows, and V^T = Cv[codes] as [dim][key]
-//    rows, V^ = f16(Cv[code] * vn) with the value norm applied by a packed f16
+//    rows (dims permuted so that the epilogue's Pi_v^T fragments are 16-byte runs),
+//    V^ = f16(Cv[code] * vn) with the value norm applied by a packed f16
 //    multiply of each (key, key+1) dword.  Decoding uses small
 //    LDS tables indexed by nibbles / bit fields (conflict-free for <= 32
 //    entries); the value table is indexed by the codes of two keys at one dim,
@@ -87,10 +88,6 @@ struct PfCfg {
 __device__ __forceinline__ uint32_t field32(const uint8_t* row, int off) {
   const uint32_t* w = reinterpret_cast<const uint32_t*>(row + (off & ~3));
   return __builtin_amdgcn_alignbyte(w[1], w[0], off & 3);
-}
-
-__device__ __forceinline__ half8 cat8h(half4 a, half4 b) {
-  return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
 // odd VB-bit fields of 8 consecutive fields
@@ -271,11 +268,15 @@ __global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_
       // V^T column order: key 16h + 4g + e sits at position 8g + 4h + e, so the 8 keys of one
       // P.V k-group (4g..4g+3 and 16+4g..16+4g+3) are one 16-byte run of a row
       const int pos = 8 * ((kp >> 1) & 3) + 4 * (kp >> 3) + 2 * (kp & 1);
-      half2v* vcol = reinterpret_cast<half2v*>(dV + (8 * dg + par) * LDV + pos);
+      // V^T row order: dim 32c + 8g + 4h + e sits in row 16(2c + h) + 4g + e, so that lane group g
+      // of O^T blocks 2c, 2c+1 holds dims 32c + 8g + 0..7 (one 16-byte run of a Pi_v^T row in the
+      // epilogue); this item's dims 8dg + par + 2e land in rows vrow + {0, 2, 16, 18}
+      const int vrow = 32 * (dg >> 2) + 4 * (dg & 3) + par;
+      half2v* vcol = reinterpret_cast<half2v*>(dV + vrow * LDV + pos);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const half2v c2 = half2v{pv8[2 * e], pv8[2 * e + 1]};
-        vcol[(2 * e) * (LDV / 2)] = c2 * vn2;
+        vcol[(16 * (e >> 1) + 2 * (e & 1)) * (LDV / 2)] = c2 * vn2;
       }
     }
     {  // per-key score factors from the key norm planes; threads past them write row 2 (unused)
@@ -451,9 +452,11 @@ __global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_
     if (t + 1 < nt) iter(t + 1, sK1, sS1, sV1, fac1, sK0, sS0, sV0, fac0);
   }
 
-  // ---- normalise and rotate back: out = (O^T / l)^T Pi_v, Pi_v^T as split-f16 A operand
-  const half4* Ph = reinterpret_cast<const half4*>(a.vpit);
-  const half4* Pl = reinterpret_cast<const half4*>(a.vpit + D * D);
+  // ---- normalise and rotate back: out = (O^T / l)^T Pi_v, Pi_v^T as split-f16 A operand.
+  // Lane group g of O^T blocks 2c, 2c+1 holds dims 32c + 8g + 0..7 (the V^T row order), so
+  // each A fragment is one 16-byte run of a Pi_v^T row, read once for both column blocks.
+  half8 oh[DB / 2][NBW], ol[DB / 2][NBW];  // split (hi, lo) B operands
+  float down[NBW];
 #pragma unroll
   for (int nb = 0; nb < NBW; ++nb) {
     float l = l_run[nb];
@@ -471,38 +474,45 @@ __global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     int ex;
     frexpf(mx, &ex);
-    const float up = ldexpf(kSplit, -ex), down = ldexpf(kUnsplit2, ex);
-    half8 bh[DB / 2], bl[DB / 2];
+    const float up = ldexpf(kSplit, -ex);
+    down[nb] = ldexpf(kUnsplit2, ex);
 #pragma unroll
     for (int c = 0; c < DB / 2; ++c)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         _Float16 h, lo;
         split_f16(oacc[2 * c][nb][e] * up, h, lo);
-        bh[c][e] = h;
-        bl[c][e] = lo;
+        oh[c][nb][e] = h;
+        ol[c][nb][e] = lo;
         split_f16(oacc[2 * c + 1][nb][e] * up, h, lo);
-        bh[c][4 + e] = h;
-        bl[c][4 + e] = lo;
+        oh[c][nb][4 + e] = h;
+        ol[c][nb][4 + e] = lo;
       }
-    const int qi = col_i[nb], h = col_h[nb];
-#pragma unroll 1
-    for (int ib = 0; ib < DB; ++ib) {
+  }
+  const _Float16* Ph = reinterpret_cast<const _Float16*>(a.vpit);
+  const _Float16* Pl = Ph + D * D;
+#pragma unroll 2
+  for (int ib = 0; ib < DB; ++ib) {
+    const int i = ib * 16 + l16;
+    half8 ah[DB / 2], al[DB / 2];
+#pragma unroll
+    for (int c = 0; c < DB / 2; ++c) {
+      ah[c] = *reinterpret_cast<const half8*>(Ph + i * D + c * 32 + lg * 8);
+      al[c] = *reinterpret_cast<const half8*>(Pl + i * D + c * 32 + lg * 8);
+    }
+#pragma unroll
+    for (int nb = 0; nb < NBW; ++nb) {
       float4v f = float4v{0.f, 0.f, 0.f, 0.f};
-      const int i = ib * 16 + l16;
 #pragma unroll
       for (int c = 0; c < DB / 2; ++c) {
-        const int j0 = c * 32 + lg * 4;
-        const half8 ah = cat8h(Ph[(i * D + j0) / 4], Ph[(i * D + j0 + 16) / 4]);
-        const half8 al = cat8h(Pl[(i * D + j0) / 4], Pl[(i * D + j0 + 16) / 4]);
-        f = mfma16x16x32(ah, bh[c], f);
-        f = mfma16x16x32(al, bh[c], f);
-        f = mfma16x16x32(ah, bl[c], f);
+        f = mfma16x16x32(ah[c], oh[c][nb], f);
+        f = mfma16x16x32(al[c], oh[c][nb], f);
+        f = mfma16x16x32(ah[c], ol[c][nb], f);
       }
       if (col_ok[nb]) {
-        const int64_t o = static_cast<int64_t>(b) * a.sob + static_cast<int64_t>(h) * a.soh +
-                          static_cast<int64_t>(qi) * a.sos + ib * 16 + lg * 4;
-        const float4v fo = f * down;
+        const int64_t o = static_cast<int64_t>(b) * a.sob + static_cast<int64_t>(col_h[nb]) * a.soh +
+                          static_cast<int64_t>(col_i[nb]) * a.sos + ib * 16 + lg * 4;
+        const float4v fo = f * down[nb];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           if (a.out_dtype == TQ_BF16) store_act<TQ_BF16>(a.out, o + e, fo[e]);
