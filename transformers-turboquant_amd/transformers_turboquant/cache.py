@@ -112,7 +112,8 @@ class TurboQuantCacheLayer(CacheLayerMixin):
         for name in _KEY_PLANES:
             src = ck[name]
             self.kp[name][:, :, lo:hi] = src.reshape(B, H, S, *src.shape[1:]) if src.dim() == 2 else src.reshape(B, H, S)
-        self.vp["packed_indices"][:, :, lo:hi] = cv["packed_indices"].reshape(B, H, S, -1)
+        vi = cv["packed_indices"]
+        self.vp["packed_indices"][:, :, lo:hi] = vi.reshape(B, H, S, vi.shape[-1])
         self.vp["vec_norms"][:, :, lo:hi] = cv["vec_norms"].reshape(B, H, S)
         self.length = need
         return self.strided()
@@ -134,10 +135,13 @@ class TurboQuantCacheLayer(CacheLayerMixin):
         B, H, D = self.shape
         L, n = self.length, self.shape[0] * self.shape[1] * self.length
         k = {name: self.kp[name][:, :, :L].contiguous() for name in _KEY_PLANES}
-        ck = {"packed_key_indices": k["packed_key_indices"].reshape(n, -1),
-              "packed_qjl_signs": k["packed_qjl_signs"].reshape(n, -1),
+        # explicit row widths: an empty cache (L = 0) has nothing for -1 to infer from
+        kw, sw = k["packed_key_indices"].shape[-1], k["packed_qjl_signs"].shape[-1]
+        vw = self.vp["packed_indices"].shape[-1]
+        ck = {"packed_key_indices": k["packed_key_indices"].reshape(n, kw),
+              "packed_qjl_signs": k["packed_qjl_signs"].reshape(n, sw),
               "residual_norm": k["residual_norm"], "vec_norms": k["vec_norms"], "shape": (B, H, L, D)}
-        cv = {"packed_indices": self.vp["packed_indices"][:, :, :L].contiguous().reshape(n, -1),
+        cv = {"packed_indices": self.vp["packed_indices"][:, :, :L].contiguous().reshape(n, vw),
               "vec_norms": self.vp["vec_norms"][:, :, :L].contiguous().reshape(n), "shape": (B, H, L, D)}
         return ck, cv
 
@@ -162,9 +166,10 @@ class TurboQuantCacheLayer(CacheLayerMixin):
         n = B * H * S
         for name in _KEY_PLANES:
             src = keys[name]
-            self.kp[name][:, :, :S] = src.reshape(B, H, S, -1) if src.dim() == 2 and src.shape[0] == n else \
-                src.reshape(B, H, S)
-        self.vp["packed_indices"][:, :, :S] = values["packed_indices"].reshape(B, H, S, -1)
+            self.kp[name][:, :, :S] = src.reshape(B, H, S, src.shape[-1]) if src.dim() == 2 and src.shape[0] == n \
+                else src.reshape(B, H, S)
+        vi = values["packed_indices"]
+        self.vp["packed_indices"][:, :, :S] = vi.reshape(B, H, S, vi.shape[-1])
         self.vp["vec_norms"][:, :, :S] = values["vec_norms"].reshape(B, H, S)
         self.length = S
 

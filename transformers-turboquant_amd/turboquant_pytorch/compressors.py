@@ -252,7 +252,8 @@ class TurboQuantCompressorMSE:
         B, H, S, D = compressed["shape"]
         n = B * H * S
         if "packed_indices" in compressed:
-            codes = compressed["packed_indices"].reshape(n, -1).contiguous()
+            packed = compressed["packed_indices"]
+            codes = packed.reshape(n, packed.shape[-1]).contiguous()  # explicit width: n may be 0
             if codes.device.type != "cuda":
                 raise ValueError("packed value planes live on the GPU")
             t = _tables(self, codes.device, with_qjl=False)
