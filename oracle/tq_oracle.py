@@ -13,7 +13,8 @@ Floating-point conventions: float32 arithmetic where the reference computes in
 float32 (so the decision inputs -- rotated coordinates y and projections -- are
 f32 BLAS results comparable to the reference's), float64 for the scoring and
 attention estimators so they serve as ground truth for the f32-accumulating
-kernels.  Pinning of every function is listed in DESIGN.md.
+kernels.  Every function is pinned by tests/test_oracle_pins.py, tests/test_setup_pins.py
+and the reference vectors under tests/golden/ (known answers, invariants, brute force).
 """
 
 from __future__ import annotations
