@@ -52,3 +52,11 @@ def test_argument_validation_without_gpu():
     with pytest.raises(RuntimeError, match="group size|multiple"):
         _native.check(lib.tq_attention_scores(*([None] * 7), 1, 6, 4, 1, 1, 128, 3, 0.0, None, None),
                       "scores")
+
+
+def test_missing_library_fails_loudly(monkeypatch):
+    """With the shared library absent the GPU path raises; nothing falls back to the CPU."""
+    monkeypatch.setattr(_native, "_LIB_PATH", os.path.join(ROOT, "no_such_dir", "libtq_amd.so"))
+    monkeypatch.setattr(_native, "_lib", None)
+    with pytest.raises(RuntimeError, match="not built"):
+        _native.lib()
