@@ -46,10 +46,12 @@ enum tq_status {
   TQ_EHIP = -3         /* HIP runtime error at launch */
 };
 
-/* Library version (major*10000 + minor*100 + patch). */
+/* Library version (major*10000 + minor*100 + patch).  Utility; no counterpart in the
+ * reference (a Python package). */
 int tq_version(void);
 
-/* Message for the most recent failing call on this thread ("" if none). */
+/* Message for the most recent failing call on this thread ("" if none).  Utility: the
+ * reference raises Python exceptions; the bindings turn this message into one. */
 const char* tq_last_error(void);
 
 /* Bytes needed for d codes of b bits: ceil(d*b/8).
