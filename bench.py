@@ -250,9 +250,9 @@ def decode_legs(kc, vc, outliers, steps: int, warmup: int) -> tuple[dict, dict]:
         "ms_per_launch": ms_scores,
         "key_heads_per_s": key_heads / (ms_scores * 1e-3),
         "roofline": {
-            "kernel": "tq::decode_scores_kernel<128, 3, 2, 64> (scores, f32 written)",
+            "kernel": "tq::decode_scores_kernel<128, 3, 3, 32> (scores, f32 written)",
             "bound": "hbm", "achieved": gbs_s, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": gbs_s / HBM_PEAK_GBS, "traffic": measured_traffic("tq::decode_scores_kernel<128, 3, 2, 64>"),
+            "frac": gbs_s / HBM_PEAK_GBS, "traffic": measured_traffic("tq::decode_scores_kernel<128, 3, 3, 32>"),
             "algorithmic_bytes_per_launch": score_bytes,
         },
     }

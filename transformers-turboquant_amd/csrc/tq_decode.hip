@@ -22,7 +22,8 @@
 #include "tq_common.h"
 #include "tq_stream.h"
 
-// Tuning knobs: scores use SNK-key wave slabs with SR slots in flight; attention
+// Tuning knobs: scores use wave slabs of score_slab_keys(bits) keys with
+// score_ring(bits) slots in flight; attention
 // uses ANB 16-key blocks per wave slab with AR slots; grids target about *_BLOCKS
 // blocks.  Scores run best with many short blocks (dynamic balancing of the last
 // round); attention with one round of resident blocks (4 per CU at 128 VGPRs and
@@ -42,12 +43,25 @@
 #ifndef TQ_DEC_PLO
 #define TQ_DEC_PLO 0
 #endif
-#ifndef TQ_DEC_SR
-#define TQ_DEC_SR 2
+// Scores slab shape per width (TQ_DEC_SR / TQ_DEC_SNK override it for every width):
+// 32-key wave slabs in a 3-slot ring at bits 3-4 (22 KB of LDS, 6 blocks per CU),
+// 64-key slabs in 2 slots at bits 2, where the shorter slabs' per-slab overhead is a
+// larger share of the lighter decode.  Measured at 16 x 32k keys: bits 3 56.3 vs
+// 57.8 us, bits 4 68.2 vs 69.1 us, bits 2 48.0 vs 46.5 us for 32/3 against 64/2.
+constexpr int score_ring(int bits) {
+#ifdef TQ_DEC_SR
+  return (void)bits, TQ_DEC_SR;
+#else
+  return bits == 2 ? 2 : 3;
 #endif
-#ifndef TQ_DEC_SNK
-#define TQ_DEC_SNK 64
+}
+constexpr int score_slab_keys(int bits) {
+#ifdef TQ_DEC_SNK
+  return (void)bits, TQ_DEC_SNK;
+#else
+  return bits == 2 ? 64 : 32;
 #endif
+}
 // minimum waves per SIMD the attention kernel's register budget must allow (0: compiler's choice)
 #ifndef TQ_DEC_AWPE
 #define TQ_DEC_AWPE 4
@@ -814,7 +828,7 @@ static DecodePlan plan_decode(int B, int Hq, int Hkv, int Sq, int Sk, int d, int
 
 static DecodePlan plan_scores(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
   if (!decode_shape(Hq, Hkv, Sq, Sk, d, bits)) return DecodePlan{false, 0, 0, 0};
-  constexpr int slab = 4 * TQ_DEC_SNK;
+  const int slab = 4 * score_slab_keys(bits);
   return plan_split(B, Hkv, Sk, TQ_DEC_SCORE_BLOCKS, slab, 2 * slab);
 }
 
@@ -867,9 +881,9 @@ int decode_scores(int64_t ldk, const uint16_t* q_rot, const uint16_t* q_proj, co
   a.scale = 1.f;
   a.scores = out;
   dim3 grid(a.nsplit, a.Hkv, a.B);
-  if (bits == 2) decode_scores_kernel<128, 2, TQ_DEC_SR, TQ_DEC_SNK><<<grid, 256, 0, s>>>(a);
-  else if (bits == 3) decode_scores_kernel<128, 3, TQ_DEC_SR, TQ_DEC_SNK><<<grid, 256, 0, s>>>(a);
-  else decode_scores_kernel<128, 4, TQ_DEC_SR, TQ_DEC_SNK><<<grid, 256, 0, s>>>(a);
+  if (bits == 2) decode_scores_kernel<128, 2, score_ring(2), score_slab_keys(2)><<<grid, 256, 0, s>>>(a);
+  else if (bits == 3) decode_scores_kernel<128, 3, score_ring(3), score_slab_keys(3)><<<grid, 256, 0, s>>>(a);
+  else decode_scores_kernel<128, 4, score_ring(4), score_slab_keys(4)><<<grid, 256, 0, s>>>(a);
   return launch_status("tq_attention_scores (decode)");
 }
 
