@@ -94,6 +94,31 @@ struct DecodeArgs {
 };
 
 
+// odd VB-bit fields of 8 consecutive fields
+template <int VB>
+constexpr uint32_t odd_fields() {
+  return VB == 2 ? 0xCCCCu : (VB == 3 ? 0xE38E38u : 0xF0F0F0F0u);
+}
+
+// Pair-table entry I (two f16 values) of a value word whose fields are VB bits each, LSB
+// first: the fields nib4x2 (VB 2), six4x2 (VB 3) and byte4x2 (VB 4) read as entry I
+template <int VB, int I>
+__device__ __forceinline__ uint32_t value_pair(const uint8_t* t, uint32_t w) {
+  static_assert(I >= 0 && I < 4, "four pair fields per word");
+  if constexpr (VB == 2) {
+    constexpr uint32_t m = 0x3Cu;
+    return lds32(t, and_byte<I / 2>(m, (I & 1) ? (w >> 2) : (w << 2)));
+  } else if constexpr (VB == 3) {
+    constexpr uint32_t m = 0xFCu;
+    if constexpr (I == 0) return lds32(t, and_byte<0>(m, w << 2));
+    else if constexpr (I == 1) return lds32(t, and_byte<0>(m, w >> 4));
+    else if constexpr (I == 2) return lds32(t, and_byte<1>(m, w >> 2));
+    else return lds32(t, and_byte<2>(m, w));
+  } else {
+    return lds32(t, byte_x4<I>(w));
+  }
+}
+
 // ---------------------------------------------------------------- small tables
 // Lookup tables of at most 32 dwords give every entry its own LDS bank, so the
 // data-dependent lookups of a wave never conflict (64-entry tables share a bank
@@ -163,13 +188,6 @@ __device__ __forceinline__ half8 key_operand(const uint8_t* t, const uint32_t (&
     const uint32_t hi32 = (wi + 1 < KW32) ? k[wi + 1] : 0u;
     return six4x2(t, sh ? __builtin_amdgcn_alignbit(hi32, lo32, sh) : lo32);
   }
-}
-// Value operand: the 8 dims of one value field (VB bits each, LSB first)
-template <int VB>
-__device__ __forceinline__ half8 value_operand(const uint8_t* t, uint32_t w) {
-  if constexpr (VB == 2) return nib4x2<0>(t, w);
-  else if constexpr (VB == 3) return six4x2(t, w);
-  else return byte4x2(t, w);
 }
 
 // Fused decode attention, LDS-staged.  Each wave streams 64-key slabs of the key
@@ -369,36 +387,57 @@ __global__ void __launch_bounds__(256) TQ_DEC_ATTN_ATTR decode_attn_lds_kernel(D
       }
     }
     const float m_use = (m_run == -INFINITY) ? 0.f : m_run + TAU;
-    // ---- values: O^T += V^T (P * vn)^T per block
+    // ---- values: O^T += V^T (P * vn)^T, two 16-key blocks per 16x16x32 MFMA.  K-slot
+    // 8lg + 4h + e of block pair jp is key 16(2jp + h) + 4lg + e: the B operand is the lane's
+    // own P values of both blocks, and each A dword is one dim of a key pair (2c, 2c + 1),
+    // read from the pair table after interleaving the two keys' code fields
+    constexpr uint32_t M = odd_fields<VB>();
 #pragma unroll
-    for (int j = 0; j < NBS; ++j) {
-      const float4v nv = *reinterpret_cast<const float4v*>(&fw[2][16 * j + 4 * lg]);
-      half4 ph, pl;
+    for (int jp = 0; jp < NBS / 2; ++jp) {
+      half8 pb, plo;
+      uint32_t w[2][4];  // value fields of keys 16(2jp + h) + 4lg + kk
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float p = __builtin_amdgcn_exp2f(sc[j][e] - m_use);
-        l_run += p;
-        const float pvv = p * nv[e];
-        const _Float16 hh = static_cast<_Float16>(pvv);
-        ph[e] = hh;
-        if constexpr (PLO) pl[e] = static_cast<_Float16>(pvv - static_cast<float>(hh));
+      for (int h = 0; h < 2; ++h) {
+        const int j = 2 * jp + h;
+        const float4v nv = *reinterpret_cast<const float4v*>(&fw[2][16 * j + 4 * lg]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float p = __builtin_amdgcn_exp2f(sc[j][e] - m_use);
+          l_run += p;
+          const float pvv = p * nv[e];
+          const _Float16 hh = static_cast<_Float16>(pvv);
+          pb[4 * h + e] = hh;
+          if constexpr (PLO) plo[4 * h + e] = static_cast<_Float16>(pvv - static_cast<float>(hh));
+        }
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const uint32_t* vp = reinterpret_cast<const uint32_t*>(src + OFF_V + (16 * j + 4 * lg + kk) * VC + vbase);
+          if constexpr (VW32 == 2)
+            w[h][kk] = __builtin_amdgcn_alignbyte(vp[1], vp[0], vbyte);
+          else
+            w[h][kk] = vp[0] >> (8 * vbyte);
+        }
       }
-      half8 vals[4];
+      // parity 0: even dims (fields of key 2c, fields of key 2c + 1 shifted into the odd slots);
+      // parity 1: odd dims.  Pair field i of a merged word is dim 2i + parity of the key pair.
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const uint32_t* vp = reinterpret_cast<const uint32_t*>(src + OFF_V + (16 * j + 4 * lg + kk) * VC + vbase);
-        uint32_t w;
-        if constexpr (VW32 == 2)
-          w = __builtin_amdgcn_alignbyte(vp[1], vp[0], vbyte);
-        else
-          w = vp[0] >> (8 * vbyte);
-        vals[kk] = value_operand<VB>(tV, w);
-      }
+      for (int par = 0; par < 2; ++par) {
+        uint32_t f[2][2];
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const half4 va = half4{vals[0][db], vals[1][db], vals[2][db], vals[3][db]};
-        oacc[db] = mfma16x16x16(va, ph, oacc[db]);
-        if constexpr (PLO) oacc[db] = mfma16x16x16(va, pl, oacc[db]);
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            const uint32_t wa = w[h][2 * c], wb = w[h][2 * c + 1];
+            f[h][c] = par ? ((wb & M) | ((wa >> VB) & ~M)) : (((wb << VB) & M) | (wa & ~M));
+          }
+        static_for<4>([&](auto ic) {
+          constexpr int i = decltype(ic)::value;
+          const int db = 2 * i + par;
+          const half8 va = __builtin_bit_cast(half8, u32x4{value_pair<VB, i>(tV, f[0][0]), value_pair<VB, i>(tV, f[0][1]),
+                                                           value_pair<VB, i>(tV, f[1][0]), value_pair<VB, i>(tV, f[1][1])});
+          oacc[db] = mfma16x16x32(va, pb, oacc[db]);
+          if constexpr (PLO) oacc[db] = mfma16x16x32(va, plo, oacc[db]);
+        });
       }
     }
   };
