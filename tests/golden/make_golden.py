@@ -56,10 +56,13 @@ def main(ref_root: str) -> None:
     with open(os.path.join(HERE, "codebooks.json"), "w") as f:
         json.dump(books, f, indent=1)
 
-    # ---- seeded set-up
+    # ---- seeded set-up: seed 0 and every per-layer seed the benchmark configurations use
+    # (patch.py:62-75: layer i takes seed+i for keys, seed+i+10000 for values and the key S);
+    # head_dim 64 covers GPT-2 small's 12 layers, head_dim 128 the 36 layers of Qwen2.5-3B
+    # (Llama-3.1-8B's 32 and DeepSeek-7B's 30 are a prefix of them)
     setup = {}
-    for d in (64, 128):
-        for seed in (42, 43, 0):
+    for d, seeds in ((64, [0] + list(range(42, 54))), (128, [0] + list(range(42, 78)))):
+        for seed in seeds:
             kc = TurboQuantCompressorV2(d, 3, seed=seed)
             vc = TurboQuantCompressorMSE(d, 3, seed=seed + 10000)
             setup[f"d{d}_s{seed}"] = {
@@ -68,6 +71,16 @@ def main(ref_root: str) -> None:
             }
     with open(os.path.join(HERE, "setup.json"), "w") as f:
         json.dump(setup, f, indent=1)
+
+    # ---- the reference's rotations themselves for the seeds the GPU tests and the bench
+    # build (GPT-2 small's 12 layers at head_dim 64, layer 0 at head_dim 128), as the
+    # fallback a host whose LAPACK rounds the QR differently pins (codebook.pin_rotations)
+    rots = {}
+    for d, seeds in ((64, range(42, 54)), (128, range(42, 43))):
+        for seed in seeds:
+            rots[f"d{d}_s{seed}"] = TurboQuantCompressorV2(d, 3, seed=seed).Pi.numpy()
+            rots[f"d{d}_s{seed + 10000}"] = TurboQuantCompressorMSE(d, 3, seed=seed + 10000).Pi.numpy()
+    np.savez_compressed(os.path.join(HERE, "rotations.npz"), **rots)
 
     # ---- CPU-branch compress / scores / decompress on a seeded input
     out = {}
@@ -93,26 +106,29 @@ def main(ref_root: str) -> None:
         out[f"{tag}_v_recon"] = vc.decompress(cv).numpy()
     np.savez_compressed(os.path.join(HERE, "cpu_compress.npz"), **out)
 
-    # ---- config 1: GPT-2 small random init, eager attention (explicit causal mask)
+    # ---- config 1: GPT-2 small random init under both attention implementations. eager
+    # passes an additive causal mask; sdpa passes none, so the wrapper (gpt2.py:99-101)
+    # attends to every position.
     from transformers import GPT2Config, GPT2LMHeadModel
     from transformers_turboquant import apply_turboquant
 
-    torch.manual_seed(0)
-    cfg = GPT2Config()
-    cfg._attn_implementation = "eager"
-    model = GPT2LMHeadModel(cfg).eval()
-    apply_turboquant(model, bits=3, seed=42)
-    ids = torch.randint(0, 50257, (1, 512), generator=torch.Generator().manual_seed(0))
-    with torch.no_grad():
-        logits = model(input_ids=ids).logits
-    np.savez_compressed(
-        os.path.join(HERE, "gpt2_logits.npz"),
-        input_ids=ids.numpy().astype(np.int32),
-        logits_head=logits[0, :8, :16].numpy(),
-        logits_tail=logits[0, -8:, -16:].numpy(),
-        row_sums=logits[0].double().sum(-1).numpy(),
-        argmax=logits[0].argmax(-1).numpy().astype(np.int32),
-    )
+    for impl, name in (("eager", "gpt2_logits.npz"), ("sdpa", "gpt2_logits_sdpa.npz")):
+        torch.manual_seed(0)
+        cfg = GPT2Config()
+        cfg._attn_implementation = impl
+        model = GPT2LMHeadModel(cfg).eval()
+        apply_turboquant(model, bits=3, seed=42)
+        ids = torch.randint(0, 50257, (1, 512), generator=torch.Generator().manual_seed(0))
+        with torch.no_grad():
+            logits = model(input_ids=ids).logits
+        np.savez_compressed(
+            os.path.join(HERE, name),
+            input_ids=ids.numpy().astype(np.int32),
+            logits_head=logits[0, :8, :16].numpy(),
+            logits_tail=logits[0, -8:, -16:].numpy(),
+            row_sums=logits[0].double().sum(-1).numpy(),
+            argmax=logits[0].argmax(-1).numpy().astype(np.int32),
+        )
     print("golden fixtures written to", HERE)
 
 

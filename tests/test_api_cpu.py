@@ -44,13 +44,16 @@ def test_cpu_branch_matches_reference_vectors(tag):
     assert np.allclose(vc.decompress(cv).numpy(), g[f"{tag}_v_recon"], rtol=1e-6, atol=1e-6)
 
 
-def test_gpt2_config1_logits_match_reference():
+@pytest.mark.parametrize("impl,fixture", [("eager", "gpt2_logits.npz"), ("sdpa", "gpt2_logits_sdpa.npz")])
+def test_gpt2_config1_logits_match_reference(impl, fixture):
+    """Config 1 with apply_turboquant's defaults: eager gets the decoder's additive causal
+    mask, sdpa gets none and (as in the reference, gpt2.py:99-101) attends to every position."""
     from transformers import GPT2Config, GPT2LMHeadModel
 
-    g = np.load(os.path.join(GOLDEN, "gpt2_logits.npz"))
+    g = np.load(os.path.join(GOLDEN, fixture))
     torch.manual_seed(0)
     cfg = GPT2Config()
-    cfg._attn_implementation = "eager"
+    cfg._attn_implementation = impl
     model = GPT2LMHeadModel(cfg).eval()
     assert apply_turboquant(model, bits=3, seed=42) is model
     with torch.no_grad():
@@ -210,17 +213,35 @@ def test_apply_turboquant_llama_like(model_type):
     assert torch.equal(layers[0].val_compressor.Pi, TurboQuantCompressorMSE(32, 3, seed=10042).Pi)
 
 
-def test_causal_auto_matches_explicit_mask():
-    """With no mask, causal='auto' equals the additive causal mask on the CPU path."""
+def _small_gpt2(impl, **kw):
     from transformers import GPT2Config, GPT2LMHeadModel
 
-    def run(impl):
-        torch.manual_seed(0)
-        cfg = GPT2Config(n_layer=2, n_embd=128, n_head=2, vocab_size=256)
-        cfg._attn_implementation = impl
-        model = GPT2LMHeadModel(cfg).eval()
-        apply_turboquant(model, bits=3, seed=42)
-        with torch.no_grad():
-            return model(input_ids=torch.arange(24).unsqueeze(0)).logits
+    torch.manual_seed(0)
+    cfg = GPT2Config(n_layer=2, n_embd=128, n_head=2, vocab_size=256)
+    cfg._attn_implementation = impl
+    return apply_turboquant(GPT2LMHeadModel(cfg).eval(), bits=3, seed=42, **kw)
 
-    assert torch.allclose(run("eager"), run("sdpa"), atol=1e-5)
+
+def test_causal_auto_matches_explicit_mask():
+    """causal='auto' under sdpa (no mask passed) equals eager with its additive causal mask."""
+    ids = torch.arange(24).unsqueeze(0)
+    with torch.no_grad():
+        eager = _small_gpt2("eager")(input_ids=ids).logits
+        auto = _small_gpt2("sdpa", causal="auto")(input_ids=ids).logits
+    assert torch.allclose(eager, auto, atol=1e-5)
+
+
+def test_default_is_reference_noncausal_under_sdpa():
+    """The default adds a mask only when one is passed (gpt2.py:99-101): under sdpa every
+    layer attends to all positions, i.e. each attention module equals itself fed an all-zero
+    additive mask, and the logits differ from the causal eager run."""
+    ids = torch.arange(24).unsqueeze(0)
+    model = _small_gpt2("sdpa")
+    attn = model.transformer.h[0].attn
+    hidden = torch.randn(1, 24, 128, generator=torch.Generator().manual_seed(3))
+    with torch.no_grad():
+        none, _ = attn(hidden)
+        zero, _ = attn(hidden, attention_mask=torch.zeros(1, 1, 24, 24))
+        assert torch.equal(none, zero)
+        assert not torch.allclose(model(input_ids=ids).logits, _small_gpt2("eager")(input_ids=ids).logits,
+                                  atol=1e-3)

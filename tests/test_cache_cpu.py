@@ -27,7 +27,10 @@ def _model(kind):
 
 @pytest.mark.parametrize("kind", ["llama", "gpt2"])
 def test_cached_generate_matches_recompute(kind):
-    model = apply_turboquant(_model(kind), bits=3, seed=42)
+    # decoding one token at a time is causal by construction, so the recomputation it is
+    # compared with must be too: causal="auto" masks the prompt when the decoder passes no
+    # mask (the default reproduces the reference, which then attends to every position)
+    model = apply_turboquant(_model(kind), bits=3, seed=42, causal="auto")
     ids = torch.randint(0, 128, (2, 11), generator=torch.Generator().manual_seed(3))
     kw = dict(max_new_tokens=6, min_new_tokens=6, do_sample=False, output_scores=True,
               return_dict_in_generate=True, attention_mask=torch.ones_like(ids))
@@ -78,3 +81,22 @@ def test_cache_rejects_uncompressed_update():
     cache = TurboQuantCache()
     with pytest.raises(NotImplementedError):
         cache.update(torch.zeros(1, 1, 1, 8), torch.zeros(1, 1, 1, 8), 0)
+
+
+def test_append_refuses_other_compressor_settings():
+    """Positions compressed under one (bits, seed) pair must not be extended under another:
+    the new compressor's Pi/S would then be applied to the old planes."""
+    d = 32
+    g = torch.Generator().manual_seed(1)
+    k = torch.randn(1, 2, 5, d, generator=g)
+    cache = TurboQuantCache()
+    cache.append(0, TurboQuantCompressorV2(d, 3, seed=1), TurboQuantCompressorMSE(d, 3, seed=10001), k, k)
+    with pytest.raises(ValueError, match="other settings"):
+        cache.append(0, TurboQuantCompressorV2(d, 3, seed=2), TurboQuantCompressorMSE(d, 3, seed=10001), k, k)
+    with pytest.raises(ValueError, match="other settings"):
+        cache.append(0, TurboQuantCompressorV2(d, 3, seed=1), TurboQuantCompressorMSE(d, 2, seed=10001), k, k)
+    # the same settings keep appending; after a reset any settings start a new sequence
+    cache.append(0, TurboQuantCompressorV2(d, 3, seed=1), TurboQuantCompressorMSE(d, 3, seed=10001), k, k)
+    assert cache.get_seq_length() == 10
+    cache.layer(0).reset()
+    cache.append(0, TurboQuantCompressorV2(d, 3, seed=2), TurboQuantCompressorMSE(d, 3, seed=10001), k, k)

@@ -114,7 +114,8 @@ def test_cached_generate_matches_recompute_gpu(dtype):
     torch.manual_seed(0)
     cfg = LlamaConfig(vocab_size=1000, hidden_size=1024, intermediate_size=1024, num_hidden_layers=2,
                       num_attention_heads=8, num_key_value_heads=2)  # head_dim 128, G = 4: decode kernels
-    model = apply_turboquant(LlamaForCausalLM(cfg).eval(), bits=3).to("cuda", dtype)
+    # causal="auto": token-by-token decoding is causal, so the recomputation must be too
+    model = apply_turboquant(LlamaForCausalLM(cfg).eval(), bits=3, causal="auto").to("cuda", dtype)
     ids = torch.randint(0, 1000, (2, 37), generator=torch.Generator().manual_seed(5)).cuda()
     kw = dict(max_new_tokens=8, min_new_tokens=8, do_sample=False, output_logits=True,
               return_dict_in_generate=True, attention_mask=torch.ones_like(ids))

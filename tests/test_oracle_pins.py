@@ -189,3 +189,155 @@ def test_oracle_detects_planted_mistakes():
     assert not np.array_equal(good["packed_key_indices"], bad_t["packed_key_indices"])
     bad_s = O.key_compress_packed(x, pi, s.T.copy(), cent, bounds, 2)
     assert not np.array_equal(good["packed_qjl_signs"], bad_s["packed_qjl_signs"])
+
+
+# ---------------------------------------------------------------- packed estimator == unpacked estimator
+#
+# The packed scorer (attention.py:419-461, with q_rot and S_eff from compressors.py:186-189)
+# and the unpacked scorer (compressors.py:201-224, pinned by the reference's golden vectors
+# in tests/golden/cpu_compress.npz) are two forms of one estimator:
+#   vn <q Pi^T, C[c]>          = <q, (C[c] Pi) vn>          = <q, k_mse>
+#   <q Pi^T (S Pi^T)^T, s>     = <q Pi^T Pi S^T, s>          = <q S^T, s>
+# so on planes of the same key compression they must agree to rounding.  Each check
+# below is evaluated with the oracle functions and then with planted mistakes, which
+# must fail it: Pi <-> Pi^T, S_eff <-> S_eff^T, vn <-> rn, a {0,1} sign used where
+# 2*bit-1 belongs, a reversed codebook, a dropped QJL term.
+
+def _exact_orthogonal(d, seed):
+    q, r = np.linalg.qr(np.random.default_rng(seed).standard_normal((d, d)))
+    return q * np.sign(np.diag(r))[None, :]
+
+
+def _f16_exact(rng, shape, scale=1.0):
+    return (rng.standard_normal(shape) * scale).astype(np.float16).astype(np.float64)
+
+
+def _packed_vs_unpacked_err(pi, s, cent, bounds, mse_bits, x, q, scores_fn=None, prep_fn=None,
+                            exact_prep=False):
+    """max |packed - unpacked| / max |unpacked| over one key set.
+
+    The packed side gets q_rot = q Pi^T and q_proj = q_rot S_eff^T (float64, unrounded, or
+    through prep_fn), S_eff = S Pi^T; the unpacked side gets q, k_mse = (C16[codes] Pi) vn
+    and +-1 signs, with the codes, sign bits and norms of one packed compression."""
+    scores_fn = scores_fn or O.scores_packed
+    d = pi.shape[0]
+    comp = O.key_compress_packed(x, pi.astype(np.float32), s.astype(np.float32), cent, bounds, mse_bits)
+    codes = O.unpack_bits(comp["packed_key_indices"], mse_bits, d)
+    sbits = O.unpack_bits(comp["packed_qjl_signs"], 1, d)
+    rn = comp["residual_norm"].astype(np.float64)
+    vn = comp["vec_norms"].astype(np.float64)
+    c16 = np.asarray(cent, np.float32).astype(np.float16)
+    s_eff = s @ pi.T
+    if prep_fn is None:
+        q_rot = q @ pi.T
+        q_proj = q_rot @ s_eff.T
+    else:
+        q_rot, q_proj = prep_fn(q, pi, s_eff)
+    packed = scores_fn(q_rot, q_proj, codes, sbits, rn, vn, c16, O.COEFF(d))
+    k_mse = (c16.astype(np.float64)[codes] @ pi) * vn[:, None]
+    unpacked = O.scores_unpacked(q, k_mse, sbits * 2.0 - 1.0, rn, s, O.COEFF(d))
+    return float(np.max(np.abs(packed - unpacked)) / np.max(np.abs(unpacked)))
+
+
+def _setup(d, bits, real):
+    """(Pi, S, centroids, boundaries) as float64: the real compressor's (f32) matrices, or an
+    exactly orthogonal float64 Pi with a Gaussian S."""
+    from turboquant_pytorch.compressors import TurboQuantCompressorV2
+
+    kc = TurboQuantCompressorV2(d, bits, seed=42)
+    cent, bounds = kc.centroids.numpy(), kc.boundaries.numpy()
+    if real:
+        return kc.Pi.double().numpy(), kc.S.double().numpy(), cent, bounds, kc.mse_bits
+    rng = np.random.default_rng(d + bits)
+    return _exact_orthogonal(d, d * 7 + bits), rng.standard_normal((d, d)), cent, bounds, kc.mse_bits
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("d", [64, 128])
+def test_packed_estimator_equals_unpacked(d, bits):
+    rng = np.random.default_rng(100 + d + bits)
+    x = rng.standard_normal((40, d)).astype(np.float32)
+    x[:, :3] *= 20  # outlier channels, as in the benchmark keys
+    q = rng.standard_normal((6, d)).astype(np.float32).astype(np.float64)  # scores_unpacked takes f32 q
+    # exactly orthogonal Pi: the identity holds to float64 rounding
+    assert _packed_vs_unpacked_err(*_setup(d, bits, real=False), x, q) < 1e-12
+    # the compressor's own f32 Pi and S: Pi^T Pi = I to f32 rounding
+    assert _packed_vs_unpacked_err(*_setup(d, bits, real=True), x, q) < 2e-6
+
+
+def _mut_vn_rn(qr, qp, codes, sb, rn, vn, c16, coeff):
+    return O.scores_packed(qr, qp, codes, sb, vn, rn, c16, coeff)
+
+
+def _mut_sign01(qr, qp, codes, sb, rn, vn, c16, coeff):
+    # 2*b' - 1 = b  <=>  the estimator uses the raw {0,1} bit where +-1 belongs
+    return O.scores_packed(qr, qp, codes, (np.asarray(sb, np.float64) + 1) / 2, rn, vn, c16, coeff)
+
+
+def _mut_codebook(qr, qp, codes, sb, rn, vn, c16, coeff):
+    return O.scores_packed(qr, qp, codes, sb, rn, vn, c16[::-1].copy(), coeff)
+
+
+def _mut_no_qjl(qr, qp, codes, sb, rn, vn, c16, coeff):
+    return O.scores_packed(qr, qp, codes, sb, rn, vn, c16, 0.0)
+
+
+@pytest.mark.parametrize("mutant", [_mut_vn_rn, _mut_sign01, _mut_codebook, _mut_no_qjl])
+@pytest.mark.parametrize("real", [False, True])
+def test_packed_estimator_identity_catches_planted_mistakes(mutant, real):
+    d, bits = 64, 3
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((40, d)).astype(np.float32)
+    q = rng.standard_normal((6, d)).astype(np.float32).astype(np.float64)
+    assert _packed_vs_unpacked_err(*_setup(d, bits, real), x, q, scores_fn=mutant) > 1e-2
+
+
+def _prep_exact(transpose_pi=False, transpose_seff=False):
+    """q_rot, q_proj through O.query_prep on inputs whose f16 roundings are exact: q is built
+    as q_rot16 Pi from f16 values and S_eff is itself f16, so every rounding the reference
+    applies (compressors.py:186, :189) is the identity and float64 equality is expected."""
+
+    def prep(q, pi, s_eff):
+        s16 = s_eff.astype(np.float16)
+        qr, qp = O.query_prep(q, pi.T if transpose_pi else pi, s16.T if transpose_seff else s16)
+        return qr.astype(np.float64), qp
+
+    return prep
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_query_prep_identities(d):
+    rng = np.random.default_rng(d)
+    pi = _exact_orthogonal(d, 5 + d)
+    s_eff16 = _f16_exact(rng, (d, d))
+    s = s_eff16 @ pi  # so that f16(S Pi^T) = s_eff16 exactly
+    qr16 = _f16_exact(rng, (8, d))
+    q = qr16 @ pi  # so that f16(q Pi^T) = qr16 exactly
+    q_rot, q_proj = O.query_prep(q, pi, s_eff16.astype(np.float16))
+    # <q_rot, y> = <q, y Pi>: the rotated query scores rotated vectors as q scores the originals
+    y = rng.standard_normal((5, d))
+    assert np.max(np.abs(q_rot.astype(np.float64) @ y.T - q @ (y @ pi).T)) < 1e-10
+    # q_proj = q S^T: the packed QJL projection equals the unpacked one
+    assert np.max(np.abs(q_proj - q @ s.T)) < 1e-9 * np.max(np.abs(q @ s.T))
+    # q_rot is the f16 rounding of q Pi^T (compressors.py:186)
+    qr_gen = (rng.standard_normal((8, d))).astype(np.float32)
+    r16, _ = O.query_prep(qr_gen, pi, s_eff16.astype(np.float16))
+    assert np.array_equal(r16, (qr_gen.astype(np.float64) @ pi.T).astype(np.float32).astype(np.float16))
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_query_prep_composes_with_packed_estimator(bits):
+    d = 128
+    pi = _exact_orthogonal(d, 31)
+    rng = np.random.default_rng(bits)
+    s = _f16_exact(rng, (d, d)) @ pi
+    from turboquant_pytorch.compressors import TurboQuantCompressorV2
+
+    kc = TurboQuantCompressorV2(d, bits, seed=42)
+    x = rng.standard_normal((32, d)).astype(np.float32)
+    q = _f16_exact(rng, (4, d)) @ pi
+    args = (pi, s, kc.centroids.numpy(), kc.boundaries.numpy(), kc.mse_bits, x, q)
+    # scores_unpacked rounds q to f32 (the reference's .float()), hence 1e-6 and not 1e-12
+    assert _packed_vs_unpacked_err(*args, prep_fn=_prep_exact()) < 1e-6
+    assert _packed_vs_unpacked_err(*args, prep_fn=_prep_exact(transpose_pi=True)) > 1e-2
+    assert _packed_vs_unpacked_err(*args, prep_fn=_prep_exact(transpose_seff=True)) > 1e-2

@@ -106,3 +106,47 @@ def test_rotation_is_unique_qr_factor(d):
     r = pi.T @ g  # = R with a non-negative diagonal
     assert torch.allclose(torch.tril(r, -1), torch.zeros_like(r), atol=1e-4)
     assert bool((torch.diagonal(r) > 0).all())
+
+
+def test_package_codebook_table_is_the_solver_and_the_reference():
+    """The shipped table (read at construction instead of re-solving) equals both the
+    solver's output and the reference's exact f32 codebooks."""
+    from turboquant_pytorch.codebook import _TABLE_PATH
+
+    with open(_TABLE_PATH) as f:
+        table = json.load(f)
+    with open(os.path.join(GOLDEN, "codebooks.json")) as f:
+        books = json.load(f)
+    assert set(table) == set(books)
+    for key, hexes in table.items():
+        d, bits = (int(s[1:]) for s in key.split("_"))
+        assert hexes == books[key]["centroids_hex"], key
+        solved = torch.tensor(lloyd_max_centroids(d, bits), dtype=torch.float32)
+        assert [float(v).hex() for v in solved.tolist()] == hexes, key
+
+
+def test_pinned_rotations_replace_the_qr():
+    """pin_rotations() is the fallback for a host whose LAPACK rounds the QR differently:
+    the reference's rotations (tests/golden/rotations.npz) pinned, compressors reproduce
+    the reference hashes whatever this host's QR gives."""
+    from turboquant_pytorch.codebook import clear_pinned_rotations, load_rotations, pin_rotations
+
+    rots = load_rotations(os.path.join(GOLDEN, "rotations.npz"))
+    with open(os.path.join(GOLDEN, "setup.json")) as f:
+        setup = json.load(f)
+    try:
+        fake = {k: torch.flip(v, dims=[0]) for k, v in rots.items()}  # a different "host QR"
+        pin_rotations(fake)
+        assert torch.equal(TurboQuantCompressorV2(64, 3, seed=42).Pi, fake[(64, 42)])
+        pin_rotations(rots)
+        for (d, seed) in rots:
+            if f"d{d}_s{seed}" in setup:
+                kc = TurboQuantCompressorV2(d, 3, seed=seed)
+                vc = TurboQuantCompressorMSE(d, 3, seed=seed + 10000)
+                rec = setup[f"d{d}_s{seed}"]
+                assert _sha(kc.Pi) == rec["key_pi"] and _sha(vc.Pi) == rec["val_pi"]
+        with pytest.raises(ValueError):
+            pin_rotations({(64, 1): torch.zeros(3, 3)})
+    finally:
+        clear_pinned_rotations()
+    assert _sha(random_rotation(64, 42)) == setup["d64_s42"]["key_pi"]

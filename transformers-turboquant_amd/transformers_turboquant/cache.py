@@ -97,10 +97,18 @@ class TurboQuantCacheLayer(CacheLayerMixin):
         B, H, S, D = k.shape
         if self.shape is not None and self.length > 0 and self.shape != (B, H, D):
             raise ValueError(f"cache holds [B, Hkv, D] = {self.shape}, got {(B, H, D)}")
+        codec = {"key_bits": key_compressor.bits, "value_bits": val_compressor.bits,
+                 "key_seed": getattr(key_compressor, "seed", None),
+                 "value_seed": getattr(val_compressor, "seed", None)}
+        if self.length > 0 and self.codec:
+            # planes written under other seeds (or bits) would be attended with the wrong Pi/S
+            stale = {k: (self.codec.get(k), v) for k, v in codec.items()
+                     if self.codec.get(k) is not None and v is not None and self.codec.get(k) != v}
+            if stale:
+                raise ValueError(f"cache layer holds {self.length} positions compressed with other "
+                                 f"settings (cached, new): {stale}")
         self.shape = (B, H, D)
-        self.codec = {"key_bits": key_compressor.bits, "value_bits": val_compressor.bits,
-                      "key_seed": getattr(key_compressor, "seed", None),
-                      "value_seed": getattr(val_compressor, "seed", None)}
+        self.codec = codec
         if k.device.type != "cuda":
             return self._append_cpu(key_compressor, val_compressor, k, v)
         ck = key_compressor.compress(k)

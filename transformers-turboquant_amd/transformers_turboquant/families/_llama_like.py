@@ -40,7 +40,7 @@ class LlamaLikeAttention(TurboQuantAttentionBase):
         obj.is_causal = getattr(original, "is_causal", True)
         obj.key_compressor = key_compressor
         obj.val_compressor = val_compressor
-        obj.causal_mode = "auto"
+        obj.causal_mode = False
         return obj
 
     def _apply(self, fn, recurse=True):

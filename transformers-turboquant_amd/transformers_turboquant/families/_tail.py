@@ -45,7 +45,8 @@ def causal_mask(sq: int, sk: int, device, dtype=torch.float32) -> torch.Tensor:
 
 
 def want_causal(module, attention_mask) -> bool:
-    mode = getattr(module, "causal_mode", "auto")
+    """Causal masking inside the kernel: only with causal_mode "auto" and no mask passed."""
+    mode = getattr(module, "causal_mode", False)
     return attention_mask is None and mode == "auto" and getattr(module, "is_causal", True)
 
 

@@ -33,7 +33,7 @@ class TurboQuantGPT2Attention(TurboQuantAttentionBase):
         obj.layer_idx = getattr(original, "layer_idx", None)
         obj.key_compressor = key_compressor
         obj.val_compressor = val_compressor
-        obj.causal_mode = "auto"
+        obj.causal_mode = False
         return obj
 
     def _apply(self, fn, recurse=True):

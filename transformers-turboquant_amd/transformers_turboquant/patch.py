@@ -16,7 +16,7 @@ def _head_dim(module, config) -> int:
     return hidden // heads
 
 
-def apply_turboquant(model, bits: int = 3, seed: int = 42, use_triton: bool = True, causal="auto"):
+def apply_turboquant(model, bits: int = 3, seed: int = 42, use_triton: bool = True, causal=False):
     """Replace every attention module of *model* with its TurboQuant family (patch.py:13-82).
 
     Layer i (in ``named_modules()`` order) gets key seed ``seed + i`` and value
@@ -24,10 +24,11 @@ def apply_turboquant(model, bits: int = 3, seed: int = 42, use_triton: bool = Tr
     ``config.use_cache`` is set to False (every forward recomputes the full
     sequence from compressed K/V), and the same object is returned.
 
-    causal: "auto" (default) applies the module's own causal masking inside the
-    kernel whenever the decoder passes no attention mask (transformers 5.x does
-    so for SDPA without padding); False reproduces the reference exactly, adding
-    a mask only when one is passed.
+    causal: False (default) reproduces the reference: the attention mask is
+    added only when the decoder passes one (families/gpt2.py:99-101), so a
+    decoder that passes none (transformers 5.x under SDPA without padding)
+    attends to every position, as the reference does.  "auto" applies the
+    module's own causal masking inside the kernel whenever no mask is passed.
     """
     family = get_attention_class(model.config.model_type)
     device = str(next(model.parameters()).device)

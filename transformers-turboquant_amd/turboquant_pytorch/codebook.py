@@ -7,8 +7,11 @@ compressors up; nothing here is on the per-token path.
 from __future__ import annotations
 
 import functools
+import json
 import math
+import os
 
+import numpy as np
 import torch
 
 
@@ -51,9 +54,42 @@ def lloyd_max_centroids(d: int, bits: int) -> tuple[float, ...]:
     return tuple(cur)
 
 
+_TABLE_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "codebooks.json")
+
+
+@functools.lru_cache(maxsize=1)
+def _codebook_table() -> dict:
+    """Solved codebooks shipped with the package: {"d{d}_b{bits}": [f32 hex, ...]}."""
+    try:
+        with open(_TABLE_PATH) as f:
+            return json.load(f)
+    except OSError:
+        return {}
+
+
 def codebook(d: int, bits: int) -> torch.Tensor:
-    """f32 centroid tensor [2^bits] (compressors.py:96)."""
+    """f32 centroid tensor [2^bits] (compressors.py:96).
+
+    Head dims 32/64/128/256 at 1-4 bits come from the table the solver wrote
+    (``python -m turboquant_pytorch.codebook`` regenerates it); anything else is
+    solved here, which takes the quadrature loop about a second."""
+    hexes = _codebook_table().get(f"d{d}_b{bits}")
+    if hexes is not None:
+        return torch.tensor([float.fromhex(h) for h in hexes], dtype=torch.float32)
     return torch.tensor(lloyd_max_centroids(d, bits), dtype=torch.float32)
+
+
+def write_codebook_table(path: str = _TABLE_PATH) -> dict:
+    """Solve the shipped (d, bits) grid and write it as f32 hex strings."""
+    table = {}
+    for d in (32, 64, 128, 256):
+        for bits in (1, 2, 3, 4):
+            c = torch.tensor(lloyd_max_centroids(d, bits), dtype=torch.float32)
+            table[f"d{d}_b{bits}"] = [float(v).hex() for v in c.tolist()]
+    with open(path, "w") as f:
+        json.dump(table, f, indent=1)
+    _codebook_table.cache_clear()
+    return table
 
 
 def midpoints(centroids: torch.Tensor) -> torch.Tensor:
@@ -61,13 +97,47 @@ def midpoints(centroids: torch.Tensor) -> torch.Tensor:
     return (centroids[:-1] + centroids[1:]) / 2
 
 
+_PINNED_ROTATIONS: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def pin_rotations(rotations: dict[tuple[int, int], torch.Tensor]) -> None:
+    """Make random_rotation(d, seed) return the given f32 [d, d] matrices.
+
+    The QR factor depends on the host's LAPACK in its last bits.  A deployment
+    that must reproduce another host's rotations exactly (for instance the
+    reference's, whose sha256 differ from this host's) pins them here; the
+    compressors built afterwards use them."""
+    for (d, seed), pi in rotations.items():
+        pi = torch.as_tensor(pi, dtype=torch.float32).cpu().contiguous()
+        if pi.shape != (d, d):
+            raise ValueError(f"pinned rotation for d={d} seed={seed} has shape {tuple(pi.shape)}")
+        _PINNED_ROTATIONS[(int(d), int(seed))] = pi
+
+
+def load_rotations(path: str) -> dict[tuple[int, int], torch.Tensor]:
+    """Read rotations saved as an .npz of f32 arrays named "d{d}_s{seed}" (no pickles)."""
+    out = {}
+    with np.load(path, allow_pickle=False) as z:
+        for name in z.files:
+            d, seed = (int(s[1:]) for s in name.split("_"))
+            out[(d, seed)] = torch.from_numpy(np.array(z[name], dtype=np.float32))
+    return out
+
+
+def clear_pinned_rotations() -> None:
+    _PINNED_ROTATIONS.clear()
+
+
 def random_rotation(d: int, seed: int) -> torch.Tensor:
     """Haar-random orthogonal Pi from a seeded Gaussian (compressors.py:50-56).
 
     QR of a CPU-generated N(0,1) matrix with the column signs fixed so that R
     has a non-negative diagonal (a zero sign counts as +1), which makes the
-    factor unique.
+    factor unique.  A rotation pinned with pin_rotations() is returned instead.
     """
+    pinned = _PINNED_ROTATIONS.get((int(d), int(seed)))
+    if pinned is not None:
+        return pinned.clone()
     gen = torch.Generator(device="cpu")
     gen.manual_seed(seed)
     g = torch.randn(d, d, generator=gen)
@@ -90,3 +160,8 @@ def split_f16(w: torch.Tensor) -> torch.Tensor:
     hi = w64.to(torch.float16)
     lo = (w64 - hi.float()).to(torch.float16)
     return torch.stack([hi, lo]).contiguous()
+
+
+if __name__ == "__main__":
+    write_codebook_table()
+    print("wrote", _TABLE_PATH)
