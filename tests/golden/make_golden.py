@@ -72,11 +72,13 @@ def main(ref_root: str) -> None:
     with open(os.path.join(HERE, "setup.json"), "w") as f:
         json.dump(setup, f, indent=1)
 
-    # ---- the reference's rotations themselves for the seeds the GPU tests and the bench
-    # build (GPT-2 small's 12 layers at head_dim 64, layer 0 at head_dim 128), as the
-    # fallback a host whose LAPACK rounds the QR differently pins (codebook.pin_rotations)
+    # ---- the reference's rotations themselves for every per-layer seed of the benchmark
+    # configurations (GPT-2 small's 12 layers at head_dim 64, Qwen2.5-3B's 36 at 128), as
+    # the fallback a host whose LAPACK rounds the QR differently pins
+    # (codebook.pin_rotations).  The MI355X boxes' MKL differs from this container's by
+    # up to ~1e-6 per element, whatever its thread count or MKL_CBWR mode.
     rots = {}
-    for d, seeds in ((64, range(42, 54)), (128, range(42, 43))):
+    for d, seeds in ((64, range(42, 54)), (128, range(42, 78))):
         for seed in seeds:
             rots[f"d{d}_s{seed}"] = TurboQuantCompressorV2(d, 3, seed=seed).Pi.numpy()
             rots[f"d{d}_s{seed + 10000}"] = TurboQuantCompressorMSE(d, 3, seed=seed + 10000).Pi.numpy()

@@ -132,3 +132,33 @@ def test_decode_long_context_slice():
         ref = O.attention(sc, vals, 1 / math.sqrt(d))[0]
         assert O.rel_err(_np(out[b, 0, h]), ref) < REL, (b, h)
         assert O.rel_err(_np(tiled[b, 0, h]), ref) < REL, (b, h)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("sk,vmul", [(16384, 1.0), (32768, 1.0), (32768, 0.01)])
+def test_decode_attention_sink_keeps_small_weights(bits, sk, vmul):
+    """One sink key ~12 nats above 16-32k ordinary keys: the ordinary keys' weights are
+    e^-12 of the sink's each, yet together they carry a fifth to a third of the mass.
+    Each must reach P.V, not only the f32 normaliser (small value norms included)."""
+    _case(what="sink", bits=bits, sk=sk, vmul=vmul)
+    B, hq, hkv, d = 1, 4, 1, 128
+    assert _on_decode_path(B, hq, hkv, 1, sk, bits)
+    g = torch.Generator().manual_seed(sk + bits)
+    u = torch.randn(d, generator=g)
+    q = (u + 0.05 * torch.randn(B, hq, 1, d, generator=g)).to(DEV)
+    k = torch.randn(B, hkv, sk, d, generator=g)
+    sink = 777
+    k[0, 0, sink] = 12.0 * math.sqrt(d) * u / (u @ u)  # score q.k / sqrt(d) ~ 12
+    v = (torch.randn(B, hkv, sk, d, generator=g) * vmul)
+    k, v = k.to(DEV), v.to(DEV)
+    kc = TurboQuantCompressorV2(d, bits, seed=42, device=DEV)
+    vc = TurboQuantCompressorMSE(d, bits, seed=10042, device=DEV)
+    ck, cv = kc.compress(k), vc.compress(v)
+    got = _np(compressed_attention(q, kc, vc, ck, cv, out_dtype=torch.float32))
+    ref = _oracle_attention(kc, vc, q, ck, cv, hq, hkv)
+    sc = _oracle_scores(kc, q, ck, hq, hkv)[0, 0, 0] / math.sqrt(d)
+    w = np.exp(sc - sc.max())
+    share = 1 - w[sink] / w.sum()
+    print(f"ordinary keys' share of the weight {share:.3f}; rel-err {O.rel_err(got, ref):.2e}", flush=True)
+    assert sc.argmax() == sink and 0.1 < share < 0.6
+    assert O.rel_err(got, ref) < REL and O.cosine(got, ref) > 0.9999

@@ -82,3 +82,24 @@ def test_llama_like_bf16_gpu_matches_cpu(model_type):
     with torch.no_grad():
         lb = gpu16(input_ids=ids.cuda()).logits.float().cpu().numpy()
     assert O.cosine(lb, lc) > 0.99  # whole model in bf16 vs f32
+
+
+@pytest.mark.parametrize("impl,fixture", [("eager", "gpt2_logits.npz"), ("sdpa", "gpt2_logits_sdpa.npz")])
+def test_gpt2_config1_gpu_against_reference_logits(impl, fixture):
+    """Config 1 on the GPU with apply_turboquant's defaults against the reference's own
+    logits (tests/golden, written by the reference's CPU code): under sdpa the decoder
+    passes no mask and, as in the reference (gpt2.py:99-101), every position is attended."""
+    import os
+
+    print("case: gpt2 reference logits", impl, flush=True)
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", fixture))
+    gpu = apply_turboquant(_gpt2(impl), bits=3, seed=42).to("cuda")
+    with torch.no_grad():
+        lg = gpu(input_ids=torch.from_numpy(g["input_ids"]).long().cuda()).logits[0].float().cpu().numpy()
+    # packed GPU format vs the reference's unpacked CPU format: same estimator, f16 vs f32
+    # centroids in the key reconstruction (compressors.py:120-122 vs :145-146)
+    # (small slices of random-init logits: the whole-vocabulary comparison with the CPU
+    # path, which reproduces these fixtures bit for bit, is test_gpt2_small_gpu_matches_cpu)
+    assert O.cosine(lg[:8, :16], g["logits_head"]) > 0.998
+    assert O.cosine(lg[-8:, -16:], g["logits_tail"]) > 0.998
+    assert (lg.argmax(-1) == g["argmax"]).mean() > 0.9

@@ -22,55 +22,23 @@
 #include "tq_common.h"
 #include "tq_stream.h"
 
-// Tuning knobs: scores use wave slabs of score_slab_keys(bits) keys with
-// score_ring(bits) slots in flight; attention
-// uses ANB 16-key blocks per wave slab with AR slots; grids target about *_BLOCKS
-// blocks.  Scores run best with many short blocks (dynamic balancing of the last
-// round); attention with one round of resident blocks (4 per CU at 128 VGPRs and
-// a 2-slot ring: 1024 on 256 CUs), which TQ_DEC_ATTN_BLOCKS = 0 asks the device for.
-#ifndef TQ_DEC_ATTN_BLOCKS
-#define TQ_DEC_ATTN_BLOCKS 0  // 0: the device's resident blocks (one round)
-#endif
-#ifndef TQ_DEC_SCORE_BLOCKS
-#define TQ_DEC_SCORE_BLOCKS 4096
-#endif
-#ifndef TQ_DEC_ANB
-#define TQ_DEC_ANB 2
-#endif
-#ifndef TQ_DEC_AR
-#define TQ_DEC_AR 2
-#endif
-#ifndef TQ_DEC_PLO
-#define TQ_DEC_PLO 0
-#endif
-// Scores slab shape per width (TQ_DEC_SR / TQ_DEC_SNK override it for every width):
-// 32-key wave slabs in a 3-slot ring at bits 3-4 (22 KB of LDS, 6 blocks per CU),
+// Launch shapes (measured on MI355X at 16 x 32k keys, bits 3):
+//   scores     wave slabs of score_slab_keys(bits) keys, score_ring(bits) slots in
+//              flight, grids of about kScoreBlocks blocks: many short blocks balance
+//              the last round better than one persistent stream per CU (57 vs 62-66 us)
+//   attention  wave slabs of 16 * kAttnNbs keys in kAttnRing slots, a grid of one
+//              round of resident blocks (4 per CU at 128 VGPRs: 1024 on 256 CUs,
+//              8% faster than 768 blocks at 3 waves per SIMD)
+// Scores: 32-key slabs in a 3-slot ring at bits 3-4 (22 KB of LDS, 6 blocks per CU),
 // 64-key slabs in 2 slots at bits 2, where the shorter slabs' per-slab overhead is a
-// larger share of the lighter decode.  Measured at 16 x 32k keys: bits 3 56.3 vs
-// 57.8 us, bits 4 68.2 vs 69.1 us, bits 2 48.0 vs 46.5 us for 32/3 against 64/2.
-constexpr int score_ring(int bits) {
-#ifdef TQ_DEC_SR
-  return (void)bits, TQ_DEC_SR;
-#else
-  return bits == 2 ? 2 : 3;
-#endif
-}
-constexpr int score_slab_keys(int bits) {
-#ifdef TQ_DEC_SNK
-  return (void)bits, TQ_DEC_SNK;
-#else
-  return bits == 2 ? 64 : 32;
-#endif
-}
-// minimum waves per SIMD the attention kernel's register budget must allow (0: compiler's choice)
-#ifndef TQ_DEC_AWPE
-#define TQ_DEC_AWPE 4
-#endif
-#if TQ_DEC_AWPE > 0
-#define TQ_DEC_ATTN_ATTR __attribute__((amdgpu_waves_per_eu(TQ_DEC_AWPE)))
-#else
-#define TQ_DEC_ATTN_ATTR
-#endif
+// larger share of the lighter decode: bits 3 56.3 vs 57.8 us, bits 4 68.2 vs 69.1 us,
+// bits 2 48.0 vs 46.5 us for 32/3 against 64/2.
+constexpr int kScoreBlocks = 4096;
+constexpr int kAttnNbs = 2;
+constexpr int kAttnRing = 2;
+constexpr int score_ring(int bits) { return bits == 2 ? 2 : 3; }
+constexpr int score_slab_keys(int bits) { return bits == 2 ? 64 : 32; }
+#define TQ_DEC_ATTN_ATTR __attribute__((amdgpu_waves_per_eu(4)))
 
 namespace tq {
 
@@ -197,7 +165,7 @@ __device__ __forceinline__ half8 key_operand(const uint8_t* t, const uint32_t (&
 // the slot.  Lane (column l16, group lg) ends each 16-key block with the scores
 // of keys 4*lg + e for its own column, which is the P^T operand layout of the
 // value MFMA, so P never leaves registers.
-template <int D, int BITS, int NBS, int R, bool PLO>
+template <int D, int BITS, int NBS, int R>
 __global__ void __launch_bounds__(256) TQ_DEC_ATTN_ATTR decode_attn_lds_kernel(DecodeArgs a) {
   static_assert(D == 128, "decode kernel is built for head_dim 128");
   using L = SmallLuts<BITS>;
@@ -218,6 +186,10 @@ __global__ void __launch_bounds__(256) TQ_DEC_ATTN_ATTR decode_attn_lds_kernel(D
   static_assert(NBS == 2 || NBS == 4, "slabs of 32 or 64 keys");
   constexpr float LOG2E = 1.4426950408889634f;
   constexpr float TAU = 8.0f;          // lazy-rescale headroom (log2 units)
+  // p = 2^(s - m_run + PUP) <= 2^(TAU + PUP): the top weight of a column sits near 2^6 ..
+  // 2^14, so keys down to ~2^-31 of it still reach the f16 P operand (the f16 subnormal
+  // floor is 2^-24), and p * vn / vcap <= 2^14 stays far from the f16 maximum
+  constexpr float PUP = 6.0f;
 
   __shared__ __attribute__((aligned(16))) uint8_t luts[L::BYTES];
   __shared__ __attribute__((aligned(16))) uint8_t stage[STAGE > MERGE ? STAGE : MERGE];
@@ -306,6 +278,9 @@ __global__ void __launch_bounds__(256) TQ_DEC_ATTN_ATTR decode_attn_lds_kernel(D
   };
 
   float m_run = -INFINITY, l_run = 0.f;
+  // value norms enter P as vn / vcap <= 1; vcap is a power of two that only grows
+  // (oacc is rescaled when it does) and multiplies oacc back before the merge
+  float vcap = 0x1p-24f, inv_vcap = 0x1p24f;
   float4v oacc[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) oacc[db] = float4v{0.f, 0.f, 0.f, 0.f};
@@ -315,14 +290,31 @@ __global__ void __launch_bounds__(256) TQ_DEC_ATTN_ATTR decode_attn_lds_kernel(D
   // branch-free stretches; rows 16j .. 16j+15 of the slot are keys ks0 + 16j ..
   float (*fw)[NK] = fac[wave];
   auto slab = [&](const uint8_t* src, int ks0) {
-    // ---- per-key factors fa*vn_k, fb*rn_k, vn_v: 3*NK values, one per lane and pass
+    // ---- per-key factors fa*vn_k, fb*rn_k, vn_v/vcap: 3*NK values, one per lane and pass
 #pragma unroll
     for (int i0 = 0; i0 < 3 * NK; i0 += 64) {
       const int i = i0 + lane, which = i / NK, k = i % NK;
-      if (i < 3 * NK) {
-        const float v = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + which * NRM + k * 4)));
-        fw[which][k] = (which == 0) ? fa * v : (which == 1 ? fb * v : v);
+      const float v = (i < 3 * NK)
+          ? h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + which * NRM + k * 4)))
+          : 0.f;
+      if (i0 + 63 >= 2 * NK) {  // this pass holds value norms: keep them <= vcap
+        const float vv = (which == 2) ? v : 0.f;
+        if (__any(vv > vcap)) {
+          float t = vv;
+#pragma unroll
+          for (int sh = 32; sh >= 1; sh >>= 1) t = fmaxf(t, __shfl_xor(t, sh, 64));
+          int ex;
+          frexpf(t, &ex);  // t < 2^ex; every lane holds the same t, so ex is wave-uniform
+          ex = __builtin_amdgcn_readfirstlane(ex);
+          const float cap = ldexpf(1.f, ex);
+          const float shrink = vcap / cap;
+#pragma unroll
+          for (int db = 0; db < DB; ++db) oacc[db] *= shrink;
+          vcap = cap;
+          inv_vcap = ldexpf(1.f, -ex);
+        }
       }
+      if (i < 3 * NK) fw[which][k] = (which == 0) ? fa * v : (which == 1 ? fb * v : v * inv_vcap);
     }
     // ---- scores S^T = K^ Q^T (term 1) and Sign Q_proj^T (term 2), NBS blocks
     float4v s1[NBS], s2[NBS];
@@ -370,7 +362,7 @@ __global__ void __launch_bounds__(256) TQ_DEC_ATTN_ATTR decode_attn_lds_kernel(D
         }
     }
     // ---- lazy online softmax over the slab: the column reference m_run moves only
-    // when a score exceeds it by more than TAU; p = 2^(s - m_run - TAU) <= 1
+    // when a score exceeds it by more than TAU; p = 2^(s - m_run + PUP)
     float lmax = -INFINITY;
 #pragma unroll
     for (int j = 0; j < NBS; ++j) lmax = fmaxf(lmax, fmaxf(fmaxf(sc[j][0], sc[j][1]), fmaxf(sc[j][2], sc[j][3])));
@@ -386,7 +378,7 @@ __global__ void __launch_bounds__(256) TQ_DEC_ATTN_ATTR decode_attn_lds_kernel(D
         for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
       }
     }
-    const float m_use = (m_run == -INFINITY) ? 0.f : m_run + TAU;
+    const float m_use = (m_run == -INFINITY) ? 0.f : m_run - PUP;
     // ---- values: O^T += V^T (P * vn)^T, two 16-key blocks per 16x16x32 MFMA.  K-slot
     // 8lg + 4h + e of block pair jp is key 16(2jp + h) + 4lg + e: the B operand is the lane's
     // own P values of both blocks, and each A dword is one dim of a key pair (2c, 2c + 1),
@@ -394,7 +386,7 @@ __global__ void __launch_bounds__(256) TQ_DEC_ATTN_ATTR decode_attn_lds_kernel(D
     constexpr uint32_t M = odd_fields<VB>();
 #pragma unroll
     for (int jp = 0; jp < NBS / 2; ++jp) {
-      half8 pb, plo;
+      half8 pb;
       uint32_t w[2][4];  // value fields of keys 16(2jp + h) + 4lg + kk
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
@@ -404,10 +396,7 @@ __global__ void __launch_bounds__(256) TQ_DEC_ATTN_ATTR decode_attn_lds_kernel(D
         for (int e = 0; e < 4; ++e) {
           const float p = __builtin_amdgcn_exp2f(sc[j][e] - m_use);
           l_run += p;
-          const float pvv = p * nv[e];
-          const _Float16 hh = static_cast<_Float16>(pvv);
-          pb[4 * h + e] = hh;
-          if constexpr (PLO) plo[4 * h + e] = static_cast<_Float16>(pvv - static_cast<float>(hh));
+          pb[4 * h + e] = static_cast<_Float16>(p * nv[e]);
         }
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
@@ -436,7 +425,6 @@ __global__ void __launch_bounds__(256) TQ_DEC_ATTN_ATTR decode_attn_lds_kernel(D
           const half8 va = __builtin_bit_cast(half8, u32x4{value_pair<VB, i>(tV, f[0][0]), value_pair<VB, i>(tV, f[0][1]),
                                                            value_pair<VB, i>(tV, f[1][0]), value_pair<VB, i>(tV, f[1][1])});
           oacc[db] = mfma16x16x32(va, pb, oacc[db]);
-          if constexpr (PLO) oacc[db] = mfma16x16x32(va, plo, oacc[db]);
         });
       }
     }
@@ -476,9 +464,9 @@ __global__ void __launch_bounds__(256) TQ_DEC_ATTN_ATTR decode_attn_lds_kernel(D
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) my[(lg * 4 + e) * (D / 16) + db] = oacc[db][e];
+    for (int e = 0; e < 4; ++e) my[(lg * 4 + e) * (D / 16) + db] = oacc[db][e] * vcap;
   if (lg == 0) {
-    my[D] = (m_run == -INFINITY) ? m_run : m_run + TAU;
+    my[D] = (m_run == -INFINITY) ? m_run : m_run - PUP;
     my[D + 1] = l;
   }
   __syncthreads();
@@ -848,17 +836,16 @@ static bool decode_shape(int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
 
 // grid target of the fused decode attention: one round of resident blocks
 static int attn_target_blocks(int bits) {
-  if (TQ_DEC_ATTN_BLOCKS > 0) return TQ_DEC_ATTN_BLOCKS;
   static int cache[3][16] = {};
-  const void* k = bits == 2 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 2, TQ_DEC_ANB, TQ_DEC_AR, TQ_DEC_PLO != 0>)
-                : bits == 3 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 3, TQ_DEC_ANB, TQ_DEC_AR, TQ_DEC_PLO != 0>)
-                            : reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 4, TQ_DEC_ANB, TQ_DEC_AR, TQ_DEC_PLO != 0>);
+  const void* k = bits == 2 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 2, kAttnNbs, kAttnRing>)
+                : bits == 3 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 3, kAttnNbs, kAttnRing>)
+                            : reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 4, kAttnNbs, kAttnRing>);
   return resident_blocks(k, 256, cache[bits - 2]);
 }
 
 static DecodePlan plan_decode(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
   if (!decode_shape(Hq, Hkv, Sq, Sk, d, bits)) return DecodePlan{false, 0, 0, 0};
-  constexpr int slab = 64 * TQ_DEC_ANB;
+  constexpr int slab = 64 * kAttnNbs;
   DecodePlan p = plan_split(B, Hkv, Sk, attn_target_blocks(bits), slab, 2 * slab);
   const int C = (Hq / Hkv) * Sq;
   p.ws_bytes = static_cast<int64_t>(B) * Hkv * p.nsplit * C * static_cast<int64_t>(d + 2) * 4;
@@ -868,7 +855,7 @@ static DecodePlan plan_decode(int B, int Hq, int Hkv, int Sq, int Sk, int d, int
 static DecodePlan plan_scores(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
   if (!decode_shape(Hq, Hkv, Sq, Sk, d, bits)) return DecodePlan{false, 0, 0, 0};
   const int slab = 4 * score_slab_keys(bits);
-  return plan_split(B, Hkv, Sk, TQ_DEC_SCORE_BLOCKS, slab, 2 * slab);
+  return plan_split(B, Hkv, Sk, kScoreBlocks, slab, 2 * slab);
 }
 
 }  // namespace tq
@@ -890,7 +877,7 @@ bool decode_applies(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
 template <int BITS>
 static void launch_decode_attn(const DecodeArgs& a, hipStream_t s) {
   dim3 grid(a.nsplit, a.Hkv, a.B);
-  decode_attn_lds_kernel<128, BITS, TQ_DEC_ANB, TQ_DEC_AR, TQ_DEC_PLO != 0><<<grid, 256, 0, s>>>(a);
+  decode_attn_lds_kernel<128, BITS, kAttnNbs, kAttnRing><<<grid, 256, 0, s>>>(a);
 }
 
 int decode_scores(int64_t ldk, const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
