@@ -223,6 +223,39 @@ int64_t tq_attention_workspace_size(int32_t B, int32_t Hq, int32_t Hkv,
                                     int32_t Sq, int32_t Sk, int32_t d,
                                     int32_t bits);
 
+/* Size of the library's per-GPU scratch array used by tq_attention_fwd_kv_noalloc. */
+#define TQ_NOALLOC_SCRATCH_BYTES (16LL << 20)
+
+/* tq_attention_fwd_kv with no caller workspace and no device allocation: the split-K
+ * decode path keeps its per-split partials in a library-owned device array of
+ * TQ_NOALLOC_SCRATCH_BYTES (16 MiB) per GPU, held from the library's first use of that GPU
+ * until the process ends.  Same arguments, results and error behaviour as
+ * tq_attention_fwd_kv otherwise (bit-identical outputs for the same inputs).
+ *   - Shapes whose partials need more than the array (tq_attention_workspace_size >
+ *     tq_noalloc_scratch_bytes(), e.g. more than 16 MiB of (batch, kv head, split)
+ *     records) fail with TQ_EINVAL and a message; shapes off the split-K path use none.
+ *   - Every call on one GPU shares that GPU's array, which keeps the last call's contents:
+ *     calls that overlap in time on one GPU (other streams, other host threads) race.
+ *     Calls queued on one stream are ordered and safe.
+ *   - Calls no hipMalloc / hipFree or other allocating routine.
+ * No counterpart in the reference.  For callers that cannot allocate device memory: code
+ * under HIP graph capture, tight serving loops, harnesses that forbid allocation. */
+int tq_attention_fwd_kv_noalloc(const uint16_t* q_rot, const uint16_t* q_proj,
+                                const uint8_t* key_codes, const uint8_t* key_signs,
+                                const uint16_t* key_rn, const uint16_t* key_vn,
+                                const uint16_t* key_centroids_f16, int32_t bits,
+                                const uint8_t* val_codes, const uint16_t* val_vn,
+                                const float* val_centroids, int32_t val_bits,
+                                const uint16_t* val_pit_split, int32_t B, int32_t Hq,
+                                int32_t Hkv, int32_t Sq, int32_t Sk, int64_t kv_stride,
+                                int32_t d, float coeff, float scale, int32_t causal,
+                                const float* mask, int64_t smb, int64_t smh, int64_t smq,
+                                int64_t smk, void* out, int32_t out_dtype, int64_t sob,
+                                int64_t soh, int64_t sos, void* stream);
+
+/* TQ_NOALLOC_SCRATCH_BYTES as built into the library.  Utility; no reference counterpart. */
+int64_t tq_noalloc_scratch_bytes(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -26,6 +26,8 @@
 // on the value side is that of the decoded V^ = f16(Cv * vn).
 #include "tq_common.h"
 
+#include <mutex>
+
 namespace tq {
 
 #ifndef TQ_ATTN_WAVES
@@ -684,6 +686,79 @@ int tq_attention_fwd_kv(const uint16_t* q_rot, const uint16_t* q_proj, const uin
   a.sos = sos;
   dispatch_attn<false>(d, bits - 1, a, as_stream(stream));
   return launch_status("tq_attention_fwd");
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- allocation-free variant
+// The split-K decode partials of tq_attention_fwd_kv_noalloc live in this array, one copy
+// per GPU, held until the process ends.  Host code never passes `scratch` itself to a
+// kernel (in host code the name is a host-side stand-in, not a device address): the
+// device address comes from hipGetSymbolAddress, once per device, with that device current.
+namespace {
+constexpr int64_t kScratchBytes = TQ_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// device address of this GPU's scratch array (nullptr after setting the error message)
+void* device_scratch() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("tq_attention_fwd_kv_noalloc: no current HIP device (or device index >= %d)", kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("tq_attention_fwd_kv_noalloc: hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" {
+
+int64_t tq_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+int tq_attention_fwd_kv_noalloc(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* key_codes,
+                                const uint8_t* key_signs, const uint16_t* key_rn, const uint16_t* key_vn,
+                                const uint16_t* key_centroids_f16, int32_t bits, const uint8_t* val_codes,
+                                const uint16_t* val_vn, const float* val_centroids, int32_t val_bits,
+                                const uint16_t* val_pit_split, int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq,
+                                int32_t Sk, int64_t kv_stride, int32_t d, float coeff, float scale,
+                                int32_t causal, const float* mask, int64_t smb, int64_t smh, int64_t smq,
+                                int64_t smk, void* out, int32_t out_dtype, int64_t sob, int64_t soh,
+                                int64_t sos, void* stream) {
+  int st = check_common("tq_attention_fwd_kv_noalloc", B, Hq, Hkv, Sq, Sk, d, bits);
+  if (st != TQ_OK) return st;
+  void* ws = nullptr;
+  int64_t ws_bytes = 0;
+  if (val_bits == bits && static_cast<int64_t>(B) * Hq * Sq > 0) {
+    const int64_t need = decode_workspace_bytes(B, Hq, Hkv, Sq, Sk, d, bits);
+    TQ_REQUIRE(need <= kScratchBytes,
+               "tq_attention_fwd_kv_noalloc: this shape's split-K partials need %lld bytes, more than the "
+               "%lld-byte scratch array; use tq_attention_fwd_kv with a caller workspace",
+               (long long)need, (long long)kScratchBytes);
+    if (need > 0) {
+      ws = device_scratch();
+      if (!ws) return TQ_EHIP;
+      ws_bytes = need;
+    }
+  }
+  // every split record is written in full before the merge reads it: nothing to clear
+  return tq_attention_fwd_kv(q_rot, q_proj, key_codes, key_signs, key_rn, key_vn, key_centroids_f16, bits,
+                             val_codes, val_vn, val_centroids, val_bits, val_pit_split, B, Hq, Hkv, Sq, Sk,
+                             kv_stride, d, coeff, scale, causal, mask, smb, smh, smq, smk, out, out_dtype, sob,
+                             soh, sos, ws, ws_bytes, stream);
 }
 
 int tq_attention_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* key_codes,

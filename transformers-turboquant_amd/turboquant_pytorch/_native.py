@@ -54,8 +54,13 @@ _SIGNATURES = {
                             _i32, _i32, _i32, _i32, _i32, _i64, _i32, _f32, _f32, _i32,
                             _p, _i64, _i64, _i64, _i64, _p, _i32, _i64, _i64, _i64, _p, _i64, _p],
     "tq_attention_workspace_size": [_i32, _i32, _i32, _i32, _i32, _i32, _i32],
+    "tq_attention_fwd_kv_noalloc": [_p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _p, _i32, _p,
+                                    _i32, _i32, _i32, _i32, _i32, _i64, _i32, _f32, _f32, _i32,
+                                    _p, _i64, _i64, _i64, _i64, _p, _i32, _i64, _i64, _i64, _p],
+    "tq_noalloc_scratch_bytes": [],
 }
-_RESTYPE = {"tq_last_error": ctypes.c_char_p, "tq_out_cols": _i64, "tq_attention_workspace_size": _i64}
+_RESTYPE = {"tq_last_error": ctypes.c_char_p, "tq_out_cols": _i64, "tq_attention_workspace_size": _i64,
+            "tq_noalloc_scratch_bytes": _i64}
 
 EXPORTED = tuple(_SIGNATURES)
 
