@@ -134,31 +134,35 @@ int tq_decompress_values(const uint8_t* codes, const uint16_t* vn, int64_t n,
 /* Query preparation for compressed-domain scoring of q[B, Hq, Sq, d]
  * (element strides sqb, sqh, sqs; unit stride on d):
  *   q_rot  = f16(q Pi^T)                      -> f16 [B, Hq, Sq, d] contiguous
- *   q_proj = f16(q_rot S_eff^T), S_eff f16[m=d, d] -> f16 [B, Hq, Sq, d]
- * (q_proj accumulates in f32 from the f16 operands and is rounded once).
+ *   q_proj = q_rot S_eff^T, S_eff f16[m=d, d] -> f32 [B, Hq, Sq, d] contiguous
+ * q_proj is the f32 accumulation of the exact f16 products, as the reference's
+ * fp32 projection; its buffer must be 16-byte aligned for the fast path.
  * Replaces compressors.py:186-189 (q_rot, S_eff) and the per-query projection
- * of kernels/attention.py:155-167. */
+ * of kernels/attention.py:155-167 (fallback :453). */
 int tq_query_prep(const void* q, int32_t dtype, int32_t B, int32_t Hq,
                   int32_t Sq, int32_t d, int64_t sqb, int64_t sqh, int64_t sqs,
                   const uint16_t* pi_split, const uint16_t* s_eff_f16,
-                  uint16_t* q_rot, uint16_t* q_proj, void* stream);
+                  uint16_t* q_rot, float* q_proj, void* stream);
 
 /* Materialised asymmetric scores out f32 [B, Hq, Sq, Sk] (contiguous):
  *   out = vn * <q_rot, C[codes]> + coeff * rn * <q_proj, 2*sign - 1>
- * from q_rot / q_proj f16 [B, Hq, Sq, d] (tq_query_prep) and key planes of
+ * from q_rot f16 / q_proj f32 [B, Hq, Sq, d] (tq_query_prep; q_proj enters as
+ * f16 hi + lo, i.e. at f32 grade) and key planes of
  * [B, Hkv, Sk] rows; query head h reads kv head h / (Hq / Hkv).
  * centroids_f16 holds the 2^(bits-1) key centroids.  bits is the total key
  * bit budget (codes use bits-1 bits), as in the reference.
  * Replaces kernels/attention.py:274-372 (asymmetric_attention_scores; fallback
  * :380-461) and compressors.py:178-200. */
-int tq_attention_scores(const uint16_t* q_rot, const uint16_t* q_proj,
+int tq_attention_scores(const uint16_t* q_rot, const float* q_proj,
                         const uint8_t* key_codes, const uint8_t* key_signs,
                         const uint16_t* key_rn, const uint16_t* key_vn,
                         const uint16_t* centroids_f16, int32_t B, int32_t Hq,
                         int32_t Hkv, int32_t Sq, int32_t Sk, int32_t d,
                         int32_t bits, float coeff, float* out, void* stream);
 
-/* Fused compressed-domain attention (one attention layer's tail):
+/* Fused compressed-domain attention (one attention layer's tail).  q_proj f32 as in
+ * tq_attention_scores; the split-K decode kernels use it at f32 grade (hi + lo), the
+ * many-query kernels use its f16 rounding:
  *   s   = (vn*<q_rot,Ck[codes]> + coeff*rn*<q_proj, 2*sign-1>) * scale
  *         (+ mask[b, h, i, j] if mask != NULL) (causal: key j > i + Sk - Sq dropped)
  *   p   = softmax_j(s)                    (f32, online)
@@ -171,7 +175,7 @@ int tq_attention_scores(const uint16_t* q_rot, const uint16_t* q_proj,
  * Replaces the family forward tail families/qwen2.py:105-117 (same in
  * llama.py:222-233, deepseek.py, gpt2.py:90-110): compress -> scores -> /sqrt(d)
  * -> +mask -> softmax -> decompress(V) -> P V. */
-int tq_attention_fwd(const uint16_t* q_rot, const uint16_t* q_proj,
+int tq_attention_fwd(const uint16_t* q_rot, const float* q_proj,
                      const uint8_t* key_codes, const uint8_t* key_signs,
                      const uint16_t* key_rn, const uint16_t* key_vn,
                      const uint16_t* key_centroids_f16, int32_t bits,
@@ -192,14 +196,14 @@ int tq_attention_fwd(const uint16_t* q_rot, const uint16_t* q_proj,
  * appends tokens in place.  No counterpart in the reference, which disables
  * the KV cache (patch.py:81); the tensor-level concept is
  * turboquant.py:199-286 (TurboQuantKVCache). */
-int tq_attention_scores_kv(const uint16_t* q_rot, const uint16_t* q_proj,
+int tq_attention_scores_kv(const uint16_t* q_rot, const float* q_proj,
                            const uint8_t* key_codes, const uint8_t* key_signs,
                            const uint16_t* key_rn, const uint16_t* key_vn,
                            const uint16_t* centroids_f16, int32_t B, int32_t Hq,
                            int32_t Hkv, int32_t Sq, int32_t Sk,
                            int64_t kv_stride, int32_t d, int32_t bits,
                            float coeff, float* out, void* stream);
-int tq_attention_fwd_kv(const uint16_t* q_rot, const uint16_t* q_proj,
+int tq_attention_fwd_kv(const uint16_t* q_rot, const float* q_proj,
                         const uint8_t* key_codes, const uint8_t* key_signs,
                         const uint16_t* key_rn, const uint16_t* key_vn,
                         const uint16_t* key_centroids_f16, int32_t bits,
@@ -240,7 +244,7 @@ int64_t tq_attention_workspace_size(int32_t B, int32_t Hq, int32_t Hkv,
  *   - Calls no hipMalloc / hipFree or other allocating routine.
  * No counterpart in the reference.  For callers that cannot allocate device memory: code
  * under HIP graph capture, tight serving loops, harnesses that forbid allocation. */
-int tq_attention_fwd_kv_noalloc(const uint16_t* q_rot, const uint16_t* q_proj,
+int tq_attention_fwd_kv_noalloc(const uint16_t* q_rot, const float* q_proj,
                                 const uint8_t* key_codes, const uint8_t* key_signs,
                                 const uint16_t* key_rn, const uint16_t* key_vn,
                                 const uint16_t* key_centroids_f16, int32_t bits,

@@ -141,7 +141,7 @@ def test_ragged_row_count_last_partial_tile():
 
 
 def test_query_prep_at_prefill_scale():
-    """q_rot / q_proj of 32 heads x 8192 rows (262,144 rows) within the f16 rounding bound."""
+    """q_rot (f16 rounding bound) and q_proj (f32 dot-product bound) of 32 heads x 8192 rows."""
     _case(what="query prep 262144 rows")
     g = torch.Generator(device=DEV).manual_seed(11)
     q = (torch.randn(1, 32, 8192, 128, device=DEV, generator=g) * 3).to(torch.bfloat16)
@@ -161,5 +161,4 @@ def test_query_prep_at_prefill_scale():
         assert excess.max() <= 2.0 ** -17, r0
         proj_ref = got[sl] @ se16.T
         proj_abs = np.abs(got[sl]) @ np.abs(se16).T
-        assert np.all(np.abs(gp[sl] - proj_ref) <= 2.0 ** -11 * np.abs(proj_ref) + 2.0 ** -25
-                      + 2.0 ** -17 * proj_abs), r0
+        assert np.all(np.abs(gp[sl] - proj_ref) <= 2.0 ** -24 * np.abs(proj_ref) + 2.0 ** -17 * proj_abs), r0

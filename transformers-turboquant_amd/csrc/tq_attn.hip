@@ -4,7 +4,9 @@
 // Scores follow the reference estimator (kernels/attention.py:380-461,
 // compressors.py:178-200):
 //   s(q, k) = vn_k * <q_rot, Ck[codes_k]> + coeff * rn_k * <q_proj, 2*sign_k - 1>
-// with q_rot = f16(q Pi^T) and q_proj = f16(q_rot S_eff^T) from tq_query_prep.
+// with q_rot = f16(q Pi^T) and q_proj = q_rot S_eff^T (f32) from tq_query_prep; scores
+// mode takes q_proj as f16 hi + lo (two MFMAs against the exact +-1 operand), attention
+// mode its f16 rounding.
 // Both inner products run as v_mfma_f32_16x16x32_f16 chains with exact f16
 // key operands (f16 centroids, +-1), so term 1 is exactly the reference's f32
 // accumulation of f16 products; the per-key factors vn and coeff * rn are
@@ -66,7 +68,8 @@ struct ATile {
 };
 
 struct AttnArgs {
-  const uint16_t *q_rot, *q_proj;
+  const uint16_t* q_rot;
+  const float* q_proj;  // f32: f16 hi + lo operands in scores mode, the f16 rounding otherwise
   const uint8_t *kcodes, *ksigns;
   const uint16_t *krn, *kvn, *kcent;
   const uint8_t* vcodes;
@@ -156,6 +159,7 @@ __global__ void __launch_bounds__(64 * TQ_ATTN_WAVES, TQ_ATTN_MINBLK) attn_kerne
   int col_i[NBW], col_h[NBW];
   bool col_ok[NBW];
   half8 qr[KS][NBW], qp[KS][NBW];
+  [[maybe_unused]] half8 qlo[SCORES ? KS : 1][NBW];  // scores mode: lo parts of q_proj
 #pragma unroll
   for (int nb = 0; nb < NBW; ++nb) {
     const int r = (wave * NBW + nb) * 16 + l16;
@@ -168,7 +172,10 @@ __global__ void __launch_bounds__(64 * TQ_ATTN_WAVES, TQ_ATTN_MINBLK) attn_kerne
     for (int ks = 0; ks < KS; ++ks) {
       const int d0 = ks * 32 + lg * 8;
       qr[ks][nb] = col_ok[nb] ? *reinterpret_cast<const half8*>(a.q_rot + qrow + d0) : half8{};
-      qp[ks][nb] = col_ok[nb] ? *reinterpret_cast<const half8*>(a.q_proj + qrow + d0) : half8{};
+      half8 hi = half8{}, lo = half8{};
+      if (col_ok[nb]) split8(a.q_proj + qrow + d0, hi, lo);
+      qp[ks][nb] = hi;
+      if constexpr (SCORES) qlo[ks][nb] = lo;
     }
   }
 
@@ -341,6 +348,7 @@ __global__ void __launch_bounds__(64 * TQ_ATTN_WAVES, TQ_ATTN_MINBLK) attn_kerne
         for (int nb = 0; nb < NBW; ++nb) {
           sacc[mb][nb] = mfma16x16x32(ka, qr[ks][nb], sacc[mb][nb]);
           tacc[mb][nb] = mfma16x16x32(sa, qp[ks][nb], tacc[mb][nb]);
+          if constexpr (SCORES) tacc[mb][nb] = mfma16x16x32(sa, qlo[ks][nb], tacc[mb][nb]);
         }
       }
     }
@@ -539,17 +547,17 @@ namespace tq {
 int64_t decode_workspace_bytes(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits);
 bool decode_applies(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits);
 bool prefill_applies(int Hq, int Hkv, int d, int bits, int val_bits);
-int prefill_attention(int64_t ldk, const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
+int prefill_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, const uint8_t* kcodes,
                       const uint8_t* ksigns, const uint16_t* krn, const uint16_t* kvn, const uint16_t* kcent,
                       int bits, const uint8_t* vcodes, const uint16_t* vvn, const float* vcent,
                       const uint16_t* vpit, int B, int Hq, int Hkv, int Sq, int Sk, float coeff, float scale,
                       int causal, const float* mask, int64_t smb, int64_t smh, int64_t smq, int64_t smk, void* out,
                       int out_dtype, int64_t sob, int64_t soh, int64_t sos, hipStream_t s);
-int decode_scores(int64_t ldk, const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
+int decode_scores(int64_t ldk, const uint16_t* q_rot, const float* q_proj, const uint8_t* kcodes,
                   const uint8_t* ksigns, const uint16_t* krn, const uint16_t* kvn, const uint16_t* kcent,
                   int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits, float coeff, float* out,
                   hipStream_t s);
-int decode_attention(int64_t ldk, const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
+int decode_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, const uint8_t* kcodes,
                      const uint8_t* ksigns, const uint16_t* krn, const uint16_t* kvn, const uint16_t* kcent,
                      int bits, const uint8_t* vcodes, const uint16_t* vvn, const float* vcent32,
                      const uint16_t* vpit, int B, int Hq, int Hkv, int Sq, int Sk, int d, float coeff,
@@ -592,7 +600,7 @@ int64_t tq_attention_workspace_size(int32_t B, int32_t Hq, int32_t Hkv, int32_t 
   return decode_workspace_bytes(B, Hq, Hkv, Sq, Sk, d, bits);
 }
 
-int tq_attention_scores_kv(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* key_codes,
+int tq_attention_scores_kv(const uint16_t* q_rot, const float* q_proj, const uint8_t* key_codes,
                            const uint8_t* key_signs, const uint16_t* key_rn, const uint16_t* key_vn,
                            const uint16_t* centroids_f16, int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq,
                            int32_t Sk, int64_t kv_stride, int32_t d, int32_t bits, float coeff, float* out,
@@ -624,7 +632,7 @@ int tq_attention_scores_kv(const uint16_t* q_rot, const uint16_t* q_proj, const 
   return launch_status("tq_attention_scores");
 }
 
-int tq_attention_fwd_kv(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* key_codes,
+int tq_attention_fwd_kv(const uint16_t* q_rot, const float* q_proj, const uint8_t* key_codes,
                         const uint8_t* key_signs, const uint16_t* key_rn, const uint16_t* key_vn,
                         const uint16_t* key_centroids_f16, int32_t bits, const uint8_t* val_codes,
                         const uint16_t* val_vn, const float* val_centroids, int32_t val_bits,
@@ -729,7 +737,7 @@ extern "C" {
 
 int64_t tq_noalloc_scratch_bytes(void) { return kScratchBytes; }
 
-int tq_attention_fwd_kv_noalloc(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* key_codes,
+int tq_attention_fwd_kv_noalloc(const uint16_t* q_rot, const float* q_proj, const uint8_t* key_codes,
                                 const uint8_t* key_signs, const uint16_t* key_rn, const uint16_t* key_vn,
                                 const uint16_t* key_centroids_f16, int32_t bits, const uint8_t* val_codes,
                                 const uint16_t* val_vn, const float* val_centroids, int32_t val_bits,
@@ -761,7 +769,7 @@ int tq_attention_fwd_kv_noalloc(const uint16_t* q_rot, const uint16_t* q_proj, c
                              soh, sos, ws, ws_bytes, stream);
 }
 
-int tq_attention_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* key_codes,
+int tq_attention_scores(const uint16_t* q_rot, const float* q_proj, const uint8_t* key_codes,
                         const uint8_t* key_signs, const uint16_t* key_rn, const uint16_t* key_vn,
                         const uint16_t* centroids_f16, int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq,
                         int32_t Sk, int32_t d, int32_t bits, float coeff, float* out, void* stream) {
@@ -769,7 +777,7 @@ int tq_attention_scores(const uint16_t* q_rot, const uint16_t* q_proj, const uin
                                 Sq, Sk, Sk, d, bits, coeff, out, stream);
 }
 
-int tq_attention_fwd(const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* key_codes,
+int tq_attention_fwd(const uint16_t* q_rot, const float* q_proj, const uint8_t* key_codes,
                      const uint8_t* key_signs, const uint16_t* key_rn, const uint16_t* key_vn,
                      const uint16_t* key_centroids_f16, int32_t bits, const uint8_t* val_codes,
                      const uint16_t* val_vn, const float* val_centroids, int32_t val_bits,

@@ -103,6 +103,29 @@ struct DivBy {
   }
 };
 
+// Eight f32 values as f16 hi + lo parts (hi = f16(x), lo = f16(x - hi)): against an
+// exact f16 operand (+-1 signs) two MFMAs reproduce an f32 operand to ~2^-22.
+__device__ __forceinline__ void split8(const float* p, half8& hi, half8& lo) {
+  const float4v a = *reinterpret_cast<const float4v*>(p);
+  const float4v b = *reinterpret_cast<const float4v*>(p + 4);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float x = j < 4 ? a[j] : b[j - 4];
+    hi[j] = static_cast<_Float16>(x);
+    lo[j] = static_cast<_Float16>(x - static_cast<float>(hi[j]));
+  }
+}
+__device__ __forceinline__ half8 round8(const float* p) {
+  half8 hi, lo;
+  split8(p, hi, lo);
+  return hi;
+}
+
+// The value of lane l ^ 8 (a rotation by 8 within each row of 16 lanes), through DPP.
+__device__ __forceinline__ float dpp_row_ror8(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xF, 0xF, false));
+}
+
 // Split a value (already scaled by kSplit) into f16 hi + lo parts.
 __device__ __forceinline__ void split_f16(float v, _Float16& hi, _Float16& lo) {
   hi = static_cast<_Float16>(v);

@@ -391,7 +391,8 @@ struct PrepArgs {
   int B, Hq, Sq;
   int64_t sqb, sqh, sqs;
   const uint16_t *pi, *seff;
-  uint16_t *q_rot, *q_proj;
+  uint16_t* q_rot;
+  float* q_proj;
 };
 
 template <int D, int DT>
@@ -466,8 +467,9 @@ __global__ void __launch_bounds__(256) query_prep_kernel(PrepArgs a) {
     }
   }
   __syncthreads();
-  // q_proj = f16(q_rot S_eff^T), f32 accumulation of exact f16 products
-  // (kernels/attention.py:158-167); S_eff is used unscaled, hi part only
+  // q_proj = q_rot S_eff^T in f32: f32 accumulation of exact f16 products, as the reference's
+  // fp32 q_rot.float() @ S_eff.float().T (kernels/attention.py:158-167, :453); S_eff is used
+  // unscaled, hi part only
   stage_gemm<D, false, false>(A, s_sc, a.seff, acc);
 #pragma unroll
   for (int t = 0; t < T::TPW; ++t) {
@@ -477,7 +479,7 @@ __global__ void __launch_bounds__(256) query_prep_kernel(PrepArgs a) {
     if (gr >= n) continue;
     const float inv = s_inv[row];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) a.q_proj[gr * D + col + e] = f2h(acc[t][e] * inv);
+    for (int e = 0; e < 4; ++e) a.q_proj[gr * D + col + e] = acc[t][e] * inv;
   }
 }
 
@@ -521,7 +523,8 @@ struct TileArgs {
   uint8_t *codes, *signs;
   uint16_t *rn, *vn;
   float *y_out, *proj_out;
-  uint16_t *q_rot, *q_proj;
+  uint16_t* q_rot;
+  float* q_proj;
 };
 
 template <int D, int NW_ = 8>
@@ -845,15 +848,21 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
       for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
         for (int j = 0; j < 8; ++j) bh[ks][j] = static_cast<_Float16>(static_cast<float>(bh[ks][j]) * sc2);
-      // q_proj = f16(q_rot S_eff^T): f32 accumulation of exact f16 products (kernels/attention.py:158-167)
+      // q_proj = q_rot S_eff^T in f32: f32 accumulation of exact f16 products, as the
+      // reference's fp32 projection (kernels/attention.py:158-167, :453)
       row_gemm<D, false, false>(P2, P2, bh, bl, acc, l16, g);
       if (gr < a.n) {
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          half8 o;
+          float4v o0, o1;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) o[j] = static_cast<_Float16>(acc_at(acc, ks, j) * inv2);
-          *reinterpret_cast<half8*>(a.q_proj + gr * D + 32 * ks + 8 * g) = o;
+          for (int j = 0; j < 4; ++j) {
+            o0[j] = acc_at(acc, ks, j) * inv2;
+            o1[j] = acc_at(acc, ks, j + 4) * inv2;
+          }
+          float* dst = a.q_proj + gr * D + 32 * ks + 8 * g;
+          *reinterpret_cast<float4v*>(dst) = o0;
+          *reinterpret_cast<float4v*>(dst + 4) = o1;
         }
       }
       raw = nxt;
@@ -1160,14 +1169,14 @@ int tq_decompress_values(const uint8_t* codes, const uint16_t* vn, int64_t n, in
 
 int tq_query_prep(const void* q, int32_t dtype, int32_t B, int32_t Hq, int32_t Sq, int32_t d,
                   int64_t sqb, int64_t sqh, int64_t sqs, const uint16_t* pi_split,
-                  const uint16_t* s_eff_f16, uint16_t* q_rot, uint16_t* q_proj, void* stream) {
+                  const uint16_t* s_eff_f16, uint16_t* q_rot, float* q_proj, void* stream) {
   TQ_CHECK_DD("tq_query_prep", d, dtype);
   TQ_REQUIRE(B >= 0 && Hq >= 0 && Sq >= 0, "tq_query_prep: bad shape");
   const int64_t n = static_cast<int64_t>(B) * Hq * Sq;
   if (n == 0) return TQ_OK;
   TQ_REQUIRE(q && pi_split && s_eff_f16 && q_rot && q_proj, "tq_query_prep: null pointer");
   if (tile_applies(d, n, 1) && reinterpret_cast<uintptr_t>(q_rot) % 8 == 0 &&
-      reinterpret_cast<uintptr_t>(q_proj) % 8 == 0) {
+      reinterpret_cast<uintptr_t>(q_proj) % 16 == 0) {
     TileArgs t{};
     t.x = q; t.n = n; t.H = make_div(static_cast<uint32_t>(Hq)); t.S = make_div(static_cast<uint32_t>(Sq));
     t.sb = sqb; t.sh = sqh; t.ss = sqs; t.vec = tile_vec(q, dtype, sqb, sqh, sqs);

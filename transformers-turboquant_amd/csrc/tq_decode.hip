@@ -1,162 +1,8 @@
-// Decode-shaped compressed attention: few query rows per head (G * Sq <= 16
-// (query row, query head) columns per kv head) against long compressed
-// caches.  The work is HBM-bound: every key and value record is streamed
-// once per step, so the kernels are organised around the byte stream.
-//
-// Split-K: a block of 4 wave64 owns a chunk of keys of one (batch, kv head).
-// Each wave streams its own slabs of the packed planes into a private LDS ring
-// with direct-to-LDS buffer loads (16 B per lane, several slabs in flight, no
-// block barriers) and builds MFMA operands from the packed bytes through small
-// LDS lookup tables; the k-slot order of each MFMA is permuted so that a lane's
-// operand bytes are one contiguous field of a packed row:
-//   scores     S = Q K^T (16x16x32), keys on the N side: lane (key n, group g)
-//              supplies dims g*D/4 + ks*8 + 0..7 of its key at k-step ks and
-//              ends with 4 columns of its own key
-//   attention  S^T = K Q^T (16x16x32), keys on the M side, so the accumulator
-//              is the P^T operand of O^T += V^T P^T (16x16x16); O^T row m of
-//              block db is dim m*(D/16)+db, so a lane's value operand comes
-//              from one contiguous code field
-// In attention mode the (m, l, O) state of the 4 waves is merged in LDS into
-// one partial per block; decode_merge_kernel combines the splits, normalises
-// and applies Pi_v.  In scores mode each block writes its keys' f32 scores.
-#include "tq_common.h"
-#include "tq_stream.h"
-
-// Launch shapes (measured on MI355X at 16 x 32k keys, bits 3):
-//   scores     wave slabs of score_slab_keys(bits) keys, score_ring(bits) slots in
-//              flight, grids of about kScoreBlocks blocks: many short blocks balance
-//              the last round better than one persistent stream per CU (57 vs 62-66 us)
-//   attention  wave slabs of 16 * kAttnNbs keys in kAttnRing slots, a grid of one
-//              round of resident blocks (4 per CU at 128 VGPRs: 1024 on 256 CUs,
-//              8% faster than 768 blocks at 3 waves per SIMD)
-// Scores: 32-key slabs in a 3-slot ring at bits 3-4 (22 KB of LDS, 6 blocks per CU),
-// 64-key slabs in 2 slots at bits 2, where the shorter slabs' per-slab overhead is a
-// larger share of the lighter decode: bits 3 56.3 vs 57.8 us, bits 4 68.2 vs 69.1 us,
-// bits 2 48.0 vs 46.5 us for 32/3 against 64/2.
-constexpr int kScoreBlocks = 4096;
-constexpr int kAttnNbs = 2;
-constexpr int kAttnRing = 2;
-constexpr int score_ring(int bits) { return bits == 2 ? 2 : 3; }
-constexpr int score_slab_keys(int bits) { return bits == 2 ? 64 : 32; }
-#define TQ_DEC_ATTN_ATTR __attribute__((amdgpu_waves_per_eu(4)))
+// Decode-shaped fused attention (split-K over keys) and the merge of the splits;
+// the shared argument block, lookup tables and split planning are in tq_decode.h.
+#include "tq_decode.h"
 
 namespace tq {
-
-
-struct DecodeArgs {
-  const uint16_t *q_rot, *q_proj;
-  const uint8_t *kcodes, *ksigns;
-  const uint16_t *krn, *kvn, *kcent;
-  const uint8_t* vcodes;
-  const uint16_t* vvn;
-  const float* vcent;            // f32 value centroids (tables hold their f16 values)
-  int B, Hq, Hkv, Sq, Sk, G, C;  // C = G * Sq valid columns
-  int64_t ldk;                   // rows between consecutive (batch, kv head) planes (>= Sk)
-  int nsplit, chunk;             // keys per block (multiple of 64)
-  float coeff, scale;
-  int causal;
-  const float* mask;
-  int64_t smb, smh, smq, smk;
-  float* scores;                 // scores mode: f32 [B, Hq, Sq, Sk]
-  float *part_o, *part_ml;       // attention mode partials
-};
-
-
-// odd VB-bit fields of 8 consecutive fields
-template <int VB>
-constexpr uint32_t odd_fields() {
-  return VB == 2 ? 0xCCCCu : (VB == 3 ? 0xE38E38u : 0xF0F0F0F0u);
-}
-
-// Pair-table entry I (two f16 values) of a value word whose fields are VB bits each, LSB
-// first: the fields nib4x2 (VB 2), six4x2 (VB 3) and byte4x2 (VB 4) read as entry I
-template <int VB, int I>
-__device__ __forceinline__ uint32_t value_pair(const uint8_t* t, uint32_t w) {
-  static_assert(I >= 0 && I < 4, "four pair fields per word");
-  if constexpr (VB == 2) {
-    constexpr uint32_t m = 0x3Cu;
-    return lds32(t, and_byte<I / 2>(m, (I & 1) ? (w >> 2) : (w << 2)));
-  } else if constexpr (VB == 3) {
-    constexpr uint32_t m = 0xFCu;
-    if constexpr (I == 0) return lds32(t, and_byte<0>(m, w << 2));
-    else if constexpr (I == 1) return lds32(t, and_byte<0>(m, w >> 4));
-    else if constexpr (I == 2) return lds32(t, and_byte<1>(m, w >> 2));
-    else return lds32(t, and_byte<2>(m, w));
-  } else {
-    return lds32(t, byte_x4<I>(w));
-  }
-}
-
-// ---------------------------------------------------------------- small tables
-// Lookup tables of at most 32 dwords give every entry its own LDS bank, so the
-// data-dependent lookups of a wave never conflict (64-entry tables share a bank
-// between two entries).  Entries are indexed by nibbles / 6-bit fields of the
-// packed rows:
-//   sign table   16 x half4: 4 sign bits -> 4 x (+-1)
-//   key table    KB=1: 16 x half4 (4 codes) | KB=2: 16 x half2 (2 codes) | KB=3: 64 x half2
-//   value table  VB=2: 16 x half2 | VB=3: 64 x half2 | VB=4: 256 x half2
-template <int BITS>
-struct SmallLuts {
-  static constexpr int KB = BITS - 1, VB = BITS;
-  static constexpr int SGN_BYTES = 16 * 8;
-  static constexpr int KEY_BYTES = (KB == 1) ? 16 * 8 : (KB == 2 ? 16 * 4 : 64 * 4);
-  static constexpr int VAL_BYTES = (VB == 2) ? 16 * 4 : (VB == 3 ? 64 * 4 : 256 * 4);
-  static constexpr int SGN_OFF = 0, KEY_OFF = SGN_BYTES, VAL_OFF = SGN_BYTES + KEY_BYTES;
-  static constexpr int BYTES = VAL_OFF + VAL_BYTES;
-};
-
-template <int BITS, bool VALUES>
-__device__ __forceinline__ void build_small_luts(const DecodeArgs& a, uint8_t* t, int tid) {
-  using L = SmallLuts<BITS>;
-  constexpr int KB = L::KB, VB = L::VB;
-  if (tid < 16) {
-    half4 v;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = ((tid >> j) & 1) ? static_cast<_Float16>(1.f) : static_cast<_Float16>(-1.f);
-    *reinterpret_cast<half4*>(t + L::SGN_OFF + tid * 8) = v;
-  }
-  auto kc = [&](int i) { return __builtin_bit_cast(_Float16, a.kcent[i]); };
-  if constexpr (KB == 1) {
-    if (tid < 16) {
-      half4 v;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = kc((tid >> j) & 1);
-      *reinterpret_cast<half4*>(t + L::KEY_OFF + tid * 8) = v;
-    }
-  } else {
-    constexpr int N = (KB == 2) ? 16 : 64;
-    if (tid < N) {
-      half2v v;
-      v[0] = kc(tid & ((1 << KB) - 1));
-      v[1] = kc(tid >> KB);
-      *reinterpret_cast<half2v*>(t + L::KEY_OFF + tid * 4) = v;
-    }
-  }
-  if constexpr (VALUES) {
-    constexpr int N = (VB == 2) ? 16 : (VB == 3 ? 64 : 256);
-    if (tid < N) {
-      half2v v;
-      v[0] = static_cast<_Float16>(a.vcent[tid & ((1 << VB) - 1)]);
-      v[1] = static_cast<_Float16>(a.vcent[tid >> VB]);
-      *reinterpret_cast<half2v*>(t + L::VAL_OFF + tid * 4) = v;
-    }
-  }
-}
-
-// Key operand of k-step KS: dims KS*8 .. KS*8+7 of the lane's 32-dim field
-template <int KB, int KW32, int KS>
-__device__ __forceinline__ half8 key_operand(const uint8_t* t, const uint32_t (&k)[KW32]) {
-  if constexpr (KB == 1) {
-    return nib2x4<KS>(t, k[0]);
-  } else if constexpr (KB == 2) {
-    return nib4x2<2 * (KS & 1)>(t, k[KS >> 1]);
-  } else {
-    constexpr int bit = 24 * KS, wi = bit >> 5, sh = bit & 31;
-    const uint32_t lo32 = k[wi];
-    const uint32_t hi32 = (wi + 1 < KW32) ? k[wi + 1] : 0u;
-    return six4x2(t, sh ? __builtin_amdgcn_alignbit(hi32, lo32, sh) : lo32);
-  }
-}
 
 // Fused decode attention, LDS-staged.  Each wave streams 64-key slabs of the key
 // codes, sign bits, value codes and the three norm planes straight into its own
@@ -165,8 +11,9 @@ __device__ __forceinline__ half8 key_operand(const uint8_t* t, const uint32_t (&
 // the slot.  Lane (column l16, group lg) ends each 16-key block with the scores
 // of keys 4*lg + e for its own column, which is the P^T operand layout of the
 // value MFMA, so P never leaves registers.
-template <int D, int BITS, int NBS, int R>
-__global__ void __launch_bounds__(256) TQ_DEC_ATTN_ATTR decode_attn_lds_kernel(DecodeArgs a) {
+template <int D, int BITS, int NBS, int R, bool PACK>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PACK ? 4 : 3)))
+decode_attn_lds_kernel(DecodeArgs a) {
   static_assert(D == 128, "decode kernel is built for head_dim 128");
   using L = SmallLuts<BITS>;
   constexpr int KB = L::KB, VB = L::VB;
@@ -207,16 +54,31 @@ __global__ void __launch_bounds__(256) TQ_DEC_ATTN_ATTR decode_attn_lds_kernel(D
 
   build_small_luts<BITS, true>(a, luts, tid);
 
-  const bool col_ok = l16 < a.C;
-  const int qi = col_ok ? l16 / a.G : 0, h = hkv * a.G + (col_ok ? l16 % a.G : 0);
+  // q_proj enters term 2 as f16 hi + lo.  PACK (C <= 8): B column l16 < 8 carries query
+  // column l16 (q_rot, hi), column l16 + 8 carries the same column's lo part (q_rot zero);
+  // after the MFMAs lane l16 adds lane l16 + 8's term 2 (DPP row rotate by 8).  Otherwise
+  // the lo parts take a second MFMA per k-step.
+  const int c = PACK ? (l16 & 7) : l16;
+  const bool lo_col = PACK && l16 >= 8;
+  const bool c_ok = c < a.C;
+  const bool col_ok = c_ok && !lo_col;
+  const int qi = c_ok ? c / a.G : 0, h = hkv * a.G + (c_ok ? c % a.G : 0);
   half8 qr[KS], qp[KS];
+  [[maybe_unused]] half8 ql[PACK ? 1 : KS];
   {
     const int64_t qrow = ((static_cast<int64_t>(b) * a.Hq + h) * a.Sq + qi) * D;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int d0 = lg * (D / 4) + ks * 8;
-      qr[ks] = col_ok ? *reinterpret_cast<const half8*>(a.q_rot + qrow + d0) : half8{};
-      qp[ks] = col_ok ? *reinterpret_cast<const half8*>(a.q_proj + qrow + d0) : half8{};
+      half8 hi = half8{}, lo = half8{};
+      if (c_ok) split8(a.q_proj + qrow + d0, hi, lo);
+      qr[ks] = (c_ok && !lo_col) ? *reinterpret_cast<const half8*>(a.q_rot + qrow + d0) : half8{};
+      if constexpr (PACK) {
+        qp[ks] = lo_col ? lo : hi;
+      } else {
+        qp[ks] = hi;
+        ql[ks] = lo;
+      }
     }
   }
 
@@ -333,11 +195,17 @@ __global__ void __launch_bounds__(256) TQ_DEC_ATTN_ATTR decode_attn_lds_kernel(D
       const uint32_t sw = *reinterpret_cast<const uint32_t*>(src + OFF_S + (16 * j + l16) * SC + lg * 4);
       s1[j] = float4v{0.f, 0.f, 0.f, 0.f};
       s2[j] = float4v{0.f, 0.f, 0.f, 0.f};
-      static_for<KS>([&](auto c) {
-        constexpr int ks = decltype(c)::value;
+      static_for<KS>([&](auto cc) {
+        constexpr int ks = decltype(cc)::value;
         s1[j] = mfma16x16x32(key_operand<KB, KW32, ks>(tK, kw), qr[ks], s1[j]);
-        s2[j] = mfma16x16x32(nib2x4<ks>(tS, sw), qp[ks], s2[j]);
+        const half8 sg = nib2x4<ks>(tS, sw);
+        s2[j] = mfma16x16x32(sg, qp[ks], s2[j]);
+        if constexpr (!PACK) s2[j] = mfma16x16x32(sg, ql[ks], s2[j]);
       });
+      if constexpr (PACK) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s2[j][e] += dpp_row_ror8(s2[j][e]);
+      }
     }
     // ---- log2-domain scores of keys ks0 + 16j + 4lg + e for this column
     float sc[NBS][4];
@@ -492,169 +360,6 @@ __global__ void __launch_bounds__(256) TQ_DEC_ATTN_ATTR decode_attn_lds_kernel(D
   }
 }
 
-// Scores: each wave DMAs NK-key slabs of the code, sign and norm planes into its
-// own R-slot LDS ring (16 B per lane; nothing is held in registers while in
-// flight) and scores them with the keys on the MFMA's N side, so lane (key l16,
-// group lg) ends with columns 4*lg + e of its own key: the two norms are
-// per-lane scalars and each column's 16 scores leave as one 64-byte run.
-template <int D, int BITS, int R, int NK>
-__global__ void __launch_bounds__(256) decode_scores_kernel(DecodeArgs a) {
-  static_assert(D == 128, "decode kernel is built for head_dim 128");
-  static_assert(R >= 2 && R <= 4, "ring of 2 to 4 slots");
-  static_assert(NK == 32 || NK == 64, "slabs of 32 or 64 keys");
-  using L = SmallLuts<BITS>;
-  constexpr int KB = L::KB;
-  constexpr int KS = D / 32;
-  constexpr int KC = D * KB / 8, SC = D / 8;
-  constexpr int KLANE = KC / 4;
-  constexpr int KW32 = KLANE / 4;
-  constexpr int NBS = NK / 16;
-  constexpr int SLAB = 4 * NK;           // keys per block slab
-  constexpr int OFF_K = 0, OFF_S = NK * KC, OFF_N = OFF_S + NK * SC;
-  constexpr int NRM = NK * 4;            // one norm plane: a dword per key
-  constexpr int SLOT = OFF_N + 2 * NRM;
-
-  __shared__ __attribute__((aligned(16))) uint8_t luts[L::BYTES];
-  __shared__ __attribute__((aligned(16))) uint8_t stage[4 * R * SLOT];
-  const uint8_t* tS = luts + L::SGN_OFF;
-  const uint8_t* tK = luts + L::KEY_OFF;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int l16 = lane & 15, lg = lane >> 4;
-  const int split = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
-  const int64_t bh = static_cast<int64_t>(b) * a.Hkv + hkv;
-
-  build_small_luts<BITS, false>(a, luts, tid);
-
-  // A operand: query column l16 (row i, head h), dims lg*D/4 + ks*8 + 0..7
-  half8 qr[KS], qp[KS];
-  {
-    const bool ok = l16 < a.C;
-    const int qi = ok ? l16 / a.G : 0, h = hkv * a.G + (ok ? l16 % a.G : 0);
-    const int64_t qrow = ((static_cast<int64_t>(b) * a.Hq + h) * a.Sq + qi) * D;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int d0 = lg * (D / 4) + ks * 8;
-      qr[ks] = ok ? *reinterpret_cast<const half8*>(a.q_rot + qrow + d0) : half8{};
-      qp[ks] = ok ? *reinterpret_cast<const half8*>(a.q_proj + qrow + d0) : half8{};
-    }
-  }
-
-  const int kbeg = split * a.chunk;
-  const int kend = min(a.Sk, kbeg + a.chunk);
-  const float fb = a.coeff;
-
-  // output: the C score rows of this (b, kv head) are contiguous [C][Sk] f32
-  // (head h = hkv*G + c%G, query row c/G); invalid columns aim past the end and
-  // are dropped by the store's range check
-  const float* pout = a.scores + (static_cast<int64_t>(b) * a.Hq + hkv * a.G) * a.Sq * a.Sk;
-  const uint32_t out_bytes = static_cast<uint32_t>(a.C) * a.Sk * 4;
-  uint32_t oo[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int c = 4 * lg + e;
-    oo[e] = c < a.C ? static_cast<uint32_t>((c % a.G) * a.Sq + c / a.G) * a.Sk * 4 + 4 * l16 : kOutOfRange;
-  }
-
-  const int64_t g0 = bh * a.ldk;
-  const uint8_t* pk = a.kcodes + g0 * KC;
-  const uint8_t* ps = a.ksigns + g0 * SC;
-  const uint16_t* pkn = a.kvn + g0;
-  const uint16_t* prn = a.krn + g0;
-
-  uint8_t* mine = stage + wave * (R * SLOT);
-  const uint32_t mine_lds = lds_offset(mine);
-  constexpr int NKD = (NK * KC + 1023) / 1024, NSD = (NK * SC + 1023) / 1024;
-  constexpr int NDMA = NKD + NSD + 2;  // DMA instructions per slot
-  // a plane of `bytes` (a multiple of 512) moves in 1 KB rounds of 64 lanes x 16 B;
-  // a final half round uses lanes 0-31 only
-  auto copy_plane = [&](const i32x4& r, uint32_t dst, int bytes, int nrounds) {
-    const uint32_t lo = lane * 16;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if (c >= nrounds) break;
-      if ((c + 1) * 1024 <= bytes || lane < 32) dma16(r, dst + c * 1024, lo + c * 1024);
-    }
-  };
-  // DMA the wave's slab of keys [kb, kb + NK) into ring slot `slot`; rows past kend read zero
-  auto issue = [&](int kb, int slot) {
-    const uint32_t dst = mine_lds + slot * SLOT;
-    wait_lds();  // earlier reads of this slot have landed
-    copy_plane(rows_desc(pk, KC, kb, kend), dst + OFF_K, NK * KC, NKD);
-    copy_plane(rows_desc(ps, SC, kb, kend), dst + OFF_S, NK * SC, NSD);
-    if (NK == 64 || lane < 32) {
-      dma_u16(rows_desc(pkn, 2, kb, kend), dst + OFF_N, lane * 2);
-      dma_u16(rows_desc(prn, 2, kb, kend), dst + OFF_N + NRM, lane * 2);
-    }
-  };
-  // wait until the slot issued `later` slots ago has landed (score stores issued
-  // in between only make the wait stronger: loads complete in issue order)
-  auto wait_slot = [&](int later) {
-    if (later >= 3) wait_vm<(R >= 4 ? 3 * NDMA : 0)>();
-    else if (later == 2) wait_vm<(R >= 3 ? 2 * NDMA : 0)>();
-    else if (later == 1) wait_vm<NDMA>();
-    else wait_vm<0>();
-  };
-
-  auto slab = [&](const uint8_t* src, int ks0) {
-#pragma unroll
-    for (int j = 0; j < NBS; ++j) {
-      uint32_t kw[KW32];
-      const uint8_t* kp = src + OFF_K + (16 * j + l16) * KC + lg * KLANE;
-      if constexpr (KW32 == 2) {
-        const u32x2 t = *reinterpret_cast<const u32x2*>(kp);
-        kw[0] = t[0];
-        kw[1] = t[1];
-      } else {
-#pragma unroll
-        for (int w = 0; w < KW32; ++w) kw[w] = reinterpret_cast<const uint32_t*>(kp)[w];
-      }
-      const uint32_t sw = *reinterpret_cast<const uint32_t*>(src + OFF_S + (16 * j + l16) * SC + lg * 4);
-      float4v s1 = float4v{0.f, 0.f, 0.f, 0.f}, s2 = float4v{0.f, 0.f, 0.f, 0.f};
-      static_for<KS>([&](auto c) {
-        constexpr int ks = decltype(c)::value;
-        s1 = mfma16x16x32(qr[ks], key_operand<KB, KW32, ks>(tK, kw), s1);
-        s2 = mfma16x16x32(qp[ks], nib2x4<ks>(tS, sw), s2);
-      });
-      const float kn = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + (16 * j + l16) * 4)));
-      const float rn =
-          fb * h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + NRM + (16 * j + l16) * 4)));
-      const int kb = ks0 + 16 * j;
-      if (kb + l16 < kend) {
-        const rsrc_t ro = make_rsrc(pout + kb, out_bytes - static_cast<uint32_t>(kb) * 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, s1[e] * kn + s2[e] * rn), ro, oo[e], 0,
-                                                2);
-      }
-    }
-  };
-
-  // the q fragments (the compiler's only outstanding loads) land before the ring
-  // starts, so none of its own waits inside the loop reach back past a DMA
-  __builtin_amdgcn_s_waitcnt(0);
-  const int k0w = kbeg + wave * NK;
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-    if (k0w + r * SLAB < kend) issue(k0w + r * SLAB, r);
-  __syncthreads();  // tables built
-  for (int k0 = k0w; k0 < kend; k0 += R * SLAB) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int ks0 = k0 + r * SLAB;
-      if (ks0 < kend) {
-        // slots issued after this one: those of the next R-1 slabs that exist
-        int later = 0;
-#pragma unroll
-        for (int q = 1; q < R; ++q) later += (ks0 + q * SLAB < kend) ? 1 : 0;
-        wait_slot(later);
-        slab(mine + r * SLOT, ks0);
-        if (ks0 + R * SLAB < kend) issue(ks0 + R * SLAB, r);
-      }
-    }
-  }
-}
-
 struct MergeArgs {
   const float *part_o, *part_ml;
   const uint16_t* vpit;  // split Pi_v^T
@@ -802,44 +507,12 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeArgs a) {
   }
 }
 
-// ---------------------------------------------------------------- planning
-struct DecodePlan {
-  bool use;
-  int nsplit, chunk;
-  int64_t ws_bytes;
-};
-
-
-// Split S_k so that about `target` blocks cover the (batch, kv head) groups, each
-// split a multiple of `quantum` keys and no shorter than `min_chunk`.
-static DecodePlan plan_split(int B, int Hkv, int Sk, int target, int quantum, int min_chunk) {
-  DecodePlan p{true, 0, 0, 0};
-  const int64_t groups = static_cast<int64_t>(B) * Hkv;
-  int nsplit = static_cast<int>((target + groups - 1) / groups);
-  const int max_split = (Sk + min_chunk - 1) / min_chunk;
-  if (nsplit > max_split) nsplit = max_split;
-  if (nsplit > 1024) nsplit = 1024;
-  if (nsplit < 1) nsplit = 1;
-  int chunk = (Sk + nsplit - 1) / nsplit;
-  chunk = (chunk + quantum - 1) / quantum * quantum;
-  p.nsplit = (Sk + chunk - 1) / chunk;
-  p.chunk = chunk;
-  return p;
-}
-
-// head_dim 128, bits 2-4, at most 16 query columns per kv head; S_k below 2^24
-// keeps every per-group byte offset of the planes and score rows under 2^31
-static bool decode_shape(int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
-  if (d != 128 || bits < 2 || bits > 4 || Hkv <= 0 || Hq % Hkv) return false;
-  return (Hq / Hkv) * Sq <= 16 && Sk >= 1 && Sk < (1 << 24);
-}
-
 // grid target of the fused decode attention: one round of resident blocks
 static int attn_target_blocks(int bits) {
   static int cache[3][16] = {};
-  const void* k = bits == 2 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 2, kAttnNbs, kAttnRing>)
-                : bits == 3 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 3, kAttnNbs, kAttnRing>)
-                            : reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 4, kAttnNbs, kAttnRing>);
+  const void* k = bits == 2 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 2, kAttnNbs, kAttnRing, true>)
+                : bits == 3 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 3, kAttnNbs, kAttnRing, true>)
+                            : reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 4, kAttnNbs, kAttnRing, true>);
   return resident_blocks(k, 256, cache[bits - 2]);
 }
 
@@ -852,17 +525,10 @@ static DecodePlan plan_decode(int B, int Hq, int Hkv, int Sq, int Sk, int d, int
   return p;
 }
 
-static DecodePlan plan_scores(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
-  if (!decode_shape(Hq, Hkv, Sq, Sk, d, bits)) return DecodePlan{false, 0, 0, 0};
-  const int slab = 4 * score_slab_keys(bits);
-  return plan_split(B, Hkv, Sk, kScoreBlocks, slab, 2 * slab);
-}
-
 }  // namespace tq
 
 using namespace tq;
 
-// Used by tq_attn.hip's entry points.
 namespace tq {
 
 int64_t decode_workspace_bytes(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
@@ -877,43 +543,11 @@ bool decode_applies(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
 template <int BITS>
 static void launch_decode_attn(const DecodeArgs& a, hipStream_t s) {
   dim3 grid(a.nsplit, a.Hkv, a.B);
-  decode_attn_lds_kernel<128, BITS, kAttnNbs, kAttnRing><<<grid, 256, 0, s>>>(a);
+  if (a.C <= 8) decode_attn_lds_kernel<128, BITS, kAttnNbs, kAttnRing, true><<<grid, 256, 0, s>>>(a);
+  else decode_attn_lds_kernel<128, BITS, kAttnNbs, kAttnRing, false><<<grid, 256, 0, s>>>(a);
 }
 
-int decode_scores(int64_t ldk, const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
-                  const uint8_t* ksigns, const uint16_t* krn, const uint16_t* kvn, const uint16_t* kcent,
-                  int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits, float coeff, float* out,
-                  hipStream_t s) {
-  const DecodePlan p = plan_scores(B, Hq, Hkv, Sq, Sk, d, bits);
-  DecodeArgs a{};
-  a.q_rot = q_rot;
-  a.q_proj = q_proj;
-  a.kcodes = kcodes;
-  a.ksigns = ksigns;
-  a.krn = krn;
-  a.kvn = kvn;
-  a.kcent = kcent;
-  a.B = B;
-  a.Hq = Hq;
-  a.Hkv = Hkv;
-  a.Sq = Sq;
-  a.Sk = Sk;
-  a.ldk = ldk;
-  a.G = Hq / Hkv;
-  a.C = a.G * Sq;
-  a.nsplit = p.nsplit;
-  a.chunk = p.chunk;
-  a.coeff = coeff;
-  a.scale = 1.f;
-  a.scores = out;
-  dim3 grid(a.nsplit, a.Hkv, a.B);
-  if (bits == 2) decode_scores_kernel<128, 2, score_ring(2), score_slab_keys(2)><<<grid, 256, 0, s>>>(a);
-  else if (bits == 3) decode_scores_kernel<128, 3, score_ring(3), score_slab_keys(3)><<<grid, 256, 0, s>>>(a);
-  else decode_scores_kernel<128, 4, score_ring(4), score_slab_keys(4)><<<grid, 256, 0, s>>>(a);
-  return launch_status("tq_attention_scores (decode)");
-}
-
-int decode_attention(int64_t ldk, const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
+int decode_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, const uint8_t* kcodes,
                      const uint8_t* ksigns, const uint16_t* krn, const uint16_t* kvn, const uint16_t* kcent,
                      int bits, const uint8_t* vcodes, const uint16_t* vvn, const float* vcent32,
                      const uint16_t* vpit, int B, int Hq, int Hkv, int Sq, int Sk, int d, float coeff,

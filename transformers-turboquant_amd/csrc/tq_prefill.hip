@@ -42,7 +42,8 @@
 namespace tq {
 
 struct PrefillArgs {
-  const uint16_t *q_rot, *q_proj;
+  const uint16_t* q_rot;
+  const float* q_proj;  // f32; this kernel's term-2 operand is its f16 rounding
   const uint8_t *kcodes, *ksigns;
   const uint16_t *krn, *kvn, *kcent;  // f16 key centroids
   const uint8_t* vcodes;
@@ -173,7 +174,7 @@ __global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_
     for (int ks = 0; ks < KS; ++ks) {
       const int d0 = ks * 32 + lg * 8;
       qr[ks][nb] = col_ok[nb] ? *reinterpret_cast<const half8*>(a.q_rot + qrow + d0) : half8{};
-      qp[ks][nb] = col_ok[nb] ? *reinterpret_cast<const half8*>(a.q_proj + qrow + d0) : half8{};
+      qp[ks][nb] = col_ok[nb] ? round8(a.q_proj + qrow + d0) : half8{};
     }
   }
 
@@ -529,7 +530,7 @@ bool prefill_applies(int Hq, int Hkv, int d, int bits, int val_bits) {
   return d == 128 && bits >= 2 && bits <= 4 && val_bits == bits && Hq / Hkv <= TQ_PF_WAVES * 32;
 }
 
-int prefill_attention(int64_t ldk, const uint16_t* q_rot, const uint16_t* q_proj, const uint8_t* kcodes,
+int prefill_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, const uint8_t* kcodes,
                       const uint8_t* ksigns, const uint16_t* krn, const uint16_t* kvn, const uint16_t* kcent,
                       int bits, const uint8_t* vcodes, const uint16_t* vvn, const float* vcent,
                       const uint16_t* vpit, int B, int Hq, int Hkv, int Sq, int Sk, float coeff, float scale,

@@ -189,12 +189,13 @@ class TurboQuantCompressorV2:
         return term1 + (math.sqrt(math.pi / 2) / m) * qjl * rnorm.unsqueeze(-2)
 
     def prepare_queries(self, queries: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-        """GPU q_rot = f16(q Pi^T) and q_proj = f16(q_rot S_eff^T), f16 [B, Hq, S_q, D]."""
+        """GPU q_rot = f16(q Pi^T) (f16 [B, Hq, S_q, D]) and q_proj = q_rot S_eff^T (f32, the
+        reference's fp32 projection, kernels/attention.py:158-167, :453)."""
         B, Hq, Sq, D = queries.shape
         q = _activation(queries)
         t = _tables(self, q.device, with_qjl=True)
         q_rot = torch.empty(B, Hq, Sq, D, dtype=torch.float16, device=q.device)
-        q_proj = torch.empty_like(q_rot)
+        q_proj = torch.empty(B, Hq, Sq, D, dtype=torch.float32, device=q.device)
         _native.check(_native.lib().tq_query_prep(
             q.data_ptr(), _native.dtype_code(q.dtype), B, Hq, Sq, D, q.stride(0), q.stride(1),
             q.stride(2), t.pi_split.data_ptr(), t.s_eff16.data_ptr(), q_rot.data_ptr(),

@@ -25,13 +25,13 @@ def _identity_split(d: int, device: str) -> torch.Tensor:
 
 
 def project_queries(q_rot: torch.Tensor, s_eff_f16: torch.Tensor) -> torch.Tensor:
-    """f16(q_rot S_eff^T) for f16 q_rot [B, H, S, d] on the GPU (attention.py:155-167)."""
+    """f32 q_rot S_eff^T for f16 q_rot [B, H, S, d] on the GPU (attention.py:155-167, :453)."""
     B, H, S, d = q_rot.shape
     q_rot = q_rot.to(torch.float16)
     if q_rot.stride(-1) != 1:
         q_rot = q_rot.contiguous()
     rot_copy = torch.empty(B, H, S, d, dtype=torch.float16, device=q_rot.device)
-    proj = torch.empty_like(rot_copy)
+    proj = torch.empty(B, H, S, d, dtype=torch.float32, device=q_rot.device)
     eye = _identity_split(d, str(q_rot.device))
     _native.check(_native.lib().tq_query_prep(
         q_rot.data_ptr(), _native.TQ_F16, B, H, S, d, q_rot.stride(0), q_rot.stride(1),
@@ -40,7 +40,7 @@ def project_queries(q_rot: torch.Tensor, s_eff_f16: torch.Tensor) -> torch.Tenso
     return proj
 
 
-def scores_from_prepared(q_rot16: torch.Tensor, q_proj16: torch.Tensor, codes: torch.Tensor,
+def scores_from_prepared(q_rot16: torch.Tensor, q_proj32: torch.Tensor, codes: torch.Tensor,
                          signs: torch.Tensor, rn: torch.Tensor, vn: torch.Tensor,
                          centroids16: torch.Tensor, bits: int, coeff: float, hkv: int,
                          sk: int | None = None, kv_stride: int = 0) -> torch.Tensor:
@@ -53,7 +53,7 @@ def scores_from_prepared(q_rot16: torch.Tensor, q_proj16: torch.Tensor, codes: t
     Sk = rn.numel() // (B * hkv) if sk is None else int(sk)
     out = torch.empty(B, Hq, Sq, Sk, dtype=torch.float32, device=q_rot16.device)
     _native.check(_native.lib().tq_attention_scores_kv(
-        q_rot16.data_ptr(), q_proj16.data_ptr(), codes.data_ptr(), signs.data_ptr(),
+        q_rot16.data_ptr(), q_proj32.data_ptr(), codes.data_ptr(), signs.data_ptr(),
         rn.data_ptr(), vn.data_ptr(), centroids16.data_ptr(), B, Hq, hkv, Sq, Sk, int(kv_stride), d,
         bits, float(coeff), out.data_ptr(), _native.stream_of(out)), "asymmetric_attention_scores")
     return out
