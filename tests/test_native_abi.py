@@ -60,3 +60,31 @@ def test_missing_library_fails_loudly(monkeypatch):
     monkeypatch.setattr(_native, "_lib", None)
     with pytest.raises(RuntimeError, match="not built"):
         _native.lib()
+
+
+OPS = ("pack_bits", "unpack_bits", "quantize_pack", "dequantize", "compress_keys", "compress_values",
+       "decompress_values", "query_prep", "scores", "attention", "workspace_size")
+
+
+def test_torch_extension_registers_every_op():
+    """torch.ops.tq (csrc/tq_torch.cpp) loads without a GPU and registers one op per C entry
+    point the product path calls; with CPU tensors the GPU ops refuse to run."""
+    import torch
+
+    from turboquant_pytorch import _ops
+
+    tq = _ops.ops()
+    for name in OPS:
+        assert hasattr(tq, name), name
+    assert "int workspace" in str(tq.attention.default._schema)
+    with pytest.raises(NotImplementedError):
+        tq.pack_bits(torch.zeros(2, 8, dtype=torch.int32), 3)
+
+
+def test_missing_extension_raises(monkeypatch):
+    from turboquant_pytorch import _ops
+
+    monkeypatch.setattr(_ops, "_OPS_PATH", os.path.join(ROOT, "no_such_dir", "_tq_torch.so"))
+    monkeypatch.setattr(_ops, "_loaded", False)
+    with pytest.raises(RuntimeError, match="not built"):
+        _ops.ops()

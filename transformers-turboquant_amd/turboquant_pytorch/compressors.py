@@ -19,7 +19,7 @@ from dataclasses import dataclass
 
 import torch
 
-from . import _native
+from ._ops import ops
 from .codebook import codebook, gaussian_matrix, midpoints, random_rotation, split_f16
 from .kernels.attention import scores_from_prepared
 
@@ -67,14 +67,6 @@ def _tables(comp, device: torch.device, with_qjl: bool) -> _DeviceTables:
     return t
 
 
-def _activation(states: torch.Tensor) -> torch.Tensor:
-    if states.dtype not in (torch.float32, torch.float16, torch.bfloat16):
-        states = states.to(torch.float32)
-    if states.stride(-1) != 1:
-        states = states.contiguous()
-    return states
-
-
 class TurboQuantCompressorV2:
     """Key compressor with the asymmetric (MSE + QJL) inner-product estimator.
 
@@ -111,25 +103,14 @@ class TurboQuantCompressorV2:
 
     def _compress_gpu(self, states: torch.Tensor, y_out=None, proj_out=None) -> dict:
         B, H, S, D = states.shape
-        x = _activation(states)
-        dev = x.device
-        t = _tables(self, dev, with_qjl=True)
-        n = B * H * S
-        codes = torch.empty(n, math.ceil(D * self.mse_bits / 8), dtype=torch.uint8, device=dev)
-        signs = torch.empty(n, math.ceil(D / 8), dtype=torch.uint8, device=dev)
-        rn = torch.empty(n, dtype=torch.float16, device=dev)
-        vn = torch.empty(n, dtype=torch.float16, device=dev)
-        _native.check(_native.lib().tq_compress_keys(
-            x.data_ptr(), _native.dtype_code(x.dtype), B, H, S, D, x.stride(0), x.stride(1),
-            x.stride(2), t.pi_split.data_ptr(), t.pit_split.data_ptr(), t.s_split.data_ptr(),
-            t.cent32.data_ptr(), t.bounds32.data_ptr(), self.mse_bits, codes.data_ptr(),
-            signs.data_ptr(), rn.data_ptr(), vn.data_ptr(), _native.ptr(y_out), _native.ptr(proj_out),
-            _native.stream_of(x)), "TurboQuantCompressorV2.compress")
+        t = _tables(self, states.device, with_qjl=True)
+        codes, signs, rn, vn = ops().compress_keys(states, t.pi_split, t.pit_split, t.s_split, t.cent32,
+                                                   t.bounds32, self.mse_bits, y_out, proj_out)
         return {
             "packed_key_indices": codes,
             "packed_qjl_signs": signs,
-            "residual_norm": rn.view(B, H, S),
-            "vec_norms": vn.view(B, H, S),
+            "residual_norm": rn,
+            "vec_norms": vn,
             "shape": (B, H, S, D),
         }
 
@@ -191,16 +172,8 @@ class TurboQuantCompressorV2:
     def prepare_queries(self, queries: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """GPU q_rot = f16(q Pi^T) (f16 [B, Hq, S_q, D]) and q_proj = q_rot S_eff^T (f32, the
         reference's fp32 projection, kernels/attention.py:158-167, :453)."""
-        B, Hq, Sq, D = queries.shape
-        q = _activation(queries)
-        t = _tables(self, q.device, with_qjl=True)
-        q_rot = torch.empty(B, Hq, Sq, D, dtype=torch.float16, device=q.device)
-        q_proj = torch.empty(B, Hq, Sq, D, dtype=torch.float32, device=q.device)
-        _native.check(_native.lib().tq_query_prep(
-            q.data_ptr(), _native.dtype_code(q.dtype), B, Hq, Sq, D, q.stride(0), q.stride(1),
-            q.stride(2), t.pi_split.data_ptr(), t.s_eff16.data_ptr(), q_rot.data_ptr(),
-            q_proj.data_ptr(), _native.stream_of(q)), "prepare_queries")
-        return q_rot, q_proj
+        t = _tables(self, queries.device, with_qjl=True)
+        return ops().query_prep(queries, t.pi_split, t.s_eff16)
 
 
 class TurboQuantCompressorMSE:
@@ -235,16 +208,8 @@ class TurboQuantCompressorMSE:
 
     def _compress_gpu(self, states: torch.Tensor, y_out=None) -> dict:
         B, H, S, D = states.shape
-        x = _activation(states)
-        dev = x.device
-        t = _tables(self, dev, with_qjl=False)
-        n = B * H * S
-        codes = torch.empty(n, math.ceil(D * self.bits / 8), dtype=torch.uint8, device=dev)
-        vn = torch.empty(n, dtype=torch.float16, device=dev)
-        _native.check(_native.lib().tq_compress_values(
-            x.data_ptr(), _native.dtype_code(x.dtype), B, H, S, D, x.stride(0), x.stride(1),
-            x.stride(2), t.pi_split.data_ptr(), t.bounds32.data_ptr(), self.bits, codes.data_ptr(),
-            vn.data_ptr(), _native.ptr(y_out), _native.stream_of(x)), "TurboQuantCompressorMSE.compress")
+        t = _tables(self, states.device, with_qjl=False)
+        codes, vn = ops().compress_values(states, t.pi_split, t.bounds32, self.bits, y_out)
         return {"packed_indices": codes, "vec_norms": vn, "shape": (B, H, S, D)}
 
     @torch.no_grad()
@@ -254,17 +219,11 @@ class TurboQuantCompressorMSE:
         n = B * H * S
         if "packed_indices" in compressed:
             packed = compressed["packed_indices"]
-            codes = packed.reshape(n, packed.shape[-1]).contiguous()  # explicit width: n may be 0
-            if codes.device.type != "cuda":
+            if packed.device.type != "cuda":
                 raise ValueError("packed value planes live on the GPU")
-            t = _tables(self, codes.device, with_qjl=False)
-            vn = compressed["vec_norms"].to(torch.float16).reshape(n).contiguous()
-            out = torch.empty(B, H, S, D, dtype=torch.float32, device=codes.device)
-            _native.check(_native.lib().tq_decompress_values(
-                codes.data_ptr(), vn.data_ptr(), n, D, t.pit_split.data_ptr(), t.cent32.data_ptr(),
-                self.bits, out.data_ptr(), _native.TQ_F32, D, _native.stream_of(out)),
-                "TurboQuantCompressorMSE.decompress")
-            return out
+            t = _tables(self, packed.device, with_qjl=False)
+            return ops().decompress_values(packed, compressed["vec_norms"], t.pit_split, t.cent32, self.bits,
+                                           [B, H, S, D])
         idx = compressed["indices"].long()
         rec = self.centroids.float()[idx] @ self.Pi.float()
         return (rec * compressed["vec_norms"].float().unsqueeze(-1)).reshape(B, H, S, D)

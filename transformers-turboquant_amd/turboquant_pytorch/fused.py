@@ -13,7 +13,8 @@ value planes once per block of query rows, runs an online softmax in f32, and
 accumulates P.V in the value compressor's rotated domain, applying Pi_v once
 per output row.  Grouped-query attention is served without expanding K/V.
 Few-query (decode) shapes take a split-K path whose partial results live in a
-workspace allocated here from torch (tq_attention_workspace_size bytes).
+workspace that the op allocates from torch (tq_attention_workspace_size bytes), or
+in the library's own scratch array (split_k="static").
 
 A compressed dict may carry ``kv_stride``: its planes then hold ``kv_stride``
 positions per (batch, kv head) of which the first ``shape[2]`` are attended
@@ -26,7 +27,7 @@ import math
 
 import torch
 
-from . import _native
+from ._ops import ops
 from .compressors import TurboQuantCompressorMSE, TurboQuantCompressorV2, _tables
 
 __all__ = ["compressed_attention", "attention_from_prepared"]
@@ -36,14 +37,17 @@ def compressed_attention(queries: torch.Tensor, key_compressor: TurboQuantCompre
                          val_compressor: TurboQuantCompressorMSE, compressed_k: dict,
                          compressed_v: dict, attention_mask: torch.Tensor | None = None,
                          causal: bool = False, scale: float | None = None,
-                         out_dtype: torch.dtype | None = None, split_k: bool = True) -> torch.Tensor:
+                         out_dtype: torch.dtype | None = None, split_k: bool | str = True) -> torch.Tensor:
     """Attention output [B, S_q, Hq, D] (heads already interleaved for o_proj).
 
     queries [B, Hq, S_q, D] (any strides with unit stride on D) on the GPU;
     compressed_k / compressed_v the packed dicts of [B, Hkv, S_k, D] keys and
     values; attention_mask an additive mask broadcastable to [B, Hq, S_q, S_k];
     causal drops keys j > i + S_k - S_q inside the kernel; split_k=False keeps
-    few-query shapes on the tiled kernel instead of the split-K decode kernels.
+    few-query shapes on the tiled kernel instead of the split-K decode kernels, and
+    split_k="static" runs the split-K kernels with their partials in the library's
+    per-GPU scratch array (tq_attention_fwd_kv_noalloc: no allocation at all; calls
+    that overlap on one GPU race).
     """
     if "packed_key_indices" not in compressed_k or "packed_indices" not in compressed_v:
         raise ValueError("compressed_attention needs the packed (GPU) formats")
@@ -58,8 +62,8 @@ def attention_from_prepared(q_rot: torch.Tensor, q_proj: torch.Tensor,
                             val_compressor: TurboQuantCompressorMSE, compressed_k: dict,
                             compressed_v: dict, attention_mask: torch.Tensor | None = None,
                             causal: bool = False, scale: float | None = None,
-                            out_dtype: torch.dtype = torch.float32, split_k: bool = True) -> torch.Tensor:
-    """The tq_attention_fwd launch on queries already prepared by prepare_queries()."""
+                            out_dtype: torch.dtype = torch.float32, split_k: bool | str = True) -> torch.Tensor:
+    """The tq::attention op (tq_attention_fwd_kv) on queries already prepared by prepare_queries()."""
     B, Hq, Sq, D = q_rot.shape
     _, Hkv, Sk, _ = compressed_k["shape"]
     kv_stride = int(compressed_k.get("kv_stride", Sk))
@@ -70,32 +74,16 @@ def attention_from_prepared(q_rot: torch.Tensor, q_proj: torch.Tensor,
     tv = _tables(val_compressor, dev, with_qjl=False)
     if out_dtype not in (torch.float32, torch.float16, torch.bfloat16):
         out_dtype = torch.float32
-    out = torch.empty(B, Sq, Hq, D, dtype=out_dtype, device=dev)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     coeff = math.sqrt(math.pi / 2) / key_compressor.S.shape[0]
-    lib = _native.lib()
     bits = key_compressor.mse_bits + 1
-    ws_bytes = 0
-    if split_k and val_compressor.bits == bits:
-        ws_bytes = lib.tq_attention_workspace_size(B, Hq, Hkv, Sq, Sk, D, bits)
-    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
-    mptr, ms, mask = 0, (0, 0, 0, 0), None
+    mask = None
     if attention_mask is not None:
         mask = attention_mask.to(dev, torch.float32)
-        while mask.dim() < 4:
-            mask = mask.unsqueeze(0)
-        mask = mask.expand(B, Hq, Sq, Sk)
-        mptr, ms = mask.data_ptr(), tuple(mask.stride())
-    _native.check(lib.tq_attention_fwd_kv(
-        q_rot.data_ptr(), q_proj.data_ptr(),
-        compressed_k["packed_key_indices"].data_ptr(), compressed_k["packed_qjl_signs"].data_ptr(),
-        compressed_k["residual_norm"].data_ptr(), compressed_k["vec_norms"].data_ptr(),
-        tk.cent16.data_ptr(), bits,
-        compressed_v["packed_indices"].data_ptr(), compressed_v["vec_norms"].data_ptr(),
-        tv.cent32.data_ptr(), val_compressor.bits, tv.pit_split.data_ptr(),
-        B, Hq, Hkv, Sq, Sk, kv_stride, D, float(coeff), float(scale), int(bool(causal)),
-        mptr, ms[0], ms[1], ms[2], ms[3],
-        out.data_ptr(), _native.dtype_code(out_dtype), out.stride(0), out.stride(2), out.stride(1),
-        _native.ptr(workspace), ws_bytes, _native.stream_of(out)), "compressed_attention")
-    return out
+    mode = {"static": 2, True: 1, False: 0}[split_k]
+    return ops().attention(
+        q_rot, q_proj, compressed_k["packed_key_indices"], compressed_k["packed_qjl_signs"],
+        compressed_k["residual_norm"], compressed_k["vec_norms"], tk.cent16, bits,
+        compressed_v["packed_indices"], compressed_v["vec_norms"], tv.cent32, val_compressor.bits,
+        tv.pit_split, Hkv, Sk, kv_stride, float(coeff), float(scale), bool(causal), mask, out_dtype, mode)

@@ -12,7 +12,7 @@ import functools
 
 import torch
 
-from .. import _native
+from .._ops import ops
 from ..codebook import split_f16
 from .bit_ops import unpack_bits
 
@@ -26,17 +26,9 @@ def _identity_split(d: int, device: str) -> torch.Tensor:
 
 def project_queries(q_rot: torch.Tensor, s_eff_f16: torch.Tensor) -> torch.Tensor:
     """f32 q_rot S_eff^T for f16 q_rot [B, H, S, d] on the GPU (attention.py:155-167, :453)."""
-    B, H, S, d = q_rot.shape
-    q_rot = q_rot.to(torch.float16)
-    if q_rot.stride(-1) != 1:
-        q_rot = q_rot.contiguous()
-    rot_copy = torch.empty(B, H, S, d, dtype=torch.float16, device=q_rot.device)
-    proj = torch.empty(B, H, S, d, dtype=torch.float32, device=q_rot.device)
+    d = q_rot.shape[-1]
     eye = _identity_split(d, str(q_rot.device))
-    _native.check(_native.lib().tq_query_prep(
-        q_rot.data_ptr(), _native.TQ_F16, B, H, S, d, q_rot.stride(0), q_rot.stride(1),
-        q_rot.stride(2), eye.data_ptr(), s_eff_f16.data_ptr(), rot_copy.data_ptr(),
-        proj.data_ptr(), _native.stream_of(q_rot)), "project_queries")
+    _, proj = ops().query_prep(q_rot.to(torch.float16), eye, s_eff_f16)
     return proj
 
 
@@ -49,14 +41,10 @@ def scores_from_prepared(q_rot16: torch.Tensor, q_proj32: torch.Tensor, codes: t
     The key planes hold B*hkv head sequences of kv_stride rows each (kv_stride
     0: contiguous, B*hkv*Sk rows); the first sk rows of each are scored.
     """
-    B, Hq, Sq, d = q_rot16.shape
+    B = q_rot16.shape[0]
     Sk = rn.numel() // (B * hkv) if sk is None else int(sk)
-    out = torch.empty(B, Hq, Sq, Sk, dtype=torch.float32, device=q_rot16.device)
-    _native.check(_native.lib().tq_attention_scores_kv(
-        q_rot16.data_ptr(), q_proj32.data_ptr(), codes.data_ptr(), signs.data_ptr(),
-        rn.data_ptr(), vn.data_ptr(), centroids16.data_ptr(), B, Hq, hkv, Sq, Sk, int(kv_stride), d,
-        bits, float(coeff), out.data_ptr(), _native.stream_of(out)), "asymmetric_attention_scores")
-    return out
+    return ops().scores(q_rot16, q_proj32, codes, signs, rn, vn, centroids16, bits, hkv, Sk, int(kv_stride),
+                        float(coeff))
 
 
 def asymmetric_attention_scores(query: torch.Tensor, packed_key_indices: torch.Tensor,

@@ -3,7 +3,8 @@
 Layout: code i of a row occupies bits [i*b, i*b + b), least-significant bit
 first; bit k of the row is bit k%8 of byte k//8 (bit_ops.py:269-283).
 
-GPU tensors go to the gfx950 library (``tq_pack_bits`` / ``tq_unpack_bits``);
+GPU tensors go to the gfx950 library (``torch.ops.tq.pack_bits`` / ``unpack_bits`` over
+``tq_pack_bits`` / ``tq_unpack_bits``);
 CPU tensors use the vectorised torch formulation below.
 """
 
@@ -13,7 +14,7 @@ import math
 
 import torch
 
-from .. import _native
+from .._ops import ops
 
 __all__ = ["pack_bits", "unpack_bits"]
 
@@ -52,11 +53,7 @@ def pack_bits(indices: torch.Tensor, b: int) -> torch.Tensor:
     n, d = indices.shape
     oc = _out_cols(d, b)
     if indices.device.type == "cuda":
-        indices = indices.contiguous()
-        out = torch.empty(n, oc, dtype=torch.uint8, device=indices.device)
-        _native.check(_native.lib().tq_pack_bits(
-            indices.data_ptr(), n, d, d, b, out.data_ptr(), oc, _native.stream_of(out)), "pack_bits")
-        return out
+        return ops().pack_bits(indices, b)
     shifts = torch.arange(b, dtype=torch.int32)
     bits = ((indices.unsqueeze(-1) >> shifts) & 1).reshape(n, d * b)
     return _bits_to_bytes(bits, oc)
@@ -67,12 +64,7 @@ def unpack_bits(packed: torch.Tensor, b: int, d: int) -> torch.Tensor:
     _check_b(b)
     n = packed.shape[0]
     if packed.device.type == "cuda":
-        packed = packed.contiguous()
-        out = torch.empty(n, d, dtype=torch.int32, device=packed.device)
-        _native.check(_native.lib().tq_unpack_bits(
-            packed.data_ptr(), n, d, packed.shape[1], b, out.data_ptr(), d,
-            _native.stream_of(out)), "unpack_bits")
-        return out
+        return ops().unpack_bits(packed, b, d)
     bits = _bytes_to_bits(packed, d * b).view(n, d, b)
     weights = (1 << torch.arange(b, dtype=torch.int32))
     return (bits * weights).sum(-1).to(torch.int32)

@@ -9,8 +9,8 @@ from __future__ import annotations
 
 import torch
 
-from .. import _native
-from .bit_ops import _out_cols, pack_bits, unpack_bits
+from .._ops import ops
+from .bit_ops import pack_bits, unpack_bits
 
 __all__ = ["lloyd_max_quantize", "lloyd_max_dequantize"]
 
@@ -26,14 +26,7 @@ def lloyd_max_quantize(rotated: torch.Tensor, boundaries: torch.Tensor, b_eff: i
     boundaries = boundaries.to(torch.float32).contiguous()
     n, d = rotated.shape
     if rotated.device.type == "cuda":
-        rotated = rotated.contiguous()
-        boundaries = boundaries.to(rotated.device)
-        oc = _out_cols(d, b_eff)
-        out = torch.empty(n, oc, dtype=torch.uint8, device=rotated.device)
-        _native.check(_native.lib().tq_quantize_pack(
-            rotated.data_ptr(), n, d, d, boundaries.data_ptr(), b_eff, out.data_ptr(), oc,
-            _native.stream_of(out)), "lloyd_max_quantize")
-        return out
+        return ops().quantize_pack(rotated, boundaries, b_eff)
     codes = torch.searchsorted(boundaries, rotated.reshape(-1).contiguous()).reshape(n, d)
     return pack_bits(codes.to(torch.int32), b_eff)
 
@@ -45,11 +38,5 @@ def lloyd_max_dequantize(packed: torch.Tensor, centroids: torch.Tensor, b: int, 
     centroids = centroids.to(torch.float16).contiguous()
     n = packed.shape[0]
     if packed.device.type == "cuda":
-        packed = packed.contiguous()
-        centroids = centroids.to(packed.device)
-        out = torch.empty(n, d, dtype=torch.float16, device=packed.device)
-        _native.check(_native.lib().tq_dequantize(
-            packed.data_ptr(), n, d, packed.shape[1], centroids.data_ptr(), b, out.data_ptr(), d,
-            _native.stream_of(out)), "lloyd_max_dequantize")
-        return out
+        return ops().dequantize(packed, centroids, b, d)
     return centroids[unpack_bits(packed, b, d).long()]
