@@ -1,21 +1,23 @@
 """Benchmark of the TurboQuant compressed-attention hot path on one MI355X.
 
-Workload: one attention layer of Llama-3-8B shape,
-32 query heads, 8 KV heads (GQA group 4), head_dim 128, bf16 Q/K/V ~ N(0,1)
-with 4 outlier channels x20 on K, bits=3.
-
-Headline (`value`, HBM roofline): decode-shaped compressed-key scoring at 32k
-context, the regime the metric's "% of HBM peak" refers to.  A step is one
+Headline (`value`, HBM roofline): the north-star target, compressed-key scoring
+of Llama-3-8B-shaped attention (32 query heads, 8 KV heads, head_dim 128,
+bits 3) at 32k context, decode-shaped (keys streamed once per query step: the
+regime the metric's "% of HBM peak" refers to).  A step is one
 tq_attention_scores launch scoring one query row of each of DEC_B sequences
-against its 32768 compressed keys (all 32 query heads; materialised f32
-scores, the reference's scoring API).  Steps rotate over DEC_ROT distinct
-caches so the working set (>1 GB) is far beyond the 256 MB MALL.  The same
-shape is also timed through the fused decode attention (softmax . V).
+against its 32768 compressed keys (all 32 query heads; materialised f32 scores,
+the reference's scoring API).  Steps rotate over DEC_ROT distinct caches so the
+working set (>1 GB) is far beyond the 256 MB MALL.  The same shape is also timed
+through the fused decode attention (softmax . V).
 
-Secondary legs in the same line: compress tokens/s and the causal prefill of
-8192 positions (scores + online softmax + P.V for every query row, MFMA
-roofline).  Prints one JSON line.  With --gpus N > 1 it exits: this build runs
-on one GPU.
+Secondary legs in the same line: BASELINE.json configs[1] (the same layer shape
+at 8192 tokens, bf16 Q/K/V ~ N(0,1) with 4 outlier channels x20 on K): compress
+tokens/s and the causal prefill (scores + online softmax + P.V for every query
+row, MFMA roofline); and one layer's eager decode step through the product path
+(torch.ops.tq) at B = 1 with 4096 cached tokens, host and device time.  CPU
+baselines: the build's torch CPU branch of the reference's PyTorch path on
+bounded samples.  Prints one JSON line.  With --gpus N > 1 it exits: this build
+runs on one GPU.
 """
 
 from __future__ import annotations
@@ -59,89 +61,96 @@ def measured_traffic(kernel: str, record: str = "traffic_bench.json"):
         return None
 
 
-def cpu_baseline_decode(seconds_budget: float) -> dict:
-    """The oracle's f32 restatement of the reference's PyTorch scoring branch
-    (compressors.py:201-224: q.k_mse^T + coeff * (q S^T).signs^T * rn) on a bounded
-    sample of the decode workload: one query row of 4 query heads against the
-    32768 keys of one KV head, repeated until the time budget is spent."""
-    import numpy as np
+def host_cpu() -> dict:
+    """The host the CPU baselines ran on: model name (from /proc/cpuinfo, as lscpu prints it),
+    logical CPUs visible to this process, and torch's intra-op thread count."""
+    import torch
 
-    from oracle import tq_oracle as O
+    model = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    cpus = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return {"model": model, "logical_cpus": cpus, "torch_threads": torch.get_num_threads()}
+
+
+def _cpu_threads() -> None:
+    import torch
+
+    cpus = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    torch.set_num_threads(max(1, cpus))
+
+
+def cpu_baseline_decode(seconds_budget: float) -> dict:
+    """The reference's PyTorch CPU branch as this build restates it (TurboQuantCompressorV2 on CPU
+    tensors: compressors.py:139-161 compress, :201-224 scores; bit-exact with the reference's own
+    outputs, tests/golden/cpu_compress.npz) on a bounded sample of the decode workload: one query
+    row of the 4 query heads of one KV head against its 32768 compressed keys, repeated until the
+    time budget is spent.  The keys are compressed once, untimed, as the GPU leg's caches are."""
+    import torch
+
     from turboquant_pytorch.compressors import TurboQuantCompressorV2
 
+    _cpu_threads()
     g = HQ // HKV
-    rng = np.random.default_rng(0)
+    gen = torch.Generator().manual_seed(0)
     kc = TurboQuantCompressorV2(D, BITS, seed=42)
-    k = rng.standard_normal((DEC_SK, D)).astype(np.float32)
-    k[:, :4] *= 20
-    kk = O.key_compress_unpacked(k, kc.Pi.numpy(), kc.S.numpy(), kc.centroids.numpy())
-    q = rng.standard_normal((g, 1, D)).astype(np.float32)
-    s_mat, coeff = kc.S.numpy(), O.COEFF(D)
-
-    def run():
-        for h in range(g):
-            O.scores_unpacked(q[h], kk["k_mse"], kk["qjl_signs"], kk["residual_norm"], s_mat, coeff,
-                              dtype=np.float32)
-
-    run()
+    k = torch.randn(1, 1, DEC_SK, D, generator=gen)
+    k[..., :4] *= 20
+    ck = kc.compress(k.to(torch.bfloat16))
+    q = torch.randn(1, g, 1, D, generator=gen).to(torch.bfloat16)
+    kc.asymmetric_attention_scores(q, ck)
     n, t0 = 0, time.perf_counter()
     while time.perf_counter() - t0 < seconds_budget or n < 3:
-        run()
+        kc.asymmetric_attention_scores(q, ck)
         n += 1
     t = (time.perf_counter() - t0) / n
+    host = host_cpu()
     return {
         "value": g * DEC_SK / t,
         "unit": "key*heads/s",
-        "cores": _blas_threads(),
+        "cores": host["torch_threads"],
         "kind": "port",
-        "sample": (f"oracle f32 scoring (reference PyTorch branch restated) of 1 query row x {g} query heads "
-                   f"against one KV head's {DEC_SK} compressed keys, {n} repetitions in {n * t:.1f} s "
-                   f"({t * 1e3:.1f} ms each); host {platform.processor() or platform.machine()}"),
+        "host": host,
+        "sample": (f"torch CPU branch (reference PyTorch scoring restated, golden-pinned): 1 query row x {g} query "
+                   f"heads against one KV head's {DEC_SK} compressed keys, {n} repetitions in {n * t:.1f} s "
+                   f"({t * 1e3:.2f} ms each), {host['torch_threads']} threads on {host['model']}"),
     }
 
 
-def _blas_threads() -> int:
-    try:
-        from threadpoolctl import threadpool_info
-        info = threadpool_info()
-        return max(int(i.get("num_threads", 1)) for i in info) if info else 1
-    except Exception:  # pragma: no cover
-        return os.cpu_count() or 1
-
-
 def cpu_baseline(seconds_budget: float) -> dict:
-    """The oracle (numpy restatement of the reference's PyTorch branch) on a bounded
-    slice of the same workload: one KV head group (4 query heads), the first S_cpu
-    positions, causal; compress + scores + softmax + P.V timed together."""
-    import numpy as np
+    """The same torch CPU branch on a bounded slice of the prefill workload: one KV head group
+    (4 query heads) of the 8192-position causal layer, the reference's whole tail (families/
+    qwen2.py:100-117): compress K and V, scores, /sqrt(d) + causal mask, softmax, decompress V,
+    P.V; median of up to 3 runs after one warm-up."""
     import torch
+    import torch.nn.functional as F
 
-    from oracle import tq_oracle as O
     from turboquant_pytorch.compressors import TurboQuantCompressorMSE, TurboQuantCompressorV2
 
-    s_cpu = S  # one KV-head group of the full 8192-token workload
+    _cpu_threads()
     g = HQ // HKV
-    rng = np.random.default_rng(0)
-    k = rng.standard_normal((s_cpu, D)).astype(np.float32)
-    k[:, :4] *= 20
-    v = rng.standard_normal((s_cpu, D)).astype(np.float32)
-    q = rng.standard_normal((g, s_cpu, D)).astype(np.float32)
+    gen = torch.Generator().manual_seed(0)
+    k = torch.randn(1, 1, S, D, generator=gen)
+    k[..., :4] *= 20
+    k = k.to(torch.bfloat16).repeat_interleave(g, dim=1)  # the reference expands K/V per query head
+    v = torch.randn(1, 1, S, D, generator=gen).to(torch.bfloat16).repeat_interleave(g, dim=1)
+    q = torch.randn(1, g, S, D, generator=gen).to(torch.bfloat16)
     kc = TurboQuantCompressorV2(D, BITS, seed=42)
     vc = TurboQuantCompressorMSE(D, BITS, seed=10042)
-    pi_k, s_k, ck_ = kc.Pi.numpy(), kc.S.numpy(), kc.centroids.numpy()
-    pi_v, cv_ = vc.Pi.numpy(), vc.centroids.numpy()
-    coeff = O.COEFF(D)
+    causal = torch.full((S, S), float("-inf")).triu(1)
 
     def run():
-        kk = O.key_compress_unpacked(k, pi_k, s_k, ck_)
-        vv = O.value_compress_unpacked(v, pi_v, cv_)
-        vals = O.value_decompress(vv["indices"], vv["vec_norms"], pi_v, cv_, dtype=np.float32)
-        for h in range(g):
-            sc = O.scores_unpacked(q[h], kk["k_mse"], kk["qjl_signs"], kk["residual_norm"], s_k, coeff,
-                                   dtype=np.float32)
-            O.attention(sc, vals, 1 / math.sqrt(D), causal=True, dtype=np.float32)
+        scores = kc.asymmetric_attention_scores(q, kc.compress(k)) / math.sqrt(D) + causal
+        w = F.softmax(scores.float(), dim=-1).to(q.dtype)
+        return torch.matmul(w, vc.decompress(vc.compress(v)).to(q.dtype))
 
-    run()  # warm-up
+    run()
     times = []
     t_start = time.perf_counter()
     while len(times) < 3 and time.perf_counter() - t_start < seconds_budget:
@@ -149,15 +158,17 @@ def cpu_baseline(seconds_budget: float) -> dict:
         run()
         times.append(time.perf_counter() - t0)
     t = sorted(times)[len(times) // 2]
-    key_heads = g * s_cpu * (s_cpu + 1) // 2
+    key_heads = g * S * (S + 1) // 2
+    host = host_cpu()
     return {
         "value": key_heads / t,
         "unit": "key*heads/s",
-        "cores": _blas_threads(),
+        "cores": host["torch_threads"],
         "kind": "port",
-        "sample": (f"oracle (numpy f32 restatement of the reference PyTorch branch) on 1 KV head x {g} query "
-                   f"heads, {s_cpu} positions causal: compress K/V + scores + softmax + P.V; median of "
-                   f"{len(times)} runs, {t * 1e3:.0f} ms/run; host {platform.processor() or platform.machine()}"),
+        "host": host,
+        "sample": (f"torch CPU branch on 1 KV head x {g} query heads, {S} positions causal: compress K/V + scores + "
+                   f"softmax + P.V; median of {len(times)} runs, {t * 1e3:.0f} ms/run, "
+                   f"{host['torch_threads']} threads on {host['model']}"),
     }
 
 
@@ -272,6 +283,80 @@ def decode_legs(kc, vc, outliers, steps: int, warmup: int) -> tuple[dict, dict]:
     return scores_leg, attn_leg
 
 
+def compress_leg(kc, vc, steps: int, warmup: int) -> dict:
+    """Compression at the north-star scale: keys and values of 4 sequences x 8 kv heads x 32768
+    tokens (1,048,576 rows each, bf16, bits 3), timed separately with HIP events.  HBM: 256 B read
+    + the record written per row (52 B keys, 50 B values).  MFMA: the f32-grade products run as
+    split-f16 passes (hi.hi + lo.hi + hi.lo): keys 6 passes of d^2 MACs per row (y = x Pi^T: 3,
+    proj = u S_eff^T on the rotated-domain residual u: 3), values 3 -- the executed MFMA work,
+    priced against the dense f16 peak."""
+    import torch
+
+    dev = "cuda"
+    shape = (4, HKV, 32768, D)
+    g = torch.Generator(device=dev).manual_seed(9)
+    x = torch.randn(*shape, device=dev, generator=g).to(torch.bfloat16)
+    rows = x.numel() // D
+    out = {}
+    for name, fn, rec, passes in (("keys", kc.compress, key_rec_bytes(BITS, D), 6),
+                                  ("values", vc.compress, val_rec_bytes(BITS, D), 3)):
+        for _ in range(warmup):
+            fn(x)
+        torch.cuda.synchronize()
+        e0, e1 = _events(2)
+        e0.record()
+        for _ in range(steps):
+            fn(x)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / steps * 1e3
+        gbs = rows * (2 * D + rec) / (us * 1e-6) / 1e9
+        tflops = rows * passes * 2 * D * D / (us * 1e-6) / 1e12
+        out[name] = {"us_per_launch": us, "rows_per_s": rows / (us * 1e-6), "hbm_gbs": gbs,
+                     "hbm_frac": gbs / HBM_PEAK_GBS, "mfma_tflops": tflops,
+                     "mfma_frac": tflops / MFMA_F16_PEAK_TFLOPS}
+    both = out["keys"]["us_per_launch"] + out["values"]["us_per_launch"]
+    return {"workload": f"B4 Hkv{HKV} S32768 d{D} bf16 bits{BITS}: {rows} key rows + {rows} value rows",
+            "tokens_per_s": 4 * 32768 / (both * 1e-6), **out}
+
+
+def decode_step_leg(kc, vc, cached: int = 4096, steps: int = 200) -> dict:
+    """One attention layer's eager decode step through the product path (torch.ops.tq): compress the
+    new token's K and V (8 kv heads), prepare the 32 query heads' query, split-K attention over the
+    cached planes.  B = 1, bits 3.  Host time per step (wall clock over `steps` back-to-back steps,
+    synchronised at the end) against device time (HIP events around the same steps)."""
+    import torch
+
+    from turboquant_pytorch import compressed_attention
+
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(5)
+    ck = kc.compress(torch.randn(1, HKV, cached, D, device=dev, generator=g).to(torch.bfloat16))
+    cv = vc.compress(torch.randn(1, HKV, cached, D, device=dev, generator=g).to(torch.bfloat16))
+    k1 = torch.randn(1, HKV, 1, D, device=dev, generator=g).to(torch.bfloat16)
+    v1 = torch.randn(1, HKV, 1, D, device=dev, generator=g).to(torch.bfloat16)
+    q1 = torch.randn(1, HQ, 1, D, device=dev, generator=g).to(torch.bfloat16)
+
+    def step():
+        kc.compress(k1)
+        vc.compress(v1)
+        return compressed_attention(q1, kc, vc, ck, cv, out_dtype=torch.bfloat16)
+
+    for _ in range(20):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = _events(2)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    host_us = (time.perf_counter() - t0) / steps * 1e6
+    return {"workload": f"B1 Hq{HQ} Hkv{HKV} d{D} bits{BITS}, {cached} cached tokens, one new token per step",
+            "host_us_per_step": host_us, "device_us_per_step": e0.elapsed_time(e1) / steps * 1e3}
+
+
 def prefill_leg(kc, vc, q, k, v, steps: int, warmup: int) -> dict:
     """Config-2 step: compress K and V, prepare queries, causal fused attention over
     all S query rows."""
@@ -315,7 +400,7 @@ def prefill_leg(kc, vc, q, k, v, steps: int, warmup: int) -> dict:
     compress_bytes = B * HKV * S * (2 * D * 2 + key_rec_bytes(BITS, D) + val_rec_bytes(BITS, D))
     tflops = attn_flops / (attn_ms * 1e-3) / 1e12
     return {
-        "workload": f"causal prefill B{B} Hq{HQ} Hkv{HKV} d{D} S{S} bits{BITS}: compress K/V + query prep + "
+        "workload": f"configs[1]: causal prefill B{B} Hq{HQ} Hkv{HKV} d{D} S{S} bits{BITS}: compress K/V + query prep + "
                     "fused scores/softmax/P.V",
         "ms_per_step": ms_per_step,
         "key_heads_per_s": key_heads / (ms_per_step * 1e-3),
@@ -388,14 +473,16 @@ def main() -> None:
         "vs_baseline": None,
         "dtype": "f16-mfma/f32-acc",
         "data": "synthetic (bf16 N(0,1) Q/K/V, 4 K channels x20 = randperm(128, seed 1)[:4]; seeds 0 and 2)",
-        "config": {"workload": (f"configs[1] Llama-3-8B attention (Hq{HQ} Hkv{HKV} d{D} bits{BITS}), decode-shaped "
-                                f"scoring: 1 query row x {DEC_B} sequences x {DEC_SK} keys per step, rotating over "
-                                f"{DEC_ROT} caches"),
+        "config": {"workload": (f"north-star target: Llama-3-8B attention (Hq{HQ} Hkv{HKV} d{D} bits{BITS}) at "
+                                f"{DEC_SK // 1024}k context, decode-shaped scoring: 1 query row x {DEC_B} sequences x "
+                                f"{DEC_SK} keys per step, rotating over {DEC_ROT} caches"),
                    "global_batch": DEC_B, "seq_len": DEC_SK, "parallelism": "single-gpu"},
         "roofline": scores_leg["roofline"],
         "compress_tokens_per_s": None if prefill is None else prefill["compress_tokens_per_s"],
         "decode_attention": attn_leg,
         "prefill": prefill,
+        "decode_step": None if args.no_prefill else decode_step_leg(kc, vc),
+        "compress_north_star": None if args.no_prefill else compress_leg(kc, vc, 5, 2),
     }
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline_decode(args.cpu_seconds / 2)

@@ -95,16 +95,19 @@ int tq_dequantize(const uint8_t* packed, int64_t n, int32_t d, int64_t ld_in,
  *   k_mse = (f16(C)[codes] Pi) * vn, r = x - k_mse, rn = ||r||,
  *   proj = r S^T, signs = (proj >= 0),
  * writing codes u8[n, ceil(d*b_eff/8)], signs u8[n, d/8], rn f16[n], vn f16[n].
- * pi_split / s_split: the rotation Pi[d,d] and QJL matrix S[d,d] (row-major)
- * as split matrices, pit_split the split of Pi^T; centroids/bounds are f32 [2^b_eff], [2^b_eff - 1].
+ * The residual is formed in the rotated domain, u = r Pi^T = (vn + 1e-8) y -
+ * vn f16(C)[codes], so rn = ||u|| and proj = u S_eff^T with S_eff = S Pi^T: the
+ * same quantities up to f32 rounding, one d x d product fewer.
+ * pi_split: the rotation Pi[d,d] (row-major) as a split matrix; seff_split: the
+ * split of the f32 product S_eff = S Pi^T (S the QJL matrix); centroids/bounds are
+ * f32 [2^b_eff], [2^b_eff - 1].
  * y_out / proj_out (nullable) receive the f32 rotated rows and projections the
  * codes and signs were taken from.
  * Replaces compressors.py:99-138 (TurboQuantCompressorV2.compress, packed
  * branch; k_mse uses f16-rounded centroids as at :120-122). */
 int tq_compress_keys(const void* x, int32_t dtype, int32_t B, int32_t H,
                      int32_t S, int32_t d, int64_t sxb, int64_t sxh, int64_t sxs,
-                     const uint16_t* pi_split,
-                     const uint16_t* pit_split, const uint16_t* s_split,
+                     const uint16_t* pi_split, const uint16_t* seff_split,
                      const float* centroids, const float* bounds, int32_t b_eff,
                      uint8_t* codes, uint8_t* signs, uint16_t* rn, uint16_t* vn,
                      float* y_out, float* proj_out, void* stream);

@@ -138,7 +138,7 @@ struct KeyArgs {
   const void* x;
   int64_t n;
   Rows4 rows;
-  const uint16_t *pi, *pit, *s;
+  const uint16_t *pi, *seff;
   const float *cent, *bounds;
   int b;
   uint8_t *codes, *signs;
@@ -197,31 +197,17 @@ __global__ void __launch_bounds__(256) compress_keys_kernel(KeyArgs a) {
   }
   __syncthreads();
 
-  // quantize (searchsorted-left on f32 boundaries), reconstruct with f16 centroids
+  // quantize (searchsorted-left on f32 boundaries); the residual in the rotated domain,
+  // u = r Pi^T = (vn + 1e-8) y - vn f16(C)[c]  (compressors.py:120-126: r = x - (yhat Pi) vn)
   for (int e = threadIdx.x; e < T::R * D; e += T::NT) {
     const int r = e / D, i = e % D;
     const float y = Bm[r * T::LDA + i];
     const uint32_t c = searchsorted_left(y, s_bnd, nb);
     idx[r * D + i] = static_cast<uint8_t>(c);
-    Bm[r * T::LDA + i] = s_cent16[c];
+    const float vn = s_vn[r];
+    Bm[r * T::LDA + i] = fmaf(vn + 1e-8f, y, -vn * s_cent16[c]);
     const int64_t gr = row0 + r;
     if (a.y_out && gr < a.n) a.y_out[gr * D + i] = y;
-  }
-  __syncthreads();
-
-  // stage 2: k_mse = (yhat Pi) * vn; r = x - k_mse   (compressors.py:120-126)
-  stage_gemm<D, false, true>(Bm, s_sc, a.pit, acc);
-  __syncthreads();
-#pragma unroll
-  for (int t = 0; t < T::TPW; ++t) {
-    const int tile = wave * T::TPW + t;
-    const int row = (tile % T::NB) * 16 + l16, col = (tile / T::NB) * 16 + 4 * g;
-    const float vn = s_vn[row];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float kmse = (acc[t][e] * kUnsplit2) * vn;
-      Bm[row * T::LDA + col + e] = A[row * T::LDA + col + e] - kmse;
-    }
   }
   __syncthreads();
   {
@@ -242,8 +228,8 @@ __global__ void __launch_bounds__(256) compress_keys_kernel(KeyArgs a) {
   }
   __syncthreads();
 
-  // stage 3: proj = r S^T; sign bit = proj >= 0   (compressors.py:128-130)
-  stage_gemm<D, true, true>(Bm, s_sc, a.s, acc);
+  // stage 2: proj = r S^T = u S_eff^T with S_eff = S Pi^T; sign bit = proj >= 0   (compressors.py:128-130)
+  stage_gemm<D, true, true>(Bm, s_sc, a.seff, acc);
   __syncthreads();
 #pragma unroll
   for (int t = 0; t < T::TPW; ++t) {
@@ -518,7 +504,7 @@ struct TileArgs {
   DivU31 H, S;          // rows enumerate (batch, head, position)
   int64_t sb, sh, ss;   // element strides; unit stride along d
   int vec;              // row starts 16-byte aligned: vector loads
-  const uint16_t *w1, *w2, *w3;  // keys: Pi, Pi^T, S split; values: Pi split; queries: Pi split, S_eff f16
+  const uint16_t *w1, *w2, *w3;  // keys: Pi, -, S_eff split; values: Pi split; queries: Pi split, S_eff f16
   const float *cent, *bounds;
   uint8_t *codes, *signs;
   uint16_t *rn, *vn;
@@ -647,11 +633,6 @@ __device__ __forceinline__ uint32_t code_of(float y, const float (&br)[7], const
 #define TQ_ROW_WAVES 8
 #endif
 constexpr int kRowWaves = TQ_ROW_WAVES;
-// wave-tiles (16 rows) a key wave carries through both phases of a chunk
-#ifndef TQ_KEY_TILES
-#define TQ_KEY_TILES 1
-#endif
-constexpr int kKeyTiles = TQ_KEY_TILES;
 
 template <int D, int DT, int MODE, int BB>
 __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
@@ -900,109 +881,84 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
       raw = nxt;
     }
   } else {
-    // keys: S stays in P2/P3; P0/P1 hold Pi for phase A and Pi^T for phase B of each chunk
+    // keys, one pass per tile: P0/P1 hold Pi, P2/P3 S_eff = S Pi^T (both split), resident for
+    // the whole block.  The residual stays in the rotated domain: with y = xn Pi^T,
+    //   u = r Pi^T = (vn + 1e-8) y - vn f16(C)[c],  rn = ||r|| = ||u||,  proj = r S^T = u S_eff^T
+    // (compressors.py:120-130 form r = x - (yhat Pi) vn in the original domain: the same values
+    // up to f32 rounding, without the yhat Pi product)
+    load_planes<D, T::NT>(P0, P1, a.w1);
     load_planes<D, T::NT>(P2, P3, a.w3);
-    const int64_t per_wave = (ntiles + nwaves - 1) / nwaves;  // tiles of the busiest wave
-    for (int64_t c0 = 0; c0 < per_wave; c0 += kKeyTiles) {
-      __syncthreads();  // the previous chunk's phase B is done with P0/P1
-      load_planes<D, T::NT>(P0, P1, a.w1);
-      wait_vm<0>();  // this wave's plane copies have landed
-      __syncthreads();
-      // ---- phase A: vn, y = xn Pi^T, codes   (compressors.py:108-116)
-      uint32_t cws[kKeyTiles][KS];
-      float vns[kKeyTiles];
-      fetch_row(gw + c0 * nwaves, raw);
+    fetch_row(gw, raw);
+    wait_vm<0>();
+    __syncthreads();
+    for (int64_t t = gw; t < ntiles; t += nwaves) {
+      const int64_t gr = t * 16 + l16;
+      unpack_row(raw, xv);
+      fetch_row(t + nwaves, nxt);  // next tile's row, in flight during the products
+      // ---- vn = ||x||; xn = x / (vn + 1e-8); y = xn Pi^T; codes   (compressors.py:108-116)
+      float ss = 0.f;
 #pragma unroll
-      for (int i = 0; i < kKeyTiles; ++i) {
-        const int64_t t = gw + (c0 + i) * nwaves;
-        const int64_t gr = t * 16 + l16;
-        unpack_row(raw, xv);
-        if (i + 1 < kKeyTiles) fetch_row(t + nwaves, nxt);
-        float ss = 0.f;
+      for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
+        for (int j = 0; j < 8; ++j) ss = fmaf(xv[ks][j], xv[ks][j], ss);
+      const float vn = sqrtf(row_sum(ss));
+      const DivBy div(vn + 1e-8f);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) ss = fmaf(xv[ks][j], xv[ks][j], ss);
-        const float vn = sqrtf(row_sum(ss));
-        vns[i] = vn;
-        const DivBy div(vn + 1e-8f);
+      for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
+        for (int j = 0; j < 8; ++j) xv[ks][j] = div(xv[ks][j]);
+      split_row(xv, kSplit, bh, bl);
+      row_gemm<D, true, true>(P0, P1, bh, bl, acc, l16, g);
+      uint32_t cw[KS];
+      quantize_stage(acc, gr, cw);
+      // ---- u = (vn + 1e-8) y - vn f16(C)[c]; rn = ||u||
+      ss = 0.f;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) xv[ks][j] = div(xv[ks][j]);
-        split_row(xv, kSplit, bh, bl);
-        row_gemm<D, true, true>(P0, P1, bh, bl, acc, l16, g);
-        if (t < ntiles) {
-          quantize_stage(acc, gr, cws[i]);
-          if (g == 0 && gr < a.n) a.vn[gr] = f2h(vn);
-          wave_sync();
-          store_rows(stg, a.codes, t * 16, KC);
-          wave_sync();
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float y = acc_at(acc, ks, j) * kUnsplit2;
+          const float u = fmaf(div.den, y, -vn * s_cent[(cw[ks] >> (BB * j)) & ((1u << BB) - 1u)]);
+          xv[ks][j] = u;
+          ss = fmaf(u, u, ss);
         }
-        raw = nxt;
-      }
-      __syncthreads();  // every wave is done with Pi
-      load_planes<D, T::NT>(P0, P1, a.w2);
-      wait_vm<0>();
-      __syncthreads();
-      // ---- phase B: k_mse = (yhat Pi) vn, r = x - k_mse, rn, proj = r S^T, signs   (compressors.py:120-136)
-      fetch_row(gw + c0 * nwaves, raw);
+      const float rn = sqrtf(row_sum(ss));
+      // split scale from ||x||: |u| <= ~||x||, so u * 2^(10 - e(vn)) keeps both parts in range
+      int e2;
+      frexpf(vn, &e2);
+      split_row(xv, ldexpf(kSplit, -e2), bh, bl);
+      // ---- proj = u S_eff^T; signs = (proj >= 0)   (compressors.py:128-130)
+      row_gemm<D, true, true>(P2, P3, bh, bl, acc, l16, g);
+      const float inv = ldexpf(kUnsplit2, e2);
+      if (t < ntiles) {
 #pragma unroll
-      for (int i = 0; i < kKeyTiles; ++i) {
-        const int64_t t = gw + (c0 + i) * nwaves;
-        const int64_t gr = t * 16 + l16;
-        if (i + 1 < kKeyTiles) fetch_row(t + nwaves, nxt);
-        // yhat = f16(C)[code] times 2^10 (exact)
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-            bh[ks][j] = static_cast<_Float16>(s_cent[(cws[i][ks] >> (BB * j)) & ((1u << BB) - 1u)] * kSplit);
-        row_gemm<D, true, false>(P0, P1, bh, bl, acc, l16, g);
-        unpack_row(raw, xv);
-        const float vn = vns[i];
-        float ss = 0.f;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
+        for (int ks = 0; ks < KS; ++ks) {
+          float4v p0, p1;
+          uint32_t bits = 0;
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            const float rr = xv[ks][j] - (acc_at(acc, ks, j) * kUnsplit2) * vn;
-            xv[ks][j] = rr;
-            ss = fmaf(rr, rr, ss);
+            const float pv = acc_at(acc, ks, j) * inv;
+            if (j < 4) p0[j] = pv;
+            else p1[j - 4] = pv;
+            bits |= (pv >= 0.f ? 1u : 0u) << j;
           }
-        const float rn = sqrtf(row_sum(ss));
-        // split scale from ||x||: |r| <= ~||x||, so r * 2^(10 - e(vn)) keeps both parts in range
-        int e2;
-        frexpf(vn, &e2);
-        split_row(xv, ldexpf(kSplit, -e2), bh, bl);
-        row_gemm<D, true, true>(P2, P3, bh, bl, acc, l16, g);
-        const float inv = ldexpf(kUnsplit2, e2);
-        if (t < ntiles) {
-#pragma unroll
-          for (int ks = 0; ks < KS; ++ks) {
-            float4v p0, p1;
-            uint32_t bits = 0;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const float pv = acc_at(acc, ks, j) * inv;
-              if (j < 4) p0[j] = pv;
-              else p1[j - 4] = pv;
-              bits |= (pv >= 0.f ? 1u : 0u) << j;
-            }
-            if (a.proj_out && gr < a.n) {
-              float4v* po = reinterpret_cast<float4v*>(a.proj_out + gr * D + 32 * ks + 8 * g);
-              po[0] = p0;
-              po[1] = p1;
-            }
-            stg[16 * KC + l16 * SC + 4 * ks + g] = static_cast<uint8_t>(bits);
+          if (a.proj_out && gr < a.n) {
+            float4v* po = reinterpret_cast<float4v*>(a.proj_out + gr * D + 32 * ks + 8 * g);
+            po[0] = p0;
+            po[1] = p1;
           }
-          if (g == 0 && gr < a.n) a.rn[gr] = f2h(rn);
-          wave_sync();
-          store_rows(stg + 16 * KC, a.signs, t * 16, SC);
-          wave_sync();
+          stg[16 * KC + l16 * SC + 4 * ks + g] = static_cast<uint8_t>(bits);
         }
-        raw = nxt;
+        if (g == 0 && gr < a.n) {
+          a.vn[gr] = f2h(vn);
+          a.rn[gr] = f2h(rn);
+        }
+        wave_sync();
+        store_rows(stg, a.codes, t * 16, KC);
+        store_rows(stg + 16 * KC, a.signs, t * 16, SC);
+        wave_sync();
       }
+      raw = nxt;
     }
     wait_vm<0>();  // no plane copy outlives the block, even with no tile to process
   }
@@ -1103,7 +1059,7 @@ using namespace tq;
 extern "C" {
 
 int tq_compress_keys(const void* x, int32_t dtype, int32_t B, int32_t H, int32_t S, int32_t d,
-                     int64_t sxb, int64_t sxh, int64_t sxs, const uint16_t* pi_split, const uint16_t* pit_split, const uint16_t* s_split,
+                     int64_t sxb, int64_t sxh, int64_t sxs, const uint16_t* pi_split, const uint16_t* seff_split,
                      const float* centroids, const float* bounds, int32_t b_eff, uint8_t* codes,
                      uint8_t* signs, uint16_t* rn, uint16_t* vn, float* y_out, float* proj_out,
                      void* stream) {
@@ -1112,20 +1068,20 @@ int tq_compress_keys(const void* x, int32_t dtype, int32_t B, int32_t H, int32_t
   TQ_REQUIRE(B >= 0 && H >= 0 && S >= 0, "tq_compress_keys: bad shape");
   const int64_t n = static_cast<int64_t>(B) * H * S;
   if (n == 0) return TQ_OK;
-  TQ_REQUIRE(x && pi_split && pit_split && s_split && centroids && bounds && codes && signs && rn && vn,
+  TQ_REQUIRE(x && pi_split && seff_split && centroids && bounds && codes && signs && rn && vn,
              "tq_compress_keys: null pointer");
   if (tile_applies(d, n, b_eff) && reinterpret_cast<uintptr_t>(codes) % 4 == 0 &&
       reinterpret_cast<uintptr_t>(signs) % 4 == 0) {
     TileArgs t{};
     t.x = x; t.n = n; t.H = make_div(static_cast<uint32_t>(H)); t.S = make_div(static_cast<uint32_t>(S));
     t.sb = sxb; t.sh = sxh; t.ss = sxs; t.vec = tile_vec(x, dtype, sxb, sxh, sxs);
-    t.w1 = pi_split; t.w2 = pit_split; t.w3 = s_split;
+    t.w1 = pi_split; t.w3 = seff_split;
     t.cent = centroids; t.bounds = bounds;
     t.codes = codes; t.signs = signs; t.rn = rn; t.vn = vn; t.y_out = y_out; t.proj_out = proj_out;
     dispatch_tile<TM_KEYS>(t, d, dtype, b_eff, as_stream(stream));
     return launch_status("tq_compress_keys");
   }
-  KeyArgs a{x, n, Rows4{H, S, sxb, sxh, sxs}, pi_split, pit_split, s_split, centroids, bounds, b_eff, codes, signs, rn, vn,
+  KeyArgs a{x, n, Rows4{H, S, sxb, sxh, sxs}, pi_split, seff_split, centroids, bounds, b_eff, codes, signs, rn, vn,
             y_out, proj_out};
   TQ_SWITCH_DD(launch_keys, d, dtype, a, n, as_stream(stream));
   return launch_status("tq_compress_keys");

@@ -124,7 +124,7 @@ Tensor dequantize(const Tensor& packed_in, const Tensor& cent_in, int64_t b, int
 
 // ---------------------------------------------------------------- compressors (compressors.py)
 std::tuple<Tensor, Tensor, Tensor, Tensor> compress_keys(const Tensor& states, const Tensor& pi_split,
-                                                         const Tensor& pit_split, const Tensor& s_split,
+                                                         const Tensor& seff_split,
                                                          const Tensor& centroids, const Tensor& bounds,
                                                          int64_t b_eff, const c10::optional<Tensor>& y_out,
                                                          const c10::optional<Tensor>& proj_out) {
@@ -141,7 +141,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> compress_keys(const Tensor& states, c
   check_status(tq_compress_keys(x.data_ptr(), dtype_code(x.scalar_type()), static_cast<int32_t>(B),
                                 static_cast<int32_t>(H), static_cast<int32_t>(S), static_cast<int32_t>(D),
                                 x.stride(0), x.stride(1), x.stride(2), ptr<uint16_t>(pi_split),
-                                ptr<uint16_t>(pit_split), ptr<uint16_t>(s_split), ptr<float>(centroids),
+                                ptr<uint16_t>(seff_split), ptr<float>(centroids),
                                 ptr<float>(bounds), static_cast<int32_t>(b_eff), ptr<uint8_t>(codes),
                                 ptr<uint8_t>(signs), ptr<uint16_t>(rn), ptr<uint16_t>(vn), optr<float>(y_out),
                                 optr<float>(proj_out), stream_of(x)),
@@ -290,8 +290,8 @@ TORCH_LIBRARY(tq, m) {
   m.def("unpack_bits(Tensor packed, int b, int d) -> Tensor");
   m.def("quantize_pack(Tensor y, Tensor bounds, int b_eff) -> Tensor");
   m.def("dequantize(Tensor packed, Tensor centroids, int b, int d) -> Tensor");
-  m.def("compress_keys(Tensor states, Tensor pi_split, Tensor pit_split, Tensor s_split, Tensor centroids, "
-        "Tensor bounds, int b_eff, Tensor? y_out=None, Tensor? proj_out=None) -> (Tensor, Tensor, Tensor, Tensor)");
+  m.def("compress_keys(Tensor states, Tensor pi_split, Tensor seff_split, Tensor centroids, Tensor bounds, "
+        "int b_eff, Tensor? y_out=None, Tensor? proj_out=None) -> (Tensor, Tensor, Tensor, Tensor)");
   m.def("compress_values(Tensor states, Tensor pi_split, Tensor bounds, int bits, Tensor? y_out=None) "
         "-> (Tensor, Tensor)");
   m.def("decompress_values(Tensor codes, Tensor vn, Tensor pit_split, Tensor centroids, int bits, int[] shape) "

@@ -38,7 +38,7 @@ _SIGNATURES = {
     "tq_quantize_pack": [_p, _i64, _i32, _i64, _p, _i32, _p, _i64, _p],
     "tq_dequantize": [_p, _i64, _i32, _i64, _p, _i32, _p, _i64, _p],
     "tq_compress_keys": [_p, _i32, _i32, _i32, _i32, _i32, _i64, _i64, _i64,
-                         _p, _p, _p, _p, _p, _i32, _p, _p, _p, _p, _p, _p, _p],
+                         _p, _p, _p, _p, _i32, _p, _p, _p, _p, _p, _p, _p],
     "tq_compress_values": [_p, _i32, _i32, _i32, _i32, _i32, _i64, _i64, _i64,
                            _p, _p, _i32, _p, _p, _p, _p],
     "tq_decompress_values": [_p, _p, _i64, _i32, _p, _p, _i32, _p, _i32, _i64, _p],

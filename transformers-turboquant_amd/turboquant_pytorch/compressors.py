@@ -32,7 +32,7 @@ class _DeviceTables:
     key: tuple
     pi_split: torch.Tensor            # f16 [2, d, d]  split of Pi
     pit_split: torch.Tensor           # f16 [2, d, d]  split of Pi^T
-    s_split: torch.Tensor | None      # f16 [2, d, d]  split of S (keys)
+    seff_split: torch.Tensor | None   # f16 [2, d, d]  split of the f32 S_eff = S Pi^T (keys)
     s_eff16: torch.Tensor | None      # f16 [d, d]     f16(S Pi^T) (keys)
     cent32: torch.Tensor              # f32 [2^b]
     cent16: torch.Tensor              # f16 [2^b]
@@ -48,16 +48,17 @@ def _tables(comp, device: torch.device, with_qjl: bool) -> _DeviceTables:
     pi = comp.Pi.detach().to("cpu", torch.float32)
     cent = comp.centroids.detach().to("cpu", torch.float32)
     bounds = comp.boundaries.detach().to("cpu", torch.float32)
-    s_split = s_eff = None
+    seff_split = s_eff = None
     if s is not None:
         s32 = s.detach().to("cpu", torch.float32)
-        s_split = split_f16(s32).to(device)
-        s_eff = (s32 @ pi.T).to(torch.float16).contiguous().to(device)  # compressors.py:189
+        s_eff32 = s32 @ pi.T  # compressors.py:189 forms S_eff as this f32 product
+        seff_split = split_f16(s_eff32).to(device)
+        s_eff = s_eff32.to(torch.float16).contiguous().to(device)
     t = _DeviceTables(
         key=key,
         pi_split=split_f16(pi).to(device),
         pit_split=split_f16(pi.T.contiguous()).to(device),
-        s_split=s_split,
+        seff_split=seff_split,
         s_eff16=s_eff,
         cent32=cent.contiguous().to(device),
         cent16=cent.to(torch.float16).contiguous().to(device),
@@ -104,8 +105,8 @@ class TurboQuantCompressorV2:
     def _compress_gpu(self, states: torch.Tensor, y_out=None, proj_out=None) -> dict:
         B, H, S, D = states.shape
         t = _tables(self, states.device, with_qjl=True)
-        codes, signs, rn, vn = ops().compress_keys(states, t.pi_split, t.pit_split, t.s_split, t.cent32,
-                                                   t.bounds32, self.mse_bits, y_out, proj_out)
+        codes, signs, rn, vn = ops().compress_keys(states, t.pi_split, t.seff_split, t.cent32, t.bounds32,
+                                                   self.mse_bits, y_out, proj_out)
         return {
             "packed_key_indices": codes,
             "packed_qjl_signs": signs,
