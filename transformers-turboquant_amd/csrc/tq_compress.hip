@@ -19,8 +19,12 @@
 //   memory, L2 resident) is the MFMA A operand and the LDS row tile is the B
 //   operand; the accumulator layout (4 consecutive output columns of one row per
 //   lane) is written straight back into the row tile.
+#include <type_traits>
+
 #include "tq_common.h"
 #include "tq_stream.h"
+
+typedef float float2v __attribute__((ext_vector_type(2)));
 
 namespace tq {
 
@@ -537,17 +541,18 @@ __device__ __forceinline__ int swz(int p, int c) {
 template <int D, int NT, int NP = 2>
 __device__ __forceinline__ void load_planes(_Float16* dst0, _Float16* dst1, const uint16_t* src) {
   constexpr int CH = D * D / 8;  // 16-byte chunks per plane
-  static_assert(CH % NT == 0 && NT % 64 == 0, "whole 64-chunk rounds per wave");
+  static_assert(CH % 64 == 0 && NT % 64 == 0, "whole 64-chunk rounds per wave");
   const uint64_t base = reinterpret_cast<uint64_t>(src);
   const i32x4 desc{static_cast<int>(static_cast<uint32_t>(base)), static_cast<int>(static_cast<uint32_t>(base >> 32) & 0xffffu),
                    NP * D * D * 2, 0x00020000};
   int t = static_cast<int>(threadIdx.x);
   asm volatile("" : "+v"(t));  // recomputed per call: hoisted offsets would hold VGPRs across the tile loop
-  const int w0 = t & ~63;
+  const int w0 = __builtin_amdgcn_readfirstlane(t & ~63);
 #pragma unroll
   for (int pl = 0; pl < NP; ++pl)
 #pragma unroll
-    for (int i = 0; i < CH / NT; ++i) {
+    for (int i = 0; i < (CH + NT - 1) / NT; ++i) {
+      if (CH % NT != 0 && i * NT + w0 >= CH) break;  // wave-uniform: the last round is partial
       const int L = i * NT + t, p = L / (D / 8);
       const int c = swz<D>(p, L % (D / 8));
       const uint32_t voff = static_cast<uint32_t>((pl * D * D + perm_row(p) * D + c * 8) * 2);
@@ -558,10 +563,7 @@ __device__ __forceinline__ void load_planes(_Float16* dst0, _Float16* dst1, cons
 // acc[mb] (output columns 32*(mb>>1) + 8g + 4*(mb&1) + e of row l16) = W . X^T for this
 // wave's 16 rows; B fragments b_hi/b_lo in registers, A from the LDS planes (hi, lo).
 // Passes hi.hi, + lo(W).hi(X) if W_LO, + hi(W).lo(X) if X_LO.
-#ifndef TQ_ROW_WAVES
-#define TQ_ROW_WAVES 8
-#endif
-template <int D, bool W_LO, bool X_LO, bool DBUF = (TQ_ROW_WAVES <= 8)>
+template <int D, bool W_LO, bool X_LO, bool DBUF = true>
 __device__ __forceinline__ void row_gemm(const _Float16* __restrict__ wh, const _Float16* __restrict__ wl,
                                          const half8 (&b_hi)[D / 32], const half8 (&b_lo)[D / 32],
                                          float4v (&acc)[D / 16], int l16, int g) {
@@ -610,15 +612,31 @@ __device__ __forceinline__ void row_gemm(const _Float16* __restrict__ wh, const 
 // value j (0..7) of k-step ks from an accumulator in the permuted layout
 __device__ __forceinline__ float acc_at(const float4v* acc, int ks, int j) { return acc[2 * ks + (j >> 2)][j & 3]; }
 
-// searchsorted-left over the 2^BB - 1 sorted boundaries (quantize.py:334-337):
-// BB <= 3 counts boundaries below y from registers, BB == 4 binary-searches the LDS copy
-template <int BB>
-__device__ __forceinline__ uint32_t code_of(float y, const float (&br)[7], const float* bnd) {
-  if constexpr (BB <= 3) {
-    uint32_t c = 0;
-#pragma unroll
-    for (int j = 0; j < (1 << BB) - 1; ++j) c += br[j] < y ? 1u : 0u;
-    return c;
+// Quantiser table for 3-4 code bits: y -> bucket qbucket(y) = floor(clamp(120 y + 128, 0, 255)),
+// a non-decreasing map (|y| <= 1.0625 stays inside the clamp), and entry k = (the boundary
+// whose bucket is k, or +inf; the number of boundaries in lower buckets).  A boundary in a
+// lower bucket than y lies below y and one in a higher bucket above it, so with at most one
+// boundary per bucket, code = T[k] + (y > B[k]) is searchsorted-left exactly.  Entries of
+// buckets holding two or more boundaries carry bit 31; the kernel then counts instead.
+__device__ __forceinline__ uint32_t qbucket(float y) {
+  return static_cast<uint32_t>(fminf(fmaxf(fmaf(y, 120.f, 128.f), 0.f), 255.f));
+}
+
+// searchsorted-left over the 2^BB - 1 sorted boundaries (quantize.py:334-337).  TAB: the
+// quantiser table; BB == 1: one compare; BB == 2: a two-level search (y > b1 decides the
+// upper bit, then y against b2 or b0 the lower one: for sorted boundaries that is the count
+// [y > b0] + [y > b1] + [y > b2]); BB >= 3 without the table: binary search of the LDS copy.
+template <int BB, bool TAB>
+__device__ __forceinline__ uint32_t code_of(float y, const float (&br)[7], const float* bnd, const uint2* qt) {
+  if constexpr (TAB) {
+    const uint2 e = qt[qbucket(y)];
+    return e.y + (y > __uint_as_float(e.x) ? 1u : 0u);
+  } else if constexpr (BB == 1) {
+    return br[0] < y ? 1u : 0u;
+  } else if constexpr (BB == 2) {
+    const bool hi = br[1] < y;
+    const bool lo = (hi ? br[2] : br[0]) < y;
+    return (hi ? 2u : 0u) + (lo ? 1u : 0u);
   } else {
     uint32_t idx = 0;
 #pragma unroll
@@ -628,15 +646,25 @@ __device__ __forceinline__ uint32_t code_of(float y, const float (&br)[7], const
   }
 }
 
-// waves per block; each holds up to 256 VGPRs and the weights sit in LDS
+// Waves per block; the weights sit in LDS (keys 128 KiB, values 64 KiB, queries 96 KiB), so
+// a compute unit holds one block.  Values of bf16 / f16 rows fit 128 VGPRs with the weight
+// fragments single-buffered: 16 waves (4 per SIMD) hide more latency than 8 (measured at 1M
+// rows, bits 3: 101 vs 122 us).  The others need up to 256 VGPRs: 8 waves.
 #ifndef TQ_ROW_WAVES
 #define TQ_ROW_WAVES 8
 #endif
-constexpr int kRowWaves = TQ_ROW_WAVES;
+#ifndef TQ_VAL_WAVES
+#define TQ_VAL_WAVES 16
+#endif
+template <int MODE, int DT>
+constexpr int row_waves() {
+  return MODE == TM_VALUES && DT != TQ_F32 ? TQ_VAL_WAVES : TQ_ROW_WAVES;
+}
 
 template <int D, int DT, int MODE, int BB>
-__global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
-  using T = RT<D, kRowWaves>;
+__global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(TileArgs a) {
+  using T = RT<D, row_waves<MODE, DT>()>;
+  constexpr bool DBUF = row_waves<MODE, DT>() <= 8;  // weight fragments double-buffered
   constexpr int KS = T::KS, MB = T::MB, NW = T::NW;
   constexpr int KC = D * BB / 8;                                         // packed code bytes per row
   constexpr int SC = D / 8;                                              // sign bytes per row
@@ -645,6 +673,8 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
   __shared__ __attribute__((aligned(16))) _Float16 wsm[NPL * D * D];
   __shared__ __attribute__((aligned(16))) uint8_t stg_all[NW * STG];
   __shared__ float s_cent[MODE == TM_KEYS ? 16 : 1], s_bnd[MODE == TM_QUERY ? 1 : 16];
+  constexpr bool QTAB = MODE != TM_QUERY && BB >= 3;  // quantiser table built (3-4 code bits)
+  __shared__ uint2 s_qt[QTAB ? 256 : 1];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, g = lane >> 4;
@@ -652,7 +682,7 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
   const int64_t ntiles = (a.n + 15) / 16;
   const int64_t nwaves = static_cast<int64_t>(gridDim.x) * NW;
   const int64_t gw = static_cast<int64_t>(blockIdx.x) * NW + wave;  // this wave's tiles: gw, gw + nwaves, ...
-  float br[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float br[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};  // BB <= 2: the boundaries in registers
   if constexpr (MODE != TM_QUERY) {
     constexpr int NC = 1 << BB;
     // keys reconstruct with the f16-rounded centroids (compressors.py:120-122)
@@ -660,11 +690,34 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
       if constexpr (MODE == TM_KEYS) s_cent[tid] = static_cast<float>(static_cast<_Float16>(a.cent[tid]));
       if (tid < NC - 1) s_bnd[tid] = a.bounds[tid];
     }
-    if constexpr (BB <= 3) {
+    if constexpr (BB <= 2) {
 #pragma unroll
       for (int j = 0; j < NC - 1; ++j) br[j] = a.bounds[j];
     }
+    if constexpr (QTAB) {
+      if (tid < 256) {
+        uint32_t below = 0, inside = 0;
+        float bk = __builtin_inff();
+        for (int j = 0; j < NC - 1; ++j) {
+          const float bj = a.bounds[j];
+          const uint32_t kb = qbucket(bj);
+          below += kb < static_cast<uint32_t>(tid) ? 1u : 0u;
+          if (kb == static_cast<uint32_t>(tid)) {
+            ++inside;
+            bk = bj;
+          }
+        }
+        s_qt[tid] = make_uint2(__float_as_uint(bk), below | (inside > 1 ? 0x80000000u : 0u));
+      }
+    }
   }
+  // after the first block barrier: every bucket holds at most one boundary (wave-uniform)
+  auto qtable_ok = [&]() {
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bad |= (s_qt[QTAB ? 4 * lane + i : 0].y >> 31) != 0u;
+    return !__any(bad);
+  };
   _Float16* const P0 = wsm;
   _Float16* const P1 = wsm + D * D;
   _Float16* const P2 = wsm + (NPL > 2 ? 2 : 0) * D * D;
@@ -676,6 +729,7 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
   struct Raw {
     u32x4 v[KS][RW];
   };
+  Raw raw, nxt;  // this tile's row and the next one, in flight
   auto fetch_row = [&](int64_t t, Raw& raw) {
     const int64_t gr = t * 16 + l16;
     if (t >= ntiles || gr >= a.n) {
@@ -727,14 +781,27 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
         }
       }
   };
-  // sum / max over the 4 lanes of a row (lanes l16, l16+16, l16+32, l16+48)
+  half8 bh[KS], bl[KS];
+  float4v acc[MB];
+  float xv[KS][8];
+  // sum / max over the 4 lanes of a row (lanes l16, l16+16, l16+32, l16+48), on the VALU:
+  // v_permlane16_swap / v_permlane32_swap of a value with itself leave, in every lane, the
+  // lane's own value in one result and its partner's (lane ^ 16, lane ^ 32) in the other
+  auto xor_pair = [](float v, auto half) {
+    const uint32_t u = __float_as_uint(v);
+    const auto r = decltype(half)::value == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                                               : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return float2v{__uint_as_float(r[0]), __uint_as_float(r[1])};
+  };
   auto row_sum = [&](float v) {
-    v += __shfl_xor(v, 16, 64);
-    return v + __shfl_xor(v, 32, 64);
+    float2v p = xor_pair(v, std::integral_constant<int, 16>{});
+    p = xor_pair(p[0] + p[1], std::integral_constant<int, 32>{});
+    return p[0] + p[1];
   };
   auto row_max = [&](float v) {
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    return fmaxf(v, __shfl_xor(v, 32, 64));
+    float2v p = xor_pair(v, std::integral_constant<int, 16>{});
+    p = xor_pair(fmaxf(p[0], p[1]), std::integral_constant<int, 32>{});
+    return fmaxf(p[0], p[1]);
   };
   auto split_row = [&](const float (&v)[KS][8], float sc, half8 (&hi)[KS], half8 (&lo)[KS]) {
 #pragma unroll
@@ -760,35 +827,95 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
     uint32_t* dst = reinterpret_cast<uint32_t*>(out + row0 * bytes);
     for (int i = lane; i < nd; i += 64) dst[i] = reinterpret_cast<const uint32_t*>(src)[i];
   };
-  // y -> codes of this lane's 8 columns per k-step, staged at the row's packed position
-  auto quantize_stage = [&](const float4v (&acc)[MB], int64_t gr, uint32_t (&cw)[KS]) {
+  // y = acc * ysc -> codes of this lane's 8 columns of k-step ks, staged at the row's packed
+  // position; each(ks, j, acc value, code) sees every element
+  auto quantize_ks = [&](auto tab, const float4v (&acc)[MB], float ysc, int64_t gr, int ks, auto&& each) {
+    constexpr bool TAB = decltype(tab)::value;
+    float4v y0, y1;
+    uint32_t v = 0;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      float4v y0, y1;
-      uint32_t v = 0;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float y = acc_at(acc, ks, j) * kUnsplit2;
-        if (j < 4) y0[j] = y;
-        else y1[j - 4] = y;
-        v |= code_of<BB>(y, br, s_bnd) << (BB * j);
-      }
-      cw[ks] = v;
-      if (a.y_out && gr < a.n) {
-        float4v* yo = reinterpret_cast<float4v*>(a.y_out + gr * D + 32 * ks + 8 * g);
-        yo[0] = y0;
-        yo[1] = y1;
-      }
-      uint8_t* dst = stg + l16 * KC + (32 * ks + 8 * g) * BB / 8;
+    for (int j = 0; j < 8; ++j) {
+      const float av = acc_at(acc, ks, j);
+      const float y = av * ysc;
+      if (j < 4) y0[j] = y;
+      else y1[j - 4] = y;
+      const uint32_t c = code_of<BB, TAB>(y, br, s_bnd, s_qt);
+      v |= c << (BB * j);
+      each(ks, j, av, c);
+    }
+    if (a.y_out && gr < a.n) {
+      float4v* yo = reinterpret_cast<float4v*>(a.y_out + gr * D + 32 * ks + 8 * g);
+      yo[0] = y0;
+      yo[1] = y1;
+    }
+    uint8_t* dst = stg + l16 * KC + (32 * ks + 8 * g) * BB / 8;
+    if constexpr (BB == 2) {
+      *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(v);
+    } else if constexpr (BB == 4) {
+      *reinterpret_cast<uint32_t*>(dst) = v;
+    } else {
 #pragma unroll
       for (int k = 0; k < BB; ++k) dst[k] = static_cast<uint8_t>(v >> (8 * k));
     }
   };
+  auto quantize_stage = [&](auto tab, const float4v (&acc)[MB], float ysc, int64_t gr, auto&& each) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) quantize_ks(tab, acc, ysc, gr, ks, each);
+  };
+  // ---- vn = ||x|| and y-side product x Pi^T of this lane's row (compressors.py:108-112,
+  // :274-276).  bf16 / f16 rows are exact in f16 under a power-of-two row scale 2^(15 - e)
+  // (vn < 2^e; elements below ~2^-32 vn round), so x Pi^T takes the weight's hi and lo parts
+  // against one x operand: 2 MFMA passes; f32 rows are split into hi + lo under 2^(10 - e):
+  // 3 passes.  On return acc * xs = x Pi^T, and y = x Pi^T / (vn + 1e-8) = acc * (xs / den).
+  constexpr bool XEXACT = DT != TQ_F32;
+  constexpr int SX = XEXACT ? 15 : 10;
+  auto front = [&](float& vn, int& e2, float& xs) {
+    float ss = 0.f;
+    if constexpr (XEXACT) {
+      // squares of the 16-bit pairs straight from the raw words (products exact in f32)
+      typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+      typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t u = raw.v[ks][0][w];
+          if constexpr (DT == TQ_BF16) {
+            const bf16x2 p = __builtin_bit_cast(bf16x2, u);
+            ss = __builtin_amdgcn_fdot2_f32_bf16(p, p, ss, false);
+          } else {
+            const f16x2 p = __builtin_bit_cast(f16x2, u);
+            ss = __builtin_amdgcn_fdot2(p, p, ss, false);
+          }
+        }
+    } else {
+      unpack_row(raw, xv);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = fmaf(xv[ks][j], xv[ks][j], ss);
+    }
+    vn = sqrtf(row_sum(ss));
+    frexpf(vn, &e2);
+    e2 = e2 < -100 ? -100 : e2;  // tiny rows: the scale stays finite
+    const float sc = ldexpf(1.f, SX - e2);
+    if constexpr (XEXACT) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t w = raw.v[ks][0][j >> 1];
+          const uint16_t h = static_cast<uint16_t>((j & 1) ? (w >> 16) : (w & 0xffffu));
+          const float x = DT == TQ_F16 ? h2f(h) : bf16_to_f32(h);
+          bh[ks][j] = static_cast<_Float16>(x * sc);
+        }
+    } else {
+      split_row(xv, sc, bh, bl);
+    }
+    row_gemm<D, true, !XEXACT, DBUF>(P0, P1, bh, bl, acc, l16, g);
+    xs = ldexpf(1.f / kSplit, e2 - SX);
+  };
 
-  half8 bh[KS], bl[KS];
-  float4v acc[MB];
-  float xv[KS][8];
-  Raw raw, nxt;
 
   if constexpr (MODE == TM_QUERY) {
     load_planes<D, T::NT>(P0, P1, a.w1);
@@ -853,37 +980,33 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
     fetch_row(gw, raw);
     wait_vm<0>();
     __syncthreads();
-    for (int64_t t = gw; t < ntiles; t += nwaves) {
-      const int64_t gr = t * 16 + l16;
-      unpack_row(raw, xv);
-      fetch_row(t + nwaves, nxt);  // next tile's row, in flight during the product
-      // ---- vn = ||x||; xn = x / (vn + 1e-8)   (compressors.py:274-275)
-      float ss = 0.f;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) ss = fmaf(xv[ks][j], xv[ks][j], ss);
-      const float vn = sqrtf(row_sum(ss));
-      const DivBy div(vn + 1e-8f);
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) xv[ks][j] = div(xv[ks][j]);
-      split_row(xv, kSplit, bh, bl);
-      // ---- y = xn Pi^T (compressors.py:276); codes = searchsorted-left, packed LSB first
-      row_gemm<D, true, true>(P0, P1, bh, bl, acc, l16, g);
-      uint32_t cw[KS];
-      quantize_stage(acc, gr, cw);
-      if (g == 0 && gr < a.n) a.vn[gr] = f2h(vn);
-      wave_sync();
-      store_rows(stg, a.codes, t * 16, KC);
-      wave_sync();
-      raw = nxt;
+    auto tiles = [&](auto tab) {
+      for (int64_t t = gw; t < ntiles; t += nwaves) {
+        const int64_t gr = t * 16 + l16;
+        fetch_row(t + nwaves, nxt);  // next tile's row, in flight during the product
+        // ---- vn = ||x||; y = (x / (vn + 1e-8)) Pi^T; codes = searchsorted-left, packed LSB
+        // first   (compressors.py:274-287)
+        float vn, xs;
+        int e2;
+        front(vn, e2, xs);
+        quantize_stage(tab, acc, xs / (vn + 1e-8f), gr, [](int, int, float, uint32_t) {});
+        if (g == 0 && gr < a.n) a.vn[gr] = f2h(vn);
+        wave_sync();
+        store_rows(stg, a.codes, t * 16, KC);
+        wave_sync();
+        raw = nxt;
+      }
+    };
+    if constexpr (QTAB) {
+      if (qtable_ok()) tiles(std::true_type{});
+      else tiles(std::false_type{});
+    } else {
+      tiles(std::false_type{});
     }
   } else {
     // keys, one pass per tile: P0/P1 hold Pi, P2/P3 S_eff = S Pi^T (both split), resident for
-    // the whole block.  The residual stays in the rotated domain: with y = xn Pi^T,
-    //   u = r Pi^T = (vn + 1e-8) y - vn f16(C)[c],  rn = ||r|| = ||u||,  proj = r S^T = u S_eff^T
+    // the whole block.  The residual stays in the rotated domain:
+    //   u = r Pi^T = x Pi^T - vn f16(C)[c],  rn = ||r|| = ||u||,  proj = r S^T = u S_eff^T
     // (compressors.py:120-130 form r = x - (yhat Pi) vn in the original domain: the same values
     // up to f32 rounding, without the yhat Pi product)
     load_planes<D, T::NT>(P0, P1, a.w1);
@@ -891,63 +1014,54 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
     fetch_row(gw, raw);
     wait_vm<0>();
     __syncthreads();
-    for (int64_t t = gw; t < ntiles; t += nwaves) {
-      const int64_t gr = t * 16 + l16;
-      unpack_row(raw, xv);
-      fetch_row(t + nwaves, nxt);  // next tile's row, in flight during the products
-      // ---- vn = ||x||; xn = x / (vn + 1e-8); y = xn Pi^T; codes   (compressors.py:108-116)
-      float ss = 0.f;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) ss = fmaf(xv[ks][j], xv[ks][j], ss);
-      const float vn = sqrtf(row_sum(ss));
-      const DivBy div(vn + 1e-8f);
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) xv[ks][j] = div(xv[ks][j]);
-      split_row(xv, kSplit, bh, bl);
-      row_gemm<D, true, true>(P0, P1, bh, bl, acc, l16, g);
-      uint32_t cw[KS];
-      quantize_stage(acc, gr, cw);
-      // ---- u = (vn + 1e-8) y - vn f16(C)[c]; rn = ||u||
-      ss = 0.f;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float y = acc_at(acc, ks, j) * kUnsplit2;
-          const float u = fmaf(div.den, y, -vn * s_cent[(cw[ks] >> (BB * j)) & ((1u << BB) - 1u)]);
-          xv[ks][j] = u;
-          ss = fmaf(u, u, ss);
-        }
-      const float rn = sqrtf(row_sum(ss));
-      // split scale from ||x||: |u| <= ~||x||, so u * 2^(10 - e(vn)) keeps both parts in range
-      int e2;
-      frexpf(vn, &e2);
-      split_row(xv, ldexpf(kSplit, -e2), bh, bl);
-      // ---- proj = u S_eff^T; signs = (proj >= 0)   (compressors.py:128-130)
-      row_gemm<D, true, true>(P2, P3, bh, bl, acc, l16, g);
-      const float inv = ldexpf(kUnsplit2, e2);
-      if (t < ntiles) {
+    auto tiles = [&](auto tab) {
+      for (int64_t t = gw; t < ntiles; t += nwaves) {
+        const int64_t gr = t * 16 + l16;
+        fetch_row(t + nwaves, nxt);  // next tile's row, in flight during the products
+        // ---- vn = ||x||; y = (x / (vn + 1e-8)) Pi^T; codes   (compressors.py:108-116)
+        float vn, xs;
+        int e2;
+        front(vn, e2, xs);
+        // ---- u = x Pi^T - vn f16(C)[c], carried as w = u / xs = acc - (vn / xs) f16(C)[c]
+        // (xs a power of two, so u = w xs and rn = ||u|| = ||w|| xs exactly)
+        const float vnw = ldexpf(vn, SX + 10 - e2);
+        // |u| <= ||x|| + ||k_mse|| < 2^(e + 1): u * 2^(10 - e) = w * 2^-SX keeps both split
+        // parts in range; each w is split as it is formed
+        float ss = 0.f;
+        quantize_stage(tab, acc, xs / (vn + 1e-8f), gr, [&](int ks, int j, float av, uint32_t c) {
+          const float w = fmaf(-vnw, s_cent[c], av);
+          ss = fmaf(w, w, ss);
+          _Float16 h, l;
+          split_f16(w * (1.f / (1 << SX)), h, l);
+          bh[ks][j] = h;
+          bl[ks][j] = l;
+        });
+        const float rn = sqrtf(row_sum(ss)) * xs;
+        // ---- proj = u S_eff^T; signs = (proj >= 0)   (compressors.py:128-130).  Read off the
+        // accumulator's sign bits: the scale to proj is positive, and an accumulator started at
+        // +0 never ends at -0
+        row_gemm<D, true, true>(P2, P3, bh, bl, acc, l16, g);
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          float4v p0, p1;
-          uint32_t bits = 0;
+          uint32_t neg = 0;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float pv = acc_at(acc, ks, j) * inv;
-            if (j < 4) p0[j] = pv;
-            else p1[j - 4] = pv;
-            bits |= (pv >= 0.f ? 1u : 0u) << j;
-          }
-          if (a.proj_out && gr < a.n) {
+          for (int j = 0; j < 8; ++j) neg |= (__float_as_uint(acc_at(acc, ks, j)) >> 31) << j;
+          stg[16 * KC + l16 * SC + 4 * ks + g] = static_cast<uint8_t>(~neg);
+        }
+        if (a.proj_out && gr < a.n) {
+          const float inv = ldexpf(kUnsplit2, e2);
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) {
+            float4v p0, p1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              p0[j] = acc_at(acc, ks, j) * inv;
+              p1[j] = acc_at(acc, ks, j + 4) * inv;
+            }
             float4v* po = reinterpret_cast<float4v*>(a.proj_out + gr * D + 32 * ks + 8 * g);
             po[0] = p0;
             po[1] = p1;
           }
-          stg[16 * KC + l16 * SC + 4 * ks + g] = static_cast<uint8_t>(bits);
         }
         if (g == 0 && gr < a.n) {
           a.vn[gr] = f2h(vn);
@@ -957,8 +1071,14 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
         store_rows(stg, a.codes, t * 16, KC);
         store_rows(stg + 16 * KC, a.signs, t * 16, SC);
         wave_sync();
+        raw = nxt;
       }
-      raw = nxt;
+    };
+    if constexpr (QTAB) {
+      if (qtable_ok()) tiles(std::true_type{});
+      else tiles(std::false_type{});
+    } else {
+      tiles(std::false_type{});
     }
     wait_vm<0>();  // no plane copy outlives the block, even with no tile to process
   }
@@ -968,7 +1088,7 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_kernel(TileArgs a) {
 template <int D, int DT, int MODE, int BB>
 static void launch_tile(const TileArgs& a, hipStream_t s) {
   static int cache[16] = {};
-  using T = RT<D, kRowWaves>;
+  using T = RT<D, row_waves<MODE, DT>()>;
   const int64_t blocks = (a.n + T::R - 1) / T::R;  // one 16-row tile per wave
   const int64_t res = resident_blocks(reinterpret_cast<const void*>(&rows_kernel<D, DT, MODE, BB>), T::NT, cache);
   const unsigned grid = static_cast<unsigned>(blocks < res ? blocks : res);
