@@ -32,28 +32,17 @@
 
 namespace tq {
 
-#ifndef TQ_ATTN_WAVES
-#define TQ_ATTN_WAVES 4
-#endif
-#ifndef TQ_ATTN_NBW
-#define TQ_ATTN_NBW 2
-#endif
-#ifndef TQ_ATTN_KT
-#define TQ_ATTN_KT 32
-#endif
-#ifndef TQ_ATTN_MINBLK
-#define TQ_ATTN_MINBLK 2
-#endif
-#ifndef TQ_ATTN_TAU
-#define TQ_ATTN_TAU 8.0f
-#endif
+constexpr int kAttnWaves = 4;      // waves per block
+constexpr int kAttnColBlocks = 2;  // 16-column blocks per wave (head_dim <= 128)
+constexpr int kAttnKeys = 32;      // keys per tile
+constexpr float kAttnTau = 8.0f;   // lazy-rescale headroom of the online softmax (log2 units)
 
 template <int D>
 struct ATile {
-  static constexpr int NW = TQ_ATTN_WAVES;          // waves per block
+  static constexpr int NW = kAttnWaves;          // waves per block
   static constexpr int NT = 64 * NW;                // threads per block
-  static constexpr int KT = TQ_ATTN_KT;             // keys per tile
-  static constexpr int NBW = (D == 256) ? 1 : TQ_ATTN_NBW;
+  static constexpr int KT = kAttnKeys;             // keys per tile
+  static constexpr int NBW = (D == 256) ? 1 : kAttnColBlocks;
   static constexpr int BR = NW * 16 * NBW;          // (query, head) columns per block
   static constexpr int KS = D / 32;                 // k-steps of the score MFMAs
   static constexpr int MBK = KT / 16;               // 16-key blocks per tile
@@ -108,7 +97,7 @@ __device__ __forceinline__ void store4(void* out, int64_t o, float4v v) {
 }
 
 template <int D, int KB, bool SCORES, bool MASK>
-__global__ void __launch_bounds__(64 * TQ_ATTN_WAVES, TQ_ATTN_MINBLK) attn_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
   using T = ATile<D>;
   constexpr int KT = T::KT, NBW = T::NBW, KS = T::KS, MBK = T::MBK, DB = T::DB, NT = T::NT;
   constexpr int KC = D * KB / 8;          // key code bytes per row
@@ -403,7 +392,7 @@ __global__ void __launch_bounds__(64 * TQ_ATTN_WAVES, TQ_ATTN_MINBLK) attn_kerne
         }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const bool grow = tmax > m_run[nb] + TQ_ATTN_TAU;
+        const bool grow = tmax > m_run[nb] + kAttnTau;
         if (__any(grow)) {
           const float m_new = grow ? tmax : m_run[nb];
           const float alpha = (m_run[nb] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[nb] - m_new);

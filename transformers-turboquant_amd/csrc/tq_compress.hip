@@ -650,15 +650,9 @@ __device__ __forceinline__ uint32_t code_of(float y, const float (&br)[7], const
 // a compute unit holds one block.  Values of bf16 / f16 rows fit 128 VGPRs with the weight
 // fragments single-buffered: 16 waves (4 per SIMD) hide more latency than 8 (measured at 1M
 // rows, bits 3: 101 vs 122 us).  The others need up to 256 VGPRs: 8 waves.
-#ifndef TQ_ROW_WAVES
-#define TQ_ROW_WAVES 8
-#endif
-#ifndef TQ_VAL_WAVES
-#define TQ_VAL_WAVES 16
-#endif
 template <int MODE, int DT>
 constexpr int row_waves() {
-  return MODE == TM_VALUES && DT != TQ_F32 ? TQ_VAL_WAVES : TQ_ROW_WAVES;
+  return MODE == TM_VALUES && DT != TQ_F32 ? 16 : 8;
 }
 
 template <int D, int DT, int MODE, int BB>

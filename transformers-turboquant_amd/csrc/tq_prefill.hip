@@ -29,17 +29,11 @@
 
 #include <type_traits>
 
-#ifndef TQ_PF_R
-#define TQ_PF_R 2  // raw tiles in the LDS ring (R-1 in flight while one is decoded)
-#endif
-#ifndef TQ_PF_WAVES
-#define TQ_PF_WAVES 4  // waves per block, each with two 16-column blocks (128 or 256 columns)
-#endif
-#ifndef TQ_PF_PRIO
-#define TQ_PF_PRIO 1  // 1: raise the wave priority while it issues MFMAs
-#endif
 
 namespace tq {
+
+constexpr int kPfRing = 2;   // raw tiles in the LDS ring (one in flight while one is decoded)
+constexpr int kPfWaves = 4;  // waves per block, each with two 16-column blocks: 128 columns
 
 struct PrefillArgs {
   const uint16_t* q_rot;
@@ -62,7 +56,7 @@ struct PrefillArgs {
 
 template <int BITS>
 struct PfCfg {
-  static constexpr int D = 128, KT = 32, R = TQ_PF_R, NW = TQ_PF_WAVES, NT = 64 * NW;
+  static constexpr int D = 128, KT = 32, R = kPfRing, NW = kPfWaves, NT = 64 * NW;
   static_assert(NW == 4 || NW == 8, "4 or 8 waves per block");
   static constexpr int KB = BITS - 1, VB = BITS;
   static constexpr int KC = D * KB / 8, SC = D / 8, VC = D * VB / 8;  // bytes per packed row
@@ -98,7 +92,7 @@ constexpr uint32_t odd_fields() {
 }
 
 template <int BITS, bool MASK>
-__global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_per_eu(2))) prefill_kernel(PrefillArgs a) {
+__global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2))) prefill_kernel(PrefillArgs a) {
   using C = PfCfg<BITS>;
   constexpr int D = C::D, KT = C::KT, R = C::R, KB = C::KB, VB = C::VB;
   constexpr int KC = C::KC, SC = C::SC, VC = C::VC, LDK = C::LDK, LDV = C::LDV;
@@ -433,20 +427,16 @@ __global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_
     if (wave == 0 && t + R < nt) issue(t + R);
     float4v sacc[2][NBW], tacc[2][NBW];
     float sc[NBW][2][4];
-    if (TQ_PF_PRIO == 2) __builtin_amdgcn_s_setprio(1);
+    // the wave's priority is raised while it issues MFMAs
     decode_ks(t + 1, nK, nS);  // overlaps the score MFMAs
-    if (TQ_PF_PRIO == 1) __builtin_amdgcn_s_setprio(1);
-    if (TQ_PF_PRIO == 3) __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_s_setprio(1);
     scores(cK, cS, sacc, tacc);
-    if (TQ_PF_PRIO == 1 || TQ_PF_PRIO == 2) __builtin_amdgcn_s_setprio(0);
-    if (TQ_PF_PRIO == 3) __builtin_amdgcn_s_setprio(1);
+    __builtin_amdgcn_s_setprio(0);
     softmax_max(t, cF, sacc, tacc, sc);
-    if (TQ_PF_PRIO == 1 || TQ_PF_PRIO == 2) __builtin_amdgcn_s_setprio(1);
-    if (TQ_PF_PRIO == 3) __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_s_setprio(1);
     pv_tile(cV, sc);
-    if (TQ_PF_PRIO == 1) __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_s_setprio(0);
     decode_v(t + 1, nV, nF);   // overlaps the P.V MFMAs
-    if (TQ_PF_PRIO == 2) __builtin_amdgcn_s_setprio(0);
   };
   for (int t = 0; t < nt; t += 2) {
     iter(t, sK0, sS0, sV0, fac0, sK1, sS1, sV1, fac1);
@@ -527,7 +517,7 @@ __global__ void __launch_bounds__(64 * TQ_PF_WAVES) __attribute__((amdgpu_waves_
 
 // Used by tq_attn.hip's entry points.
 bool prefill_applies(int Hq, int Hkv, int d, int bits, int val_bits) {
-  return d == 128 && bits >= 2 && bits <= 4 && val_bits == bits && Hq / Hkv <= TQ_PF_WAVES * 32;
+  return d == 128 && bits >= 2 && bits <= 4 && val_bits == bits && Hq / Hkv <= kPfWaves * 32;
 }
 
 int prefill_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, const uint8_t* kcodes,
