@@ -17,6 +17,7 @@ from oracle import tq_oracle as O
 from test_gpu_kernels import _np, _oracle_attention, _oracle_scores, _planes
 from turboquant_pytorch import _native, compressed_attention
 from turboquant_pytorch.compressors import TurboQuantCompressorMSE, TurboQuantCompressorV2
+from turboquant_pytorch.kernels.attention import scores_from_prepared
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -34,6 +35,7 @@ def _on_decode_path(B, hq, hkv, sq, sk, bits, d=128):
 @pytest.mark.parametrize("bits", [2, 3, 4])
 @pytest.mark.parametrize("hq,hkv,sq,sk", [
     (32, 8, 1, 4097), (8, 8, 1, 300), (16, 2, 2, 1000), (4, 1, 4, 65), (32, 8, 1, 1),
+    (24, 4, 1, 2500), (16, 2, 1, 3000), (3, 1, 1, 999), (6, 2, 2, 513),
 ])
 def test_decode_scores_match_oracle(bits, hq, hkv, sq, sk):
     _case(bits=bits, hq=hq, hkv=hkv, sq=sq, sk=sk)
@@ -48,6 +50,46 @@ def test_decode_scores_match_oracle(bits, hq, hkv, sq, sk):
     ref = _oracle_scores(kc, q, ck, hq, hkv)
     assert got.shape == ref.shape
     assert O.rel_err(got, ref) < REL
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("cb", ["nonaffine", "shifted", "reference"])
+@pytest.mark.parametrize("qmul", [1.0, 300.0, 1e-5])
+def test_decode_scores_any_codebook(bits, cb, qmul):
+    """Decode scores with key codebooks that are not odd (shifted, and for 2-bit codes
+    not affine in the code bits: c3 - c2 != c1 - c0), and queries scaled far from 1,
+    against the oracle evaluated with the same f16 codebook.  One query column is all
+    zero."""
+    _case(bits=bits, cb=cb, qmul=qmul)
+    B, hq, hkv, sq, sk, d = 2, 12, 2, 1, 1500, 128
+    assert _on_decode_path(B, hq, hkv, sq, sk, bits)
+    torch.manual_seed(7 * bits + len(cb))
+    k = torch.randn(B, hkv, sk, d, device=DEV, dtype=torch.bfloat16)
+    q = torch.randn(B, hq, sq, d, device=DEV) * qmul
+    q[1, 5] = 0.0
+    kc = TurboQuantCompressorV2(d, bits, seed=42, device=DEV)
+    ck = kc.compress(k)
+    cent = kc.centroids.cpu().double()
+    if cb == "shifted":
+        cent = cent + 0.3 * cent.abs().max()
+    elif cb == "nonaffine":
+        cent = cent * torch.linspace(0.6, 1.7, len(cent), dtype=torch.float64)
+    cent16 = cent.to(torch.float16)
+    q_rot, q_proj = kc.prepare_queries(q)
+    got = _np(scores_from_prepared(q_rot, q_proj, ck["packed_key_indices"], ck["packed_qjl_signs"],
+                                   ck["residual_norm"], ck["vec_norms"], cent16.to(DEV), bits,
+                                   O.COEFF(d), hkv, sk))
+    codes, signs, rn, vn = _planes(ck, d, kc.mse_bits)
+    qr = _np(q_rot.float()).reshape(B, hq, sq, d)
+    qp = _np(q_proj).reshape(B, hq, sq, d)
+    ref = np.zeros((B, hq, sq, sk))
+    for b in range(B):
+        for h in range(hq):
+            r = slice((b * hkv + h // (hq // hkv)) * sk, (b * hkv + h // (hq // hkv) + 1) * sk)
+            ref[b, h] = O.scores_packed(qr[b, h], qp[b, h], codes[r], signs[r], rn[r], vn[r],
+                                        cent16.numpy(), O.COEFF(d))
+    assert np.all(got[1, 5] == 0.0)
+    assert O.rel_err(got, ref) < REL, O.rel_err(got, ref)
 
 
 @pytest.mark.parametrize("bits", [2, 3, 4])
