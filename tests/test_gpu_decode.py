@@ -99,6 +99,9 @@ def test_decode_scores_any_codebook(bits, cb, qmul):
     (4, 4, 1, 1, False, 1.0, 1.0),
     (16, 1, 1, 700, True, 8.0, 1.0),     # sharp softmax, 16 heads per kv head
     (2, 1, 8, 3000, True, 1.0, 3000.0),  # value norms ~3e4: near the f16 range
+    (8, 4, 2, 1025, True, 1.0, 1.0),     # 4 columns (2 heads x 2 rows), causal
+    (12, 4, 1, 3001, False, 8.0, 3000.0),
+    (6, 2, 1, 2048, True, 1.0, 0.01),
 ])
 def test_decode_attention_matches_oracle_and_tiled(bits, hq, hkv, sq, sk, causal, qmul, vmul):
     _case(bits=bits, hq=hq, hkv=hkv, sq=sq, sk=sk, causal=causal, qmul=qmul, vmul=vmul)
@@ -120,10 +123,11 @@ def test_decode_attention_matches_oracle_and_tiled(bits, hq, hkv, sq, sk, causal
     assert O.rel_err(tiled, ref) < REL
 
 
-def test_decode_attention_mask_and_dtypes():
-    _case(what="decode mask")
+@pytest.mark.parametrize("hq,hkv,sq", [(8, 2, 2), (4, 2, 2)])
+def test_decode_attention_mask_and_dtypes(hq, hkv, sq):
+    _case(what="decode mask", hq=hq, hkv=hkv, sq=sq)
     torch.manual_seed(12)
-    B, hq, hkv, sq, sk, d = 2, 8, 2, 2, 600, 128
+    B, sk, d = 2, 600, 128
     assert _on_decode_path(B, hq, hkv, sq, sk, 3)
     q = torch.randn(B, hq, sq, d, device=DEV)
     k = torch.randn(B, hkv, sk, d, device=DEV)

@@ -360,6 +360,281 @@ decode_attn_lds_kernel(DecodeArgs a) {
   }
 }
 
+// Fused decode attention for 1- and 2-bit key codes and at most 4 columns, scores on the
+// integer MFMA in bit-plane form (PlaneQuery, tq_decode.h) with the keys on the N side:
+// lane (key n, group g) scores key n of each 16-key block for column g, so the softmax
+// runs once per (column, key) instead of once per MFMA column.  P goes through a small
+// per-wave LDS tile into the P^T operand of the value MFMA (the same O^T += V^T P^T step
+// as decode_attn_lds_kernel, with column n of O^T serving column n & 3).
+template <int KB, int R>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+decode_attn_i8_kernel(DecodeArgs a) {
+  constexpr int D = 128, BITS = KB + 1;
+  using L = SmallLuts<BITS>;
+  using PQ = PlaneQuery<KB>;
+  constexpr int VB = L::VB;
+  constexpr int DB = D / 16;
+  constexpr int KC = D * KB / 8, SC = D / 8, VC = D * VB / 8;
+  constexpr int KLANE = KC / 4;
+  constexpr int VW32 = (VB == 3) ? 2 : 1;
+  constexpr int NK = 32;
+  constexpr int SLAB = 4 * NK;
+  constexpr int OFF_K = 0, OFF_S = NK * KC, OFF_V = OFF_S + NK * SC, OFF_N = OFF_V + NK * VC;
+  constexpr int NRM = NK * 4;
+  constexpr int SLOT = OFF_N + 3 * NRM;
+  constexpr int STG = 4 * SLOT;  // slot r of the four waves; slot R - 1 first stages the set-up
+  constexpr int MERGE = 4 * 4 * (D + 2) * 4;
+  constexpr int STAGE = R * STG > MERGE ? R * STG : MERGE;
+  static_assert(STG >= PQ::STAGE_BYTES, "set-up staging fits in one ring slot per wave");
+  static_assert(R >= 2 && R <= 3, "ring of 2 or 3 slots");
+  constexpr float LOG2E = 1.4426950408889634f;
+  constexpr float TAU = 8.0f;
+  constexpr float PUP = 6.0f;  // the same weight scaling as decode_attn_lds_kernel
+
+  __shared__ __attribute__((aligned(16))) uint8_t luts[L::BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t stage[STAGE];
+  __shared__ __attribute__((aligned(16))) _Float16 ptile[4][4][NK];  // per wave: P [column][key]
+  const uint8_t* tV = luts + L::VAL_OFF;
+  uint8_t* const stg = stage + (R - 1) * STG;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int split = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
+  const int64_t bh = static_cast<int64_t>(b) * a.Hkv + hkv;
+
+  build_small_luts<BITS, true>(a, luts, tid);
+
+  // this lane's score column lg
+  const bool c_ok = lg < a.C;
+  const int qi = c_ok ? lg / a.G : 0, h = hkv * a.G + (c_ok ? lg % a.G : 0);
+  const float fa = a.scale * LOG2E;
+  const float fb = a.coeff * fa;
+  const int lim = a.causal ? qi + (a.Sk - a.Sq) : 0x7fffffff;
+  const int causal_from = a.causal ? a.Sk - a.Sq : 0x7fffffff;
+  const int kbeg = split * a.chunk;
+  const int kend = min(a.Sk, kbeg + a.chunk);
+
+  // value field of the lane (value-MFMA row l16): dims l16*8 .. l16*8+7
+  const int voff = l16 * VB;
+  const int vbase = voff & ~3;
+  const int vbyte = voff & 3;
+
+  const int64_t g0 = bh * a.ldk;
+  const uint8_t* pk = a.kcodes + g0 * KC;
+  const uint8_t* ps = a.ksigns + g0 * SC;
+  const uint16_t* pkn = a.kvn + g0;
+  const uint16_t* prn = a.krn + g0;
+  const uint16_t* pvn = a.vvn + g0;
+  const uint8_t* pv = a.vcodes + g0 * VC;
+  const uint32_t ring_lds = lds_offset(stage) + wave * SLOT;
+  constexpr int NKD = (NK * KC + 1023) / 1024, NSD = (NK * SC + 1023) / 1024, NVD = (NK * VC + 1023) / 1024;
+  constexpr int NDMA = NKD + NSD + NVD + 3;
+  auto copy_plane = [&](const i32x4& r, uint32_t dst, int bytes, int nrounds) {
+    const uint32_t lo = lane * 16;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (c >= nrounds) break;
+      if ((c + 1) * 1024 <= bytes || lane < 32) dma16(r, dst + c * 1024, lo + c * 1024);
+    }
+  };
+  auto issue = [&](int kb, int slot) {
+    const uint32_t dst = ring_lds + slot * STG;
+    wait_lds();
+    copy_plane(rows_desc(pk, KC, kb, kend), dst + OFF_K, NK * KC, NKD);
+    copy_plane(rows_desc(ps, SC, kb, kend), dst + OFF_S, NK * SC, NSD);
+    copy_plane(rows_desc(pv, VC, kb, kend), dst + OFF_V, NK * VC, NVD);
+    if (lane < 32) {
+      dma_u16(rows_desc(pkn, 2, kb, kend), dst + OFF_N, lane * 2);
+      dma_u16(rows_desc(prn, 2, kb, kend), dst + OFF_N + NRM, lane * 2);
+      dma_u16(rows_desc(pvn, 2, kb, kend), dst + OFF_N + 2 * NRM, lane * 2);
+    }
+  };
+  auto wait_slot = [&](int later) {
+    if (later >= 2) wait_vm<(R >= 3 ? 2 * NDMA : 0)>();
+    else if (later == 1) wait_vm<NDMA>();
+    else wait_vm<0>();
+  };
+  const int k0w = kbeg + wave * NK;
+#pragma unroll
+  for (int r = 0; r < R - 1; ++r)
+    if (k0w + r * SLAB < kend) issue(k0w + r * SLAB, r);
+
+  PQ pq;
+  pq.setup(a, b, hkv, stg, tid);
+  __syncthreads();  // fragments held (and tables built): the staging slot joins the ring
+  if (k0w + (R - 1) * SLAB < kend) issue(k0w + (R - 1) * SLAB, R - 1);
+
+  float m_run = -INFINITY, l_run = 0.f;  // column lg, this lane's keys
+  float vcap = 0x1p-24f, inv_vcap = 0x1p24f;
+  float4v oacc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) oacc[db] = float4v{0.f, 0.f, 0.f, 0.f};
+  _Float16* const pt = &ptile[wave][0][0];
+
+  auto slab = [&](const uint8_t* src, int ks0) {
+    // ---- scores of keys ks0 + 16j + l16 (j = 0, 1) for column lg, log2 domain
+    float sc[2], nv[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int row = 16 * j + l16;
+      float t1, t2;
+      pq.dots(src + OFF_K + row * KC + lg * KLANE, src + OFF_S + row * SC + lg * 4, t1, t2);
+      const float kn = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + row * 4)));
+      const float rn = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + NRM + row * 4)));
+      nv[j] = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + 2 * NRM + row * 4)));
+      sc[j] = fmaf(t1, fa * kn, t2 * (fb * rn));
+    }
+    // ---- value norms enter P as vn / vcap <= 1; vcap is a power of two that only grows
+    {
+      const float vmx = fmaxf(nv[0], nv[1]);
+      if (__any(vmx > vcap)) {
+        float t = vmx;
+#pragma unroll
+        for (int sh = 32; sh >= 1; sh >>= 1) t = fmaxf(t, __shfl_xor(t, sh, 64));
+        int ex;
+        frexpf(t, &ex);
+        ex = __builtin_amdgcn_readfirstlane(ex);
+        const float cap = ldexpf(1.f, ex);
+        const float shrink = vcap / cap;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) oacc[db] *= shrink;
+        vcap = cap;
+        inv_vcap = ldexpf(1.f, -ex);
+      }
+    }
+    if (ks0 + NK > kend || ks0 + NK - 1 > causal_from || a.mask) {  // wave-uniform edge test
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int key = ks0 + 16 * j + l16;
+        if (a.mask && c_ok && key < kend)
+          sc[j] += fmaxf(a.mask[b * a.smb + h * a.smh + static_cast<int64_t>(qi) * a.smq +
+                                static_cast<int64_t>(key) * a.smk] * LOG2E,
+                         -3.0e38f);
+        if (key >= kend || key > lim) sc[j] = -INFINITY;
+      }
+    }
+    // ---- lazy online softmax: column lg's reference m_run (uniform over the 16 lanes of the
+    // column) moves only when a score exceeds it by more than TAU; p = 2^(s - m_run + PUP)
+    const float lmax = fmaxf(sc[0], sc[1]);
+    if (__any(lmax > m_run + TAU)) {
+      float t = lmax;
+#pragma unroll
+      for (int sh = 8; sh >= 1; sh >>= 1) t = fmaxf(t, __shfl_xor(t, sh, 64));
+      float alpha = 1.f;
+      if (t > m_run + TAU) {
+        alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - t);
+        m_run = t;
+        l_run *= alpha;
+      }
+      const float ac = __shfl(alpha, 16 * (l16 & 3), 64);  // O^T column l16 serves column l16 & 3
+#pragma unroll
+      for (int db = 0; db < DB; ++db) oacc[db] *= ac;
+    }
+    const float m_use = (m_run == -INFINITY) ? 0.f : m_run - PUP;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float p = __builtin_amdgcn_exp2f(sc[j] - m_use);
+      l_run += p;
+      pt[lg * NK + 16 * j + l16] = static_cast<_Float16>(p * (nv[j] * inv_vcap));
+    }
+    // ---- values: O^T += V^T (P * vn)^T over the slab's 32 keys in one 16x16x32 MFMA per row
+    // block: K-slot 8lg + 4j + e is key 16j + 4lg + e; the B operand (column l16) reads
+    // column l16 & 3 of the P tile
+    half8 pb;
+    {
+      const _Float16* pr = pt + (l16 & 3) * NK + 4 * lg;
+      const u32x2 p0 = *reinterpret_cast<const u32x2*>(pr);
+      const u32x2 p1 = *reinterpret_cast<const u32x2*>(pr + 16);
+      pb = __builtin_bit_cast(half8, u32x4{p0[0], p0[1], p1[0], p1[1]});
+    }
+    constexpr uint32_t M = odd_fields<VB>();
+    uint32_t w[2][4];  // value fields of keys 16j + 4lg + kk
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const uint32_t* vp = reinterpret_cast<const uint32_t*>(src + OFF_V + (16 * j + 4 * lg + kk) * VC + vbase);
+        if constexpr (VW32 == 2)
+          w[j][kk] = __builtin_amdgcn_alignbyte(vp[1], vp[0], vbyte);
+        else
+          w[j][kk] = vp[0] >> (8 * vbyte);
+      }
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+      uint32_t f[2][2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const uint32_t wa = w[j][2 * c], wb = w[j][2 * c + 1];
+          f[j][c] = par ? ((wb & M) | ((wa >> VB) & ~M)) : (((wb << VB) & M) | (wa & ~M));
+        }
+      static_for<4>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        const int db = 2 * i + par;
+        const half8 va = __builtin_bit_cast(half8, u32x4{value_pair<VB, i>(tV, f[0][0]), value_pair<VB, i>(tV, f[0][1]),
+                                                         value_pair<VB, i>(tV, f[1][0]), value_pair<VB, i>(tV, f[1][1])});
+        oacc[db] = mfma16x16x32(va, pb, oacc[db]);
+      });
+    }
+  };
+
+  for (int k0 = k0w; k0 < kend; k0 += R * SLAB) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int ks0 = k0 + r * SLAB;
+      if (ks0 < kend) {
+        int later = 0;
+#pragma unroll
+        for (int q = 1; q < R; ++q) later += (ks0 + q * SLAB < kend) ? 1 : 0;
+        wait_slot(later);
+        slab(stage + r * STG + wave * SLOT, ks0);
+        if (ks0 + R * SLAB < kend) issue(ks0 + R * SLAB, r);
+      }
+    }
+  }
+
+  // ---- merge the 4 waves of the block in LDS (reusing the staging area)
+  __syncthreads();
+  float* mrg = reinterpret_cast<float*>(stage);  // [wave][column < 4][D + 2]
+  float l = l_run;
+#pragma unroll
+  for (int sh = 8; sh >= 1; sh >>= 1) l += __shfl_xor(l, sh, 64);
+  if (l16 < 4) {
+    float* my = mrg + (wave * 4 + l16) * (D + 2);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) my[(lg * 4 + e) * (D / 16) + db] = oacc[db][e] * vcap;
+  }
+  if (l16 == 0) {
+    float* my = mrg + (wave * 4 + lg) * (D + 2);
+    my[D] = (m_run == -INFINITY) ? m_run : m_run - PUP;
+    my[D + 1] = l;
+  }
+  __syncthreads();
+  const int64_t pbase = (bh * a.nsplit + split) * a.C;
+  for (int it = tid; it < a.C * D; it += 256) {
+    const int c = it / D, d = it % D;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, mrg[(w * 4 + c) * (D + 2) + D]);
+    float o = 0.f, ls = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float* srcm = mrg + (w * 4 + c) * (D + 2);
+      const float scw = (srcm[D] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(srcm[D] - mx);
+      o += scw * srcm[d];
+      ls += scw * srcm[D + 1];
+    }
+    a.part_o[(pbase + c) * D + d] = o;
+    if (d == 0) {
+      a.part_ml[(pbase + c) * 2] = mx;
+      a.part_ml[(pbase + c) * 2 + 1] = ls;
+    }
+  }
+}
+
 struct MergeArgs {
   const float *part_o, *part_ml;
   const uint16_t* vpit;  // split Pi_v^T
@@ -507,9 +782,18 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeArgs a) {
   }
 }
 
+// bit-plane kernel for 1- and 2-bit key codes and at most 4 columns
+static bool attn_planes(int bits, int C) { return bits <= 3 && C <= 4; }
+constexpr int kAttnPlaneRing = 2;
+
 // grid target of the fused decode attention: one round of resident blocks
-static int attn_target_blocks(int bits) {
-  static int cache[3][16] = {};
+static int attn_target_blocks(int bits, int C) {
+  static int cache[5][16] = {};
+  if (attn_planes(bits, C)) {
+    const void* k = bits == 2 ? reinterpret_cast<const void*>(&decode_attn_i8_kernel<1, kAttnPlaneRing>)
+                              : reinterpret_cast<const void*>(&decode_attn_i8_kernel<2, kAttnPlaneRing>);
+    return resident_blocks(k, 256, cache[bits + 1]);
+  }
   const void* k = bits == 2 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 2, kAttnNbs, kAttnRing, true>)
                 : bits == 3 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 3, kAttnNbs, kAttnRing, true>)
                             : reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 4, kAttnNbs, kAttnRing, true>);
@@ -518,9 +802,9 @@ static int attn_target_blocks(int bits) {
 
 static DecodePlan plan_decode(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
   if (!decode_shape(Hq, Hkv, Sq, Sk, d, bits)) return DecodePlan{false, 0, 0, 0};
-  constexpr int slab = 64 * kAttnNbs;
-  DecodePlan p = plan_split(B, Hkv, Sk, attn_target_blocks(bits), slab, 2 * slab);
+  constexpr int slab = 64 * kAttnNbs;  // 4 waves x 32 keys for both kernels
   const int C = (Hq / Hkv) * Sq;
+  DecodePlan p = plan_split(B, Hkv, Sk, attn_target_blocks(bits, C), slab, 2 * slab);
   p.ws_bytes = static_cast<int64_t>(B) * Hkv * p.nsplit * C * static_cast<int64_t>(d + 2) * 4;
   return p;
 }
@@ -543,6 +827,12 @@ bool decode_applies(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
 template <int BITS>
 static void launch_decode_attn(const DecodeArgs& a, hipStream_t s) {
   dim3 grid(a.nsplit, a.Hkv, a.B);
+  if constexpr (BITS <= 3) {
+    if (attn_planes(BITS, a.C)) {
+      decode_attn_i8_kernel<BITS - 1, kAttnPlaneRing><<<grid, 256, 0, s>>>(a);
+      return;
+    }
+  }
   if (a.C <= 8) decode_attn_lds_kernel<128, BITS, kAttnNbs, kAttnRing, true><<<grid, 256, 0, s>>>(a);
   else decode_attn_lds_kernel<128, BITS, kAttnNbs, kAttnRing, false><<<grid, 256, 0, s>>>(a);
 }

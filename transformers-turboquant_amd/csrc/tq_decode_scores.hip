@@ -292,58 +292,17 @@ __global__ void __launch_bounds__(256) decode_scores_c1_kernel(DecodeArgs a) {
   }
 }
 
-// Bit-plane scores on the integer MFMA (1- and 2-bit key codes, at most 8 columns).
-// Both terms are sums of query values over the set bits of key bit-planes:
-//   term 1: f16(C)[code] = c0 + (c1 - c0) b0 [+ (c2 - c0) b1 + (c3 - c2 - c1 + c0) b0 b1]
-//           (b0, b1: low / high code bit), so q_rot . f16(C)[codes] =
-//           c0 sum(q_rot) + sum over planes of (coefficient q_rot) . plane
-//   term 2: q_proj . (2 s - 1) = (2 q_proj) . s - sum(q_proj)
-// (attention.py:419-461).  A plane operand needs no lookup: byte j of
-// w & (0x01010101 << i) is bit 8j + i of the packed word w, weighted 2^i (i = 7: -128
-// as int8), and feeds v_mfma_i32_16x16x64_i8 as is.  The query side carries, for the
-// K slot of bit i, W 2^(7 - i) (i = 7: -W), W = rint(v 2^F) with F per (query, term)
-// such that |W| <= 2^23; the int32 A values are split into four signed base-256
-// digits, and the 16 MFMA rows of a row group are 4 queries x 4 digits, so lane (key n,
-// group g) ends with the 4 digit sums of query g and of its own key:
-//   dot = 2^(-7 - F) (acc0 + 2^8 acc1 + 2^16 acc2 + 2^24 acc3)
-// exact up to the rounding of v to 24 significant bits of the largest |v|, i.e. f32
-// grade for q_proj as well.  The interaction plane b0 b1 is only used when the
-// codebook is not affine in its bits (every Lloyd-Max codebook is odd, hence affine).
-typedef int i32x4v __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ i32x4v mfma_i8(i32x4v a, i32x4v b, i32x4v c) {
-  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
-}
-// plane dwords i0 .. i0 + 3 of word w: byte j of element e is bit 8j + i0 + e
-template <int I0>
-__device__ __forceinline__ i32x4v planes4(uint32_t w) {
-  constexpr uint32_t m = 0x01010101u;
-  return i32x4v{static_cast<int>(w & (m << I0)), static_cast<int>(w & (m << (I0 + 1))),
-                static_cast<int>(w & (m << (I0 + 2))), static_cast<int>(w & (m << (I0 + 3)))};
-}
-// even bit positions 0, 2, 4, 6 of each byte
-__device__ __forceinline__ i32x4v planes_even(uint32_t w) {
-  constexpr uint32_t m = 0x01010101u;
-  return i32x4v{static_cast<int>(w & m), static_cast<int>(w & (m << 2)), static_cast<int>(w & (m << 4)),
-                static_cast<int>(w & (m << 6))};
-}
-// digit sums -> f32: (acc3 2^8 + acc2) 2^16 + (acc1 2^8 + acc0), both halves exact in int32
-__device__ __forceinline__ float digits_f32(i32x4v acc) {
-  const int hi = (acc[3] << 8) + acc[2], lo = (acc[1] << 8) + acc[0];
-  return fmaf(static_cast<float>(hi), 65536.f, static_cast<float>(lo));
-}
-
+// Materialised scores on the integer MFMA (bit-plane form, PlaneQuery in tq_decode.h): one
+// column per lane group, keys on the N side; unit u of a 32-key slab scores keys 2n + u
+// (n = l16), so each lane ends with two adjacent keys of its column and a score row's 32
+// values leave as one 128-byte run.
 template <int KB, int R>
 __global__ void __launch_bounds__(256) decode_scores_i8_kernel(DecodeArgs a) {
-  static_assert(KB == 1 || KB == 2, "1- or 2-bit key codes");
   static_assert(R >= 2 && R <= 4, "ring of 2 to 4 slots");
+  using PQ = PlaneQuery<KB>;
   constexpr int D = 128, NK = 32;
   constexpr int KC = D * KB / 8, SC = D / 8;
-  constexpr int KLANE = KC / 4;          // code bytes of a lane's 32-dim field
-  constexpr int NT1 = 2 * KB;            // code-plane MFMAs per 16 keys
-  constexpr int NFM = NT1 + 2;           // A fragments: code planes, then sign planes
-  constexpr int NDL = KB == 2 ? 2 : 0;   // interaction-plane fragments (non-affine codebooks)
-  constexpr int NF = NFM + NDL;
+  constexpr int KLANE = KC / 4;
   constexpr int SLAB = 4 * NK;
   constexpr int OFF_K = 0, OFF_S = NK * KC, OFF_N = OFF_S + NK * SC;
   constexpr int NRM = NK * 4;
@@ -351,11 +310,9 @@ __global__ void __launch_bounds__(256) decode_scores_i8_kernel(DecodeArgs a) {
   // ring slot r of wave w at (r * 4 + w) * SLOT; slot R - 1 of the four waves (issued after
   // the query set-up) first serves as the set-up's staging area
   constexpr int STG = 4 * SLOT;
-  static_assert(STG >= 4 * 2 * D * 4 && STG >= NFM * 1024 && STG >= NDL * 1024, "set-up staging fits in one ring slot per wave");
+  static_assert(STG >= PQ::STAGE_BYTES, "set-up staging fits in one ring slot per wave");
 
   __shared__ __attribute__((aligned(16))) uint8_t stage[R * STG];
-  __shared__ float st_k1[4], st_k2[4];
-  __shared__ int st_f1[4], st_f2[4];
   uint8_t* const stg = stage + (R - 1) * STG;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -364,12 +321,6 @@ __global__ void __launch_bounds__(256) decode_scores_i8_kernel(DecodeArgs a) {
   const int64_t bh = static_cast<int64_t>(b) * a.Hkv + hkv;
   const int kbeg = split * a.chunk;
   const int kend = min(a.Sk, kbeg + a.chunk);
-
-  // codebook in plane form: c(b0, b1) = c0 + alo b0 + ahi b1 + adl b0 b1
-  const float c0 = h2f(a.kcent[0]), alo = h2f(a.kcent[1]) - c0;
-  const float ahi = KB == 2 ? h2f(a.kcent[2]) - c0 : 0.f;
-  const float adl = KB == 2 ? (h2f(a.kcent[3]) - h2f(a.kcent[2])) - alo : 0.f;
-  const bool inter = adl != 0.f;  // block-uniform
 
   const int64_t g0 = bh * a.ldk;
   const uint8_t* pk = a.kcodes + g0 * KC;
@@ -409,124 +360,8 @@ __global__ void __launch_bounds__(256) decode_scores_i8_kernel(DecodeArgs a) {
   for (int r = 0; r < R - 1; ++r)
     if (k0w + r * SLAB < kend) issue(k0w + r * SLAB, r);
 
-  // ---- query set-up, phase 1: wave c stages column c (f32) and its scales
-  float* const qst = reinterpret_cast<float*>(stg);  // [4][2][D]: q_rot, q_proj
-  const float cmax = fmaxf(fabsf(alo), fmaxf(fabsf(ahi), fabsf(adl)));
-  {
-    const int c = wave;
-    float r0 = 0.f, r1 = 0.f, p0 = 0.f, p1 = 0.f;
-    if (c < a.C) {
-      const int qi = c / a.G, h = hkv * a.G + c % a.G;
-      const int64_t qrow = ((static_cast<int64_t>(b) * a.Hq + h) * a.Sq + qi) * D + 2 * lane;
-      const uint32_t rr = *reinterpret_cast<const uint32_t*>(a.q_rot + qrow);
-      r0 = h2f(static_cast<uint16_t>(rr));
-      r1 = h2f(static_cast<uint16_t>(rr >> 16));
-      const float2 pp = *reinterpret_cast<const float2*>(a.q_proj + qrow);
-      p0 = pp.x;
-      p1 = pp.y;
-    }
-    *reinterpret_cast<float2*>(qst + (c * 2) * D + 2 * lane) = float2{r0, r1};
-    *reinterpret_cast<float2*>(qst + (c * 2 + 1) * D + 2 * lane) = float2{p0, p1};
-    float mr = fmaxf(fabsf(r0), fabsf(r1)), mp = fmaxf(fabsf(p0), fabsf(p1));
-    float sr = r0 + r1, sp = p0 + p1;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      mr = fmaxf(mr, __shfl_xor(mr, o));
-      mp = fmaxf(mp, __shfl_xor(mp, o));
-      sr += __shfl_xor(sr, o);
-      sp += __shfl_xor(sp, o);
-    }
-    if (lane == 0) {
-      int e1 = 0, e2 = 0;
-      frexpf(mr * cmax, &e1);
-      frexpf(2.f * mp, &e2);
-      st_f1[c] = mr * cmax > 0.f ? 23 - e1 : 0;
-      st_f2[c] = mp > 0.f ? 23 - e2 : 0;
-      st_k1[c] = c0 * sr;
-      st_k2[c] = sp;
-    }
-  }
-  __syncthreads();
-
-  // ---- phase 2: each thread builds dword groups (fragment f, column cq, lane group lg',
-  // element e): 4 A values (bytes j = 0..3) -> one dword per digit row 4 cq + t
-  constexpr int NGRP = NF * 64;
-  constexpr int PER = (NGRP + 255) / 256;
-  uint32_t outw[PER][4];
-  int oaddr[PER], ofrag[PER];
-#pragma unroll
-  for (int r = 0; r < PER; ++r) {
-    const int gi = tid + 256 * r;
-    const int e = gi & 3, lgp = (gi >> 2) & 3, cq = (gi >> 4) & 3, f = gi >> 6;
-    ofrag[r] = f;
-    int i = 0, m0 = 0, mstep = 8, term = 1;  // slot bit i; dims m0 + j * mstep
-    float coef = 0.f;
-    if (f < NT1) {
-      const int w = f >> 1;
-      i = 4 * (f & 1) + e;
-      const int p0 = 32 * w + i;  // + 8j
-      m0 = 32 * lgp + (KB == 1 ? p0 : (p0 >> 1));
-      mstep = KB == 1 ? 8 : 4;
-      coef = (KB == 2 && (i & 1)) ? ahi : alo;
-    } else if (f < NFM) {
-      i = 4 * (f - NT1) + e;
-      m0 = 32 * lgp + i;
-      coef = 2.f;
-      term = 2;
-    } else if (f < NF) {
-      const int w = f - NFM;
-      i = 2 * e;
-      m0 = 32 * lgp + 16 * w + e;
-      mstep = 4;
-      coef = adl;
-    }
-    const int F = term == 1 ? st_f1[cq] : st_f2[cq];
-    const float* qv = qst + (cq * 2 + (term - 1)) * D;
-    uint32_t u[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int wv = f < NF ? __float2int_rn(ldexpf(coef * qv[m0 + j * mstep], F)) : 0;
-      const int av = i < 7 ? wv * (1 << (7 - i)) : -wv;
-      u[j] = (static_cast<uint32_t>(av) + 0x808080u) ^ 0x808080u;
-    }
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-      outw[r][t] = ((u[0] >> (8 * t)) & 0xFFu) | (((u[1] >> (8 * t)) & 0xFFu) << 8) |
-                   (((u[2] >> (8 * t)) & 0xFFu) << 16) | (((u[3] >> (8 * t)) & 0xFFu) << 24);
-    oaddr[r] = (((f < NFM ? f : f - NFM) * 64 + 4 * cq + 16 * lgp) * 4 + e) * 4;
-  }
-  // the staged queries are read; fragments overwrite them (row 4 cq + t = lane + t)
-  auto put = [&](bool second) {
-#pragma unroll
-    for (int r = 0; r < PER; ++r) {
-      if (ofrag[r] < NF && (ofrag[r] >= NFM) == second) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) *reinterpret_cast<uint32_t*>(stg + oaddr[r] + t * 16) = outw[r][t];
-      }
-    }
-  };
-  __syncthreads();
-  put(false);
-  __syncthreads();
-
-  // ---- phase 3: the lane's fragments and its column's constants
-  i32x4v A[NF];
-#pragma unroll
-  for (int f = 0; f < NFM; ++f) A[f] = *reinterpret_cast<const i32x4v*>(stg + (f * 64 + lane) * 16);
-  if constexpr (NDL > 0) {
-    if (inter) {
-      __syncthreads();
-      put(true);
-      __syncthreads();
-#pragma unroll
-      for (int f = NFM; f < NF; ++f) A[f] = *reinterpret_cast<const i32x4v*>(stg + ((f - NFM) * 64 + lane) * 16);
-    } else {
-#pragma unroll
-      for (int f = NFM; f < NF; ++f) A[f] = i32x4v{0, 0, 0, 0};
-    }
-  }
-  const int x1 = -7 - st_f1[lg], x2 = -7 - st_f2[lg];
-  const float k1 = st_k1[lg], k2 = st_k2[lg];
+  PQ pq;
+  pq.setup(a, b, hkv, stg, tid);
   const float* pout = a.scores + (static_cast<int64_t>(b) * a.Hq + hkv * a.G) * a.Sq * a.Sk;
   const uint32_t out_bytes = static_cast<uint32_t>(a.C) * a.Sk * 4;
   const uint32_t oo = lg < a.C ? static_cast<uint32_t>((lg % a.G) * a.Sq + lg / a.G) * a.Sk * 4 + 8 * l16 : kOutOfRange;
@@ -534,43 +369,15 @@ __global__ void __launch_bounds__(256) decode_scores_i8_kernel(DecodeArgs a) {
   __syncthreads();  // every wave holds its fragments: the staging slot joins the ring
   if (k0w + (R - 1) * SLAB < kend) issue(k0w + (R - 1) * SLAB, R - 1);
 
-  // unit u of a slab scores keys 2n + u (n = l16), so each lane ends with two adjacent
-  // keys of its column and a row's 32 scores leave as one 128-byte run
   auto slab = [&](const uint8_t* src, int ks0) {
     float sc[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int row = 2 * l16 + u;
-      uint32_t kw[KB];
-      if constexpr (KB == 2) {
-        const u32x2 t = *reinterpret_cast<const u32x2*>(src + OFF_K + row * KC + lg * KLANE);
-        kw[0] = t[0];
-        kw[1] = t[1];
-      } else {
-        kw[0] = *reinterpret_cast<const uint32_t*>(src + OFF_K + row * KC + lg * KLANE);
-      }
-      const uint32_t sw = *reinterpret_cast<const uint32_t*>(src + OFF_S + row * SC + lg * 4);
-      i32x4v s1 = i32x4v{0, 0, 0, 0}, s2 = i32x4v{0, 0, 0, 0};
-      static_for<NT1>([&](auto ff) {
-        constexpr int f = decltype(ff)::value;
-        s1 = mfma_i8(A[f], planes4<4 * (f & 1)>(kw[f >> 1]), s1);
-      });
-      static_for<2>([&](auto ff) {
-        constexpr int f = decltype(ff)::value;
-        s2 = mfma_i8(A[NT1 + f], planes4<4 * f>(sw), s2);
-      });
-      if constexpr (NDL > 0) {
-        if (inter) {
-          static_for<NDL>([&](auto ff) {
-            constexpr int w = decltype(ff)::value;
-            s1 = mfma_i8(A[NFM + w], planes_even(kw[w] & (kw[w] >> 1)), s1);
-          });
-        }
-      }
+      float t1, t2;
+      pq.dots(src + OFF_K + row * KC + lg * KLANE, src + OFF_S + row * SC + lg * 4, t1, t2);
       const float kn = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + row * 4)));
       const float rn = fb * h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + NRM + row * 4)));
-      const float t1 = ldexpf(digits_f32(s1), x1) + k1;
-      const float t2 = ldexpf(digits_f32(s2), x2) - k2;
       sc[u] = t1 * kn + t2 * rn;
     }
     const int key = ks0 + 2 * l16;
