@@ -286,9 +286,9 @@ def decode_legs(kc, vc, outliers, steps: int, warmup: int) -> tuple[dict, dict]:
         "ms_per_launch": ms_scores,
         "key_heads_per_s": key_heads / (ms_scores * 1e-3),
         "roofline": {
-            "kernel": "tq::decode_scores_kernel<128, 3, 3, 32, true> (scores, f32 written)",
+            "kernel": "tq::decode_scores_i8_kernel<2, 3> (scores, f32 written)",
             "bound": "hbm", "achieved": gbs_s, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": gbs_s / HBM_PEAK_GBS, "traffic": measured_traffic("tq::decode_scores_kernel<128, 3, 3, 32, true>"),
+            "frac": gbs_s / HBM_PEAK_GBS, "traffic": measured_traffic("tq::decode_scores_i8_kernel<2, 3>"),
             "algorithmic_bytes_per_launch": score_bytes,
         },
     }
@@ -297,7 +297,7 @@ def decode_legs(kc, vc, outliers, steps: int, warmup: int) -> tuple[dict, dict]:
         "ms_per_launch": ms_attn,
         "key_heads_per_s": key_heads / (ms_attn * 1e-3),
         "roofline": {
-            "kernel": "tq::decode_attn_lds_kernel<128, 3, 2, 2, true> + tq::decode_merge_kernel<128>",
+            "kernel": "tq::decode_attn_i8_kernel<2, 2> + tq::decode_merge_kernel<128>",
             "bound": "hbm", "achieved": gbs_a, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": gbs_a / HBM_PEAK_GBS, "traffic": measured_traffic("decode_attention (attention + merge)"),
             "algorithmic_bytes_per_launch": attn_bytes,

@@ -648,94 +648,100 @@ struct MergeArgs {
 // log-sum-exp weights into o[c][:] (LDS), then out^T = Pi_v^T o^T on MFMA with
 // Pi_v^T as the split-f16 A operand (rows i = output dim) and o^T as split-f16 B
 // operand (columns c, scaled per column by a power of two), hi.hi + lo.hi + hi.lo.
+// The kernel is latency-bound (a few KB per block), so it is laid out as few dependent
+// round trips as possible: each wave first issues the loads of its Pi_v^T fragments,
+// then combines whole columns (c = wave, wave + 4, ...) on its own: split maxima and
+// weights by wave reductions, and 2 dims per lane summed over all splits with the loads
+// of a batch issued together; one block barrier precedes the Pi_v product.
 template <int D>
 __global__ void __launch_bounds__(256) decode_merge_kernel(MergeArgs a) {
   static_assert(D == 128, "merge is built for head_dim 128");
-  constexpr int SW = 64;  // splits per weight batch
+  constexpr int SW = 64;  // splits per weight batch (one per lane)
   __shared__ float o_s[16 * D];
-  __shared__ float s_w[16 * SW];
-  __shared__ float s_red[16 * 16];
-  __shared__ float s_mx[16], s_l[16], s_up[16];
+  __shared__ float s_w[4][SW];
+  __shared__ float s_up[16];
   const int hkv = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6, l16 = lane & 15, lg = lane >> 4;
   const int C = a.C, ns = a.nsplit;
   const int64_t base = (static_cast<int64_t>(b) * a.Hkv + hkv) * ns;  // first split record
-  auto ml = [&](int s, int c, int k) { return a.part_ml[((base + s) * C + c) * 2 + k]; };
 
-  // ---- column maxima: thread (c, r) scans splits r, r + 16, ...
-  {
-    const int c = tid & 15, r = tid >> 4;
+  // ---- Pi_v^T fragments of this wave's output rows 32w .. 32w+31 (in flight meanwhile)
+  const _Float16* Ph = reinterpret_cast<const _Float16*>(a.vpit);
+  const _Float16* Pl = Ph + D * D;
+  half8 ah[2][D / 32], al[2][D / 32];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const int i = wave * 32 + rb * 16 + l16;
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) {
+      ah[rb][ks] = *reinterpret_cast<const half8*>(Ph + i * D + ks * 32 + lg * 8);
+      al[rb][ks] = *reinterpret_cast<const half8*>(Pl + i * D + ks * 32 + lg * 8);
+    }
+  }
+
+  // ---- columns c = wave, wave + 4, ...: o[c] = sum_s w_s o_s / sum_s w_s l_s
+  for (int c = wave; c < 16; c += 4) {
+    float* oc = o_s + c * D;
+    if (c >= C) {
+      oc[2 * lane] = 0.f;
+      oc[2 * lane + 1] = 0.f;
+      if (lane == 0) s_up[c] = 1.f;
+      continue;
+    }
+    auto ml = [&](int s, int k) { return a.part_ml[((base + s) * C + c) * 2 + k]; };
     float mx = -INFINITY;
-    if (c < C)
-      for (int s = r; s < ns; s += 16) mx = fmaxf(mx, ml(s, c, 0));
-    s_red[r * 16 + c] = mx;
-    __syncthreads();
-    if (tid < 16) {
-      float m = -INFINITY;
-      for (int i = 0; i < 16; ++i) m = fmaxf(m, s_red[i * 16 + tid]);
-      s_mx[tid] = m;
-      s_l[tid] = 0.f;
-    }
-    __syncthreads();
-  }
-
-  // ---- weighted sum of the splits; thread owns outputs it, it + 256, ... of the 16 x D tile
-  constexpr int PER = 16 * D / 256;
-  float acc[PER];
+    for (int s = lane; s < ns; s += SW) mx = fmaxf(mx, ml(s, 0));
 #pragma unroll
-  for (int k = 0; k < PER; ++k) acc[k] = 0.f;
-  for (int s0 = 0; s0 < ns; s0 += SW) {
-    const int nb = min(SW, ns - s0);
-    for (int i = tid; i < C * SW; i += 256) {
-      const int c = i / SW, s = i % SW;
+    for (int sh = 32; sh >= 1; sh >>= 1) mx = fmaxf(mx, __shfl_xor(mx, sh, 64));
+    float lsum = 0.f, o0 = 0.f, o1 = 0.f;
+    for (int s0 = 0; s0 < ns; s0 += SW) {
+      const int s = s0 + lane;
       float w = 0.f;
-      if (s < nb) {
-        const float m = ml(s0 + s, c, 0);
-        w = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - s_mx[c]);
+      if (s < ns) {
+        const float m = ml(s, 0);
+        w = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - mx);
+        lsum += w * ml(s, 1);
       }
-      s_w[c * SW + s] = w;
-    }
-    __syncthreads();
-    if (tid < C) {
-      float l = s_l[tid];
-      for (int s = 0; s < nb; ++s) l += s_w[tid * SW + s] * ml(s0 + s, tid, 1);
-      s_l[tid] = l;
+      s_w[wave][lane] = w;  // read back by the same wave only: LDS order suffices
+      const int nb = min(SW, ns - s0);
+      const float* src = a.part_o + ((base + s0) * C + c) * D + 2 * lane;
+      const int64_t step = static_cast<int64_t>(C) * D;
+      int k = 0;
+      for (; k + 8 <= nb; k += 8) {
+        float2 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const float2*>(src + (k + u) * step);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const float ww = s_w[wave][k + u];
+          o0 = fmaf(ww, v[u].x, o0);
+          o1 = fmaf(ww, v[u].y, o1);
+        }
+      }
+      for (; k < nb; ++k) {
+        const float2 v = *reinterpret_cast<const float2*>(src + k * step);
+        const float ww = s_w[wave][k];
+        o0 = fmaf(ww, v.x, o0);
+        o1 = fmaf(ww, v.y, o1);
+      }
     }
 #pragma unroll
-    for (int k = 0; k < PER; ++k) {
-      const int it = tid + 256 * k, c = it / D, j = it % D;
-      if (c < C) {
-        const float* src = a.part_o + ((base + s0) * C + c) * D + j;
-        float o = acc[k];
-        for (int s = 0; s < nb; ++s) o += s_w[c * SW + s] * src[static_cast<int64_t>(s) * C * D];
-        acc[k] = o;
-      }
-    }
-    __syncthreads();
-  }
-  // normalised o in LDS (columns >= C are zero) and per-column max |o|
+    for (int sh = 32; sh >= 1; sh >>= 1) lsum += __shfl_xor(lsum, sh, 64);
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    o0 *= inv;
+    o1 *= inv;
+    oc[2 * lane] = o0;
+    oc[2 * lane + 1] = o1;
+    float m = fmaxf(fabsf(o0), fabsf(o1));
 #pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const int it = tid + 256 * k, c = it / D, j = it % D;
-    o_s[c * D + j] = (c < C && s_l[c] > 0.f) ? acc[k] / s_l[c] : 0.f;
-  }
-  __syncthreads();
-  {
-    // 16 lanes per column: lane r of column c scans dims r, r + 16, ...
-    const int c = tid >> 4, r = tid & 15;
-    float mx = 0.f;
-    for (int j = r; j < D; j += 16) mx = fmaxf(mx, fabsf(o_s[c * D + j]));
-    s_red[c * 16 + r] = mx;
-    __syncthreads();
-    if (tid < 16) {
-      float m = 0.f;
-      for (int i = 0; i < 16; ++i) m = fmaxf(m, s_red[tid * 16 + i]);
+    for (int sh = 32; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh, 64));
+    if (lane == 0) {
       int ex;
       frexpf(m, &ex);
-      s_up[tid] = ldexpf(kSplit, -ex);  // scaled |o| < kSplit
+      s_up[c] = ldexpf(kSplit, -ex);  // scaled |o| < kSplit
     }
-    __syncthreads();
   }
+  __syncthreads();
 
   // ---- out^T[i][c] = sum_j Pi_v^T[i][j] o[c][j]; wave w owns output rows 32w .. 32w+31
   const float up = s_up[l16];
@@ -751,22 +757,17 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeArgs a) {
       bl[ks][e] = lo;
     }
   }
-  const _Float16* Ph = reinterpret_cast<const _Float16*>(a.vpit);
-  const _Float16* Pl = Ph + D * D;
   const bool col_ok = l16 < C;
   const int qi = col_ok ? l16 / a.G : 0, h = hkv * a.G + (col_ok ? l16 % a.G : 0);
   const float down = kUnsplit2 / up;  // 1/(kSplit * up) * (1/kSplit) for Pi_v^T's scale
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
-    const int i = wave * 32 + rb * 16 + l16;  // A-operand row (output dim)
     float4v f = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < D / 32; ++ks) {
-      const half8 ah = *reinterpret_cast<const half8*>(Ph + i * D + ks * 32 + lg * 8);
-      const half8 al = *reinterpret_cast<const half8*>(Pl + i * D + ks * 32 + lg * 8);
-      f = mfma16x16x32(ah, bh[ks], f);
-      f = mfma16x16x32(al, bh[ks], f);
-      f = mfma16x16x32(ah, bl[ks], f);
+      f = mfma16x16x32(ah[rb][ks], bh[ks], f);
+      f = mfma16x16x32(al[rb][ks], bh[ks], f);
+      f = mfma16x16x32(ah[rb][ks], bl[ks], f);
     }
     if (col_ok) {
       const int64_t off = static_cast<int64_t>(b) * a.sob + static_cast<int64_t>(h) * a.soh +
