@@ -188,110 +188,6 @@ __global__ void __launch_bounds__(256) decode_scores_kernel(DecodeArgs a) {
   }
 }
 
-// Single-column scores (one query row per kv head: G * Sq == 1, the MHA decode step) with 1-
-// bit key codes (the template also takes 2-bit codes, KB = 2, which measured slower than the
-// MFMA kernel, so the dispatch instantiates KB = 1 only).  The MFMA kernel above would fill
-// one of its 16 columns; here each lane
-// owns one key and sums per-query tables held in LDS:
-//   term 1 over groups of dims whose packed code bits form a nibble (4 dims of 1-bit codes,
-//          2 dims of 2-bit codes): T1[g][v] = sum_j q_rot[d_j] f16(C)[code_j(v)]
-//   term 2 over groups of 4 sign bits: T2[g][v] = sum_j q_proj[4g + j] (bit_j(v) ? 1 : -1)
-// (attention.py:419-461: term 1 is q_rot . f16(C)[codes], term 2 is q_proj . (2 signs - 1),
-// both in f32; the products here are exact in f32 and only the summation order differs.)
-// A table has 16 f32 entries in 16 banks, so a lookup by 64 lanes touches at most 16 dwords
-// of distinct banks: conflict-free.  Keys arrive straight from HBM, one 16-byte row piece per
-// lane (64 consecutive keys per wave: coalesced), one iteration ahead.
-template <int KB>
-__global__ void __launch_bounds__(256) decode_scores_c1_kernel(DecodeArgs a) {
-  constexpr int D = 128;
-  constexpr int G1 = KB == 1 ? D / 4 : D / 2;  // term-1 tables
-  constexpr int G2 = D / 4;                     // term-2 tables
-  constexpr int KC = D * KB / 8, SC = D / 8;    // code / sign bytes per key
-  constexpr int NW = KC / 4;                    // code dwords per key
-  __shared__ __attribute__((aligned(16))) float tab[(G1 + G2) * 16];
-  float* const t1 = tab;
-  float* const t2 = tab + G1 * 16;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int split = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
-  const int64_t qrow = (static_cast<int64_t>(b) * a.Hq + hkv) * D;  // G = Sq = 1: head hkv, row 0
-  for (int e = tid; e < (G1 + G2) * 16; e += 256) {
-    const int g = (e >> 4) - (e < G1 * 16 ? 0 : G1), v = e & 15;
-    float acc = 0.f;
-    if (e < G1 * 16) {
-      if constexpr (KB == 1) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc += h2f(a.q_rot[qrow + 4 * g + j]) * h2f(a.kcent[(v >> j) & 1]);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc += h2f(a.q_rot[qrow + 2 * g + j]) * h2f(a.kcent[(v >> (2 * j)) & 3]);
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float q = a.q_proj[qrow + 4 * g + j];
-        acc += ((v >> j) & 1) ? q : -q;
-      }
-    }
-    tab[e] = acc;
-  }
-
-  const int kbeg = split * a.chunk;
-  const int kend = min(a.Sk, kbeg + a.chunk);
-  const int64_t g0 = (static_cast<int64_t>(b) * a.Hkv + hkv) * a.ldk;
-  // resources over rows [kbeg, kend): loads past the split's last key return zero
-  const rsrc_t rk = rows_rsrc(a.kcodes + g0 * KC, KC, kbeg, kend);
-  const rsrc_t rs = rows_rsrc(a.ksigns + g0 * SC, SC, kbeg, kend);
-  const rsrc_t rv = rows_rsrc(a.kvn + g0, 2, kbeg, kend);
-  const rsrc_t rr = rows_rsrc(a.krn + g0, 2, kbeg, kend);
-  float* const out = a.scores + (static_cast<int64_t>(b) * a.Hq + hkv) * a.Sk;
-  const float fb = a.coeff;
-
-  struct Key {
-    u32x4 c[NW / 4];
-    u32x4 s;
-    uint32_t vn, rn;
-  };
-  auto fetch = [&](int k0, Key& x) {  // key k0 + lane
-    const uint32_t r = static_cast<uint32_t>(k0 + lane - kbeg);
-#pragma unroll
-    for (int i = 0; i < NW / 4; ++i)
-      x.c[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, r * KC + 16 * i, 0, kStream));
-    x.s = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, r * SC, 0, kStream));
-    x.vn = __builtin_amdgcn_raw_buffer_load_b16(rv, r * 2, 0, kStream);
-    x.rn = __builtin_amdgcn_raw_buffer_load_b16(rr, r * 2, 0, kStream);
-  };
-  // sum of the 8 nibble lookups of word w (bytes 4i .. 4i + 3 of a row) in table t
-  auto word = [&](const float* t, uint32_t w, int i, float& s0, float& s1) {
-    const uint8_t* tb = reinterpret_cast<const uint8_t*>(t);
-    const uint32_t lo = w << 2, hi = w >> 2;
-    static_for<4>([&](auto kk) {
-      constexpr int K = decltype(kk)::value;
-      const int g = 2 * (4 * i + K);  // low nibble: group g, high nibble: g + 1
-      s0 += __uint_as_float(lds32(tb + 64 * g, and_byte<K>(0x3Cu, lo)));
-      s1 += __uint_as_float(lds32(tb + 64 * (g + 1), and_byte<K>(0x3Cu, hi)));
-    });
-  };
-
-  __syncthreads();  // tables built
-  constexpr int STEP = 4 * 64;  // keys per block iteration
-  int k0 = kbeg + wave * 64;
-  Key cur, nxt;
-  if (k0 < kend) fetch(k0, cur);
-  for (; k0 < kend; k0 += STEP) {
-    if (k0 + STEP < kend) fetch(k0 + STEP, nxt);
-    float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
-#pragma unroll
-    for (int i = 0; i < NW; ++i) word(t1, cur.c[i >> 2][i & 3], i, a0, a1);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) word(t2, cur.s[i], i, b0, b1);
-    const int key = k0 + lane;
-    if (key < kend) out[key] = (a0 + a1) * h2f(static_cast<uint16_t>(cur.vn)) +
-                               (b0 + b1) * (fb * h2f(static_cast<uint16_t>(cur.rn)));
-    cur = nxt;
-  }
-}
-
 // Materialised scores on the integer MFMA (bit-plane form, PlaneQuery in tq_decode.h): one
 // column per lane group, keys on the N side; unit u of a 32-key slab scores keys 2n + u
 // (n = l16), so each lane ends with two adjacent keys of its column and a score row's 32
@@ -442,16 +338,6 @@ int decode_scores(int64_t ldk, const uint16_t* q_rot, const float* q_proj, const
   a.coeff = coeff;
   a.scale = 1.f;
   a.scores = out;
-  if (a.C == 1 && bits == 2) {
-    // one column, 1-bit key codes: per-query tables instead of 16-column MFMAs (MI355X, MHA
-    // 8 x 32 heads x 16384 keys: 37.5 vs 42.1 us; with 2-bit codes the tables lose, 59 vs 52)
-    const DecodePlan p1 = plan_split(B, Hkv, Sk, kScoreBlocks, 256, 1024);
-    a.nsplit = p1.nsplit;
-    a.chunk = p1.chunk;
-    dim3 grid1(a.nsplit, a.Hkv, a.B);
-    decode_scores_c1_kernel<1><<<grid1, 256, 0, s>>>(a);
-    return launch_status("tq_attention_scores (decode, one column)");
-  }
   dim3 grid(a.nsplit, a.Hkv, a.B);
   if (bits <= 3 && a.C <= 4) {
     if (bits == 2) decode_scores_i8_kernel<1, 3><<<grid, 256, 0, s>>>(a);
