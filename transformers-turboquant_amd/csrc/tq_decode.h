@@ -390,6 +390,10 @@ struct PlaneQuery {
   }
 };
 
+// materialised scores for bits 2-3 and at most 4 columns (tq_decode.hip), on a plan of
+// tq_decode_scores.hip
+void launch_scores_planes(const DecodeArgs& a, int bits, hipStream_t s);
+
 // ---------------------------------------------------------------- planning
 struct DecodePlan {
   bool use;

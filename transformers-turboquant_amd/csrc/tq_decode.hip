@@ -360,6 +360,130 @@ decode_attn_lds_kernel(DecodeArgs a) {
   }
 }
 
+// Materialised scores on the integer MFMA (bit-plane form, PlaneQuery in tq_decode.h), with
+// the MFMA accumulators in VGPRs like every kernel of this file: one
+// column per lane group, keys on the N side; unit u of a 32-key slab scores keys 2n + u
+// (n = l16), so each lane ends with two adjacent keys of its column and a score row's 32
+// values leave as one 128-byte run.
+template <int KB, int R>
+__global__ void __launch_bounds__(256) decode_scores_i8_kernel(DecodeArgs a) {
+  static_assert(R >= 2 && R <= 4, "ring of 2 to 4 slots");
+  using PQ = PlaneQuery<KB>;
+  constexpr int D = 128, NK = 32;
+  constexpr int KC = D * KB / 8, SC = D / 8;
+  constexpr int KLANE = KC / 4;
+  constexpr int SLAB = 4 * NK;
+  constexpr int OFF_K = 0, OFF_S = NK * KC, OFF_N = OFF_S + NK * SC;
+  constexpr int NRM = NK * 4;
+  constexpr int SLOT = OFF_N + 2 * NRM;
+  // ring slot r of wave w at (r * 4 + w) * SLOT; slot R - 1 of the four waves (issued after
+  // the query set-up) first serves as the set-up's staging area
+  constexpr int STG = 4 * SLOT;
+  static_assert(STG >= PQ::STAGE_BYTES, "set-up staging fits in one ring slot per wave");
+
+  __shared__ __attribute__((aligned(16))) uint8_t stage[R * STG];
+  uint8_t* const stg = stage + (R - 1) * STG;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int split = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
+  const int64_t bh = static_cast<int64_t>(b) * a.Hkv + hkv;
+  const int kbeg = split * a.chunk;
+  const int kend = min(a.Sk, kbeg + a.chunk);
+
+  const int64_t g0 = bh * a.ldk;
+  const uint8_t* pk = a.kcodes + g0 * KC;
+  const uint8_t* ps = a.ksigns + g0 * SC;
+  const uint16_t* pkn = a.kvn + g0;
+  const uint16_t* prn = a.krn + g0;
+  const uint32_t ring_lds = lds_offset(stage) + wave * SLOT;
+  constexpr int NKD = (NK * KC + 1023) / 1024, NSD = (NK * SC + 1023) / 1024;
+  constexpr int NDMA = NKD + NSD + 2;
+  auto copy_plane = [&](const i32x4& r, uint32_t dst, int bytes, int nrounds) {
+    const uint32_t lo = lane * 16;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (c >= nrounds) break;
+      if ((c + 1) * 1024 <= bytes || lane < 32) dma16(r, dst + c * 1024, lo + c * 1024);
+    }
+  };
+  auto issue = [&](int kb, int slot) {
+    const uint32_t dst = ring_lds + slot * STG;
+    wait_lds();
+    copy_plane(rows_desc(pk, KC, kb, kend), dst + OFF_K, NK * KC, NKD);
+    copy_plane(rows_desc(ps, SC, kb, kend), dst + OFF_S, NK * SC, NSD);
+    if (lane < 32) {
+      dma_u16(rows_desc(pkn, 2, kb, kend), dst + OFF_N, lane * 2);
+      dma_u16(rows_desc(prn, 2, kb, kend), dst + OFF_N + NRM, lane * 2);
+    }
+  };
+  auto wait_slot = [&](int later) {
+    if (later >= 3) wait_vm<(R >= 4 ? 3 * NDMA : 0)>();
+    else if (later == 2) wait_vm<(R >= 3 ? 2 * NDMA : 0)>();
+    else if (later == 1) wait_vm<NDMA>();
+    else wait_vm<0>();
+  };
+  // slots 0 .. R-2 stream while the queries are set up
+  const int k0w = kbeg + wave * NK;
+#pragma unroll
+  for (int r = 0; r < R - 1; ++r)
+    if (k0w + r * SLAB < kend) issue(k0w + r * SLAB, r);
+
+  PQ pq;
+  pq.setup(a, b, hkv, stg, tid);
+  const float* pout = a.scores + (static_cast<int64_t>(b) * a.Hq + hkv * a.G) * a.Sq * a.Sk;
+  const uint32_t out_bytes = static_cast<uint32_t>(a.C) * a.Sk * 4;
+  const uint32_t oo = lg < a.C ? static_cast<uint32_t>((lg % a.G) * a.Sq + lg / a.G) * a.Sk * 4 + 8 * l16 : kOutOfRange;
+  const float fb = a.coeff;
+  __syncthreads();  // every wave holds its fragments: the staging slot joins the ring
+  if (k0w + (R - 1) * SLAB < kend) issue(k0w + (R - 1) * SLAB, R - 1);
+
+  auto slab = [&](const uint8_t* src, int ks0) {
+    float sc[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int row = 2 * l16 + u;
+      float t1, t2;
+      pq.dots(src + OFF_K + row * KC + lg * KLANE, src + OFF_S + row * SC + lg * 4, t1, t2);
+      const float kn = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + row * 4)));
+      const float rn = fb * h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + NRM + row * 4)));
+      sc[u] = t1 * kn + t2 * rn;
+    }
+    const int key = ks0 + 2 * l16;
+    if (key < kend) {
+      const rsrc_t ro = make_rsrc(pout + ks0, out_bytes - static_cast<uint32_t>(ks0) * 4);
+      if (key + 1 < kend)
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{__builtin_bit_cast(uint32_t, sc[0]), __builtin_bit_cast(uint32_t, sc[1])},
+                                              ro, oo, 0, 2);
+      else
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sc[0]), ro, oo, 0, 2);
+    }
+  };
+
+  // every outstanding load of the compiler's own (the query reads) has landed at the
+  // barriers above, so its waits inside the loop never reach back past a DMA
+  for (int k0 = k0w; k0 < kend; k0 += R * SLAB) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int ks0 = k0 + r * SLAB;
+      if (ks0 < kend) {
+        int later = 0;
+#pragma unroll
+        for (int q = 1; q < R; ++q) later += (ks0 + q * SLAB < kend) ? 1 : 0;
+        wait_slot(later);
+        slab(stage + r * STG + wave * SLOT, ks0);
+        if (ks0 + R * SLAB < kend) issue(ks0 + R * SLAB, r);
+      }
+    }
+  }
+}
+
+void launch_scores_planes(const DecodeArgs& a, int bits, hipStream_t s) {
+  const dim3 grid(a.nsplit, a.Hkv, a.B);
+  if (bits == 2) decode_scores_i8_kernel<1, 3><<<grid, 256, 0, s>>>(a);
+  else decode_scores_i8_kernel<2, 3><<<grid, 256, 0, s>>>(a);
+}
+
 // Fused decode attention for 1- and 2-bit key codes and at most 4 columns, scores on the
 // integer MFMA in bit-plane form (PlaneQuery, tq_decode.h) with the keys on the N side:
 // lane (key n, group g) scores key n of each 16-key block for column g, so the softmax
