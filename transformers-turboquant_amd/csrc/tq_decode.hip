@@ -361,10 +361,9 @@ decode_attn_lds_kernel(DecodeArgs a) {
 }
 
 // Materialised scores on the integer MFMA (bit-plane form, PlaneQuery in tq_decode.h), with
-// the MFMA accumulators in VGPRs like every kernel of this file: one
-// column per lane group, keys on the N side; unit u of a 32-key slab scores keys 2n + u
-// (n = l16), so each lane ends with two adjacent keys of its column and a score row's 32
-// values leave as one 128-byte run.
+// the MFMA accumulators in VGPRs like every kernel of this file: one column per lane group,
+// keys on the N side; unit u of a 32-key slab scores keys 2n + u (n = l16), so each lane ends
+// with two adjacent keys of its column and a score row's 32 values leave as one 128-byte run.
 template <int KB, int R>
 __global__ void __launch_bounds__(256) decode_scores_i8_kernel(DecodeArgs a) {
   static_assert(R >= 2 && R <= 4, "ring of 2 to 4 slots");
