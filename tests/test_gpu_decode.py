@@ -92,6 +92,49 @@ def test_decode_scores_any_codebook(bits, cb, qmul):
     assert O.rel_err(got, ref) < REL, O.rel_err(got, ref)
 
 
+@pytest.mark.parametrize("bits", [2, 3])
+@pytest.mark.parametrize("cb", ["nonaffine", "shifted"])
+def test_decode_attention_any_codebook(bits, cb):
+    """Fused decode attention with key codebooks that are not odd (and, for 2-bit codes, not
+    affine in the code bits) against the oracle evaluated with the same f16 codebook."""
+    _case(bits=bits, cb=cb)
+    from turboquant_pytorch._ops import ops
+    from turboquant_pytorch.compressors import _tables
+
+    B, hq, hkv, sq, sk, d = 2, 8, 2, 1, 2000, 128
+    assert _on_decode_path(B, hq, hkv, sq, sk, bits)
+    torch.manual_seed(11 * bits + len(cb))
+    q = torch.randn(B, hq, sq, d, device=DEV, dtype=torch.bfloat16)
+    k = torch.randn(B, hkv, sk, d, device=DEV, dtype=torch.bfloat16)
+    v = torch.randn(B, hkv, sk, d, device=DEV, dtype=torch.bfloat16)
+    kc = TurboQuantCompressorV2(d, bits, seed=42, device=DEV)
+    vc = TurboQuantCompressorMSE(d, bits, seed=10042, device=DEV)
+    ck, cv = kc.compress(k), vc.compress(v)
+    cent = kc.centroids.cpu().double()
+    cent = cent + 0.3 * cent.abs().max() if cb == "shifted" else cent * torch.linspace(0.6, 1.7, len(cent), dtype=torch.float64)
+    cent16 = cent.to(torch.float16)
+    q_rot, q_proj = kc.prepare_queries(q)
+    tv = _tables(vc, q.device, with_qjl=False)
+    got = _np(ops().attention(q_rot, q_proj, ck["packed_key_indices"], ck["packed_qjl_signs"], ck["residual_norm"],
+                              ck["vec_norms"], cent16.to(DEV), bits, cv["packed_indices"], cv["vec_norms"], tv.cent32,
+                              vc.bits, tv.pit_split, hkv, sk, sk, O.COEFF(d), 1 / math.sqrt(d), False, None,
+                              torch.float32, 1))
+    codes, signs, rn, vn = _planes(ck, d, kc.mse_bits)
+    qr = _np(q_rot.float()).reshape(B, hq, sq, d)
+    qp = _np(q_proj).reshape(B, hq, sq, d)
+    codes_v = O.unpack_bits(_np(cv["packed_indices"]), vc.bits, d)
+    vals = O.value_decompress(codes_v, _np(cv["vec_norms"]).reshape(-1), vc.Pi.cpu().numpy(),
+                              vc.centroids.cpu().numpy()).reshape(B, hkv, sk, d)
+    ref = np.zeros((B, sq, hq, d))
+    g = hq // hkv
+    for b in range(B):
+        for h in range(hq):
+            r = slice((b * hkv + h // g) * sk, (b * hkv + h // g + 1) * sk)
+            sc = O.scores_packed(qr[b, h], qp[b, h], codes[r], signs[r], rn[r], vn[r], cent16.numpy(), O.COEFF(d))
+            ref[b, :, h] = O.attention(sc, vals[b, h // g], 1 / math.sqrt(d))
+    assert O.rel_err(got, ref) < REL, O.rel_err(got, ref)
+
+
 @pytest.mark.parametrize("bits", [2, 3, 4])
 @pytest.mark.parametrize("hq,hkv,sq,sk,causal,qmul,vmul", [
     (32, 8, 1, 5000, False, 1.0, 1.0),
