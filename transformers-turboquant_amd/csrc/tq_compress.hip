@@ -622,21 +622,23 @@ __device__ __forceinline__ uint32_t qbucket(float y) {
   return static_cast<uint32_t>(fminf(fmaxf(fmaf(y, 120.f, 128.f), 0.f), 255.f));
 }
 
-// searchsorted-left over the 2^BB - 1 sorted boundaries (quantize.py:334-337).  TAB: the
+// searchsorted-left over the 2^BB - 1 sorted boundaries (quantize.py:334-337), times CS (the
+// key path takes 4 x the code: the byte offset of its centroid in LDS).  TAB: the
 // quantiser table; BB == 1: one compare; BB == 2: a two-level search (y > b1 decides the
 // upper bit, then y against b2 or b0 the lower one: for sorted boundaries that is the count
 // [y > b0] + [y > b1] + [y > b2]); BB >= 3 without the table: binary search of the LDS copy.
-template <int BB, bool TAB>
+template <int BB, bool TAB, uint32_t CS = 1>
 __device__ __forceinline__ uint32_t code_of(float y, const float (&br)[7], const float* bnd, const uint2* qt) {
+  static_assert(CS == 1 || (BB <= 2 && !TAB), "scaled codes for 1-2 code bits");
   if constexpr (TAB) {
     const uint2 e = qt[qbucket(y)];
     return e.y + (y > __uint_as_float(e.x) ? 1u : 0u);
   } else if constexpr (BB == 1) {
-    return br[0] < y ? 1u : 0u;
+    return br[0] < y ? CS : 0u;
   } else if constexpr (BB == 2) {
     const bool hi = br[1] < y;
     const bool lo = (hi ? br[2] : br[0]) < y;
-    return (hi ? 2u : 0u) + (lo ? 1u : 0u);
+    return (hi ? 2u * CS : 0u) + (lo ? CS : 0u);
   } else {
     uint32_t idx = 0;
 #pragma unroll
@@ -825,6 +827,8 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
   // position; each(ks, j, acc value, code) sees every element
   auto quantize_ks = [&](auto tab, const float4v (&acc)[MB], float ysc, int64_t gr, int ks, auto&& each) {
     constexpr bool TAB = decltype(tab)::value;
+    // keys with 1-2 code bits: codes come as 4 c, their centroid's byte offset in LDS
+    constexpr uint32_t CSC = (MODE == TM_KEYS && BB <= 2 && !TAB) ? 4u : 1u;
     float4v y0, y1;
     uint32_t v = 0;
 #pragma unroll
@@ -833,10 +837,11 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
       const float y = av * ysc;
       if (j < 4) y0[j] = y;
       else y1[j - 4] = y;
-      const uint32_t c = code_of<BB, TAB>(y, br, s_bnd, s_qt);
+      const uint32_t c = code_of<BB, TAB, CSC>(y, br, s_bnd, s_qt);
       v |= c << (BB * j);
       each(ks, j, av, c);
     }
+    if constexpr (CSC == 4) v >>= 2;
     if (a.y_out && gr < a.n) {
       float4v* yo = reinterpret_cast<float4v*>(a.y_out + gr * D + 32 * ks + 8 * g);
       yo[0] = y0;
@@ -1030,7 +1035,10 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
         __builtin_amdgcn_s_setprio(1);
         float ss = 0.f;
         quantize_stage(tab, acc, xs / (vn + 1e-8f), gr, [&](int ks, int j, float av, uint32_t c) {
-          const float w = fmaf(-vnw, s_cent[c], av);
+          // f16-rounded centroid of the code (1-2 code bits: c arrives as its byte offset)
+          const float cc = BB <= 2 ? *reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(s_cent) + c)
+                                   : s_cent[c];
+          const float w = fmaf(-vnw, cc, av);
           ss = fmaf(w, w, ss);
           _Float16 h, l;
           split_f16(w * (1.f / (1 << SX)), h, l);
@@ -1045,9 +1053,9 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
         row_gemm<D, true, true>(P2, P3, bh, bl, acc, l16, g);
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          uint32_t neg = 0;
+          uint32_t neg = 0;  // bit j = sign of value j: v_alignbit shifts one sign bit in per value
 #pragma unroll
-          for (int j = 0; j < 8; ++j) neg |= (__float_as_uint(acc_at(acc, ks, j)) >> 31) << j;
+          for (int j = 7; j >= 0; --j) neg = __builtin_amdgcn_alignbit(neg, __float_as_uint(acc_at(acc, ks, j)), 31);
           stg[16 * KC + l16 * SC + 4 * ks + g] = static_cast<uint8_t>(~neg);
         }
         if (a.proj_out && gr < a.n) {
