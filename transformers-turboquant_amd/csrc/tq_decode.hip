@@ -285,7 +285,7 @@ decode_attn_lds_kernel(DecodeArgs a) {
 #pragma unroll
           for (int c = 0; c < 2; ++c) {
             const uint32_t wa = w[h][2 * c], wb = w[h][2 * c + 1];
-            f[h][c] = par ? ((wb & M) | ((wa >> VB) & ~M)) : (((wb << VB) & M) | (wa & ~M));
+            f[h][c] = par ? bfi32(M, wb, wa >> VB) : bfi32(M, wb << VB, wa);
           }
         static_for<4>([&](auto ic) {
           constexpr int i = decltype(ic)::value;
@@ -690,7 +690,7 @@ decode_attn_i8_kernel(DecodeArgs a) {
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
           const uint32_t wa = w[j][2 * c], wb = w[j][2 * c + 1];
-          f[j][c] = par ? ((wb & M) | ((wa >> VB) & ~M)) : (((wb << VB) & M) | (wa & ~M));
+          f[j][c] = par ? bfi32(M, wb, wa >> VB) : bfi32(M, wb << VB, wa);
         }
       static_for<4>([&](auto ic) {
         constexpr int i = decltype(ic)::value;
@@ -812,8 +812,18 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeArgs a) {
       continue;
     }
     auto ml = [&](int s, int k) { return a.part_ml[((base + s) * C + c) * 2 + k]; };
-    float mx = -INFINITY;
-    for (int s = lane; s < ns; s += SW) mx = fmaxf(mx, ml(s, 0));
+    const int64_t step = static_cast<int64_t>(C) * D;
+    const float* src0 = a.part_o + (base * C + c) * D + 2 * lane;
+    // one memory round trip for the common case (at most 8 splits): the first 8 splits'
+    // partial o and this lane's split maximum and sum are all issued before any is used
+    float2 v0[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      v0[u] = u < ns ? *reinterpret_cast<const float2*>(src0 + u * step) : float2{0.f, 0.f};
+    const float m_first = lane < ns ? ml(lane, 0) : -INFINITY;
+    const float l_first = lane < ns ? ml(lane, 1) : 0.f;
+    float mx = m_first;
+    for (int s = lane + SW; s < ns; s += SW) mx = fmaxf(mx, ml(s, 0));
 #pragma unroll
     for (int sh = 32; sh >= 1; sh >>= 1) mx = fmaxf(mx, __shfl_xor(mx, sh, 64));
     float lsum = 0.f, o0 = 0.f, o1 = 0.f;
@@ -821,15 +831,24 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeArgs a) {
       const int s = s0 + lane;
       float w = 0.f;
       if (s < ns) {
-        const float m = ml(s, 0);
+        const float m = s0 == 0 ? m_first : ml(s, 0);
         w = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - mx);
-        lsum += w * ml(s, 1);
+        lsum += w * (s0 == 0 ? l_first : ml(s, 1));
       }
       s_w[wave][lane] = w;  // read back by the same wave only: LDS order suffices
       const int nb = min(SW, ns - s0);
-      const float* src = a.part_o + ((base + s0) * C + c) * D + 2 * lane;
-      const int64_t step = static_cast<int64_t>(C) * D;
+      const float* src = src0 + s0 * step;
       int k = 0;
+      if (s0 == 0) {
+        // the preloaded first batch (splits past ns hold zeros and weight 0)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const float ww = u < nb ? s_w[wave][u] : 0.f;
+          o0 = fmaf(ww, v0[u].x, o0);
+          o1 = fmaf(ww, v0[u].y, o1);
+        }
+        k = min(8, nb);
+      }
       for (; k + 8 <= nb; k += 8) {
         float2 v[8];
 #pragma unroll

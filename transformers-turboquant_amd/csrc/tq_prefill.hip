@@ -251,7 +251,7 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
       const uint32_t w0 = field32(r0, dg * VB), w1 = field32(r0 + VC, dg * VB);
       constexpr uint32_t M = odd_fields<VB>();
       const uint32_t x = par ? (w0 >> VB) : w0, y = par ? w1 : (w1 << VB);
-      const uint32_t f = (y & M) | (x & ~M);
+      const uint32_t f = bfi32(M, y, x);
       half8 pv8;
       if constexpr (VB == 2) pv8 = nib4x2<0>(tV, f);
       else if constexpr (VB == 3) pv8 = six4x2(tV, f);

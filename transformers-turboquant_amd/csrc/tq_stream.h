@@ -122,6 +122,13 @@ __device__ __forceinline__ u32x2 lds64(const uint8_t* t, uint32_t off) {
 // Table offsets are built with SDWA byte selects: (byte K of x) & mask in one
 // instruction, on copies of the packed word pre-shifted so that each field lands
 // at the entry stride (x4 or x8 bytes) inside a byte.
+// (y & mask) | (x & ~mask) in one v_bfi_b32: for x = w >> k the compiler folds ~mask into
+// a narrower constant first and then emits a shift, an and and an and-or
+__device__ __forceinline__ uint32_t bfi32(uint32_t mask, uint32_t y, uint32_t x) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(y), "v"(x));
+  return r;
+}
 template <int K>
 __device__ __forceinline__ uint32_t and_byte(uint32_t mask, uint32_t x) {
   static_assert(K >= 0 && K < 4, "byte select");
