@@ -921,6 +921,7 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
     load_planes<D, T::NT, 1>(P2, P2, a.w2);
     fetch_row(gw, raw);
     wait_vm<0>();
+    wait_vm0_visible();  // the row fetched above counts as arrived inside the tile loop
     __syncthreads();
     for (int64_t t = gw; t < ntiles; t += nwaves) {
       const int64_t gr = t * 16 + l16;
@@ -978,6 +979,7 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
     load_planes<D, T::NT>(P0, P1, a.w1);
     fetch_row(gw, raw);
     wait_vm<0>();
+    wait_vm0_visible();  // the row fetched above counts as arrived inside the tile loop
     __syncthreads();
     auto tiles = [&](auto tab) {
       for (int64_t t = gw; t < ntiles; t += nwaves) {
@@ -1015,6 +1017,7 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
     load_planes<D, T::NT>(P2, P3, a.w3);
     fetch_row(gw, raw);
     wait_vm<0>();
+    wait_vm0_visible();  // the row fetched above counts as arrived inside the tile loop
     __syncthreads();
     auto tiles = [&](auto tab) {
       for (int64_t t = gw; t < ntiles; t += nwaves) {

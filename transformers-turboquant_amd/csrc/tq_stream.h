@@ -109,6 +109,11 @@ __device__ __forceinline__ void wait_vm() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
 }
+// vmcnt(0) as a compiler-visible s_waitcnt (vmcnt 0, expcnt and lgkmcnt unconstrained).  The
+// compiler's wait-insertion pass does not read inline asm, so after wait_vm<0>() it still takes
+// earlier loads as pending and waits again at their first use, which inside a loop means every
+// iteration (with the loads issued in between included); after this one they count as done.
+__device__ __forceinline__ void wait_vm0_visible() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
