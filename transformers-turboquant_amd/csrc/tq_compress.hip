@@ -982,9 +982,20 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
     wait_vm0_visible();  // the row fetched above counts as arrived inside the tile loop
     __syncthreads();
     auto tiles = [&](auto tab) {
+      // a tile's outputs leave at the start of the next one (see the key path)
+      int64_t tp = -1;
+      float vn_p = 0.f;
+      auto flush = [&]() {
+        const int64_t grp = tp * 16 + l16;
+        if (g == 0 && grp < a.n) a.vn[grp] = f2h(vn_p);
+        wave_sync();
+        store_rows(stg, a.codes, tp * 16, KC);
+        wave_sync();
+      };
       for (int64_t t = gw; t < ntiles; t += nwaves) {
         const int64_t gr = t * 16 + l16;
         fetch_row(t + nwaves, nxt);  // next tile's row, in flight during the product
+        if (tp >= 0) flush();
         // ---- vn = ||x||; y = (x / (vn + 1e-8)) Pi^T; codes = searchsorted-left, packed LSB
         // first   (compressors.py:274-287)
         float vn, xs;
@@ -994,12 +1005,11 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
         __builtin_amdgcn_s_setprio(1);
         quantize_stage(tab, acc, xs / (vn + 1e-8f), gr, [](int, int, float, uint32_t) {});
         __builtin_amdgcn_s_setprio(0);
-        if (g == 0 && gr < a.n) a.vn[gr] = f2h(vn);
-        wave_sync();
-        store_rows(stg, a.codes, t * 16, KC);
-        wave_sync();
+        tp = t;
+        vn_p = vn;
         raw = nxt;
       }
+      if (tp >= 0) flush();
     };
     if constexpr (QTAB) {
       if (qtable_ok()) tiles(std::true_type{});
@@ -1020,9 +1030,27 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
     wait_vm0_visible();  // the row fetched above counts as arrived inside the tile loop
     __syncthreads();
     auto tiles = [&](auto tab) {
+      // A tile's outputs (staged codes and signs, vn, rn) leave at the start of the next tile,
+      // after its row fetch: the wait for that fetch at the end of the tile (vmcnt counts
+      // stores too, in issue order) then finds the stores long complete instead of waiting
+      // for the ones just issued.
+      int64_t tp = -1;
+      float vn_p = 0.f, rn_p = 0.f;
+      auto flush = [&]() {
+        const int64_t grp = tp * 16 + l16;
+        if (g == 0 && grp < a.n) {
+          a.vn[grp] = f2h(vn_p);
+          a.rn[grp] = f2h(rn_p);
+        }
+        wave_sync();
+        store_rows(stg, a.codes, tp * 16, KC);
+        store_rows(stg + 16 * KC, a.signs, tp * 16, SC);
+        wave_sync();
+      };
       for (int64_t t = gw; t < ntiles; t += nwaves) {
         const int64_t gr = t * 16 + l16;
         fetch_row(t + nwaves, nxt);  // next tile's row, in flight during the products
+        if (tp >= 0) flush();
         // ---- vn = ||x||; y = (x / (vn + 1e-8)) Pi^T; codes   (compressors.py:108-116)
         float vn, xs;
         int e2;
@@ -1076,16 +1104,12 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
             po[1] = p1;
           }
         }
-        if (g == 0 && gr < a.n) {
-          a.vn[gr] = f2h(vn);
-          a.rn[gr] = f2h(rn);
-        }
-        wave_sync();
-        store_rows(stg, a.codes, t * 16, KC);
-        store_rows(stg + 16 * KC, a.signs, t * 16, SC);
-        wave_sync();
+        tp = t;
+        vn_p = vn;
+        rn_p = rn;
         raw = nxt;
       }
+      if (tp >= 0) flush();
     };
     if constexpr (QTAB) {
       if (qtable_ok()) tiles(std::true_type{});
