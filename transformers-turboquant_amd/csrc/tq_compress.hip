@@ -1065,17 +1065,23 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
         // 201.6 vs 209.2 us median)
         __builtin_amdgcn_s_setprio(1);
         float ss = 0.f;
+        float w_even = 0.f;
+        uint32_t wh[KS][4], wl[KS][4];
         quantize_stage(tab, acc, xs / (vn + 1e-8f), gr, [&](int ks, int j, float av, uint32_t c) {
           // f16-rounded centroid of the code (1-2 code bits: c arrives as its byte offset)
           const float cc = BB <= 2 ? *reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(s_cent) + c)
                                    : s_cent[c];
           const float w = fmaf(-vnw, cc, av);
           ss = fmaf(w, w, ss);
-          _Float16 h, l;
-          split_f16(w * (1.f / (1 << SX)), h, l);
-          bh[ks][j] = h;
-          bl[ks][j] = l;
+          // split as (even, odd) pairs: the next product's B operand dwords
+          if (j & 1) split_f16x2_scaled(w_even, w, 1.f / (1 << SX), wh[ks][j >> 1], wl[ks][j >> 1]);
+          else w_even = w;
         });
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          bh[ks] = __builtin_bit_cast(half8, u32x4{wh[ks][0], wh[ks][1], wh[ks][2], wh[ks][3]});
+          bl[ks] = __builtin_bit_cast(half8, u32x4{wl[ks][0], wl[ks][1], wl[ks][2], wl[ks][3]});
+        }
         const float rn = sqrtf(row_sum(ss)) * xs;
         __builtin_amdgcn_s_setprio(0);
         // ---- proj = u S_eff^T; signs = (proj >= 0)   (compressors.py:128-130).  Read off the
