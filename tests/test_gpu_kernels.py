@@ -303,6 +303,35 @@ def test_attention_additive_mask_and_dtypes(d):
         assert O.rel_err(_np(got.float()), ref) < tol
 
 
+@pytest.mark.parametrize("layout", ["per_head", "broadcast"])
+def test_attention_additive_mask_vector_loads(layout):
+    """d = 128 with key counts that are multiples of 4 and 16-byte aligned mask rows: the prefill
+    kernel's masked form reads each lane's 4 consecutive mask values as one 16-byte load. Real
+    bias values (ALiBi-like slopes, per head) on top of causal and padding masks, and a mask
+    broadcast over batch and heads (zero strides), against the float64 oracle."""
+    _case(what=f"mask vector loads {layout}")
+    torch.manual_seed(12)
+    B, hq, hkv, S, d = 2, 8, 2, 160, 128
+    q = torch.randn(B, hq, S, d, device=DEV)
+    k = torch.randn(B, hkv, S, d, device=DEV)
+    v = torch.randn(B, hkv, S, d, device=DEV)
+    kc = TurboQuantCompressorV2(d, 3, seed=42, device=DEV)
+    vc = TurboQuantCompressorMSE(d, 3, seed=10042, device=DEV)
+    ck, cv = kc.compress(k), vc.compress(v)
+    causal = torch.triu(torch.full((S, S), torch.finfo(torch.float32).min), 1)
+    if layout == "per_head":
+        pos = torch.arange(S, dtype=torch.float32)
+        slopes = torch.tensor([2.0 ** (-(h + 1)) for h in range(hq)])
+        mask = -(slopes[None, :, None, None] * (pos[:, None] - pos[None, :]).abs()[None, None]).expand(B, hq, S, S).clone()
+        mask[1, :, :, 100:] = torch.finfo(torch.float32).min  # padding on batch 1
+        mask = mask + causal
+    else:
+        mask = (causal + 0.25 * torch.randn(S, S))[None, None]
+    ref = _oracle_attention(kc, vc, q, ck, cv, hq, hkv, mask=mask.numpy())
+    got = compressed_attention(q, kc, vc, ck, cv, attention_mask=mask.to(DEV), out_dtype=torch.float32)
+    assert O.rel_err(_np(got.float()), ref) < REL
+
+
 def test_attention_full_size_slice():
     """Config-2 shape (1 x 32 x 8192, 8 KV heads, bits=3), causal; oracle on a slice of query rows."""
     _case(what="config2 slice")

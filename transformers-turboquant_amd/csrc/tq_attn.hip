@@ -535,7 +535,7 @@ using namespace tq;
 namespace tq {
 int64_t decode_workspace_bytes(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits);
 bool decode_applies(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits);
-bool prefill_applies(int Hq, int Hkv, int d, int bits, int val_bits);
+bool prefill_applies(int Hq, int Hkv, int d, int bits, int val_bits, bool masked);
 int prefill_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, const uint8_t* kcodes,
                       const uint8_t* ksigns, const uint16_t* krn, const uint16_t* kvn, const uint16_t* kcent,
                       int bits, const uint8_t* vcodes, const uint16_t* vvn, const float* vcent,
@@ -650,7 +650,7 @@ int tq_attention_fwd_kv(const uint16_t* q_rot, const float* q_proj, const uint8_
                             val_codes, val_vn, val_centroids, val_pit_split, B, Hq, Hkv, Sq, Sk, d, coeff,
                             scale, causal, mask, smb, smh, smq, smk, out, out_dtype, sob, soh, sos,
                             workspace, as_stream(stream));
-  if (prefill_applies(Hq, Hkv, d, bits, val_bits))
+  if (prefill_applies(Hq, Hkv, d, bits, val_bits, mask != nullptr))
     return prefill_attention(ldk, q_rot, q_proj, key_codes, key_signs, key_rn, key_vn, key_centroids_f16, bits,
                              val_codes, val_vn, val_centroids, val_pit_split, B, Hq, Hkv, Sq, Sk, coeff, scale,
                              causal, mask, smb, smh, smq, smk, out, out_dtype, sob, soh, sos, as_stream(stream));

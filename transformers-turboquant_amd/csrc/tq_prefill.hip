@@ -20,7 +20,9 @@
 //    every wave decodes its share of tile t+1 and runs the MFMAs and softmax of
 //    tile t, one block barrier per tile.
 //  * A block of 4 wave64 owns 128 (query row, query head) columns of one
-//    (batch, kv head); each wave owns two 16-column blocks.  S^T = K^ Q^T comes
+//    (batch, kv head); each wave owns two 16-column blocks (one, 64 columns per
+//    block, when an additive mask is applied: its loads and addresses do not fit
+//    the 256 VGPRs of the two-block form, which spilled ~56 of them).  S^T = K^ Q^T comes
 //    out of v_mfma_f32_16x16x32_f16 with 4 consecutive keys of one column per
 //    lane, the P^T operand layout of O^T += V^T P^T, so P stays in registers.
 //    P = f16(2^(s - m)) enters the P.V product (one f16 rounding, P <= 2^TAU).
@@ -34,6 +36,9 @@ namespace tq {
 
 constexpr int kPfRing = 2;   // raw tiles in the LDS ring (one in flight while one is decoded)
 constexpr int kPfWaves = 4;  // waves per block, each with two 16-column blocks: 128 columns
+// 16-column MFMA blocks per wave: 2, or 1 with an additive mask
+template <bool MASK>
+constexpr int pf_nbw() { return MASK ? 1 : 2; }
 
 struct PrefillArgs {
   const uint16_t* q_rot;
@@ -96,7 +101,7 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
   using C = PfCfg<BITS>;
   constexpr int D = C::D, KT = C::KT, R = C::R, KB = C::KB, VB = C::VB;
   constexpr int KC = C::KC, SC = C::SC, VC = C::VC, LDK = C::LDK, LDV = C::LDV;
-  constexpr int KS = D / 32, DB = D / 16, NT = C::NT, NBW = 2;  // 32 columns per wave
+  constexpr int KS = D / 32, DB = D / 16, NT = C::NT, NBW = pf_nbw<MASK>();  // 16 columns per block
   constexpr float LOG2E = 1.4426950408889634f;
   constexpr float TAU = 8.0f;  // lazy-rescale headroom (log2 units)
 
@@ -170,6 +175,18 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
       qr[ks][nb] = col_ok[nb] ? *reinterpret_cast<const half8*>(a.q_rot + qrow + d0) : half8{};
       qp[ks][nb] = col_ok[nb] ? round8(a.q_proj + qrow + d0) : half8{};
     }
+  }
+  // additive-mask rows of this lane's columns (row 0 for padding columns, whose scores are
+  // never written).  A lane's keys 4lg + 0..3 of a 16-key block are consecutive: one 16-byte
+  // load when the rows are contiguous in keys and 16-byte aligned (wave-uniform test)
+  const float* mrow[NBW];
+  bool mvec = false;
+  if constexpr (MASK) {
+#pragma unroll
+    for (int nb = 0; nb < NBW; ++nb)
+      mrow[nb] = a.mask + static_cast<int64_t>(b) * a.smb + static_cast<int64_t>(col_h[nb]) * a.smh +
+                 static_cast<int64_t>(col_ok[nb] ? col_i[nb] : 0) * a.smq;
+    mvec = a.smk == 1 && (reinterpret_cast<uintptr_t>(a.mask) & 15) == 0 && ((a.smb | a.smh | a.smq) & 3) == 0;
   }
 
   // keys this block needs; tiles past `kfull` need per-element masking
@@ -325,6 +342,22 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
     const bool edge = k0 + KT > kfull;
     float lmax[NBW];
     bool grow_any = false;
+    float4v mk[NBW][2];  // mask values of keys k0 + 16mb + 4lg + e (0 past Sk)
+    if constexpr (MASK) {
+#pragma unroll
+      for (int nb = 0; nb < NBW; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+          const int kb = k0 + mb * 16 + 4 * lg;
+          if (mvec && kb + 4 <= a.Sk) {
+            mk[nb][mb] = *reinterpret_cast<const float4v*>(mrow[nb] + kb);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              mk[nb][mb][e] = kb + e < a.Sk ? mrow[nb][static_cast<int64_t>(kb + e) * a.smk] : 0.f;
+          }
+        }
+    }
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb) {
 #pragma unroll
@@ -332,13 +365,7 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           float v = fmaf(tacc[mb][nb][e], mb ? fB1[e] : fB0[e], sacc[mb][nb][e] * (mb ? fA1[e] : fA0[e]));
-          if constexpr (MASK) {
-            const int key = k0 + mb * 16 + 4 * lg + e;
-            if (col_ok[nb] && key < a.Sk)
-              v += fmaxf(a.mask[b * a.smb + col_h[nb] * a.smh + static_cast<int64_t>(col_i[nb]) * a.smq +
-                                static_cast<int64_t>(key) * a.smk] * LOG2E,
-                         -3.0e38f);
-          }
+          if constexpr (MASK) v += fmaxf(mk[nb][mb][e] * LOG2E, -3.0e38f);
           sc[nb][mb][e] = v;
         }
     }
@@ -516,8 +543,9 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
 }
 
 // Used by tq_attn.hip's entry points.
-bool prefill_applies(int Hq, int Hkv, int d, int bits, int val_bits) {
-  return d == 128 && bits >= 2 && bits <= 4 && val_bits == bits && Hq / Hkv <= kPfWaves * 32;
+bool prefill_applies(int Hq, int Hkv, int d, int bits, int val_bits, bool masked) {
+  const int cols = kPfWaves * 16 * (masked ? pf_nbw<true>() : pf_nbw<false>());
+  return d == 128 && bits >= 2 && bits <= 4 && val_bits == bits && Hq / Hkv <= cols;
 }
 
 int prefill_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, const uint8_t* kcodes,
@@ -544,7 +572,7 @@ int prefill_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, c
   a.Sq = Sq;
   a.Sk = Sk;
   a.G = Hq / Hkv;
-  a.QT = PfCfg<3>::NW * 32 / a.G;  // 32 columns per wave
+  a.QT = PfCfg<3>::NW * 16 * (mask ? pf_nbw<true>() : pf_nbw<false>()) / a.G;  // query rows per block
   a.nqb = (Sq + a.QT - 1) / a.QT;
   a.ldk = ldk;
   a.coeff = coeff;
