@@ -814,11 +814,13 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeArgs a) {
     auto ml = [&](int s, int k) { return a.part_ml[((base + s) * C + c) * 2 + k]; };
     const int64_t step = static_cast<int64_t>(C) * D;
     const float* src0 = a.part_o + (base * C + c) * D + 2 * lane;
-    // one memory round trip for the common case (at most 8 splits): the first 8 splits'
-    // partial o and this lane's split maximum and sum are all issued before any is used
-    float2 v0[8];
+    // one memory round trip for up to NB0 splits (the decode shapes: 8 at 16 sequences x 32k
+    // keys, 16 at one sequence x 4k): the first NB0 splits' partial o and this lane's split
+    // maximum and sum are all issued before any is used
+    constexpr int NB0 = 16;
+    float2 v0[NB0];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < NB0; ++u)
       v0[u] = u < ns ? *reinterpret_cast<const float2*>(src0 + u * step) : float2{0.f, 0.f};
     const float m_first = lane < ns ? ml(lane, 0) : -INFINITY;
     const float l_first = lane < ns ? ml(lane, 1) : 0.f;
@@ -842,19 +844,19 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeArgs a) {
       if (s0 == 0) {
         // the preloaded first batch (splits past ns hold zeros and weight 0)
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < NB0; ++u) {
           const float ww = u < nb ? s_w[wave][u] : 0.f;
           o0 = fmaf(ww, v0[u].x, o0);
           o1 = fmaf(ww, v0[u].y, o1);
         }
-        k = min(8, nb);
+        k = min(NB0, nb);
       }
-      for (; k + 8 <= nb; k += 8) {
-        float2 v[8];
+      for (; k + 16 <= nb; k += 16) {
+        float2 v[16];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const float2*>(src + (k + u) * step);
+        for (int u = 0; u < 16; ++u) v[u] = *reinterpret_cast<const float2*>(src + (k + u) * step);
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < 16; ++u) {
           const float ww = s_w[wave][k + u];
           o0 = fmaf(ww, v[u].x, o0);
           o1 = fmaf(ww, v[u].y, o1);
