@@ -672,15 +672,26 @@ decode_attn_i8_kernel(DecodeArgs a) {
     }
     constexpr uint32_t M = odd_fields<VB>();
     uint32_t w[2][4];  // value fields of keys 16j + 4lg + kk
+    // the 8 row reads issued as one batch (the compiler otherwise reuses one register pair and
+    // waits after each)
+    uint32_t r0[2][4], r1[2][4];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         const uint32_t* vp = reinterpret_cast<const uint32_t*>(src + OFF_V + (16 * j + 4 * lg + kk) * VC + vbase);
+        r0[j][kk] = vp[0];
+        if constexpr (VW32 == 2) r1[j][kk] = vp[1];
+      }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
         if constexpr (VW32 == 2)
-          w[j][kk] = __builtin_amdgcn_alignbyte(vp[1], vp[0], vbyte);
+          w[j][kk] = __builtin_amdgcn_alignbyte(r1[j][kk], r0[j][kk], vbyte);
         else
-          w[j][kk] = vp[0] >> (8 * vbyte);
+          w[j][kk] = r0[j][kk] >> (8 * vbyte);
       }
 #pragma unroll
     for (int par = 0; par < 2; ++par) {
