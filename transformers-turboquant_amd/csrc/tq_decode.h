@@ -388,6 +388,54 @@ struct PlaneQuery {
     t1 = ldexpf(digits_f32(s1), x1) + k1;
     t2 = ldexpf(digits_f32(s2), x2) - k2;
   }
+  // dots() of two keys: both keys' fields are read before any MFMA, and the (block-uniform,
+  // rare) interaction-plane branch is taken once for both, so that it does not split the
+  // keys' work into separate basic blocks
+  __device__ __forceinline__ void dots2(const uint8_t* kp0, const uint8_t* sp0, const uint8_t* kp1,
+                                        const uint8_t* sp1, float (&t1)[2], float (&t2)[2]) const {
+    uint32_t kw[2][KB], sw[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint8_t* kp = j ? kp1 : kp0;
+      if constexpr (KB == 2) {
+        const u32x2 t = *reinterpret_cast<const u32x2*>(kp);
+        kw[j][0] = t[0];
+        kw[j][1] = t[1];
+      } else {
+        kw[j][0] = *reinterpret_cast<const uint32_t*>(kp);
+      }
+      sw[j] = *reinterpret_cast<const uint32_t*>(j ? sp1 : sp0);
+    }
+    i32x4v s1[2], s2[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      s1[j] = i32x4v{0, 0, 0, 0};
+      s2[j] = i32x4v{0, 0, 0, 0};
+      static_for<NT1>([&](auto ff) {
+        constexpr int f = decltype(ff)::value;
+        s1[j] = mfma_i8(A[f], planes4<4 * (f & 1)>(kw[j][f >> 1]), s1[j]);
+      });
+      static_for<2>([&](auto ff) {
+        constexpr int f = decltype(ff)::value;
+        s2[j] = mfma_i8(A[NT1 + f], planes4<4 * f>(sw[j]), s2[j]);
+      });
+    }
+    if constexpr (NDL > 0) {
+      if (inter) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          static_for<NDL>([&](auto ff) {
+            constexpr int w = decltype(ff)::value;
+            s1[j] = mfma_i8(A[NFM + w], planes_even(kw[j][w] & (kw[j][w] >> 1)), s1[j]);
+          });
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      t1[j] = ldexpf(digits_f32(s1[j]), x1) + k1;
+      t2[j] = ldexpf(digits_f32(s2[j]), x2) - k2;
+    }
+  }
 };
 
 // materialised scores for bits 2-3 and at most 4 columns (tq_decode.hip), on a plan of

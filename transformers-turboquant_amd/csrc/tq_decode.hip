@@ -438,15 +438,15 @@ __global__ void __launch_bounds__(256) decode_scores_i8_kernel(DecodeArgs a) {
   if (k0w + (R - 1) * SLAB < kend) issue(k0w + (R - 1) * SLAB, R - 1);
 
   auto slab = [&](const uint8_t* src, int ks0) {
-    float sc[2];
+    float sc[2], t1[2], t2[2];
+    pq.dots2(src + OFF_K + (2 * l16) * KC + lg * KLANE, src + OFF_S + (2 * l16) * SC + lg * 4,
+             src + OFF_K + (2 * l16 + 1) * KC + lg * KLANE, src + OFF_S + (2 * l16 + 1) * SC + lg * 4, t1, t2);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int row = 2 * l16 + u;
-      float t1, t2;
-      pq.dots(src + OFF_K + row * KC + lg * KLANE, src + OFF_S + row * SC + lg * 4, t1, t2);
       const float kn = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + row * 4)));
       const float rn = fb * h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + NRM + row * 4)));
-      sc[u] = t1 * kn + t2 * rn;
+      sc[u] = fmaf(t1[u], kn, t2[u] * rn);
     }
     const int key = ks0 + 2 * l16;
     if (key < kend) {
@@ -596,16 +596,16 @@ decode_attn_i8_kernel(DecodeArgs a) {
 
   auto slab = [&](const uint8_t* src, int ks0) {
     // ---- scores of keys ks0 + 16j + l16 (j = 0, 1) for column lg, log2 domain
-    float sc[2], nv[2];
+    float sc[2], nv[2], t1[2], t2[2];
+    pq.dots2(src + OFF_K + l16 * KC + lg * KLANE, src + OFF_S + l16 * SC + lg * 4,
+             src + OFF_K + (16 + l16) * KC + lg * KLANE, src + OFF_S + (16 + l16) * SC + lg * 4, t1, t2);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int row = 16 * j + l16;
-      float t1, t2;
-      pq.dots(src + OFF_K + row * KC + lg * KLANE, src + OFF_S + row * SC + lg * 4, t1, t2);
       const float kn = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + row * 4)));
       const float rn = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + NRM + row * 4)));
       nv[j] = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + 2 * NRM + row * 4)));
-      sc[j] = fmaf(t1, fa * kn, t2 * (fb * rn));
+      sc[j] = fmaf(t1[j], fa * kn, t2[j] * (fb * rn));
     }
     // ---- value norms enter P as vn / vcap <= 1; vcap is a power of two that only grows
     {
