@@ -703,12 +703,20 @@ decode_attn_i8_kernel(DecodeArgs a) {
           const uint32_t wa = w[j][2 * c], wb = w[j][2 * c + 1];
           f[j][c] = par ? bfi32(M, wb, wa >> VB) : bfi32(M, wb << VB, wa);
         }
+      // pair-table lookups one MFMA ahead: group i + 1 is read while the MFMA of group i runs
+      auto look = [&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        return __builtin_bit_cast(half8, u32x4{value_pair<VB, i>(tV, f[0][0]), value_pair<VB, i>(tV, f[0][1]),
+                                               value_pair<VB, i>(tV, f[1][0]), value_pair<VB, i>(tV, f[1][1])});
+      };
+      half8 va = look(std::integral_constant<int, 0>{});
       static_for<4>([&](auto ic) {
         constexpr int i = decltype(ic)::value;
-        const int db = 2 * i + par;
-        const half8 va = __builtin_bit_cast(half8, u32x4{value_pair<VB, i>(tV, f[0][0]), value_pair<VB, i>(tV, f[0][1]),
-                                                         value_pair<VB, i>(tV, f[1][0]), value_pair<VB, i>(tV, f[1][1])});
-        oacc[db] = mfma16x16x32(va, pb, oacc[db]);
+        half8 vn = va;
+        if constexpr (i + 1 < 4) vn = look(std::integral_constant<int, i + 1>{});
+        __builtin_amdgcn_sched_barrier(0);
+        oacc[2 * i + par] = mfma16x16x32(va, pb, oacc[2 * i + par]);
+        va = vn;
       });
     }
   };
