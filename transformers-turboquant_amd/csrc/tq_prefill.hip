@@ -426,11 +426,17 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
       l_run[nb] += psum;
     }
     // k-slots 8*lg+0..3 <-> keys 4lg+0..3, 8*lg+4..7 <-> keys 16+4lg+0..3: positions 8lg..8lg+7
+    // V^T fragments two blocks ahead of their MFMAs
+    constexpr int PD = 2;
+    half8 va[PD + 1];
+#pragma unroll
+    for (int q = 0; q < PD; ++q) va[q] = *reinterpret_cast<const half8*>(cV + (q * 16 + l16) * LDV + 8 * lg);
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
-      const half8 va = *reinterpret_cast<const half8*>(cV + (db * 16 + l16) * LDV + 8 * lg);
+      if (db + PD < DB) va[(db + PD) % (PD + 1)] = *reinterpret_cast<const half8*>(cV + ((db + PD) * 16 + l16) * LDV + 8 * lg);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int nb = 0; nb < NBW; ++nb) oacc[db][nb] = mfma16x16x32(va, pb[nb], oacc[db][nb]);
+      for (int nb = 0; nb < NBW; ++nb) oacc[db][nb] = mfma16x16x32(va[db % (PD + 1)], pb[nb], oacc[db][nb]);
     }
   };
 
