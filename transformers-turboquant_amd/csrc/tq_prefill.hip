@@ -317,19 +317,25 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
         sacc[mb][nb] = float4v{0.f, 0.f, 0.f, 0.f};
         tacc[mb][nb] = float4v{0.f, 0.f, 0.f, 0.f};
       }
+    // K^ and sign fragments one (k-step, key block) step ahead of their MFMAs
+    half8 ka[2], sa[2];
+    auto frag = [&](int i, int slot) {
+      const int off = ((i & 1) * 16 + l16) * LDK + (i >> 1) * 32 + lg * 8;
+      ka[slot] = *reinterpret_cast<const half8*>(cK + off);
+      sa[slot] = *reinterpret_cast<const half8*>(cS + off);
+    };
+    frag(0, 0);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
+    for (int i = 0; i < 2 * KS; ++i) {
+      const int ks = i >> 1, mb = i & 1, c = i & 1;
+      if (i + 1 < 2 * KS) frag(i + 1, c ^ 1);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        const int off = (mb * 16 + l16) * LDK + ks * 32 + lg * 8;
-        const half8 ka = *reinterpret_cast<const half8*>(cK + off);
-        const half8 sa = *reinterpret_cast<const half8*>(cS + off);
-#pragma unroll
-        for (int nb = 0; nb < NBW; ++nb) {
-          sacc[mb][nb] = mfma16x16x32(ka, qr[ks][nb], sacc[mb][nb]);
-          tacc[mb][nb] = mfma16x16x32(sa, qp[ks][nb], tacc[mb][nb]);
-        }
+      for (int nb = 0; nb < NBW; ++nb) {
+        sacc[mb][nb] = mfma16x16x32(ka[c], qr[ks][nb], sacc[mb][nb]);
+        tacc[mb][nb] = mfma16x16x32(sa[c], qp[ks][nb], tacc[mb][nb]);
       }
+    }
   };
   // ---- log2-domain scores with masking, column maxima, lazy rescale (one rare branch per tile)
   auto softmax_max = [&](int j, const float (*cF)[KT], const float4v (&sacc)[2][NBW],
