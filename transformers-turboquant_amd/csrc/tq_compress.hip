@@ -938,6 +938,12 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
       split_row(xv, ldexpf(kSplit, -e2), bh, bl);
       // q_rot = f16(q Pi^T)   (compressors.py:186)
       row_gemm<D, true, true>(P0, P1, bh, bl, acc, l16, g);
+      // the tile's outputs go through range-checked buffer stores (lanes of rows past n are
+      // dropped by the hardware): no branch around them, so the compiler's wait for the next
+      // row at the end of the tile counts them instead of waiting for them
+      const uint32_t nrows = static_cast<uint32_t>(a.n - t * 16 < 16 ? a.n - t * 16 : 16);
+      const rsrc_t rq = make_rsrc(a.q_rot + t * 16 * D, nrows * D * 2);
+      const rsrc_t rp = make_rsrc(a.q_proj + t * 16 * D, nrows * D * 4);
       const float inv = ldexpf(kUnsplit2, e2);
       mx = 0.f;
 #pragma unroll
@@ -947,7 +953,7 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
           bh[ks][j] = static_cast<_Float16>(acc_at(acc, ks, j) * inv);
           mx = fmaxf(mx, fabsf(static_cast<float>(bh[ks][j])));
         }
-        if (gr < a.n) *reinterpret_cast<half8*>(a.q_rot + gr * D + 32 * ks + 8 * g) = bh[ks];
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, bh[ks]), rq, (l16 * D + 32 * ks + 8 * g) * 2, 0, 0);
       }
       // q_rot holds f16 values: scaling by 2^(12-e) keeps them exact in f16
       frexpf(row_max(mx), &e2);
@@ -959,19 +965,17 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
       // q_proj = q_rot S_eff^T in f32: f32 accumulation of exact f16 products, as the
       // reference's fp32 projection (kernels/attention.py:158-167, :453)
       row_gemm<D, false, false>(P2, P2, bh, bl, acc, l16, g);
-      if (gr < a.n) {
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          float4v o0, o1;
+      for (int ks = 0; ks < KS; ++ks) {
+        float4v o0, o1;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            o0[j] = acc_at(acc, ks, j) * inv2;
-            o1[j] = acc_at(acc, ks, j + 4) * inv2;
-          }
-          float* dst = a.q_proj + gr * D + 32 * ks + 8 * g;
-          *reinterpret_cast<float4v*>(dst) = o0;
-          *reinterpret_cast<float4v*>(dst + 4) = o1;
+        for (int j = 0; j < 4; ++j) {
+          o0[j] = acc_at(acc, ks, j) * inv2;
+          o1[j] = acc_at(acc, ks, j + 4) * inv2;
         }
+        const uint32_t off = (l16 * D + 32 * ks + 8 * g) * 4;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o0), rp, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o1), rp, off + 16, 0, 0);
       }
       raw = nxt;
     }
