@@ -924,7 +924,6 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
     wait_vm0_visible();  // the row fetched above counts as arrived inside the tile loop
     __syncthreads();
     for (int64_t t = gw; t < ntiles; t += nwaves) {
-      const int64_t gr = t * 16 + l16;
       unpack_row(raw, xv);
       fetch_row(t + nwaves, nxt);  // next tile's row, in flight during the products
       // per-row power-of-two scale so the split parts stay in range (|q| * scale < kSplit)
