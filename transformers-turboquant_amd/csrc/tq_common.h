@@ -156,6 +156,26 @@ __device__ __forceinline__ void split_f16x2_scaled(float v0, float v1, float s, 
   lo = l;
 }
 
+// Maximum of values that are never NaN (attention scores, finite or -inf; norms) as
+// v_max3_f32 / v_max_f32 on the raw operands.  fmaxf on values that reach it through a select or a phi (the masked and
+// unmasked paths of a tile) makes the compiler quiet each operand first, one
+// `v_max_f32 x, x` per operand: 12 of the ~150 VALU per tile per wave of the prefill loop.
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float max_raw(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+// maximum of 8 scores: 3 VALU
+__device__ __forceinline__ float max8_raw(float s0, float s1, float s2, float s3, float s4, float s5, float s6,
+                                          float s7) {
+  return max3_raw(max3_raw(s0, s1, s2), max3_raw(s3, s4, s5), max_raw(s6, s7));
+}
+
 // ---------------------------------------------------------------- bits
 // Code i of a packed row: bits [i*b, i*b + b), LSB first.
 __device__ __forceinline__ uint32_t read_code(const uint8_t* row, int i, int b) {

@@ -233,7 +233,7 @@ decode_attn_lds_kernel(DecodeArgs a) {
     // when a score exceeds it by more than TAU; p = 2^(s - m_run + PUP)
     float lmax = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < NBS; ++j) lmax = fmaxf(lmax, fmaxf(fmaxf(sc[j][0], sc[j][1]), fmaxf(sc[j][2], sc[j][3])));
+    for (int j = 0; j < NBS; ++j) lmax = max3_raw(lmax, max3_raw(sc[j][0], sc[j][1], sc[j][2]), sc[j][3]);
     if (__any(lmax > m_run + TAU)) {
       float t = lmax;
       t = fmaxf(t, __shfl_xor(t, 16, 64));
@@ -609,7 +609,7 @@ decode_attn_i8_kernel(DecodeArgs a) {
     }
     // ---- value norms enter P as vn / vcap <= 1; vcap is a power of two that only grows
     {
-      const float vmx = fmaxf(nv[0], nv[1]);
+      const float vmx = max_raw(nv[0], nv[1]);
       if (__any(vmx > vcap)) {
         float t = vmx;
 #pragma unroll
@@ -638,7 +638,7 @@ decode_attn_i8_kernel(DecodeArgs a) {
     }
     // ---- lazy online softmax: column lg's reference m_run (uniform over the 16 lanes of the
     // column) moves only when a score exceeds it by more than TAU; p = 2^(s - m_run + PUP)
-    const float lmax = fmaxf(sc[0], sc[1]);
+    const float lmax = max_raw(sc[0], sc[1]);
     if (__any(lmax > m_run + TAU)) {
       float t = lmax;
 #pragma unroll

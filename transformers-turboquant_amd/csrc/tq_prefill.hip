@@ -394,8 +394,8 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
     // (cross-lane) only when some lane triggers
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb) {
-      lmax[nb] = fmaxf(fmaxf(fmaxf(sc[nb][0][0], sc[nb][0][1]), fmaxf(sc[nb][0][2], sc[nb][0][3])),
-                       fmaxf(fmaxf(sc[nb][1][0], sc[nb][1][1]), fmaxf(sc[nb][1][2], sc[nb][1][3])));
+      lmax[nb] = max8_raw(sc[nb][0][0], sc[nb][0][1], sc[nb][0][2], sc[nb][0][3], sc[nb][1][0], sc[nb][1][1],
+                          sc[nb][1][2], sc[nb][1][3]);
       grow_any = grow_any || (lmax[nb] > m_run[nb] + TAU);
     }
     if (__any(grow_any)) {
