@@ -364,13 +364,17 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
           }
         }
     }
+    // scores leave here relative to the column's reference maximum (0 while it is -inf):
+    // s - m in the same two fmas, so P = 2^(s - m) needs no subtraction per score
+    float mu[NBW];
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb) {
+      mu[nb] = (m_run[nb] == -INFINITY) ? 0.f : m_run[nb];
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float v = fmaf(tacc[mb][nb][e], mb ? fB1[e] : fB0[e], sacc[mb][nb][e] * (mb ? fA1[e] : fA0[e]));
+          float v = fmaf(tacc[mb][nb][e], mb ? fB1[e] : fB0[e], fmaf(sacc[mb][nb][e], mb ? fA1[e] : fA0[e], -mu[nb]));
           if constexpr (MASK) v += fmaxf(mk[nb][mb][e] * LOG2E, -3.0e38f);
           sc[nb][mb][e] = v;
         }
@@ -396,7 +400,7 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
     for (int nb = 0; nb < NBW; ++nb) {
       lmax[nb] = max8_raw(sc[nb][0][0], sc[nb][0][1], sc[nb][0][2], sc[nb][0][3], sc[nb][1][0], sc[nb][1][1],
                           sc[nb][1][2], sc[nb][1][3]);
-      grow_any = grow_any || (lmax[nb] > m_run[nb] + TAU);
+      grow_any = grow_any || (lmax[nb] > (m_run[nb] == -INFINITY ? -INFINITY : TAU));
     }
     if (__any(grow_any)) {
       asm volatile("; rescale");  // a side effect: the rare rescale stays a branch, never speculated
@@ -405,8 +409,15 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
         float tmax = lmax[nb];
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float m_new = tmax > m_run[nb] + TAU ? tmax : m_run[nb];
+        const bool grow = tmax > (m_run[nb] == -INFINITY ? -INFINITY : TAU);
+        const float m_new = grow ? tmax + mu[nb] : m_run[nb];
         const float alpha = (m_run[nb] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[nb] - m_new);
+        // the tile's scores move to the new reference
+        const float shift = grow ? m_new - mu[nb] : 0.f;
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sc[nb][mb][e] -= shift;
         m_run[nb] = m_new;
         l_run[nb] *= alpha;
 #pragma unroll
@@ -419,13 +430,12 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
     half8 pb[NBW];
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb) {
-      const float m_use = (m_run[nb] == -INFINITY) ? 0.f : m_run[nb];
       float psum = 0.f;
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float p = __builtin_amdgcn_exp2f(sc[nb][mb][e] - m_use);
+          const float p = __builtin_amdgcn_exp2f(sc[nb][mb][e]);  // sc holds s - m
           psum += p;
           pb[nb][mb * 4 + e] = static_cast<_Float16>(p);
         }
