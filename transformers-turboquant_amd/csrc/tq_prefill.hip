@@ -430,16 +430,16 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
     half8 pb[NBW];
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb) {
-      float psum = 0.f;
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p = __builtin_amdgcn_exp2f(sc[nb][mb][e]);  // sc holds s - m
-          psum += p;
-          pb[nb][mb * 4 + e] = static_cast<_Float16>(p);
-        }
-      l_run[nb] += psum;
+        for (int e = 0; e < 4; ++e) pb[nb][mb * 4 + e] = static_cast<_Float16>(__builtin_amdgcn_exp2f(sc[nb][mb][e]));
+      // the row sums add the f16 weights that enter the product, two per v_dot2_f32_f16
+      const half2v one2 = {static_cast<_Float16>(1.f), static_cast<_Float16>(1.f)};
+      float l = l_run[nb];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) l = __builtin_amdgcn_fdot2(half2v{pb[nb][2 * q], pb[nb][2 * q + 1]}, one2, l, false);
+      l_run[nb] = l;
     }
     // k-slots 8*lg+0..3 <-> keys 4lg+0..3, 8*lg+4..7 <-> keys 16+4lg+0..3: positions 8lg..8lg+7
     // V^T fragments two blocks ahead of their MFMAs
