@@ -263,7 +263,8 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
     for (int rep = 0; rep < 512 / NT; ++rep) {
       // values: item (key pair kp, 8-dim group dg, parity par) -> dwords (C[code 2kp], C[code 2kp+1])
       // of the even (par 0) or odd (par 1) dims of the group
-      const int i = tid + rep * NT, kp = i & 15, dg = (i >> 4) & 15, par = i >> 8;
+      static_assert(NT == 256, "item (kp, dg, par) = (tid & 15, tid >> 4, rep)");
+      const int kp = tid & 15, dg = tid >> 4, par = rep;
       const uint8_t* r0 = raw + C::OFF_V + (2 * kp) * VC;
       const uint32_t w0 = field32(r0, dg * VB), w1 = field32(r0 + VC, dg * VB);
       constexpr uint32_t M = odd_fields<VB>();
@@ -298,11 +299,14 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
     }
   };
 
-  float m_run[NBW], l_run[NBW];
+  // per column: the reference maximum mref (0 until the column has one) and the threshold a
+  // lane's score (relative to mref) must exceed to move it: -inf until then, TAU after
+  float mref[NBW], thr[NBW], l_run[NBW];
   float4v oacc[DB][NBW];
 #pragma unroll
   for (int nb = 0; nb < NBW; ++nb) {
-    m_run[nb] = -INFINITY;
+    mref[nb] = 0.f;
+    thr[nb] = -INFINITY;
     l_run[nb] = 0.f;
 #pragma unroll
     for (int db = 0; db < DB; ++db) oacc[db][nb] = float4v{0.f, 0.f, 0.f, 0.f};
@@ -364,17 +368,15 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
           }
         }
     }
-    // scores leave here relative to the column's reference maximum (0 while it is -inf):
-    // s - m in the same two fmas, so P = 2^(s - m) needs no subtraction per score
-    float mu[NBW];
+    // scores leave here relative to the column's reference maximum: s - m in the same two
+    // fmas, so P = 2^(s - m) needs no subtraction per score
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb) {
-      mu[nb] = (m_run[nb] == -INFINITY) ? 0.f : m_run[nb];
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float v = fmaf(tacc[mb][nb][e], mb ? fB1[e] : fB0[e], fmaf(sacc[mb][nb][e], mb ? fA1[e] : fA0[e], -mu[nb]));
+          float v = fmaf(tacc[mb][nb][e], mb ? fB1[e] : fB0[e], fmaf(sacc[mb][nb][e], mb ? fA1[e] : fA0[e], -mref[nb]));
           if constexpr (MASK) v += fmaxf(mk[nb][mb][e] * LOG2E, -3.0e38f);
           sc[nb][mb][e] = v;
         }
@@ -400,7 +402,7 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
     for (int nb = 0; nb < NBW; ++nb) {
       lmax[nb] = max8_raw(sc[nb][0][0], sc[nb][0][1], sc[nb][0][2], sc[nb][0][3], sc[nb][1][0], sc[nb][1][1],
                           sc[nb][1][2], sc[nb][1][3]);
-      grow_any = grow_any || (lmax[nb] > (m_run[nb] == -INFINITY ? -INFINITY : TAU));
+      grow_any = grow_any || (lmax[nb] > thr[nb]);
     }
     if (__any(grow_any)) {
       asm volatile("; rescale");  // a side effect: the rare rescale stays a branch, never speculated
@@ -409,16 +411,18 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
         float tmax = lmax[nb];
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const bool grow = tmax > (m_run[nb] == -INFINITY ? -INFINITY : TAU);
-        const float m_new = grow ? tmax + mu[nb] : m_run[nb];
-        const float alpha = (m_run[nb] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[nb] - m_new);
+        const bool grow = tmax > thr[nb];
+        const float m_new = grow ? tmax + mref[nb] : mref[nb];
+        // O and l of a column without a reference are still zero
+        const float alpha = (grow && thr[nb] != -INFINITY) ? __builtin_amdgcn_exp2f(mref[nb] - m_new) : 1.f;
         // the tile's scores move to the new reference
-        const float shift = grow ? m_new - mu[nb] : 0.f;
+        const float shift = m_new - mref[nb];
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
           for (int e = 0; e < 4; ++e) sc[nb][mb][e] -= shift;
-        m_run[nb] = m_new;
+        mref[nb] = m_new;
+        thr[nb] = grow ? TAU : thr[nb];
         l_run[nb] *= alpha;
 #pragma unroll
         for (int db = 0; db < DB; ++db) oacc[db][nb] *= alpha;
