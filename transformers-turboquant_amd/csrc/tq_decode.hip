@@ -587,7 +587,9 @@ decode_attn_i8_kernel(DecodeArgs a) {
   __syncthreads();  // fragments held (and tables built): the staging slot joins the ring
   if (k0w + (R - 1) * SLAB < kend) issue(k0w + (R - 1) * SLAB, R - 1);
 
-  float m_run = -INFINITY, l_run = 0.f;  // column lg, this lane's keys
+  // column lg: reference mref = m - PUP (0 until the column has a maximum m) and the threshold
+  // a score relative to mref must exceed to move it (-inf until then, TAU + PUP after)
+  float mref = 0.f, thr = -INFINITY, l_run = 0.f;
   float vcap = 0x1p-24f, inv_vcap = 0x1p24f;
   float4v oacc[DB];
 #pragma unroll
@@ -605,7 +607,7 @@ decode_attn_i8_kernel(DecodeArgs a) {
       const float kn = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + row * 4)));
       const float rn = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + NRM + row * 4)));
       nv[j] = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + 2 * NRM + row * 4)));
-      sc[j] = fmaf(t1[j], fa * kn, t2[j] * (fb * rn));
+      sc[j] = fmaf(t1[j], fa * kn, fmaf(t2[j], fb * rn, -mref));  // s - mref
     }
     // ---- value norms enter P as vn / vcap <= 1; vcap is a power of two that only grows
     {
@@ -636,27 +638,31 @@ decode_attn_i8_kernel(DecodeArgs a) {
         if (key >= kend || key > lim) sc[j] = -INFINITY;
       }
     }
-    // ---- lazy online softmax: column lg's reference m_run (uniform over the 16 lanes of the
-    // column) moves only when a score exceeds it by more than TAU; p = 2^(s - m_run + PUP)
+    // ---- lazy online softmax: column lg's maximum m (uniform over the 16 lanes of the column)
+    // moves only when a score exceeds it by more than TAU; p = 2^(s - m + PUP) = 2^sc
     const float lmax = max_raw(sc[0], sc[1]);
-    if (__any(lmax > m_run + TAU)) {
+    if (__any(lmax > thr)) {
       float t = lmax;
 #pragma unroll
       for (int sh = 8; sh >= 1; sh >>= 1) t = fmaxf(t, __shfl_xor(t, sh, 64));
       float alpha = 1.f;
-      if (t > m_run + TAU) {
-        alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - t);
-        m_run = t;
+      if (t > thr) {
+        const float mref_new = (t + mref) - PUP;
+        alpha = (thr == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mref - mref_new);
+        const float shift = mref_new - mref;
+        sc[0] -= shift;
+        sc[1] -= shift;
+        mref = mref_new;
+        thr = TAU + PUP;
         l_run *= alpha;
       }
       const float ac = __shfl(alpha, 16 * (l16 & 3), 64);  // O^T column l16 serves column l16 & 3
 #pragma unroll
       for (int db = 0; db < DB; ++db) oacc[db] *= ac;
     }
-    const float m_use = (m_run == -INFINITY) ? 0.f : m_run - PUP;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const float p = __builtin_amdgcn_exp2f(sc[j] - m_use);
+      const float p = __builtin_amdgcn_exp2f(sc[j]);
       l_run += p;
       pt[lg * NK + 16 * j + l16] = static_cast<_Float16>(p * (nv[j] * inv_vcap));
     }
@@ -751,7 +757,7 @@ decode_attn_i8_kernel(DecodeArgs a) {
   }
   if (l16 == 0) {
     float* my = mrg + (wave * 4 + lg) * (D + 2);
-    my[D] = (m_run == -INFINITY) ? m_run : m_run - PUP;
+    my[D] = (thr == -INFINITY) ? -INFINITY : mref;
     my[D + 1] = l;
   }
   __syncthreads();
