@@ -332,6 +332,42 @@ def test_attention_additive_mask_vector_loads(layout):
     assert O.rel_err(_np(got.float()), ref) < REL
 
 
+@pytest.mark.parametrize("bits,sq,sk,causal,masked", [
+    (3, 160, 160, True, False),   # head_dim-128 prefill kernel, causal
+    (2, 96, 224, False, False),   # prefill kernel, Sk > Sq
+    (3, 160, 160, True, True),    # the prefill kernel's additive-mask form
+    (3, 1, 2048, False, False),   # split-K decode kernels (bit-plane keys), 3 bits
+    (2, 1, 2048, False, False),   # split-K decode kernels, 2 bits
+])
+def test_attention_rising_scores_rescale(bits, sq, sk, causal, masked):
+    """Keys whose norms grow along the sequence (x1 to x9), so a column's scores climb by several
+    times the lazy-rescale headroom (8 log2 units) over the keys: the rescale branch runs again and
+    again, moving each column's reference and shifting the scores of the tile (held relative to
+    the reference) before P = 2^(s - m). Against the float64 oracle."""
+    _case(what="rising scores", bits=bits, sq=sq, sk=sk, causal=causal, masked=masked)
+    torch.manual_seed(21 + sk + bits)
+    B, hq, hkv, d = 2, 8, 2, 128
+    q = 2.0 * torch.randn(B, hq, sq, d, device=DEV)
+    ramp = 1.0 + 8.0 * torch.arange(sk, dtype=torch.float32) / sk
+    k = torch.randn(B, hkv, sk, d) * ramp[None, None, :, None]
+    k = k.to(DEV)
+    v = torch.randn(B, hkv, sk, d, device=DEV)
+    kc = TurboQuantCompressorV2(d, bits, seed=42, device=DEV)
+    vc = TurboQuantCompressorMSE(d, bits, seed=10042, device=DEV)
+    ck, cv = kc.compress(k), vc.compress(v)
+    if masked:
+        mask = torch.triu(torch.full((sq, sk), torch.finfo(torch.float32).min), 1 + sk - sq) + 0.5 * torch.randn(sq, sk)
+        mask = mask[None, None]
+        ref = _oracle_attention(kc, vc, q, ck, cv, hq, hkv, mask=mask.numpy())
+        got = compressed_attention(q, kc, vc, ck, cv, attention_mask=mask.to(DEV), out_dtype=torch.float32)
+    else:
+        ref = _oracle_attention(kc, vc, q, ck, cv, hq, hkv, causal=causal)
+        got = compressed_attention(q, kc, vc, ck, cv, causal=causal, out_dtype=torch.float32)
+    got = _np(got.float())
+    assert got.shape == ref.shape
+    assert O.rel_err(got, ref) < REL and O.cosine(got, ref) > 0.9999
+
+
 def test_attention_full_size_slice():
     """Config-2 shape (1 x 32 x 8192, 8 KV heads, bits=3), causal; oracle on a slice of query rows."""
     _case(what="config2 slice")
