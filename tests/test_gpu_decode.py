@@ -251,3 +251,35 @@ def test_decode_attention_sink_keeps_small_weights(bits, sk, vmul):
     print(f"ordinary keys' share of the weight {share:.3f}; rel-err {O.rel_err(got, ref):.2e}", flush=True)
     assert sc.argmax() == sink and 0.1 < share < 0.6
     assert O.rel_err(got, ref) < REL and O.cosine(got, ref) > 0.9999
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("sq,npad", [(1, 64), (1, 200), (1, 1000), (2, 100)])
+def test_decode_attention_left_padding(bits, sq, npad):
+    """Left padding with finfo.min on the first `npad` keys of batch row 0: whole 32-key slabs,
+    and at npad = 1000 whole splits, see only masked keys before the first real one.  Batch row
+    1 masks one key with a moderate bias, batch row 2 masks every key (the reference's softmax
+    of equal scores gives every key the same weight).  Sq = 1 takes the bit-plane kernels at
+    bits 2-3 (4 columns), Sq = 2 the table kernels (8 columns).  Against the float64 oracle."""
+    _case(what="decode left padding", bits=bits, sq=sq, npad=npad)
+    B, hq, hkv, sk, d = 3, 16, 4, 1500, 128
+    assert _on_decode_path(B, hq, hkv, sq, sk, bits)
+    torch.manual_seed(31 * bits + npad + sq)
+    q = torch.randn(B, hq, sq, d, device=DEV, dtype=torch.bfloat16)
+    k = torch.randn(B, hkv, sk, d, device=DEV, dtype=torch.bfloat16)
+    v = torch.randn(B, hkv, sk, d, device=DEV, dtype=torch.bfloat16)
+    kc = TurboQuantCompressorV2(d, bits, seed=42, device=DEV)
+    vc = TurboQuantCompressorMSE(d, bits, seed=10042, device=DEV)
+    ck, cv = kc.compress(k), vc.compress(v)
+    fmin = torch.finfo(torch.float32).min
+    mask = torch.zeros(B, 1, sq, sk)
+    mask[0, 0, :, :npad] = fmin
+    mask[1, 0, :, 5] = -3.0
+    mask[2] = fmin
+    ref = _oracle_attention(kc, vc, q, ck, cv, hq, hkv, mask=mask.numpy())
+    got = _np(compressed_attention(q, kc, vc, ck, cv, attention_mask=mask.to(DEV), out_dtype=torch.float32))
+    assert np.isfinite(got).all()
+    for b in range(B):
+        err = O.rel_err(got[b], ref[b])
+        print(f"batch row {b}: rel-err {err:.2e}", flush=True)
+        assert err < REL, (b, err)

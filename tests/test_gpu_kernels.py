@@ -332,6 +332,36 @@ def test_attention_additive_mask_vector_loads(layout):
     assert O.rel_err(_np(got.float()), ref) < REL
 
 
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("npad", [40, 64, 100])
+def test_attention_left_padding_mask(bits, npad):
+    """An eager-style mask (causal plus left padding, both finfo.min) with `npad` padded keys on
+    batch row 0: the first one to three 32-key tiles of every real query's column are fully
+    masked before its first real key.  The padded query rows see only masked keys, which the
+    reference's softmax of equal scores weighs equally.  Through the prefill kernel's
+    additive-mask form (head_dim 128) against the float64 oracle, per batch row."""
+    _case(what="left padding prefill", bits=bits, npad=npad)
+    torch.manual_seed(5 * bits + npad)
+    B, hq, hkv, S, d = 2, 8, 2, 200, 128
+    q = torch.randn(B, hq, S, d, device=DEV, dtype=torch.bfloat16)
+    k = torch.randn(B, hkv, S, d, device=DEV, dtype=torch.bfloat16)
+    v = torch.randn(B, hkv, S, d, device=DEV, dtype=torch.bfloat16)
+    kc = TurboQuantCompressorV2(d, bits, seed=42, device=DEV)
+    vc = TurboQuantCompressorMSE(d, bits, seed=10042, device=DEV)
+    ck, cv = kc.compress(k), vc.compress(v)
+    fmin = torch.finfo(torch.float32).min
+    mask = torch.triu(torch.full((S, S), fmin), 1).expand(B, 1, S, S).clone()
+    mask[0, 0, :, :npad] = fmin
+    ref = _oracle_attention(kc, vc, q, ck, cv, hq, hkv, mask=mask.numpy())
+    got = _np(compressed_attention(q, kc, vc, ck, cv, attention_mask=mask.to(DEV), out_dtype=torch.float32))
+    assert np.isfinite(got).all()
+    for b in range(B):
+        err = O.rel_err(got[b], ref[b])
+        real = O.rel_err(got[b, npad:], ref[b, npad:])
+        print(f"batch row {b}: rel-err {err:.2e} (real query rows {real:.2e})", flush=True)
+        assert err < REL and real < REL, (b, err, real)
+
+
 @pytest.mark.parametrize("bits,sq,sk,causal,masked", [
     (3, 160, 160, True, False),   # head_dim-128 prefill kernel, causal
     (2, 96, 224, False, False),   # prefill kernel, Sk > Sq

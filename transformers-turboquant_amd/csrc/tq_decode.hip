@@ -489,7 +489,13 @@ void launch_scores_planes(const DecodeArgs& a, int bits, hipStream_t s) {
 // runs once per (column, key) instead of once per MFMA column.  P goes through a small
 // per-wave LDS tile into the P^T operand of the value MFMA (the same O^T += V^T P^T step
 // as decode_attn_lds_kernel, with column n of O^T serving column n & 3).
-template <int KB, int R>
+//
+// MASK (an additive mask is applied): scores stay absolute until the column maximum is
+// settled and are made relative to it after the rescale test.  The unmasked form folds the
+// reference into the score fmas (s - mref), which is exact only while mref is of the order
+// of real scores: a leading slab masked with finfo.min (clamped to -3e38) would set mref to
+// -3e38, and s - mref would then round every later real score to the same value.
+template <int KB, int R, bool MASK>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 decode_attn_i8_kernel(DecodeArgs a) {
   constexpr int D = 128, BITS = KB + 1;
@@ -607,7 +613,8 @@ decode_attn_i8_kernel(DecodeArgs a) {
       const float kn = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + row * 4)));
       const float rn = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + NRM + row * 4)));
       nv[j] = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + 2 * NRM + row * 4)));
-      sc[j] = fmaf(t1[j], fa * kn, fmaf(t2[j], fb * rn, -mref));  // s - mref
+      // s - mref; absolute s under a mask (made relative after the rescale test)
+      sc[j] = fmaf(t1[j], fa * kn, MASK ? t2[j] * (fb * rn) : fmaf(t2[j], fb * rn, -mref));
     }
     // ---- value norms enter P as vn / vcap <= 1; vcap is a power of two that only grows
     {
@@ -627,11 +634,11 @@ decode_attn_i8_kernel(DecodeArgs a) {
         inv_vcap = ldexpf(1.f, -ex);
       }
     }
-    if (ks0 + NK > kend || ks0 + NK - 1 > causal_from || a.mask) {  // wave-uniform edge test
+    if (MASK || ks0 + NK > kend || ks0 + NK - 1 > causal_from) {  // wave-uniform edge test
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int key = ks0 + 16 * j + l16;
-        if (a.mask && c_ok && key < kend)
+        if (MASK && c_ok && key < kend)
           sc[j] += fmaxf(a.mask[b * a.smb + h * a.smh + static_cast<int64_t>(qi) * a.smq +
                                 static_cast<int64_t>(key) * a.smk] * LOG2E,
                          -3.0e38f);
@@ -641,17 +648,19 @@ decode_attn_i8_kernel(DecodeArgs a) {
     // ---- lazy online softmax: column lg's maximum m (uniform over the 16 lanes of the column)
     // moves only when a score exceeds it by more than TAU; p = 2^(s - m + PUP) = 2^sc
     const float lmax = max_raw(sc[0], sc[1]);
-    if (__any(lmax > thr)) {
+    if (__any((MASK ? lmax - mref : lmax) > thr)) {
       float t = lmax;
 #pragma unroll
       for (int sh = 8; sh >= 1; sh >>= 1) t = fmaxf(t, __shfl_xor(t, sh, 64));
       float alpha = 1.f;
-      if (t > thr) {
-        const float mref_new = (t + mref) - PUP;
+      if ((MASK ? t - mref : t) > thr) {
+        const float mref_new = (MASK ? t : t + mref) - PUP;
         alpha = (thr == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mref - mref_new);
-        const float shift = mref_new - mref;
-        sc[0] -= shift;
-        sc[1] -= shift;
+        if constexpr (!MASK) {
+          const float shift = mref_new - mref;
+          sc[0] -= shift;
+          sc[1] -= shift;
+        }
         mref = mref_new;
         thr = TAU + PUP;
         l_run *= alpha;
@@ -659,6 +668,12 @@ decode_attn_i8_kernel(DecodeArgs a) {
       const float ac = __shfl(alpha, 16 * (l16 & 3), 64);  // O^T column l16 serves column l16 & 3
 #pragma unroll
       for (int db = 0; db < DB; ++db) oacc[db] *= ac;
+    }
+    if constexpr (MASK) {
+      // relative to the settled reference: a column that has seen only masked keys (all at
+      // -3e38) gives them equal weights, as the reference's softmax of equal scores does
+      sc[0] -= mref;
+      sc[1] -= mref;
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -960,8 +975,8 @@ constexpr int kAttnPlaneRing = 2;
 static int attn_target_blocks(int bits, int C) {
   static int cache[5][16] = {};
   if (attn_planes(bits, C)) {
-    const void* k = bits == 2 ? reinterpret_cast<const void*>(&decode_attn_i8_kernel<1, kAttnPlaneRing>)
-                              : reinterpret_cast<const void*>(&decode_attn_i8_kernel<2, kAttnPlaneRing>);
+    const void* k = bits == 2 ? reinterpret_cast<const void*>(&decode_attn_i8_kernel<1, kAttnPlaneRing, false>)
+                              : reinterpret_cast<const void*>(&decode_attn_i8_kernel<2, kAttnPlaneRing, false>);
     return resident_blocks(k, 256, cache[bits + 1]);
   }
   const void* k = bits == 2 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 2, kAttnNbs, kAttnRing, true>)
@@ -999,7 +1014,8 @@ static void launch_decode_attn(const DecodeArgs& a, hipStream_t s) {
   dim3 grid(a.nsplit, a.Hkv, a.B);
   if constexpr (BITS <= 3) {
     if (attn_planes(BITS, a.C)) {
-      decode_attn_i8_kernel<BITS - 1, kAttnPlaneRing><<<grid, 256, 0, s>>>(a);
+      if (a.mask) decode_attn_i8_kernel<BITS - 1, kAttnPlaneRing, true><<<grid, 256, 0, s>>>(a);
+      else decode_attn_i8_kernel<BITS - 1, kAttnPlaneRing, false><<<grid, 256, 0, s>>>(a);
       return;
     }
   }

@@ -369,15 +369,23 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
         }
     }
     // scores leave here relative to the column's reference maximum: s - m in the same two
-    // fmas, so P = 2^(s - m) needs no subtraction per score
+    // fmas, so P = 2^(s - m) needs no subtraction per score.  Under an additive mask they stay
+    // absolute until the rescale test and are made relative after it: folding -m into the
+    // fmas is exact only while m is of the order of real scores, and a column whose first
+    // tile is masked with finfo.min (clamped to -3e38) would set m to -3e38, after which
+    // s - m would round every real score of the next tile to the same value
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb) {
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float v = fmaf(tacc[mb][nb][e], mb ? fB1[e] : fB0[e], fmaf(sacc[mb][nb][e], mb ? fA1[e] : fA0[e], -mref[nb]));
-          if constexpr (MASK) v += fmaxf(mk[nb][mb][e] * LOG2E, -3.0e38f);
+          float v;
+          if constexpr (MASK)
+            v = fmaf(tacc[mb][nb][e], mb ? fB1[e] : fB0[e], sacc[mb][nb][e] * (mb ? fA1[e] : fA0[e])) +
+                fmaxf(mk[nb][mb][e] * LOG2E, -3.0e38f);
+          else
+            v = fmaf(tacc[mb][nb][e], mb ? fB1[e] : fB0[e], fmaf(sacc[mb][nb][e], mb ? fA1[e] : fA0[e], -mref[nb]));
           sc[nb][mb][e] = v;
         }
     }
@@ -402,7 +410,7 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
     for (int nb = 0; nb < NBW; ++nb) {
       lmax[nb] = max8_raw(sc[nb][0][0], sc[nb][0][1], sc[nb][0][2], sc[nb][0][3], sc[nb][1][0], sc[nb][1][1],
                           sc[nb][1][2], sc[nb][1][3]);
-      grow_any = grow_any || (lmax[nb] > thr[nb]);
+      grow_any = grow_any || ((MASK ? lmax[nb] - mref[nb] : lmax[nb]) > thr[nb]);
     }
     if (__any(grow_any)) {
       asm volatile("; rescale");  // a side effect: the rare rescale stays a branch, never speculated
@@ -411,22 +419,33 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
         float tmax = lmax[nb];
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const bool grow = tmax > thr[nb];
-        const float m_new = grow ? tmax + mref[nb] : mref[nb];
+        const bool grow = (MASK ? tmax - mref[nb] : tmax) > thr[nb];
+        const float m_new = grow ? (MASK ? tmax : tmax + mref[nb]) : mref[nb];
         // O and l of a column without a reference are still zero
         const float alpha = (grow && thr[nb] != -INFINITY) ? __builtin_amdgcn_exp2f(mref[nb] - m_new) : 1.f;
-        // the tile's scores move to the new reference
-        const float shift = m_new - mref[nb];
+        if constexpr (!MASK) {  // the tile's scores move to the new reference
+          const float shift = m_new - mref[nb];
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
+          for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) sc[nb][mb][e] -= shift;
+            for (int e = 0; e < 4; ++e) sc[nb][mb][e] -= shift;
+        }
         mref[nb] = m_new;
         thr[nb] = grow ? TAU : thr[nb];
         l_run[nb] *= alpha;
 #pragma unroll
         for (int db = 0; db < DB; ++db) oacc[db][nb] *= alpha;
       }
+    }
+    if constexpr (MASK) {
+      // relative to the settled reference: a column that has seen only masked keys (all at
+      // -3e38) gives them equal weights, as the reference's softmax of equal scores does
+#pragma unroll
+      for (int nb = 0; nb < NBW; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sc[nb][mb][e] -= mref[nb];
     }
   };
   // ---- P = f16(2^(s - m)) (<= 2^TAU), row sums, O^T += V^T P^T
