@@ -1,8 +1,14 @@
 // torch.ops.tq: the PyTorch-ROCm operator layer over the C ABI of libtq_amd.so
-// (include/tq_api.h).  Each op checks its tensors, allocates its outputs with torch
-// (the caching allocator, so calls are capturable into HIP graphs), and calls one
-// C entry point on torch's current stream of the tensors' device.  No kernel code
-// lives here: the HIP kernels are the C library's.
+// (include/tq_api.h).  Each op checks every tensor it hands to the library (device,
+// dtype, contiguity, row width and the number of rows or entries the kernels will
+// read), allocates its outputs with torch (the caching allocator, so calls are
+// capturable into HIP graphs), and calls one C entry point on torch's current stream
+// of the tensors' device.  No kernel code lives here: the HIP kernels are the C
+// library's.
+//
+// The checks read tensor metadata only.  They are shared with a Meta kernel per op,
+// which runs them and returns empty outputs of the right shapes: shape inference for
+// meta / fake tensors, and the CPU-side tests of the checks themselves.
 //
 // Reference call sites these ops serve: compressors.py:99-317 (compress /
 // asymmetric_attention_scores / decompress) and kernels/__init__.py:1-11 (pack_bits,
@@ -29,10 +35,6 @@ void* stream_of(const Tensor& t) {
   return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream();
 }
 
-void require_gpu(const Tensor& t, const char* what) {
-  TORCH_CHECK(t.is_cuda(), what, ": expected a GPU tensor, got ", t.device());
-}
-
 int32_t dtype_code(at::ScalarType s) {
   switch (s) {
     case at::kFloat: return TQ_F32;
@@ -43,11 +45,12 @@ int32_t dtype_code(at::ScalarType s) {
   return -1;
 }
 
+bool is_act(at::ScalarType s) { return s == at::kFloat || s == at::kHalf || s == at::kBFloat16; }
+
 // activations: float32 / float16 / bfloat16 with unit stride along the last dim
 Tensor activation(const Tensor& x) {
   Tensor y = x;
-  const auto s = y.scalar_type();
-  if (s != at::kFloat && s != at::kHalf && s != at::kBFloat16) y = y.to(at::kFloat);
+  if (!is_act(y.scalar_type())) y = y.to(at::kFloat);
   if (y.stride(-1) != 1) y = y.contiguous();
   return y;
 }
@@ -67,10 +70,101 @@ T* optr(const c10::optional<Tensor>& t) {
 
 int64_t out_cols(int64_t d, int64_t b) { return (d * b + 7) / 8; }
 
+// ---------------------------------------------------------------- argument checks
+// A plane or table the library reads through a raw pointer: on the op's device, of the
+// dtype the kernel reads, contiguous (rows are addressed by index), `width` elements per
+// row when width > 1, and at least rows * width elements.
+struct Checker {
+  const char* op;
+  c10::Device dev;
+
+  void same_device(const Tensor& t, const char* name) const {
+    TORCH_CHECK(t.defined(), op, ": ", name, " is undefined");
+    TORCH_CHECK(t.device() == dev, op, ": ", name, " is on ", t.device(), ", expected ", dev);
+  }
+  void plane(const Tensor& t, const char* name, at::ScalarType dt, int64_t rows, int64_t width = 1) const {
+    same_device(t, name);
+    TORCH_CHECK(t.scalar_type() == dt, op, ": ", name, " must be ", dt, ", got ", t.scalar_type());
+    TORCH_CHECK(t.is_contiguous(), op, ": ", name, " must be contiguous");
+    if (width > 1)
+      TORCH_CHECK(t.dim() >= 1 && t.size(-1) == width, op, ": ", name, " rows must hold ", width,
+                  " elements, got shape ", t.sizes());
+    TORCH_CHECK(t.numel() >= rows * width, op, ": ", name, " holds ", t.numel(), " elements, the kernels read ",
+                rows * width);
+  }
+  void table(const Tensor& t, const char* name, at::ScalarType dt, int64_t entries) const {
+    plane(t, name, dt, entries, 1);
+  }
+  void optional_out(const c10::optional<Tensor>& t, const char* name, int64_t n) const {
+    if (t.has_value() && t->defined()) plane(*t, name, at::kFloat, n, 1);
+  }
+};
+
+// rows the kernels read from B * hkv head sequences of `sk` rows that start kv_stride apart
+// (0: sk, i.e. contiguous)
+int64_t kv_rows(int64_t B, int64_t hkv, int64_t sk, int64_t kv_stride) {
+  const int64_t stride = kv_stride > 0 ? kv_stride : sk;
+  return B * hkv > 0 ? (B * hkv - 1) * stride + sk : 0;
+}
+
+// prepared queries and the key planes of tq::scores / tq::attention
+void check_prepared_keys(const Checker& c, const Tensor& q_rot, const Tensor& q_proj, const Tensor& codes,
+                         const Tensor& signs, const Tensor& rn, const Tensor& vn, const Tensor& cent16, int64_t bits,
+                         int64_t hkv, int64_t sk, int64_t kv_stride) {
+  TORCH_CHECK(q_rot.dim() == 4, c.op, ": prepared queries must be [B, Hq, Sq, D], got ", q_rot.sizes());
+  TORCH_CHECK(q_rot.scalar_type() == at::kHalf && q_proj.scalar_type() == at::kFloat, c.op,
+              ": q_rot must be float16 and q_proj float32 (tq::query_prep)");
+  TORCH_CHECK(q_rot.is_contiguous() && q_proj.is_contiguous(), c.op, ": prepared queries must be contiguous");
+  c.same_device(q_proj, "q_proj");
+  TORCH_CHECK(q_proj.sizes() == q_rot.sizes(), c.op, ": q_proj ", q_proj.sizes(), " differs from q_rot ",
+              q_rot.sizes());
+  const int64_t B = q_rot.size(0), Hq = q_rot.size(1), D = q_rot.size(3);
+  TORCH_CHECK(bits >= 2 && bits <= 9, c.op, ": key bits must be 2..9, got ", bits);
+  TORCH_CHECK(hkv >= 1 && Hq % hkv == 0, c.op, ": ", Hq, " query heads are not a multiple of ", hkv, " kv heads");
+  TORCH_CHECK(sk >= 0 && (kv_stride == 0 || kv_stride >= sk), c.op, ": kv_stride ", kv_stride,
+              " must be 0 or at least Sk = ", sk);
+  const int64_t rows = kv_rows(B, hkv, sk, kv_stride);
+  c.plane(codes, "packed_key_indices", at::kByte, rows, out_cols(D, bits - 1));
+  c.plane(signs, "packed_qjl_signs", at::kByte, rows, out_cols(D, 1));
+  c.plane(rn, "residual_norm", at::kHalf, rows);
+  c.plane(vn, "vec_norms (keys)", at::kHalf, rows);
+  c.table(cent16, "key centroids", at::kHalf, int64_t{1} << (bits - 1));
+}
+
+void check_values(const Checker& c, const Tensor& q_rot, const Tensor& vcodes, const Tensor& vvn,
+                  const Tensor& vcent32, int64_t val_bits, const Tensor& vpit, int64_t hkv, int64_t sk,
+                  int64_t kv_stride) {
+  const int64_t B = q_rot.size(0), D = q_rot.size(3);
+  TORCH_CHECK(val_bits >= 1 && val_bits <= 8, c.op, ": value bits must be 1..8, got ", val_bits);
+  const int64_t rows = kv_rows(B, hkv, sk, kv_stride);
+  c.plane(vcodes, "packed_indices (values)", at::kByte, rows, out_cols(D, val_bits));
+  c.plane(vvn, "vec_norms (values)", at::kHalf, rows);
+  c.table(vcent32, "value centroids", at::kFloat, int64_t{1} << val_bits);
+  c.table(vpit, "split Pi_v^T", at::kHalf, 2 * D * D);
+}
+
+// the additive mask as a float32 view broadcast to [B, Hq, Sq, Sk] (no copy when it already
+// is float32 on the device)
+Tensor attention_mask(const Checker& c, const c10::optional<Tensor>& mask_in, const Tensor& q_rot, int64_t sk) {
+  if (!mask_in.has_value() || !mask_in->defined()) return Tensor();
+  Tensor mask = *mask_in;
+  TORCH_CHECK(mask.dim() <= 4, c.op, ": the mask must broadcast to [B, Hq, Sq, Sk], got ", mask.sizes());
+  if (mask.device() != q_rot.device() || mask.scalar_type() != at::kFloat) mask = mask.to(q_rot.device(), at::kFloat);
+  while (mask.dim() < 4) mask = mask.unsqueeze(0);
+  return mask.expand({q_rot.size(0), q_rot.size(1), q_rot.size(2), sk});
+}
+
 // ---------------------------------------------------------------- bit ops (kernels/bit_ops.py)
+void check_bits(const char* op, int64_t b) { TORCH_CHECK(b >= 1 && b <= 8, op, ": b must be 1..8, got ", b); }
+
+Tensor pack_bits_meta(const Tensor& idx, int64_t b) {
+  TORCH_CHECK(idx.dim() == 2, "tq::pack_bits: expected [N, d] codes");
+  check_bits("tq::pack_bits", b);
+  return at::empty({idx.size(0), out_cols(idx.size(1), b)}, idx.options().dtype(at::kByte));
+}
+
 Tensor pack_bits(const Tensor& idx_in, int64_t b) {
-  require_gpu(idx_in, "tq::pack_bits");
-  TORCH_CHECK(idx_in.dim() == 2, "tq::pack_bits: expected [N, d] codes");
+  pack_bits_meta(idx_in, b);
   const c10::DeviceGuard g(idx_in.device());
   Tensor idx = idx_in.to(at::kInt).contiguous();
   const int64_t n = idx.size(0), d = idx.size(1);
@@ -81,9 +175,17 @@ Tensor pack_bits(const Tensor& idx_in, int64_t b) {
   return out;
 }
 
+Tensor unpack_bits_meta(const Tensor& packed, int64_t b, int64_t d) {
+  TORCH_CHECK(packed.dim() == 2, "tq::unpack_bits: expected [N, bytes] packed rows");
+  check_bits("tq::unpack_bits", b);
+  TORCH_CHECK(packed.scalar_type() == at::kByte, "tq::unpack_bits: packed rows must be uint8");
+  TORCH_CHECK(packed.size(1) >= out_cols(d, b), "tq::unpack_bits: rows of ", packed.size(1), " bytes hold fewer than ",
+              d, " codes of ", b, " bits");
+  return at::empty({packed.size(0), d}, packed.options().dtype(at::kInt));
+}
+
 Tensor unpack_bits(const Tensor& packed_in, int64_t b, int64_t d) {
-  require_gpu(packed_in, "tq::unpack_bits");
-  TORCH_CHECK(packed_in.dim() == 2, "tq::unpack_bits: expected [N, bytes] packed rows");
+  unpack_bits_meta(packed_in, b, d);
   const c10::DeviceGuard g(packed_in.device());
   Tensor packed = packed_in.contiguous();
   const int64_t n = packed.size(0);
@@ -95,9 +197,17 @@ Tensor unpack_bits(const Tensor& packed_in, int64_t b, int64_t d) {
 }
 
 // ---------------------------------------------------------------- quantize (kernels/quantize.py)
+Tensor quantize_pack_meta(const Tensor& y, const Tensor& bounds, int64_t b_eff) {
+  TORCH_CHECK(y.dim() == 2, "tq::quantize_pack: expected [N, d] rotated rows");
+  check_bits("tq::quantize_pack", b_eff);
+  // the reference asserts the boundary count (quantize.py:223-227)
+  TORCH_CHECK(bounds.numel() == (int64_t{1} << b_eff) - 1, "tq::quantize_pack: expected ",
+              (int64_t{1} << b_eff) - 1, " boundaries for ", b_eff, " bits, got ", bounds.numel());
+  return at::empty({y.size(0), out_cols(y.size(1), b_eff)}, y.options().dtype(at::kByte));
+}
+
 Tensor quantize_pack(const Tensor& y_in, const Tensor& bounds_in, int64_t b_eff) {
-  require_gpu(y_in, "tq::quantize_pack");
-  TORCH_CHECK(y_in.dim() == 2, "tq::quantize_pack: expected [N, d] rotated rows");
+  quantize_pack_meta(y_in, bounds_in, b_eff);
   const c10::DeviceGuard g(y_in.device());
   Tensor y = y_in.to(at::kFloat).contiguous();
   Tensor bounds = on(bounds_in, y, at::kFloat);
@@ -109,8 +219,17 @@ Tensor quantize_pack(const Tensor& y_in, const Tensor& bounds_in, int64_t b_eff)
   return out;
 }
 
+Tensor dequantize_meta(const Tensor& packed, const Tensor& cent, int64_t b, int64_t d) {
+  TORCH_CHECK(packed.dim() == 2 && packed.scalar_type() == at::kByte, "tq::dequantize: expected uint8 [N, bytes]");
+  check_bits("tq::dequantize", b);
+  TORCH_CHECK(packed.size(1) >= out_cols(d, b), "tq::dequantize: rows of ", packed.size(1), " bytes hold fewer than ",
+              d, " codes of ", b, " bits");
+  TORCH_CHECK(cent.numel() >= (int64_t{1} << b), "tq::dequantize: ", cent.numel(), " centroids for ", b, "-bit codes");
+  return at::empty({packed.size(0), d}, packed.options().dtype(at::kHalf));
+}
+
 Tensor dequantize(const Tensor& packed_in, const Tensor& cent_in, int64_t b, int64_t d) {
-  require_gpu(packed_in, "tq::dequantize");
+  dequantize_meta(packed_in, cent_in, b, d);
   const c10::DeviceGuard g(packed_in.device());
   Tensor packed = packed_in.contiguous();
   Tensor cent = on(cent_in, packed, at::kHalf);
@@ -123,19 +242,36 @@ Tensor dequantize(const Tensor& packed_in, const Tensor& cent_in, int64_t b, int
 }
 
 // ---------------------------------------------------------------- compressors (compressors.py)
-std::tuple<Tensor, Tensor, Tensor, Tensor> compress_keys(const Tensor& states, const Tensor& pi_split,
-                                                         const Tensor& seff_split,
-                                                         const Tensor& centroids, const Tensor& bounds,
-                                                         int64_t b_eff, const c10::optional<Tensor>& y_out,
-                                                         const c10::optional<Tensor>& proj_out) {
-  require_gpu(states, "tq::compress_keys");
-  TORCH_CHECK(states.dim() == 4, "tq::compress_keys: expected [B, H, S, D] states");
+using KeyPlanes = std::tuple<Tensor, Tensor, Tensor, Tensor>;
+
+KeyPlanes compress_keys_meta(const Tensor& states, const Tensor& pi_split, const Tensor& seff_split,
+                             const Tensor& centroids, const Tensor& bounds, int64_t b_eff,
+                             const c10::optional<Tensor>& y_out, const c10::optional<Tensor>& proj_out) {
+  const Checker c{"tq::compress_keys", states.device()};
+  TORCH_CHECK(states.dim() == 4, c.op, ": expected [B, H, S, D] states");
+  TORCH_CHECK(b_eff >= 1 && b_eff <= 8, c.op, ": key code bits must be 1..8, got ", b_eff);
+  const int64_t B = states.size(0), H = states.size(1), S = states.size(2), D = states.size(3), n = B * H * S;
+  c.table(pi_split, "split Pi", at::kHalf, 2 * D * D);
+  c.table(seff_split, "split S_eff", at::kHalf, 2 * D * D);
+  c.table(centroids, "centroids", at::kFloat, int64_t{1} << b_eff);
+  c.table(bounds, "boundaries", at::kFloat, (int64_t{1} << b_eff) - 1);
+  c.optional_out(y_out, "y_out", n * D);
+  c.optional_out(proj_out, "proj_out", n * D);
+  auto u8 = states.options().dtype(at::kByte);
+  return {at::empty({n, out_cols(D, b_eff)}, u8), at::empty({n, out_cols(D, 1)}, u8),
+          at::empty({B, H, S}, states.options().dtype(at::kHalf)), at::empty({B, H, S}, states.options().dtype(at::kHalf))};
+}
+
+KeyPlanes compress_keys(const Tensor& states, const Tensor& pi_split, const Tensor& seff_split, const Tensor& centroids,
+                        const Tensor& bounds, int64_t b_eff, const c10::optional<Tensor>& y_out,
+                        const c10::optional<Tensor>& proj_out) {
+  compress_keys_meta(states, pi_split, seff_split, centroids, bounds, b_eff, y_out, proj_out);
   const c10::DeviceGuard g(states.device());
   Tensor x = activation(states);
   const int64_t B = x.size(0), H = x.size(1), S = x.size(2), D = x.size(3), n = B * H * S;
   auto u8 = x.options().dtype(at::kByte);
   Tensor codes = at::empty({n, out_cols(D, b_eff)}, u8);
-  Tensor signs = at::empty({n, (D + 7) / 8}, u8);
+  Tensor signs = at::empty({n, out_cols(D, 1)}, u8);
   Tensor rn = at::empty({B, H, S}, x.options().dtype(at::kHalf));
   Tensor vn = at::empty({B, H, S}, x.options().dtype(at::kHalf));
   check_status(tq_compress_keys(x.data_ptr(), dtype_code(x.scalar_type()), static_cast<int32_t>(B),
@@ -149,10 +285,22 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> compress_keys(const Tensor& states, c
   return {codes, signs, rn, vn};
 }
 
+std::tuple<Tensor, Tensor> compress_values_meta(const Tensor& states, const Tensor& pi_split, const Tensor& bounds,
+                                                int64_t bits, const c10::optional<Tensor>& y_out) {
+  const Checker c{"tq::compress_values", states.device()};
+  TORCH_CHECK(states.dim() == 4, c.op, ": expected [B, H, S, D] states");
+  TORCH_CHECK(bits >= 1 && bits <= 8, c.op, ": value bits must be 1..8, got ", bits);
+  const int64_t B = states.size(0), H = states.size(1), S = states.size(2), D = states.size(3), n = B * H * S;
+  c.table(pi_split, "split Pi", at::kHalf, 2 * D * D);
+  c.table(bounds, "boundaries", at::kFloat, (int64_t{1} << bits) - 1);
+  c.optional_out(y_out, "y_out", n * D);
+  return {at::empty({n, out_cols(D, bits)}, states.options().dtype(at::kByte)),
+          at::empty({n}, states.options().dtype(at::kHalf))};
+}
+
 std::tuple<Tensor, Tensor> compress_values(const Tensor& states, const Tensor& pi_split, const Tensor& bounds,
                                            int64_t bits, const c10::optional<Tensor>& y_out) {
-  require_gpu(states, "tq::compress_values");
-  TORCH_CHECK(states.dim() == 4, "tq::compress_values: expected [B, H, S, D] states");
+  compress_values_meta(states, pi_split, bounds, bits, y_out);
   const c10::DeviceGuard g(states.device());
   Tensor x = activation(states);
   const int64_t B = x.size(0), H = x.size(1), S = x.size(2), D = x.size(3), n = B * H * S;
@@ -167,10 +315,27 @@ std::tuple<Tensor, Tensor> compress_values(const Tensor& states, const Tensor& p
   return {codes, vn};
 }
 
+Tensor decompress_values_meta(const Tensor& codes, const Tensor& vn, const Tensor& pit_split, const Tensor& centroids,
+                              int64_t bits, at::IntArrayRef shape) {
+  const Checker c{"tq::decompress_values", codes.device()};
+  TORCH_CHECK(shape.size() == 4, c.op, ": shape must be [B, H, S, D]");
+  TORCH_CHECK(bits >= 1 && bits <= 8, c.op, ": value bits must be 1..8, got ", bits);
+  const int64_t n = shape[0] * shape[1] * shape[2], D = shape[3];
+  c.same_device(codes, "packed_indices");
+  TORCH_CHECK(codes.scalar_type() == at::kByte && codes.dim() >= 1 && codes.size(-1) == out_cols(D, bits) &&
+                  codes.numel() == n * out_cols(D, bits),
+              c.op, ": packed_indices must be uint8 rows of ", out_cols(D, bits), " bytes for ", n, " rows, got ",
+              codes.scalar_type(), " ", codes.sizes());
+  c.same_device(vn, "vec_norms");
+  TORCH_CHECK(vn.numel() == n, c.op, ": ", vn.numel(), " value norms for ", n, " rows");
+  c.table(pit_split, "split Pi^T", at::kHalf, 2 * D * D);
+  c.table(centroids, "centroids", at::kFloat, int64_t{1} << bits);
+  return at::empty(shape, codes.options().dtype(at::kFloat));
+}
+
 Tensor decompress_values(const Tensor& codes_in, const Tensor& vn_in, const Tensor& pit_split,
                          const Tensor& centroids, int64_t bits, at::IntArrayRef shape) {
-  require_gpu(codes_in, "tq::decompress_values");
-  TORCH_CHECK(shape.size() == 4, "tq::decompress_values: shape must be [B, H, S, D]");
+  decompress_values_meta(codes_in, vn_in, pit_split, centroids, bits, shape);
   const c10::DeviceGuard g(codes_in.device());
   const int64_t n = shape[0] * shape[1] * shape[2], D = shape[3];
   Tensor codes = codes_in.reshape({n, codes_in.size(-1)}).contiguous();
@@ -183,9 +348,18 @@ Tensor decompress_values(const Tensor& codes_in, const Tensor& vn_in, const Tens
   return out;
 }
 
+std::tuple<Tensor, Tensor> query_prep_meta(const Tensor& queries, const Tensor& pi_split, const Tensor& s_eff16) {
+  const Checker c{"tq::query_prep", queries.device()};
+  TORCH_CHECK(queries.dim() == 4, c.op, ": expected [B, Hq, Sq, D] queries");
+  const int64_t B = queries.size(0), Hq = queries.size(1), Sq = queries.size(2), D = queries.size(3);
+  c.table(pi_split, "split Pi", at::kHalf, 2 * D * D);
+  c.table(s_eff16, "f16 S_eff", at::kHalf, D * D);
+  return {at::empty({B, Hq, Sq, D}, queries.options().dtype(at::kHalf)),
+          at::empty({B, Hq, Sq, D}, queries.options().dtype(at::kFloat))};
+}
+
 std::tuple<Tensor, Tensor> query_prep(const Tensor& queries, const Tensor& pi_split, const Tensor& s_eff16) {
-  require_gpu(queries, "tq::query_prep");
-  TORCH_CHECK(queries.dim() == 4, "tq::query_prep: expected [B, Hq, Sq, D] queries");
+  query_prep_meta(queries, pi_split, s_eff16);
   const c10::DeviceGuard g(queries.device());
   Tensor q = activation(queries);
   const int64_t B = q.size(0), Hq = q.size(1), Sq = q.size(2), D = q.size(3);
@@ -200,13 +374,18 @@ std::tuple<Tensor, Tensor> query_prep(const Tensor& queries, const Tensor& pi_sp
 }
 
 // ---------------------------------------------------------------- scores and attention
+Tensor scores_meta(const Tensor& q_rot, const Tensor& q_proj, const Tensor& codes, const Tensor& signs, const Tensor& rn,
+                   const Tensor& vn, const Tensor& cent16, int64_t bits, int64_t hkv, int64_t sk, int64_t kv_stride,
+                   double coeff) {
+  const Checker c{"tq::scores", q_rot.device()};
+  check_prepared_keys(c, q_rot, q_proj, codes, signs, rn, vn, cent16, bits, hkv, sk, kv_stride);
+  return at::empty({q_rot.size(0), q_rot.size(1), q_rot.size(2), sk}, q_rot.options().dtype(at::kFloat));
+}
+
 Tensor scores(const Tensor& q_rot, const Tensor& q_proj, const Tensor& codes, const Tensor& signs,
               const Tensor& rn, const Tensor& vn, const Tensor& cent16, int64_t bits, int64_t hkv, int64_t sk,
               int64_t kv_stride, double coeff) {
-  require_gpu(q_rot, "tq::scores");
-  TORCH_CHECK(q_rot.scalar_type() == at::kHalf && q_proj.scalar_type() == at::kFloat,
-              "tq::scores: q_rot must be float16 and q_proj float32 (tq::query_prep)");
-  TORCH_CHECK(q_rot.is_contiguous() && q_proj.is_contiguous(), "tq::scores: prepared queries must be contiguous");
+  scores_meta(q_rot, q_proj, codes, signs, rn, vn, cent16, bits, hkv, sk, kv_stride, coeff);
   const c10::DeviceGuard g(q_rot.device());
   const int64_t B = q_rot.size(0), Hq = q_rot.size(1), Sq = q_rot.size(2), D = q_rot.size(3);
   Tensor out = at::empty({B, Hq, Sq, sk}, q_rot.options().dtype(at::kFloat));
@@ -220,6 +399,20 @@ Tensor scores(const Tensor& q_rot, const Tensor& q_proj, const Tensor& codes, co
   return out;
 }
 
+Tensor attention_meta(const Tensor& q_rot, const Tensor& q_proj, const Tensor& kcodes, const Tensor& ksigns,
+                      const Tensor& krn, const Tensor& kvn, const Tensor& kcent16, int64_t bits, const Tensor& vcodes,
+                      const Tensor& vvn, const Tensor& vcent32, int64_t val_bits, const Tensor& vpit, int64_t hkv,
+                      int64_t sk, int64_t kv_stride, double coeff, double scale, bool causal,
+                      const c10::optional<Tensor>& mask_in, at::ScalarType out_dtype, int64_t workspace) {
+  const Checker c{"tq::attention", q_rot.device()};
+  TORCH_CHECK(workspace >= 0 && workspace <= 2, c.op, ": workspace mode must be 0, 1 or 2");
+  TORCH_CHECK(is_act(out_dtype), c.op, ": out_dtype must be float32, float16 or bfloat16");
+  check_prepared_keys(c, q_rot, q_proj, kcodes, ksigns, krn, kvn, kcent16, bits, hkv, sk, kv_stride);
+  check_values(c, q_rot, vcodes, vvn, vcent32, val_bits, vpit, hkv, sk, kv_stride);
+  attention_mask(c, mask_in, q_rot, sk);  // broadcastable to [B, Hq, Sq, Sk]
+  return at::empty({q_rot.size(0), q_rot.size(2), q_rot.size(1), q_rot.size(3)}, q_rot.options().dtype(out_dtype));
+}
+
 // workspace: 0 = none (many-query kernels only), 1 = split-K partials allocated here from
 // torch, 2 = the library's per-GPU scratch array (tq_attention_fwd_kv_noalloc)
 Tensor attention(const Tensor& q_rot, const Tensor& q_proj, const Tensor& kcodes, const Tensor& ksigns,
@@ -227,22 +420,16 @@ Tensor attention(const Tensor& q_rot, const Tensor& q_proj, const Tensor& kcodes
                  const Tensor& vvn, const Tensor& vcent32, int64_t val_bits, const Tensor& vpit, int64_t hkv,
                  int64_t sk, int64_t kv_stride, double coeff, double scale, bool causal,
                  const c10::optional<Tensor>& mask_in, at::ScalarType out_dtype, int64_t workspace) {
-  require_gpu(q_rot, "tq::attention");
-  TORCH_CHECK(q_rot.scalar_type() == at::kHalf && q_proj.scalar_type() == at::kFloat,
-              "tq::attention: q_rot must be float16 and q_proj float32 (tq::query_prep)");
-  TORCH_CHECK(q_rot.is_contiguous() && q_proj.is_contiguous(), "tq::attention: prepared queries must be contiguous");
-  TORCH_CHECK(workspace >= 0 && workspace <= 2, "tq::attention: workspace mode must be 0, 1 or 2");
+  attention_meta(q_rot, q_proj, kcodes, ksigns, krn, kvn, kcent16, bits, vcodes, vvn, vcent32, val_bits, vpit, hkv, sk,
+                 kv_stride, coeff, scale, causal, mask_in, out_dtype, workspace);
+  const Checker c{"tq::attention", q_rot.device()};
   const c10::DeviceGuard g(q_rot.device());
   const int64_t B = q_rot.size(0), Hq = q_rot.size(1), Sq = q_rot.size(2), D = q_rot.size(3);
   Tensor out = at::empty({B, Sq, Hq, D}, q_rot.options().dtype(out_dtype));
-  Tensor mask;
+  Tensor mask = attention_mask(c, mask_in, q_rot, sk);
   int64_t ms[4] = {0, 0, 0, 0};
-  if (mask_in.has_value() && mask_in->defined()) {
-    mask = mask_in->to(q_rot.device(), at::kFloat);
-    while (mask.dim() < 4) mask = mask.unsqueeze(0);
-    mask = mask.expand({B, Hq, Sq, sk});
+  if (mask.defined())
     for (int i = 0; i < 4; ++i) ms[i] = mask.stride(i);
-  }
   const float* mptr = mask.defined() ? ptr<float>(mask) : nullptr;
   void* s = stream_of(out);
   const int32_t b32 = static_cast<int32_t>(bits), B32 = static_cast<int32_t>(B), Hq32 = static_cast<int32_t>(Hq),
@@ -317,4 +504,18 @@ TORCH_LIBRARY_IMPL(tq, CUDA, m) {
   m.impl("query_prep", &query_prep);
   m.impl("scores", &scores);
   m.impl("attention", &attention);
+}
+
+// the same checks on tensor metadata, returning empty outputs of the right shapes
+TORCH_LIBRARY_IMPL(tq, Meta, m) {
+  m.impl("pack_bits", &pack_bits_meta);
+  m.impl("unpack_bits", &unpack_bits_meta);
+  m.impl("quantize_pack", &quantize_pack_meta);
+  m.impl("dequantize", &dequantize_meta);
+  m.impl("compress_keys", &compress_keys_meta);
+  m.impl("compress_values", &compress_values_meta);
+  m.impl("decompress_values", &decompress_values_meta);
+  m.impl("query_prep", &query_prep_meta);
+  m.impl("scores", &scores_meta);
+  m.impl("attention", &attention_meta);
 }
