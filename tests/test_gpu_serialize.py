@@ -70,3 +70,51 @@ def test_gpu_cache_save_load_continues_generation(tmp_path):
                     assert torch.equal(va[name], vb[name]), name
         rest = model.generate(part, max_new_tokens=3, min_new_tokens=3, past_key_values=loaded, **kw)
     assert torch.equal(rest, full)
+
+
+def _to(groups, device):
+    out = []
+    for g in groups:
+        g = dict(g)
+        for which in ("keys", "values"):
+            if g.get(which) is not None:
+                g[which] = {k: (v if k == "shape" else v.to(device)) for k, v in g[which].items()}
+        out.append(g)
+    return out
+
+
+def test_gpu_golden_format_fixture(tmp_path):
+    """The committed format fixture (tests/golden/kv_format_v1.safetensors) read straight onto
+    the GPU holds exactly the planes its generator describes, and the same planes written from
+    device tensors give a file byte-identical to the committed one."""
+    print("case: serialize golden fixture on gpu", flush=True)
+    import os
+    import sys
+
+    golden = os.path.join(os.path.dirname(__file__), "golden")
+    sys.path.insert(0, golden)
+    import make_kv_format
+
+    path = os.path.join(golden, "kv_format_v1.safetensors")
+    groups, user = SZ.load_groups(path, device="cuda")
+    assert user == {"note": "format fixture"}
+    want = _to(make_kv_format.planes(), "cuda")
+    assert [g["name"] for g in groups] == [g["name"] for g in want]
+    for got, exp in zip(groups, want):
+        for which in ("keys", "values"):
+            if exp.get(which) is None:
+                assert got[which] is None
+                continue
+            assert set(got[which]) == set(exp[which]), which
+            for name, t in exp[which].items():
+                if name == "shape":
+                    assert tuple(got[which][name]) == tuple(t)
+                    continue
+                g = got[which][name]
+                assert g.device.type == "cuda" and g.dtype == t.dtype, (which, name)
+                assert torch.equal(g.reshape(t.shape), t), (which, name)
+    out = tmp_path / "from_gpu.safetensors"
+    SZ.save_groups(out, want, metadata={"note": "format fixture"})
+    with open(path, "rb") as f:
+        committed = f.read()
+    assert out.read_bytes() == committed

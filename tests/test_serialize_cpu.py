@@ -190,3 +190,12 @@ def test_cache_load_rejects_packed_on_cpu(tmp_path):
     SZ.save_groups(path, [{"name": "kv", "keys": k, "values": v}])
     with pytest.raises(SZ.FormatError):
         TurboQuantCache.load(path, device="cpu")
+
+
+def test_writer_reproduces_fixture_bytes(tmp_path):
+    """The writer is deterministic across processes (the container's metadata keys are emitted
+    sorted), so the fixture's planes written now give the committed file byte for byte."""
+    out = tmp_path / "again.safetensors"
+    SZ.save_groups(out, make_kv_format.planes(), metadata={"note": "format fixture"})
+    with open(os.path.join(GOLDEN, "kv_format_v1.safetensors"), "rb") as f:
+        assert out.read_bytes() == f.read()

@@ -48,7 +48,6 @@ import torch
 from safetensors.torch import load as _st_load
 from safetensors.torch import load_file as _st_load_file
 from safetensors.torch import save as _st_save
-from safetensors.torch import save_file as _st_save_file
 
 __all__ = ["FORMAT", "VERSION", "FormatError", "save_compressed", "load_compressed", "dumps", "loads",
            "save_groups", "load_groups", "pack_groups", "unpack_groups"]
@@ -233,14 +232,32 @@ def save_compressed(path, keys: dict | None = None, values: dict | None = None, 
                     value_compressor=None, metadata: dict | None = None) -> None:
     """Write one compressed (keys, values) pair; the compressors supply bits and seeds."""
     tensors, infos = pack_groups([_group_arg(keys, values, key_compressor, value_compressor)])
-    _st_save_file(tensors, str(path), metadata=_header(infos, metadata))
+    with open(path, "wb") as f:
+        f.write(_container(tensors, _header(infos, metadata)))
 
 
 def dumps(keys: dict | None = None, values: dict | None = None, key_compressor=None, value_compressor=None,
           metadata: dict | None = None) -> bytes:
     """The bytes `save_compressed` would write."""
     tensors, infos = pack_groups([_group_arg(keys, values, key_compressor, value_compressor)])
-    return _st_save(tensors, metadata=_header(infos, metadata))
+    return _container(tensors, _header(infos, metadata))
+
+
+def _container(tensors: dict[str, torch.Tensor], meta: dict[str, str]) -> bytes:
+    """The container's bytes, deterministic for the same planes and metadata: the safetensors
+    writer keeps ``__metadata__`` in a hash map, so its key order (and the file's bytes) would
+    differ between processes.  The header is re-emitted with ``__metadata__`` first, its keys
+    sorted, and the tensor entries in the writer's data order, space-padded to 8 bytes as
+    safetensors pads it; the tensor data is unchanged."""
+    raw = _st_save(tensors, metadata=meta)  # pack_groups made the tensors contiguous CPU copies
+    n = int.from_bytes(raw[:8], "little")
+    head = json.loads(raw[8:8 + n])
+    entries = sorted(((k, v) for k, v in head.items() if k != "__metadata__"), key=lambda kv: kv[1]["data_offsets"])
+    canon = {"__metadata__": dict(sorted(head.get("__metadata__", {}).items()))}
+    canon.update(entries)
+    text = json.dumps(canon, separators=(",", ":")).encode()
+    text += b" " * (-len(text) % 8)
+    return len(text).to_bytes(8, "little") + text + raw[8 + n:]
 
 
 def _read_meta(path) -> dict:
@@ -304,7 +321,8 @@ def loads(data: bytes, device="cpu") -> tuple[dict | None, dict | None, dict]:
 def save_groups(path, groups: list[dict], metadata: dict | None = None) -> None:
     """Write several named (keys, values) groups (see `pack_groups`) into one container."""
     tensors, infos = pack_groups(groups)
-    _st_save_file(tensors, str(path), metadata=_header(infos, metadata))
+    with open(path, "wb") as f:
+        f.write(_container(tensors, _header(infos, metadata)))
 
 
 def load_groups(path, device="cpu") -> tuple[list[dict], dict]:
