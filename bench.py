@@ -23,6 +23,7 @@ runs on one GPU.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -41,8 +42,37 @@ DEC_B, DEC_SK, DEC_ROT = 16, 32768, 4
 # the decode attention kernel); each decode leg runs this long untimed before its W
 # warmup + K timed steps, so the timed steps see the clock a serving loop runs at
 SETTLE_MS = 200.0
+LEAD = 3  # untimed launches queued just before each decode leg's start event
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+class _ProfilerRegions:
+    """Brackets the timed steps for `rocprofv3 --selected-regions`, which collects only between
+    roctxProfilerResume(0) and roctxProfilerPause(0): a kernel trace of bench.py then holds the
+    timed launches of every leg and none of the clock-settling or warm-up launches, so its
+    per-kernel averages are those of the timed region.  Without the profiler the calls do
+    nothing; without the roctx library they are skipped."""
+
+    def __init__(self):
+        self._lib = None
+        for name in ("librocprofiler-sdk-roctx.so.1", "librocprofiler-sdk-roctx.so"):
+            try:
+                self._lib = ctypes.CDLL(name)
+                break
+            except OSError:
+                continue
+
+    def resume(self):
+        if self._lib is not None:
+            self._lib.roctxProfilerResume(0)
+
+    def pause(self):
+        if self._lib is not None:
+            self._lib.roctxProfilerPause(0)
+
+
+REGIONS = _ProfilerRegions()
 
 
 def key_rec_bytes(bits: int, d: int) -> int:
@@ -64,6 +94,61 @@ def measured_traffic(kernel: str, record: str = "traffic_bench.json"):
         return rec["kernels"][kernel]["traffic_bytes"]
     except (OSError, KeyError, ValueError):
         return None
+
+
+def pmc_summary(paths: list[str], copy_mib: int) -> dict:
+    """HBM traffic per dispatch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE counter CSVs of a
+    bench.py run with --calibrate-copy: per (kernel, grid size), the mean counter value (KiB) over
+    its dispatches; the device-to-device copy of `copy_mib` MiB calibrates each counter (factor =
+    true KiB / counted KiB), and traffic_bytes = (FETCH_SIZE * fetch_factor + WRITE_SIZE *
+    write_factor) * 1024.  Each kernel's record is its dispatch group with the largest grid (the
+    bench leg's workload)."""
+    import csv
+
+    def short(name: str) -> str:  # "void tq::k<2, 3>(tq::Args)" -> "tq::k<2, 3>"
+        name = name[5:] if name.startswith("void ") else name
+        return name[:name.rfind("(")] if name.endswith(")") and "(" in name else name
+
+    sums: dict = {}
+    for path in paths:
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                key = (short(r["Kernel_Name"]), int(r["Grid_Size"]), r["Counter_Name"])
+                acc = sums.setdefault(key, [0.0, 0])
+                acc[0] += float(r["Counter_Value"])
+                acc[1] += 1
+    mean = {k: v[0] / v[1] for k, v in sums.items()}
+    count = {k: v[1] for k, v in sums.items()}
+    copy_kib = copy_mib * 1024.0
+    copies = [k for k in mean if "copyBuffer" in k[0]]
+
+    def biggest(name, counter):
+        ks = [k for k in mean if k[0] == name and k[2] == counter]
+        return max(ks, key=lambda k: k[1]) if ks else None
+
+    cal = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        ks = [k for k in copies if k[2] == counter]
+        k = max(ks, key=lambda k: mean[k]) if ks else None
+        cal[counter] = copy_kib / mean[k] if k and mean[k] > 0 else None
+    kernels = {}
+    for name in sorted({k[0] for k in mean if "copyBuffer" not in k[0]}):
+        kf, kw = biggest(name, "FETCH_SIZE"), biggest(name, "WRITE_SIZE")
+        if kf is None or kw is None or None in cal.values():
+            continue
+        fetch, write = mean[kf], mean[kw]
+        kernels[name] = {"grid_size": kf[1], "dispatches": count[kf], "fetch_kib": fetch, "write_kib": write,
+                         "traffic_bytes": int(round((fetch * cal["FETCH_SIZE"] + write * cal["WRITE_SIZE"]) * 1024))}
+    a, m = "tq::decode_attn_i8_kernel<2, 2, false>", "tq::decode_merge_kernel<128>"
+    if a in kernels and m in kernels:
+        kernels["decode_attention (attention + merge)"] = {
+            "name": f"{a} + {m}", "traffic_bytes": kernels[a]["traffic_bytes"] + kernels[m]["traffic_bytes"]}
+    return {"calibration": {"copy_bytes": copy_mib << 20, "fetch_factor": cal["FETCH_SIZE"],
+                            "write_factor": cal["WRITE_SIZE"]},
+            "sources": [os.path.basename(p) for p in paths],
+            "method": ("mean counter KiB per dispatch per (kernel, grid size); the largest grid per kernel; "
+                       "traffic_bytes = (FETCH_SIZE * fetch_factor + WRITE_SIZE * write_factor) * 1024"),
+            "kernels": kernels}
 
 
 def host_cpu() -> dict:
@@ -228,8 +313,12 @@ def decode_legs(kc, vc, outliers, steps: int, warmup: int) -> tuple[dict, dict]:
         cv = vc.compress(v)
         del v
         caches.append((ck, cv))
-    q = torch.randn(DEC_B, HQ, 1, D, device=dev, generator=gen).to(torch.bfloat16)
+    # fresh queries per step for the API-level step (query preparation + scores)
+    qs = [torch.randn(DEC_B, HQ, 1, D, device=dev, generator=gen).to(torch.bfloat16) for _ in range(DEC_ROT)]
+    q = qs[0]
     q_rot, q_proj = kc.prepare_queries(q)
+    api_rot = [torch.empty_like(q_rot) for _ in range(DEC_ROT)]
+    api_proj = [torch.empty_like(q_proj) for _ in range(DEC_ROT)]
     tk = _tables(kc, dev, with_qjl=True)
     tv = _tables(vc, dev, with_qjl=False)
     coeff = math.sqrt(math.pi / 2) / D
@@ -247,6 +336,21 @@ def decode_legs(kc, vc, outliers, steps: int, warmup: int) -> tuple[dict, dict]:
             tk.cent16.data_ptr(), DEC_B, HQ, HKV, 1, DEC_SK, D, BITS, coeff,
             scores[i % DEC_ROT].data_ptr(), stream)
 
+    def launch_api(i):
+        # the reference's scoring call (compressors.py:178-200 with attention.py:158-167): rotate and
+        # project this step's queries, then score them against the compressed keys
+        j = i % DEC_ROT
+        qj, ck = qs[j], caches[j][0]
+        st = lib.tq_query_prep(qj.data_ptr(), _native.TQ_BF16, DEC_B, HQ, 1, D, qj.stride(0), qj.stride(1),
+                               qj.stride(2), tk.pi_split.data_ptr(), tk.s_eff16.data_ptr(), api_rot[j].data_ptr(),
+                               api_proj[j].data_ptr(), stream)
+        if st:
+            return st
+        return lib.tq_attention_scores(
+            api_rot[j].data_ptr(), api_proj[j].data_ptr(), ck["packed_key_indices"].data_ptr(),
+            ck["packed_qjl_signs"].data_ptr(), ck["residual_norm"].data_ptr(), ck["vec_norms"].data_ptr(),
+            tk.cent16.data_ptr(), DEC_B, HQ, HKV, 1, DEC_SK, D, BITS, coeff, scores[j].data_ptr(), stream)
+
     def launch_attn(i):
         ck, cv = caches[i % DEC_ROT]
         o = outs[i % DEC_ROT]
@@ -263,6 +367,12 @@ def decode_legs(kc, vc, outliers, steps: int, warmup: int) -> tuple[dict, dict]:
         for i in range(warmup):
             _native.check(launch(i), "decode warmup")
         torch.cuda.synchronize()
+        # a few untimed launches queued right before the start event keep the stream busy while
+        # the host issues the first timed one: the events then hold the K timed steps back to
+        # back, not the host's latency to its first launch after an idle GPU
+        for i in range(LEAD):
+            _native.check(launch(i), "decode lead-in")
+        REGIONS.resume()
         e0, e1 = _events(2)
         e0.record()
         for i in range(steps):
@@ -271,16 +381,21 @@ def decode_legs(kc, vc, outliers, steps: int, warmup: int) -> tuple[dict, dict]:
                 _native.check(st, "decode launch")
         e1.record()
         torch.cuda.synchronize()
+        REGIONS.pause()
         return e0.elapsed_time(e1) / steps
 
     ms_scores = timed(launch_scores)
+    ms_api = timed(launch_api)
     ms_attn = timed(launch_attn)
     key_heads = DEC_B * HQ * DEC_SK
-    q_bytes = DEC_B * HQ * D * 2 * 2
+    q_bytes = DEC_B * HQ * D * (2 + 4)  # prepared queries read: f16 q_rot + f32 q_proj
     score_bytes = DEC_B * HKV * DEC_SK * key_rec_bytes(BITS, D) + key_heads * 4 + q_bytes
+    # the API step also reads the bf16 queries and writes the prepared ones
+    api_bytes = score_bytes + DEC_B * HQ * D * (2 + 2 + 4)
     attn_bytes = (DEC_B * HKV * DEC_SK * (key_rec_bytes(BITS, D) + val_rec_bytes(BITS, D)) + q_bytes
                   + DEC_B * HQ * D * 2)
     gbs_s = score_bytes / (ms_scores * 1e-3) / 1e9
+    gbs_api = api_bytes / (ms_api * 1e-3) / 1e9
     gbs_a = attn_bytes / (ms_attn * 1e-3) / 1e9
     scores_leg = {
         "ms_per_launch": ms_scores,
@@ -291,21 +406,84 @@ def decode_legs(kc, vc, outliers, steps: int, warmup: int) -> tuple[dict, dict]:
             "frac": gbs_s / HBM_PEAK_GBS, "traffic": measured_traffic("tq::decode_scores_i8_kernel<2, 3>"),
             "algorithmic_bytes_per_launch": score_bytes,
         },
+        "api_step": {
+            "what": ("the reference's scoring call per step: tq_query_prep (rotate + project this step's "
+                     f"{DEC_B}x{HQ} bf16 query rows) then tq_attention_scores, fresh queries every step"),
+            "ms_per_step": ms_api,
+            "key_heads_per_s": key_heads / (ms_api * 1e-3),
+            "roofline": {"bound": "hbm", "achieved": gbs_api, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs_api / HBM_PEAK_GBS, "algorithmic_bytes_per_step": api_bytes},
+        },
     }
     attn_leg = {
         "workload": f"fused decode attention, same caches: B{DEC_B} Hq{HQ} Hkv{HKV} Sq1 Sk{DEC_SK} bits{BITS}",
         "ms_per_launch": ms_attn,
         "key_heads_per_s": key_heads / (ms_attn * 1e-3),
         "roofline": {
-            "kernel": "tq::decode_attn_i8_kernel<2, 2> + tq::decode_merge_kernel<128>",
+            "kernel": "tq::decode_attn_i8_kernel<2, 2, false> + tq::decode_merge_kernel<128>",
             "bound": "hbm", "achieved": gbs_a, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": gbs_a / HBM_PEAK_GBS, "traffic": measured_traffic("decode_attention (attention + merge)"),
             "algorithmic_bytes_per_launch": attn_bytes,
         },
     }
-    del caches, scores, outs, ws
+    del caches, scores, outs, ws, api_rot, api_proj
     torch.cuda.empty_cache()
     return scores_leg, attn_leg
+
+
+def hbm_ceiling_leg(steps: int, warmup: int) -> dict:
+    """What the memory system delivers to a kernel that only streams, measured in the same run as
+    the headline (csrc/tq_probe.hip: non-temporal 16-byte loads and stores, as the decode kernels
+    issue them): read-only over the headline's 218 MB of key planes, write-only over its 67 MB of
+    scores, and the two mixed 13 KiB : 4 KiB per wave as the scores kernel mixes them; each over
+    DEC_ROT rotating buffers, the best of three grid sizes."""
+    import torch
+
+    from turboquant_pytorch import _native
+
+    path = os.path.join(os.path.dirname(_native.library_path()), "libtq_probe.so")
+    probe = ctypes.CDLL(path)
+    probe.tq_probe_stream.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
+                                      ctypes.c_int32, ctypes.c_void_p]
+    probe.tq_probe_unit_bytes.restype = ctypes.c_int64
+    probe.tq_probe_unit_bytes.argtypes = [ctypes.c_int32, ctypes.c_int32]
+    read_total = DEC_B * HKV * DEC_SK * key_rec_bytes(BITS, D)
+    write_total = DEC_B * HQ * DEC_SK * 4
+    stream = torch.cuda.current_stream().cuda_stream
+    out = {}
+    for name, mode, units in (("read_only", 0, read_total // probe.tq_probe_unit_bytes(0, 0)),
+                              ("write_only", 1, write_total // probe.tq_probe_unit_bytes(1, 1)),
+                              ("mix_13_4", 2, read_total // probe.tq_probe_unit_bytes(2, 0))):
+        rb, wb = units * probe.tq_probe_unit_bytes(mode, 0), units * probe.tq_probe_unit_bytes(mode, 1)
+        srcs = [torch.empty(max(rb, 16), dtype=torch.uint8, device="cuda").fill_(i + 1) for i in range(DEC_ROT)]
+        dsts = [torch.empty(max(wb, 4096), dtype=torch.uint8, device="cuda") for _ in range(DEC_ROT)]
+        best = None
+        for blocks in (1024, 2048, 4096):
+            def launch(i):
+                return probe.tq_probe_stream(srcs[i % DEC_ROT].data_ptr(), dsts[i % DEC_ROT].data_ptr(), units,
+                                             mode, blocks, stream)
+            settle_clock(launch, SETTLE_MS / 4)
+            for i in range(warmup):
+                _native.check(launch(i), "probe warmup")
+            torch.cuda.synchronize()
+            for i in range(LEAD):
+                _native.check(launch(i), "probe lead-in")
+            e0, e1 = _events(2)
+            e0.record()
+            for i in range(steps):
+                _native.check(launch(i), "probe")
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) / steps * 1e3
+            if best is None or us < best[0]:
+                best = (us, blocks)
+        us, blocks = best
+        gbs = (rb + wb) / (us * 1e-6) / 1e9
+        out[name] = {"read_bytes": rb, "write_bytes": wb, "us_per_launch": us, "gbs": gbs,
+                     "frac_of_peak": gbs / HBM_PEAK_GBS, "blocks": blocks}
+        del srcs, dsts
+    torch.cuda.empty_cache()
+    return out
 
 
 def compress_leg(kc, vc, steps: int, warmup: int) -> dict:
@@ -329,12 +507,16 @@ def compress_leg(kc, vc, steps: int, warmup: int) -> dict:
         for _ in range(warmup):
             fn(x)
         torch.cuda.synchronize()
+        for _ in range(2):  # lead-in: the stream is busy when the start event is recorded
+            fn(x)
+        REGIONS.resume()
         e0, e1 = _events(2)
         e0.record()
         for _ in range(steps):
             fn(x)
         e1.record()
         torch.cuda.synchronize()
+        REGIONS.pause()
         us = e0.elapsed_time(e1) / steps * 1e3
         gbs = rows * (2 * D + rec) / (us * 1e-6) / 1e9
         tflops = rows * passes * 2 * D * D / (us * 1e-6) / 1e12
@@ -371,6 +553,7 @@ def decode_step_leg(kc, vc, cached: int = 4096, steps: int = 200) -> dict:
     for _ in range(20):
         step()
     torch.cuda.synchronize()
+    REGIONS.resume()
     e0, e1 = _events(2)
     t0 = time.perf_counter()
     e0.record()
@@ -379,6 +562,7 @@ def decode_step_leg(kc, vc, cached: int = 4096, steps: int = 200) -> dict:
     e1.record()
     torch.cuda.synchronize()
     host_us = (time.perf_counter() - t0) / steps * 1e6
+    REGIONS.pause()
     return {"workload": f"B1 Hq{HQ} Hkv{HKV} d{D} bits{BITS}, {cached} cached tokens, one new token per step",
             "host_us_per_step": host_us, "device_us_per_step": e0.elapsed_time(e1) / steps * 1e3}
 
@@ -412,11 +596,14 @@ def prefill_leg(kc, vc, q, k, v, steps: int, warmup: int) -> dict:
     for _ in range(warmup):
         step(False)
     torch.cuda.synchronize()
+    step(False)  # lead-in: the stream is busy when the first timed step's events are recorded
+    REGIONS.resume()
     t0 = time.perf_counter()
     for _ in range(steps):
         step(True)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    REGIONS.pause()
     compress_ms = sum(m[0].elapsed_time(m[1]) for m in marks) / len(marks)
     prep_ms = sum(m[1].elapsed_time(m[2]) for m in marks) / len(marks)
     attn_ms = sum(m[2].elapsed_time(m[3]) for m in marks) / len(marks)
@@ -451,11 +638,20 @@ def main() -> None:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-prefill", action="store_true", help="skip the causal prefill / compress leg")
+    ap.add_argument("--no-ceiling", action="store_true", help="skip the HBM stream-ceiling leg")
     ap.add_argument("--compress-only", action="store_true",
                     help="run only the north-star compression leg (1M key + 1M value rows) and print its record")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="run one device-to-device copy of MIB MiB first (PMC byte-counter calibration)")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="CSV",
+                    help="summarise rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE counter CSVs of a bench run "
+                         "(with --calibrate-copy) into the traffic record; no GPU work")
+    ap.add_argument("--copy-mib", type=int, default=256, help="size of the calibration copy in those CSVs")
     args = ap.parse_args()
+    if args.pmc_summary:
+        print(json.dumps(pmc_summary(args.pmc_summary, args.copy_mib), indent=1))
+        return
+    REGIONS.pause()  # a profiler collects only the timed regions from here on
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "multi-GPU runs are not part of it.", file=sys.stderr)
@@ -481,8 +677,10 @@ def main() -> None:
         src = torch.ones(n, device=dev)
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
+        REGIONS.resume()
         dst.copy_(src)
         torch.cuda.synchronize()
+        REGIONS.pause()
         del src, dst
 
     if args.compress_only:
@@ -490,6 +688,11 @@ def main() -> None:
         return
 
     scores_leg, attn_leg = decode_legs(kc, vc, outliers, args.steps, args.warmup)
+    ceiling = None if args.no_ceiling else hbm_ceiling_leg(args.steps, args.warmup)
+    if ceiling is not None:
+        mix = ceiling["mix_13_4"]["gbs"]
+        ceiling["scores_kernel_of_mix"] = scores_leg["roofline"]["achieved"] / mix
+        ceiling["api_step_of_mix"] = scores_leg["api_step"]["roofline"]["achieved"] / mix
     prefill = None if args.no_prefill else prefill_leg(kc, vc, q, k, v, args.steps, args.warmup)
 
     rec = {
@@ -503,7 +706,8 @@ def main() -> None:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16-mfma/f32-acc",
+        "dtype": ("int8-mfma bit-plane keys x 24-bit fixed-point queries (four int8 digits, exact int32 sums: "
+                  "f32-grade q_rot.C and q_proj), f32 scores"),
         "data": "synthetic (bf16 N(0,1) Q/K/V, 4 K channels x20 = randperm(128, seed 1)[:4]; seeds 0 and 2)",
         "config": {"workload": (f"north-star target: Llama-3-8B attention (Hq{HQ} Hkv{HKV} d{D} bits{BITS}) at "
                                 f"{DEC_SK // 1024}k context, decode-shaped scoring: 1 query row x {DEC_B} sequences x "
@@ -511,6 +715,8 @@ def main() -> None:
                    "global_batch": DEC_B, "seq_len": DEC_SK, "parallelism": "single-gpu",
                    "clock_settle_ms": SETTLE_MS},
         "roofline": scores_leg["roofline"],
+        "api_step": scores_leg["api_step"],
+        "hbm_ceiling": ceiling,
         "compress_tokens_per_s": None if prefill is None else prefill["compress_tokens_per_s"],
         "decode_attention": attn_leg,
         "prefill": prefill,
