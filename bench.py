@@ -47,12 +47,14 @@ HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
 
-class _ProfilerRegions:
-    """Brackets the timed steps for `rocprofv3 --selected-regions`, which collects only between
-    roctxProfilerResume(0) and roctxProfilerPause(0): a kernel trace of bench.py then holds the
-    timed launches of every leg and none of the clock-settling or warm-up launches, so its
-    per-kernel averages are those of the timed region.  Without the profiler the calls do
-    nothing; without the roctx library they are skipped."""
+class _TimedRanges:
+    """Names the timed steps for a profiler: each timed loop runs inside a roctx range
+    "timed:<leg>:<steps>" (roctxRangePushA / roctxRangePop).  A `rocprofv3 --kernel-trace
+    --marker-trace` run of bench.py then records those ranges beside the kernels, and
+    `bench.py --trace-summary` keeps, per range, the last <steps> dispatches of each kernel:
+    the timed launches only, without the clock-settling, warm-up and lead-in launches that
+    precede them.  Without the profiler the calls do nothing; without the roctx library they
+    are skipped."""
 
     def __init__(self):
         self._lib = None
@@ -62,17 +64,22 @@ class _ProfilerRegions:
                 break
             except OSError:
                 continue
-
-    def resume(self):
         if self._lib is not None:
-            self._lib.roctxProfilerResume(0)
+            self._lib.roctxRangePushA.argtypes = [ctypes.c_char_p]
+        self._open = False
 
-    def pause(self):
-        if self._lib is not None:
-            self._lib.roctxProfilerPause(0)
+    def push(self, leg: str, steps: int):
+        if self._lib is not None and not self._open:
+            self._lib.roctxRangePushA(f"timed:{leg}:{steps}".encode())
+            self._open = True
+
+    def pop(self):
+        if self._lib is not None and self._open:
+            self._lib.roctxRangePop()
+            self._open = False
 
 
-REGIONS = _ProfilerRegions()
+RANGES = _TimedRanges()
 
 
 def key_rec_bytes(bits: int, d: int) -> int:
@@ -149,6 +156,47 @@ def pmc_summary(paths: list[str], copy_mib: int) -> dict:
             "method": ("mean counter KiB per dispatch per (kernel, grid size); the largest grid per kernel; "
                        "traffic_bytes = (FETCH_SIZE * fetch_factor + WRITE_SIZE * write_factor) * 1024"),
             "kernels": kernels}
+
+
+def trace_summary(kernel_csv: str, marker_csv: str) -> str:
+    """Markdown table of the timed launches in a `rocprofv3 --kernel-trace --marker-trace` run of
+    bench.py: for every "timed:<leg>:<steps>" roctx range, the kernels that started and ended
+    inside it, grouped by (kernel, grid size), each group cut to its last <steps> dispatches (the
+    lead-in launches queued just before the range can still start inside it)."""
+    import csv
+
+    def short(name: str) -> str:
+        name = name[5:] if name.startswith("void ") else name
+        return name[:name.rfind("(")] if name.endswith(")") and "(" in name else name
+
+    ranges = []
+    with open(marker_csv, newline="") as f:
+        for r in csv.DictReader(f):
+            msg = next((r[c] for c in ("Function", "Message", "Name", "Operation") if r.get(c, "").startswith("timed:")),
+                       None)
+            if msg is None:
+                continue
+            _, leg, steps = msg.split(":")
+            ranges.append((leg, int(steps), int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    kernels = []
+    with open(kernel_csv, newline="") as f:
+        for r in csv.DictReader(f):
+            grid = int(r["Grid_Size"]) if "Grid_Size" in r else (
+                int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"]))
+            kernels.append((short(r["Kernel_Name"]), grid, int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    kernels.sort(key=lambda k: k[2])
+    lines = ["| timed range (steps) | kernel | grid (work-items) | launches | avg us | min us | max us |",
+             "|---|---|---|---|---|---|---|"]
+    for leg, steps, t0, t1 in sorted(ranges, key=lambda r: r[2]):
+        groups: dict = {}
+        for name, grid, k0, k1 in kernels:
+            if t0 <= k0 and k1 <= t1:
+                groups.setdefault((name, grid), []).append((k1 - k0) / 1e3)
+        for (name, grid), us in sorted(groups.items(), key=lambda g: -sum(g[1][-steps:])):
+            us = us[-steps:]
+            lines.append(f"| {leg} ({steps}) | `{name}` | {grid} | {len(us)} | {sum(us) / len(us):.1f} | "
+                         f"{min(us):.1f} | {max(us):.1f} |")
+    return "\n".join(lines)
 
 
 def host_cpu() -> dict:
@@ -362,7 +410,7 @@ def decode_legs(kc, vc, outliers, steps: int, warmup: int) -> tuple[dict, dict]:
             1.0 / math.sqrt(D), 1, None, 0, 0, 0, 0, o.data_ptr(), _native.TQ_BF16,
             o.stride(0), o.stride(2), o.stride(1), ws.data_ptr(), ws_bytes, stream)
 
-    def timed(launch):
+    def timed(launch, leg):
         settle_clock(launch)
         for i in range(warmup):
             _native.check(launch(i), "decode warmup")
@@ -372,7 +420,7 @@ def decode_legs(kc, vc, outliers, steps: int, warmup: int) -> tuple[dict, dict]:
         # back, not the host's latency to its first launch after an idle GPU
         for i in range(LEAD):
             _native.check(launch(i), "decode lead-in")
-        REGIONS.resume()
+        RANGES.push(leg, steps)
         e0, e1 = _events(2)
         e0.record()
         for i in range(steps):
@@ -381,12 +429,12 @@ def decode_legs(kc, vc, outliers, steps: int, warmup: int) -> tuple[dict, dict]:
                 _native.check(st, "decode launch")
         e1.record()
         torch.cuda.synchronize()
-        REGIONS.pause()
+        RANGES.pop()
         return e0.elapsed_time(e1) / steps
 
-    ms_scores = timed(launch_scores)
-    ms_api = timed(launch_api)
-    ms_attn = timed(launch_attn)
+    ms_scores = timed(launch_scores, "decode_scores")
+    ms_api = timed(launch_api, "api_step")
+    ms_attn = timed(launch_attn, "decode_attention")
     key_heads = DEC_B * HQ * DEC_SK
     q_bytes = DEC_B * HQ * D * (2 + 4)  # prepared queries read: f16 q_rot + f32 q_proj
     score_bytes = DEC_B * HKV * DEC_SK * key_rec_bytes(BITS, D) + key_heads * 4 + q_bytes
@@ -509,14 +557,14 @@ def compress_leg(kc, vc, steps: int, warmup: int) -> dict:
         torch.cuda.synchronize()
         for _ in range(2):  # lead-in: the stream is busy when the start event is recorded
             fn(x)
-        REGIONS.resume()
+        RANGES.push(f"compress_{name}", steps)
         e0, e1 = _events(2)
         e0.record()
         for _ in range(steps):
             fn(x)
         e1.record()
         torch.cuda.synchronize()
-        REGIONS.pause()
+        RANGES.pop()
         us = e0.elapsed_time(e1) / steps * 1e3
         gbs = rows * (2 * D + rec) / (us * 1e-6) / 1e9
         tflops = rows * passes * 2 * D * D / (us * 1e-6) / 1e12
@@ -553,7 +601,7 @@ def decode_step_leg(kc, vc, cached: int = 4096, steps: int = 200) -> dict:
     for _ in range(20):
         step()
     torch.cuda.synchronize()
-    REGIONS.resume()
+    RANGES.push("decode_step", steps)
     e0, e1 = _events(2)
     t0 = time.perf_counter()
     e0.record()
@@ -562,7 +610,7 @@ def decode_step_leg(kc, vc, cached: int = 4096, steps: int = 200) -> dict:
     e1.record()
     torch.cuda.synchronize()
     host_us = (time.perf_counter() - t0) / steps * 1e6
-    REGIONS.pause()
+    RANGES.pop()
     return {"workload": f"B1 Hq{HQ} Hkv{HKV} d{D} bits{BITS}, {cached} cached tokens, one new token per step",
             "host_us_per_step": host_us, "device_us_per_step": e0.elapsed_time(e1) / steps * 1e3}
 
@@ -597,13 +645,13 @@ def prefill_leg(kc, vc, q, k, v, steps: int, warmup: int) -> dict:
         step(False)
     torch.cuda.synchronize()
     step(False)  # lead-in: the stream is busy when the first timed step's events are recorded
-    REGIONS.resume()
+    RANGES.push("prefill", steps)
     t0 = time.perf_counter()
     for _ in range(steps):
         step(True)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    REGIONS.pause()
+    RANGES.pop()
     compress_ms = sum(m[0].elapsed_time(m[1]) for m in marks) / len(marks)
     prep_ms = sum(m[1].elapsed_time(m[2]) for m in marks) / len(marks)
     attn_ms = sum(m[2].elapsed_time(m[3]) for m in marks) / len(marks)
@@ -647,11 +695,16 @@ def main() -> None:
                     help="summarise rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE counter CSVs of a bench run "
                          "(with --calibrate-copy) into the traffic record; no GPU work")
     ap.add_argument("--copy-mib", type=int, default=256, help="size of the calibration copy in those CSVs")
+    ap.add_argument("--trace-summary", nargs=2, metavar=("KERNEL_CSV", "MARKER_CSV"),
+                    help="summarise the timed launches of a rocprofv3 --kernel-trace --marker-trace run of "
+                         "bench.py (kernel_trace.csv, marker_api_trace.csv); no GPU work")
     args = ap.parse_args()
+    if args.trace_summary:
+        print(trace_summary(*args.trace_summary))
+        return
     if args.pmc_summary:
         print(json.dumps(pmc_summary(args.pmc_summary, args.copy_mib), indent=1))
         return
-    REGIONS.pause()  # a profiler collects only the timed regions from here on
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "multi-GPU runs are not part of it.", file=sys.stderr)
@@ -677,10 +730,8 @@ def main() -> None:
         src = torch.ones(n, device=dev)
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
-        REGIONS.resume()
         dst.copy_(src)
         torch.cuda.synchronize()
-        REGIONS.pause()
         del src, dst
 
     if args.compress_only:
