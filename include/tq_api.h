@@ -42,7 +42,7 @@ enum tq_dtype { TQ_F32 = 0, TQ_F16 = 1, TQ_BF16 = 2 };
 enum tq_status {
   TQ_OK = 0,
   TQ_EINVAL = -1,      /* bad argument (shape, bits, alignment, null pointer) */
-  TQ_EUNSUPPORTED = -2,/* valid but not built (e.g. head_dim outside 32/64/128/256) */
+  TQ_EUNSUPPORTED = -2,/* valid but not built (e.g. head_dim not a multiple of 8 or above 256) */
   TQ_EHIP = -3         /* HIP runtime error at launch */
 };
 

@@ -39,9 +39,11 @@ def test_argument_validation_without_gpu():
     assert lib.tq_out_cols(128, 3) == 48 and lib.tq_out_cols(7, 3) == 3
     assert lib.tq_pack_bits(None, 4, 128, 128, 9, None, 144, None) == -1
     assert b"between 1 and 8" in lib.tq_last_error()
-    assert lib.tq_compress_keys(None, 0, 1, 1, 1, 96, 0, 0, 0, None, None, None, None, 2,
+    assert lib.tq_compress_keys(None, 0, 1, 1, 1, 100, 0, 0, 0, None, None, None, None, 2,
                                 None, None, None, None, None, None, None) == -2
-    assert b"head_dim 96" in lib.tq_last_error()
+    assert b"head_dim 100" in lib.tq_last_error()
+    assert lib.tq_compress_keys(None, 0, 1, 1, 1, 264, 0, 0, 0, None, None, None, None, 2,
+                                None, None, None, None, None, None, None) == -2
     assert lib.tq_attention_fwd(*([None] * 7), 5, None, None, None, 3, None, 1, 8, 8, 1, 1, 128, 0.0, 1.0, 0,
                                 None, 0, 0, 0, 0, None, 0, 0, 0, 0, None, 0, None) == -1
     assert b"key bits" in lib.tq_last_error()

@@ -1,12 +1,14 @@
 // Compressed-domain attention on gfx950: asymmetric scores from packed keys,
-// online softmax, and P.V over packed values, in one kernel.
+// online softmax, and P.V over packed values, in one kernel.  This tiled kernel
+// serves every head dim that is a multiple of 8 up to 256 (the prefill and
+// split-K decode kernels cover head_dim 128 at their shapes).
 //
 // Scores follow the reference estimator (kernels/attention.py:380-461,
 // compressors.py:178-200):
 //   s(q, k) = vn_k * <q_rot, Ck[codes_k]> + coeff * rn_k * <q_proj, 2*sign_k - 1>
-// with q_rot = f16(q Pi^T) and q_proj = q_rot S_eff^T (f32) from tq_query_prep; scores
-// mode takes q_proj as f16 hi + lo (two MFMAs against the exact +-1 operand), attention
-// mode its f16 rounding.
+// with q_rot = f16(q Pi^T) and q_proj = q_rot S_eff^T (f32) from tq_query_prep;
+// q_proj enters as f16 hi + lo (two MFMAs against the exact +-1 operand, ~2^-22
+// of f32), as the reference keeps it in fp32 (attention.py:158-167).
 // Both inner products run as v_mfma_f32_16x16x32_f16 chains with exact f16
 // key operands (f16 centroids, +-1), so term 1 is exactly the reference's f32
 // accumulation of f16 products; the per-key factors vn and coeff * rn are
@@ -16,13 +18,13 @@
 // (query row, query head) columns -- all G = Hq/Hkv heads of the group share
 // each key tile (the reference expands K/V with repeat_interleave instead,
 // families/qwen2.py:101-102).  Key tiles of KT keys are streamed through LDS
-// as raw packed planes (software pipelined: the next tile's planes are loaded
-// into registers while the current tile computes).  Key and sign MFMA operands
-// are fetched straight from byte -> 8 x f16 lookup tables indexed by the packed
-// bytes (no decode pass); 3-bit keys and the values are decoded once per tile
-// into LDS.  S^T's accumulator layout (4 consecutive keys of one column per
-// lane) is the B-operand layout P^T needs for O^T += V^T P^T, so P stays in
-// registers.  Values stay in the rotated domain:
+// as raw packed byte streams (rows of d*b/8 bytes; software pipelined: the next
+// tile's planes are loaded into registers while the current tile computes) and
+// decoded once per tile into f16 K^, sign and V^T tiles through byte-indexed
+// lookup tables.  Head dims are padded to a multiple of 32 with zeros.  S^T's
+// accumulator layout (4 consecutive keys of one column per lane) is the
+// B-operand layout P^T needs for O^T += V^T P^T, so P stays in registers.
+// Values stay in the rotated domain:
 // O = (sum_j p_j vn_j Cv[c_j]) Pi_v, with Pi_v applied once per output row.
 // P enters the P.V product as an f16 (hi, lo) pair, so the only f16 rounding
 // on the value side is that of the decoded V^ = f16(Cv * vn).
@@ -33,38 +35,45 @@
 namespace tq {
 
 constexpr int kAttnWaves = 4;      // waves per block
-constexpr int kAttnColBlocks = 2;  // 16-column blocks per wave (head_dim <= 128)
 constexpr int kAttnKeys = 32;      // keys per tile
 constexpr float kAttnTau = 8.0f;   // lazy-rescale headroom of the online softmax (log2 units)
 
-template <int D>
+// D is the head dim padded to a multiple of 32 (the MFMA k-step); the real head dim d
+// (a multiple of 8) comes at run time.  Query fragments, decoded key / sign / value tiles
+// and Pi_v read zero past d, so the padding adds nothing to any product.
+template <int D, bool SCORES>
 struct ATile {
   static constexpr int NW = kAttnWaves;          // waves per block
-  static constexpr int NT = 64 * NW;                // threads per block
-  static constexpr int KT = kAttnKeys;             // keys per tile
-  static constexpr int NBW = (D == 256) ? 1 : kAttnColBlocks;
-  static constexpr int BR = NW * 16 * NBW;          // (query, head) columns per block
-  static constexpr int KS = D / 32;                 // k-steps of the score MFMAs
-  static constexpr int MBK = KT / 16;               // 16-key blocks per tile
-  static constexpr int DB = D / 16;                 // 16-dim blocks
-  static constexpr int LDK = D + 8;                 // f16 row stride of decoded key / sign tiles
-  static constexpr int LDV = KT + 8;                // f16 row stride of the V^T tile
-  static constexpr int SCP = D / 8 + 4;             // padded raw sign row (bytes)
-  static constexpr int VCP_MAX = D * 4 / 8 + 4;     // padded raw value-code row, <= 4 bits
-  static constexpr int KREG = (KT * D * 3 / 32 + NT - 1) / NT;  // per-thread dwords of a tile
-  static constexpr int SREG = (KT * D / 32 + NT - 1) / NT;
-  static constexpr int VREG = (KT * D * 4 / 32 + NT - 1) / NT;
+  static constexpr int NT = 64 * NW;             // threads per block
+  static constexpr int KT = kAttnKeys;           // keys per tile
+  // 16-column blocks per wave: two where the q_rot / q_proj (hi, lo) fragments and, in
+  // attention mode, the O^T accumulators of both fit in registers
+  static constexpr int NBW = SCORES ? (D <= 128 ? 2 : 1) : (D <= 64 ? 2 : 1);
+  static constexpr int BR = NW * 16 * NBW;       // (query, head) columns per block
+  static constexpr int KS = D / 32;              // k-steps of the score MFMAs
+  static constexpr int MBK = KT / 16;            // 16-key blocks per tile
+  static constexpr int DB = D / 16;              // 16-dim blocks
+  static constexpr int LDK = D + 8;              // f16 row stride of decoded key / sign tiles
+  static constexpr int LDV = KT + 8;             // f16 row stride of the V^T tile
+  // raw planes of a tile as a byte stream (rows of d*b/8 bytes, not dword aligned in
+  // general), staged from the dword-aligned address at or below the tile's first byte;
+  // 8 bytes of slack cover that shift and the dword-pair reads of the last row
+  static constexpr int KRAW = KT * D * 3 / 8 + 8, SRAW = KT * D / 8 + 8, VRAW = KT * D * 4 / 8 + 8;
+  static constexpr int KREG = (KRAW / 4 + NT - 1) / NT;  // per-thread dwords of a tile
+  static constexpr int SREG = (SRAW / 4 + NT - 1) / NT;
+  static constexpr int VREG = (VRAW / 4 + NT - 1) / NT;
 };
 
 struct AttnArgs {
   const uint16_t* q_rot;
-  const float* q_proj;  // f32: f16 hi + lo operands in scores mode, the f16 rounding otherwise
+  const float* q_proj;  // f32, taken as f16 hi + lo operands (two MFMAs against the exact +-1 signs)
   const uint8_t *kcodes, *ksigns;
   const uint16_t *krn, *kvn, *kcent;
   const uint8_t* vcodes;
   const uint16_t *vvn, *vpit;
   const float* vcent32;
   int vb;
+  int d;  // head dim (multiple of 8, <= D)
   int B, Hq, Hkv, Sq, Sk, G, QT, nqb;
   int64_t ldk;  // rows between consecutive (batch, kv head) planes (>= Sk)
   float coeff, scale;
@@ -81,36 +90,32 @@ __device__ __forceinline__ half8 cat8(half4 a, half4 b) {
   return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
-// 32 bits of a packed row starting at byte `off` (row base 4-byte aligned, one
-// readable dword past the last code byte).
-__device__ __forceinline__ uint32_t bits32_at(const uint8_t* row, int off) {
-  const uint32_t* w = reinterpret_cast<const uint32_t*>(row + (off & ~3));
-  const int sh = off & 3;
-  if (sh == 0) return w[0];
-  return __builtin_amdgcn_alignbyte(w[1], w[0], sh);
+// 32 bits of a byte stream from byte `off` on (base 4-byte aligned, one readable dword
+// past the dword holding byte off + 3).
+__device__ __forceinline__ uint32_t bits32_at(const uint8_t* base, int off) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(base + (off & ~3));
+  return __builtin_amdgcn_alignbyte(w[1], w[0], off & 3);
 }
 
 template <int DT>
-__device__ __forceinline__ void store4(void* out, int64_t o, float4v v) {
+__device__ __forceinline__ void store4(void* out, int64_t o, float4v v, int n) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) store_act<DT>(out, o + e, v[e]);
+  for (int e = 0; e < 4; ++e)
+    if (e < n) store_act<DT>(out, o + e, v[e]);
 }
 
 template <int D, int KB, bool SCORES, bool MASK>
 __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
-  using T = ATile<D>;
+  using T = ATile<D, SCORES>;
   constexpr int KT = T::KT, NBW = T::NBW, KS = T::KS, MBK = T::MBK, DB = T::DB, NT = T::NT;
-  constexpr int KC = D * KB / 8;          // key code bytes per row
-  constexpr int KCP = KC + 4;             // padded
-  constexpr int SC = D / 8;
   constexpr int LUTK_W = (KB == 1) ? 8 : 4;  // f16 values per key-LUT entry (KB <= 2)
   constexpr int KITEMS = KT * (D / 8);       // (key, 8-dim group) decode items
   constexpr int VITEMS = (D / 8) * (KT / 4);  // (8-dim group, 4-key quad) decode items
 
-  // double-buffered raw planes, decoded tiles, lookup tables
-  __shared__ __attribute__((aligned(16))) uint8_t rawK[2][KT * KCP];
-  __shared__ __attribute__((aligned(16))) uint8_t rawS[2][KT * T::SCP];
-  __shared__ __attribute__((aligned(16))) uint8_t rawV[SCORES ? 1 : 2][SCORES ? 4 : KT * T::VCP_MAX];
+  // double-buffered raw planes (byte streams), decoded tiles, lookup tables
+  __shared__ __attribute__((aligned(16))) uint8_t rawK[2][T::KRAW];
+  __shared__ __attribute__((aligned(16))) uint8_t rawS[2][T::SRAW];
+  __shared__ __attribute__((aligned(16))) uint8_t rawV[SCORES ? 1 : 2][SCORES ? 4 : T::VRAW];
   __shared__ __attribute__((aligned(16))) float skA[2][KT];      // vn * scale * log2(e)
   __shared__ __attribute__((aligned(16))) float skB[2][KT];      // coeff * rn * scale * log2(e)
   __shared__ __attribute__((aligned(16))) float svv[2][KT];      // value norms
@@ -126,7 +131,9 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
   const int qblk = a.nqb - 1 - static_cast<int>(blockIdx.x);  // heavy causal blocks first
   const int hkv = blockIdx.y, b = blockIdx.z;
   const int q0 = qblk * a.QT;
-  const int vc = D * a.vb / 8, vcp = vc + 4;
+  const int d = a.d;
+  const int KC = d * KB / 8, SC = d / 8, vc = d * a.vb / 8;  // bytes per packed row
+  const int ng = d / 8;                                       // real 8-dim groups
   const int64_t bh_kv = static_cast<int64_t>(b) * a.Hkv + hkv;
 
   // ---- lookup tables: byte -> 8 x (+-1); byte -> key centroids; value centroids (f32)
@@ -144,11 +151,10 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
     if (!SCORES && tid < (1 << a.vb)) lutV[tid] = a.vcent32[tid];
   }
 
-  // ---- this lane's columns and their q fragments (B operands)
+  // ---- this lane's columns and their q fragments (B operands): q_rot, q_proj hi and lo
   int col_i[NBW], col_h[NBW];
   bool col_ok[NBW];
-  half8 qr[KS][NBW], qp[KS][NBW];
-  [[maybe_unused]] half8 qlo[SCORES ? KS : 1][NBW];  // scores mode: lo parts of q_proj
+  half8 qr[KS][NBW], qp[KS][NBW], qlo[KS][NBW];
 #pragma unroll
   for (int nb = 0; nb < NBW; ++nb) {
     const int r = (wave * NBW + nb) * 16 + l16;
@@ -156,15 +162,16 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
     col_i[nb] = q0 + ql;
     col_h[nb] = hkv * a.G + gi;
     col_ok[nb] = (ql < a.QT) && (col_i[nb] < a.Sq);
-    const int64_t qrow = ((static_cast<int64_t>(b) * a.Hq + col_h[nb]) * a.Sq + col_i[nb]) * D;
+    const int64_t qrow = ((static_cast<int64_t>(b) * a.Hq + col_h[nb]) * a.Sq + col_i[nb]) * d;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int d0 = ks * 32 + lg * 8;
-      qr[ks][nb] = col_ok[nb] ? *reinterpret_cast<const half8*>(a.q_rot + qrow + d0) : half8{};
+      const bool ok = col_ok[nb] && d0 < d;  // d % 8 == 0: the 8 dims from d0 are all real or all padding
+      qr[ks][nb] = ok ? *reinterpret_cast<const half8*>(a.q_rot + qrow + d0) : half8{};
       half8 hi = half8{}, lo = half8{};
-      if (col_ok[nb]) split8(a.q_proj + qrow + d0, hi, lo);
+      if (ok) split8(a.q_proj + qrow + d0, hi, lo);
       qp[ks][nb] = hi;
-      if constexpr (SCORES) qlo[ks][nb] = lo;
+      qlo[ks][nb] = lo;
     }
   }
 
@@ -179,31 +186,30 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
   constexpr float LOG2E = 1.4426950408889634f;
   const float fa = SCORES ? 1.f : a.scale * LOG2E;  // scores kept in log2 units
 
-  // ---- register staging of one tile's planes
+  // byte offset of tile k0's first row in a plane of `rowbytes`-byte rows, and that byte's
+  // position within its dword (the staged stream starts at the dword)
+  auto plane_off = [&](int k0, int rowbytes) { return (bh_kv * a.ldk + k0) * rowbytes; };
+  auto shift_of = [&](const uint8_t* plane, int k0, int rowbytes) {
+    return static_cast<int>((reinterpret_cast<uintptr_t>(plane) + plane_off(k0, rowbytes)) & 3);
+  };
+
+  // ---- register staging of one tile's planes: dwords from the aligned start on
   uint32_t rk[T::KREG], rs[T::SREG], rv[SCORES ? 1 : T::VREG];
   float r_a = 0.f, r_b = 0.f, r_v = 0.f;
+  auto fetch_stream = [&](const uint8_t* plane, int k0, int rowbytes, int bytes, uint32_t* regs, int nreg) {
+    const int shift = shift_of(plane, k0, rowbytes);
+    const uint32_t* g = reinterpret_cast<const uint32_t*>(plane + (plane_off(k0, rowbytes) - shift));
+    const int ndw = (shift + bytes + 3) >> 2;  // dwords holding the tile's bytes
+    for (int j = 0; j < nreg; ++j) {
+      const int w = tid + j * NT;
+      regs[j] = (w < ndw) ? g[w] : 0u;
+    }
+  };
   auto fetch = [&](int k0) {
     const int nk = min(KT, a.Sk - k0);
-    const uint32_t* gk = reinterpret_cast<const uint32_t*>(a.kcodes + (bh_kv * a.ldk + k0) * KC);
-    const uint32_t* gs = reinterpret_cast<const uint32_t*>(a.ksigns + (bh_kv * a.ldk + k0) * SC);
-#pragma unroll
-    for (int j = 0; j < T::KREG; ++j) {
-      const int w = tid + j * NT;
-      rk[j] = (w < nk * KC / 4) ? gk[w] : 0u;
-    }
-#pragma unroll
-    for (int j = 0; j < T::SREG; ++j) {
-      const int w = tid + j * NT;
-      rs[j] = (w < nk * SC / 4) ? gs[w] : 0u;
-    }
-    if constexpr (!SCORES) {
-      const uint32_t* gv = reinterpret_cast<const uint32_t*>(a.vcodes + (bh_kv * a.ldk + k0) * vc);
-#pragma unroll
-      for (int j = 0; j < T::VREG; ++j) {
-        const int w = tid + j * NT;
-        rv[j] = (w < nk * vc / 4) ? gv[w] : 0u;
-      }
-    }
+    fetch_stream(a.kcodes, k0, KC, nk * KC, rk, T::KREG);
+    fetch_stream(a.ksigns, k0, SC, nk * SC, rs, T::SREG);
+    if constexpr (!SCORES) fetch_stream(a.vcodes, k0, vc, nk * vc, rv, T::VREG);
     if (tid < KT) {
       const int64_t kr = bh_kv * a.ldk + k0 + tid;
       const bool ok = tid < nk;
@@ -218,27 +224,18 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int j = 0; j < T::KREG; ++j) {
       const int w = tid + j * NT;
-      if (w < KT * KC / 4) {
-        const int row = w / (KC / 4), col = w % (KC / 4);
-        *reinterpret_cast<uint32_t*>(&rawK[buf][row * KCP + col * 4]) = rk[j];
-      }
+      if (w < T::KRAW / 4) reinterpret_cast<uint32_t*>(rawK[buf])[w] = rk[j];
     }
 #pragma unroll
     for (int j = 0; j < T::SREG; ++j) {
       const int w = tid + j * NT;
-      if (w < KT * SC / 4) {
-        const int row = w / (SC / 4), col = w % (SC / 4);
-        *reinterpret_cast<uint32_t*>(&rawS[buf][row * T::SCP + col * 4]) = rs[j];
-      }
+      if (w < T::SRAW / 4) reinterpret_cast<uint32_t*>(rawS[buf])[w] = rs[j];
     }
     if constexpr (!SCORES) {
 #pragma unroll
       for (int j = 0; j < T::VREG; ++j) {
         const int w = tid + j * NT;
-        if (w < KT * vc / 4) {
-          const int row = w / (vc / 4), col = w % (vc / 4);
-          *reinterpret_cast<uint32_t*>(&rawV[buf][row * vcp + col * 4]) = rv[j];
-        }
+        if (w < T::VRAW / 4) reinterpret_cast<uint32_t*>(rawV[buf])[w] = rv[j];
       }
     }
     if (tid < KT) {
@@ -267,32 +264,38 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
   int cur = 0;
   for (int k0 = 0; k0 < kend; k0 += KT) {
     __syncthreads();  // tile k0 staged in buffer `cur`; previous tile's decoded tiles consumed
-    // ---- decode this tile once per block: K^ and sign tiles [key][dim], V^T [dim][key]
+    // ---- decode this tile once per block: K^ and sign tiles [key][dim], V^T [dim][key];
+    // groups past d decode to zeros
+    const int shk = shift_of(a.kcodes, k0, KC);
+    const int shs = shift_of(a.ksigns, k0, SC);
 #pragma unroll
     for (int j = 0; j < (KITEMS + NT - 1) / NT; ++j) {
       const int it = tid + j * NT;
       if (KITEMS % NT == 0 || it < KITEMS) {
         const int key = it / (D / 8), dg = it % (D / 8);
-        half8 kv;
-        if constexpr (KB == 1) {
-          kv = *reinterpret_cast<const half8*>(&lutK[rawK[cur][key * KCP + dg] * 8]);
-        } else if constexpr (KB == 2) {
-          const uint32_t two = *reinterpret_cast<const uint16_t*>(&rawK[cur][key * KCP + dg * 2]);
-          kv = cat8(*reinterpret_cast<const half4*>(&lutK[(two & 0xffu) * 4]),
-                    *reinterpret_cast<const half4*>(&lutK[(two >> 8) * 4]));
-        } else {
-          const uint32_t w = bits32_at(&rawK[cur][key * KCP], dg * 3);
+        half8 kv = half8{}, sv = half8{};
+        if (dg < ng) {
+          const int ko = shk + key * KC + dg * KB;  // the group's KB bytes
+          if constexpr (KB == 1) {
+            kv = *reinterpret_cast<const half8*>(&lutK[rawK[cur][ko] * 8]);
+          } else if constexpr (KB == 2) {
+            kv = cat8(*reinterpret_cast<const half4*>(&lutK[rawK[cur][ko] * 4]),
+                      *reinterpret_cast<const half4*>(&lutK[rawK[cur][ko + 1] * 4]));
+          } else {
+            const uint32_t w = bits32_at(rawK[cur], ko);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) kv[e] = lutK[(w >> (e * 3)) & 7u];
+            for (int e = 0; e < 8; ++e) kv[e] = lutK[(w >> (e * 3)) & 7u];
+          }
+          sv = *reinterpret_cast<const half8*>(&lutS[rawS[cur][shs + key * SC + dg] * 8]);
         }
         *reinterpret_cast<half8*>(&sK[key * T::LDK + dg * 8]) = kv;
-        *reinterpret_cast<half8*>(&sS[key * T::LDK + dg * 8]) =
-            *reinterpret_cast<const half8*>(&lutS[rawS[cur][key * T::SCP + dg] * 8]);
+        *reinterpret_cast<half8*>(&sS[key * T::LDK + dg * 8]) = sv;
       }
     }
     if constexpr (!SCORES) {
       // V^ = f16(Cv[code] * vn_v); item = (8-dim group dg, 4-key quad kq)
       const uint32_t mv = (1u << a.vb) - 1u;
+      const int shv = shift_of(a.vcodes, k0, vc);
 #pragma unroll
       for (int j = 0; j < (VITEMS + NT - 1) / NT; ++j) {
         const int it = tid + j * NT;
@@ -302,10 +305,11 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
           half4 col[8];
 #pragma unroll
           for (int kk = 0; kk < 4; ++kk) {
-            const uint32_t w = bits32_at(&rawV[cur][(kq * 4 + kk) * vcp], dg * a.vb);
+            const uint32_t w = dg < ng ? bits32_at(rawV[cur], shv + (kq * 4 + kk) * vc + dg * a.vb) : 0u;
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-              col[e][kk] = static_cast<_Float16>(lutV[(w >> (e * a.vb)) & mv] * vn4[kk]);
+              col[e][kk] = dg < ng ? static_cast<_Float16>(lutV[(w >> (e * a.vb)) & mv] * vn4[kk])
+                                   : static_cast<_Float16>(0.f);
           }
 #pragma unroll
           for (int e = 0; e < 8; ++e)
@@ -317,7 +321,7 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
     if (more) fetch(k0 + KT);  // global loads in flight during this tile's math
     __syncthreads();
 
-    // ---- S^T = K^ Q_rot^T (term 1) and Sign Q_proj^T (term 2)
+    // ---- S^T = K^ Q_rot^T (term 1) and Sign (Q_proj hi + lo)^T (term 2)
     float4v sacc[MBK][NBW], tacc[MBK][NBW];
 #pragma unroll
     for (int mb = 0; mb < MBK; ++mb)
@@ -337,7 +341,7 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
         for (int nb = 0; nb < NBW; ++nb) {
           sacc[mb][nb] = mfma16x16x32(ka, qr[ks][nb], sacc[mb][nb]);
           tacc[mb][nb] = mfma16x16x32(sa, qp[ks][nb], tacc[mb][nb]);
-          if constexpr (SCORES) tacc[mb][nb] = mfma16x16x32(sa, qlo[ks][nb], tacc[mb][nb]);
+          tacc[mb][nb] = mfma16x16x32(sa, qlo[ks][nb], tacc[mb][nb]);
         }
       }
     }
@@ -436,9 +440,10 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
   }
 
   if constexpr (!SCORES) {
-    // ---- normalise and rotate back: out = (O^T / l)^T Pi_v, Pi_v^T as A operand
+    // ---- normalise and rotate back: out = (O^T / l)^T Pi_v, Pi_v^T [2][d][d] as A operand
+    // (rows and columns past d read as zero)
     const half4* Ph = reinterpret_cast<const half4*>(a.vpit);
-    const half4* Pl = reinterpret_cast<const half4*>(a.vpit + D * D);
+    const half4* Pl = reinterpret_cast<const half4*>(a.vpit + static_cast<int64_t>(d) * d);
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb) {
       float l = l_run[nb];
@@ -478,19 +483,25 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int c = 0; c < DB / 2; ++c) {
           const int j0 = c * 32 + lg * 4;
-          const half8 ah = cat8(Ph[(i * D + j0) / 4], Ph[(i * D + j0 + 16) / 4]);
-          const half8 al = cat8(Pl[(i * D + j0) / 4], Pl[(i * D + j0 + 16) / 4]);
+          // d % 8 == 0: each 4-column run is all real or all padding
+          const bool r0 = i < d && j0 < d, r1 = i < d && j0 + 16 < d;
+          const int64_t p0 = (static_cast<int64_t>(i) * d + j0) / 4, p1 = (static_cast<int64_t>(i) * d + j0 + 16) / 4;
+          const half4 z = half4{};
+          const half8 ah = cat8(r0 ? Ph[p0] : z, r1 ? Ph[p1] : z);
+          const half8 al = cat8(r0 ? Pl[p0] : z, r1 ? Pl[p1] : z);
           f = mfma16x16x32(ah, bh[c], f);
           f = mfma16x16x32(al, bh[c], f);
           f = mfma16x16x32(ah, bl[c], f);
         }
-        if (col_ok[nb]) {
+        const int c0 = ib * 16 + lg * 4;
+        if (col_ok[nb] && c0 < d) {
           const int64_t o = static_cast<int64_t>(b) * a.sob + static_cast<int64_t>(h) * a.soh +
-                            static_cast<int64_t>(qi) * a.sos + ib * 16 + lg * 4;
+                            static_cast<int64_t>(qi) * a.sos + c0;
           const float4v fo = f * down;
-          if (a.out_dtype == TQ_BF16) store4<TQ_BF16>(a.out, o, fo);
-          else if (a.out_dtype == TQ_F16) store4<TQ_F16>(a.out, o, fo);
-          else store4<TQ_F32>(a.out, o, fo);
+          const int n = min(4, d - c0);
+          if (a.out_dtype == TQ_BF16) store4<TQ_BF16>(a.out, o, fo, n);
+          else if (a.out_dtype == TQ_F16) store4<TQ_F16>(a.out, o, fo, n);
+          else store4<TQ_F32>(a.out, o, fo, n);
         }
       }
     }
@@ -500,31 +511,43 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
 template <int D, int KB, bool SCORES>
 static void launch_attn(const AttnArgs& a, hipStream_t s) {
   dim3 grid(a.nqb, a.Hkv, a.B);
-  if (!SCORES && a.mask) attn_kernel<D, KB, SCORES, !SCORES><<<grid, ATile<D>::NT, 0, s>>>(a);
-  else attn_kernel<D, KB, SCORES, false><<<grid, ATile<D>::NT, 0, s>>>(a);
+  if (!SCORES && a.mask) attn_kernel<D, KB, SCORES, !SCORES><<<grid, ATile<D, SCORES>::NT, 0, s>>>(a);
+  else attn_kernel<D, KB, SCORES, false><<<grid, ATile<D, SCORES>::NT, 0, s>>>(a);
 }
 
+// the tiled kernel for head dim d: D = d rounded up to a multiple of 32
 template <bool SCORES>
 static void dispatch_attn(int d, int kb, const AttnArgs& a, hipStream_t s) {
 #define TQ_KB_CASES(DD)                                 \
-  if (kb == 1) launch_attn<DD, 1, SCORES>(a, s);        \
-  else if (kb == 2) launch_attn<DD, 2, SCORES>(a, s);   \
-  else launch_attn<DD, 3, SCORES>(a, s);
-  switch (d) {
-    case 32: TQ_KB_CASES(32) break;
-    case 64: TQ_KB_CASES(64) break;
-    case 128: TQ_KB_CASES(128) break;
-    default: TQ_KB_CASES(256) break;
+  case DD:                                              \
+    if (kb == 1) launch_attn<DD, 1, SCORES>(a, s);      \
+    else if (kb == 2) launch_attn<DD, 2, SCORES>(a, s); \
+    else launch_attn<DD, 3, SCORES>(a, s);              \
+    break;
+  switch (pad_dim(d)) {
+    TQ_KB_CASES(32)
+    TQ_KB_CASES(64)
+    TQ_KB_CASES(96)
+    TQ_KB_CASES(128)
+    TQ_KB_CASES(160)
+    TQ_KB_CASES(192)
+    TQ_KB_CASES(224)
+    default: TQ_KB_CASES(256)
   }
 #undef TQ_KB_CASES
 }
 
-static int block_rows(int d) {
-  switch (d) {
-    case 32: return ATile<32>::BR;
-    case 64: return ATile<64>::BR;
-    case 128: return ATile<128>::BR;
-    default: return ATile<256>::BR;
+// (query row, query head) columns per block of the tiled kernel: the largest GQA group it serves
+static int block_rows(int d, bool scores) {
+  switch (pad_dim(d)) {
+    case 32: return scores ? ATile<32, true>::BR : ATile<32, false>::BR;
+    case 64: return scores ? ATile<64, true>::BR : ATile<64, false>::BR;
+    case 96: return scores ? ATile<96, true>::BR : ATile<96, false>::BR;
+    case 128: return scores ? ATile<128, true>::BR : ATile<128, false>::BR;
+    case 160: return scores ? ATile<160, true>::BR : ATile<160, false>::BR;
+    case 192: return scores ? ATile<192, true>::BR : ATile<192, false>::BR;
+    case 224: return scores ? ATile<224, true>::BR : ATile<224, false>::BR;
+    default: return scores ? ATile<256, true>::BR : ATile<256, false>::BR;
   }
 }
 
@@ -558,19 +581,25 @@ int decode_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, co
 static int check_common(const char* what, int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq, int32_t Sk,
                         int32_t d, int32_t bits) {
   if (!supported_dim(d)) {
-    set_error("%s: head_dim %d not built (supported: 32, 64, 128, 256)", what, (int)d);
+    set_error("%s: head_dim %d not supported (multiples of 8 from 8 to 256)", what, (int)d);
     return TQ_EUNSUPPORTED;
   }
   TQ_REQUIRE(bits >= 2 && bits <= 4, "%s: key bits must be in [2, 4], got %d", what, (int)bits);
   TQ_REQUIRE(B >= 0 && Hq >= 0 && Hkv >= 1 && Sq >= 0 && Sk >= 0, "%s: bad shape", what);
   TQ_REQUIRE(Hq % Hkv == 0, "%s: Hq=%d is not a multiple of Hkv=%d", what, (int)Hq, (int)Hkv);
-  TQ_REQUIRE(Hq / Hkv <= block_rows(d), "%s: group size %d exceeds %d", what, (int)(Hq / Hkv),
-             block_rows(d));
+  return TQ_OK;
+}
+
+// the tiled kernel serves GQA groups of at most block_rows(d, scores) query heads
+static int check_group(const char* what, int32_t Hq, int32_t Hkv, int32_t d, bool scores) {
+  TQ_REQUIRE(Hq / Hkv <= block_rows(d, scores), "%s: group size %d exceeds %d at head_dim %d", what,
+             (int)(Hq / Hkv), block_rows(d, scores), (int)d);
   return TQ_OK;
 }
 
 static void fill_common(AttnArgs& a, int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq, int32_t Sk, int64_t ldk,
-                        int32_t d) {
+                        int32_t d, bool scores) {
+  a.d = d;
   a.B = B;
   a.Hq = Hq;
   a.Hkv = Hkv;
@@ -578,7 +607,7 @@ static void fill_common(AttnArgs& a, int32_t B, int32_t Hq, int32_t Hkv, int32_t
   a.Sk = Sk;
   a.ldk = ldk;
   a.G = Hq / Hkv;
-  a.QT = block_rows(d) / a.G;
+  a.QT = block_rows(d, scores) / a.G;
   a.nqb = (Sq + a.QT - 1) / a.QT;
 }
 
@@ -604,6 +633,8 @@ int tq_attention_scores_kv(const uint16_t* q_rot, const float* q_proj, const uin
   if (decode_applies(B, Hq, Hkv, Sq, Sk, d, bits))
     return decode_scores(ldk, q_rot, q_proj, key_codes, key_signs, key_rn, key_vn, centroids_f16, B, Hq, Hkv,
                          Sq, Sk, d, bits, coeff, out, as_stream(stream));
+  st = check_group("tq_attention_scores", Hq, Hkv, d, true);
+  if (st != TQ_OK) return st;
   AttnArgs a{};
   a.q_rot = q_rot;
   a.q_proj = q_proj;
@@ -613,7 +644,7 @@ int tq_attention_scores_kv(const uint16_t* q_rot, const float* q_proj, const uin
   a.kvn = key_vn;
   a.kcent = centroids_f16;
   a.vb = 1;
-  fill_common(a, B, Hq, Hkv, Sq, Sk, ldk, d);
+  fill_common(a, B, Hq, Hkv, Sq, Sk, ldk, d, true);
   a.coeff = coeff;
   a.scale = 1.f;
   a.scores = out;
@@ -654,6 +685,8 @@ int tq_attention_fwd_kv(const uint16_t* q_rot, const float* q_proj, const uint8_
     return prefill_attention(ldk, q_rot, q_proj, key_codes, key_signs, key_rn, key_vn, key_centroids_f16, bits,
                              val_codes, val_vn, val_centroids, val_pit_split, B, Hq, Hkv, Sq, Sk, coeff, scale,
                              causal, mask, smb, smh, smq, smk, out, out_dtype, sob, soh, sos, as_stream(stream));
+  st = check_group("tq_attention_fwd", Hq, Hkv, d, false);
+  if (st != TQ_OK) return st;
   AttnArgs a{};
   a.q_rot = q_rot;
   a.q_proj = q_proj;
@@ -667,7 +700,7 @@ int tq_attention_fwd_kv(const uint16_t* q_rot, const float* q_proj, const uint8_
   a.vcent32 = val_centroids;
   a.vpit = val_pit_split;
   a.vb = val_bits;
-  fill_common(a, B, Hq, Hkv, Sq, Sk, ldk, d);
+  fill_common(a, B, Hq, Hkv, Sq, Sk, ldk, d, false);
   a.coeff = coeff;
   a.scale = scale;
   a.causal = causal;

@@ -24,7 +24,10 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 inline int64_t out_cols(int64_t d, int b) { return (d * b + 7) / 8; }
 
-inline bool supported_dim(int d) { return d == 32 || d == 64 || d == 128 || d == 256; }
+// Head dims with byte-aligned packed rows (d * b / 8 whole bytes for every bit width) up to 256;
+// the tile kernels run them at d rounded up to a multiple of 32 (pad_dim) with zero padding.
+inline bool supported_dim(int d) { return d >= 8 && d <= 256 && d % 8 == 0; }
+inline int pad_dim(int d) { return (d + 31) / 32 * 32; }
 
 // Blocks of `kernel` (launched with `threads` threads) resident on the whole current
 // device at once: occupancy per CU x CU count, cached per device in `cache[16]`.

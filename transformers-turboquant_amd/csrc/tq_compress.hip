@@ -28,9 +28,12 @@ typedef float float2v __attribute__((ext_vector_type(2)));
 
 namespace tq {
 
+// D is the head dim padded to a multiple of 32 (the MFMA k-step); a row's d <= D real
+// coordinates are followed by zeros in every LDS tile, and weight rows and columns past d
+// read as zero, so padded coordinates add nothing to any product.
 template <int D>
 struct CTile {
-  static constexpr int R = (D == 256) ? 16 : (D == 128 ? 32 : 64);  // rows per block tile
+  static constexpr int R = (D <= 64) ? 64 : (D <= 224 ? 32 : 16);  // rows per block tile
   static constexpr int LDA = D + 8;                                  // padded f32 row stride
   static constexpr int MB = D / 16, NB = R / 16, TPW = MB * NB / 4, KS = D / 32;
   static constexpr int NT = 256;
@@ -39,19 +42,19 @@ struct CTile {
 };
 
 // Z[row][j] = sum_i X[row][i] * W[j][i] for the R x D tile X (LDS, f32).
-// wsplit: f16 bits, [2][D][D] = (hi, lo) of kSplit*W.  xscale[row] multiplies
+// wsplit: f16 bits, [2][d][d] = (hi, lo) of kSplit*W (rows and columns past d read as 0).  xscale[row] multiplies
 // the row before it is split (it includes the factor kSplit).  Result left in
 // acc (times kSplit * xscale); tile t of this wave covers columns
 // j = mb*16 + 4*(lane/16) + 0..3 of row nb*16 + lane%16.
 template <int D, bool X_SPLIT, bool W_SPLIT>
 __device__ __forceinline__ void stage_gemm(const float* __restrict__ X, const float* __restrict__ xscale,
-                                           const uint16_t* __restrict__ wsplit,
+                                           const uint16_t* __restrict__ wsplit, int d,
                                            float4v (&acc)[CTile<D>::TPW]) {
   using T = CTile<D>;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g = lane >> 4;
   const half8* Wh = reinterpret_cast<const half8*>(wsplit);
-  const half8* Wl = reinterpret_cast<const half8*>(wsplit + D * D);
+  const half8* Wl = reinterpret_cast<const half8*>(wsplit + static_cast<int64_t>(d) * d);
 #pragma unroll
   for (int t = 0; t < T::TPW; ++t) acc[t] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -62,7 +65,8 @@ __device__ __forceinline__ void stage_gemm(const float* __restrict__ X, const fl
       const int tile = wave * T::TPW + t;
       const int mb = tile / T::NB, nb = tile % T::NB;
       const int j = mb * 16 + l16;
-      const half8 ahi = Wh[(j * D + k0) / 8];
+      const bool win = j < d && k0 < d;  // d % 8 == 0: the 8 columns from k0 are all real or all padding
+      const half8 ahi = win ? Wh[(j * d + k0) / 8] : half8{};
       const int row = nb * 16 + l16;
       const float s = xscale[row];
       const float4v* xr = reinterpret_cast<const float4v*>(X + row * T::LDA + k0);
@@ -80,7 +84,7 @@ __device__ __forceinline__ void stage_gemm(const float* __restrict__ X, const fl
       }
       acc[t] = mfma16x16x32(ahi, bhi, acc[t]);
       if constexpr (W_SPLIT) {
-        const half8 alo = Wl[(j * D + k0) / 8];
+        const half8 alo = win ? Wl[(j * d + k0) / 8] : half8{};
         acc[t] = mfma16x16x32(alo, bhi, acc[t]);
       }
       if constexpr (X_SPLIT) acc[t] = mfma16x16x32(ahi, blo, acc[t]);
@@ -97,16 +101,24 @@ struct Rows4 {
   }
 };
 
-// Load R rows of activations into the f32 tile (zero rows past n).
+// Load R rows of d activations into the f32 tile (zero rows past n, zero columns past d).
 template <int D, int DT>
 __device__ __forceinline__ void load_rows(float* __restrict__ A, const void* __restrict__ x,
-                                          int64_t row0, int64_t n, const Rows4& rows) {
+                                          int64_t row0, int64_t n, int d, const Rows4& rows) {
   using T = CTile<D>;
   for (int e = threadIdx.x; e < T::R * D; e += T::NT) {
     const int r = e / D, i = e % D;
     const int64_t gr = row0 + r;
-    A[r * T::LDA + i] = (gr < n) ? load_act<DT>(x, rows.offset(gr) + i) : 0.f;
+    A[r * T::LDA + i] = (gr < n && i < d) ? load_act<DT>(x, rows.offset(gr) + i) : 0.f;
   }
+}
+
+// Bytes [0, nbytes) of a packed row from its 32-bit words, byte by byte (rows of d * b / 8
+// bytes need not be dword aligned).
+__device__ __forceinline__ void store_word_bytes(uint8_t* row, int w, int nbytes, uint32_t word) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    if (4 * w + k < nbytes) row[4 * w + k] = static_cast<uint8_t>(word >> (8 * k));
 }
 
 // Row reduction: every thread of the TPR-thread group of row r returns the
@@ -148,6 +160,7 @@ struct KeyArgs {
   uint8_t *codes, *signs;
   uint16_t *rn, *vn;
   float *y_out, *proj_out;
+  int d;  // head dim, d <= D, d % 8 == 0
 };
 
 template <int D, int DT>
@@ -165,7 +178,8 @@ __global__ void __launch_bounds__(256) compress_keys_kernel(KeyArgs a) {
     if (j < nb) s_bnd[j] = a.bounds[j];
   }
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * T::R;
-  load_rows<D, DT>(A, a.x, row0, a.n, a.rows);
+  const int d = a.d;
+  load_rows<D, DT>(A, a.x, row0, a.n, d, a.rows);
   if (threadIdx.x < T::R) s_sc[threadIdx.x] = kSplit;
   __syncthreads();
 
@@ -190,7 +204,7 @@ __global__ void __launch_bounds__(256) compress_keys_kernel(KeyArgs a) {
   const int l16 = lane & 15, g = lane >> 4;
 
   // stage 1: y = xn Pi^T (compressors.py:112)
-  stage_gemm<D, true, true>(Bm, s_sc, a.pi, acc);
+  stage_gemm<D, true, true>(Bm, s_sc, a.pi, d, acc);
   __syncthreads();
 #pragma unroll
   for (int t = 0; t < T::TPW; ++t) {
@@ -205,13 +219,17 @@ __global__ void __launch_bounds__(256) compress_keys_kernel(KeyArgs a) {
   // u = r Pi^T = (vn + 1e-8) y - vn f16(C)[c]  (compressors.py:120-126: r = x - (yhat Pi) vn)
   for (int e = threadIdx.x; e < T::R * D; e += T::NT) {
     const int r = e / D, i = e % D;
+    if (i >= d) {  // padding: no code, zero residual
+      Bm[r * T::LDA + i] = 0.f;
+      continue;
+    }
     const float y = Bm[r * T::LDA + i];
     const uint32_t c = searchsorted_left(y, s_bnd, nb);
     idx[r * D + i] = static_cast<uint8_t>(c);
     const float vn = s_vn[r];
     Bm[r * T::LDA + i] = fmaf(vn + 1e-8f, y, -vn * s_cent16[c]);
     const int64_t gr = row0 + r;
-    if (a.y_out && gr < a.n) a.y_out[gr * D + i] = y;
+    if (a.y_out && gr < a.n) a.y_out[gr * d + i] = y;
   }
   __syncthreads();
   {
@@ -233,7 +251,7 @@ __global__ void __launch_bounds__(256) compress_keys_kernel(KeyArgs a) {
   __syncthreads();
 
   // stage 2: proj = r S^T = u S_eff^T with S_eff = S Pi^T; sign bit = proj >= 0   (compressors.py:128-130)
-  stage_gemm<D, true, true>(Bm, s_sc, a.seff, acc);
+  stage_gemm<D, true, true>(Bm, s_sc, a.seff, d, acc);
   __syncthreads();
 #pragma unroll
   for (int t = 0; t < T::TPW; ++t) {
@@ -245,26 +263,32 @@ __global__ void __launch_bounds__(256) compress_keys_kernel(KeyArgs a) {
   }
   __syncthreads();
 
-  // pack codes (b bits) and signs (1 bit) a 32-bit word per thread
-  const int kw = D * a.b / 32, sw = D / 32;
+  // pack codes (b bits) and signs (1 bit) a 32-bit word per thread; rows of d * b / 8 and d / 8
+  // bytes, stored bytewise when they are not whole words
+  const int kbytes = d * a.b / 8, sbytes = d / 8;
+  const int kw = (kbytes + 3) / 4, sw = (sbytes + 3) / 4;
+  const bool whole = (kbytes % 4 == 0) && (sbytes % 4 == 0);
   for (int e = threadIdx.x; e < T::R * (kw + sw); e += T::NT) {
     const int r = e / (kw + sw), w = e % (kw + sw);
     const int64_t gr = row0 + r;
     if (gr >= a.n) continue;
     if (w < kw) {
-      reinterpret_cast<uint32_t*>(a.codes + gr * (D * a.b / 8))[w] = pack_word(idx + r * D, D, a.b, w);
+      const uint32_t word = pack_word(idx + r * D, d, a.b, w);
+      if (whole) reinterpret_cast<uint32_t*>(a.codes + gr * kbytes)[w] = word;
+      else store_word_bytes(a.codes + gr * kbytes, w, kbytes, word);
     } else {
       const int ws = w - kw;
       uint32_t bits = 0;
       for (int k = 0; k < 32; ++k) bits |= (Bm[r * T::LDA + ws * 32 + k] >= 0.f ? 1u : 0u) << k;
-      reinterpret_cast<uint32_t*>(a.signs + gr * (D / 8))[ws] = bits;
+      if (whole) reinterpret_cast<uint32_t*>(a.signs + gr * sbytes)[ws] = bits;
+      else store_word_bytes(a.signs + gr * sbytes, ws, sbytes, bits);
     }
   }
   if (a.proj_out) {
     for (int e = threadIdx.x; e < T::R * D; e += T::NT) {
       const int r = e / D, i = e % D;
       const int64_t gr = row0 + r;
-      if (gr < a.n) a.proj_out[gr * D + i] = Bm[r * T::LDA + i];
+      if (gr < a.n && i < d) a.proj_out[gr * d + i] = Bm[r * T::LDA + i];
     }
   }
 }
@@ -279,6 +303,7 @@ struct ValArgs {
   uint8_t* codes;
   uint16_t* vn;
   float* y_out;
+  int d;  // head dim, d <= D, d % 8 == 0
 };
 
 template <int D, int DT>
@@ -290,7 +315,8 @@ __global__ void __launch_bounds__(256) compress_values_kernel(ValArgs a) {
   const int nb = (1 << a.b) - 1;
   for (int j = threadIdx.x; j < nb; j += T::NT) s_bnd[j] = a.bounds[j];
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * T::R;
-  load_rows<D, DT>(A, a.x, row0, a.n, a.rows);
+  const int d = a.d;
+  load_rows<D, DT>(A, a.x, row0, a.n, d, a.rows);
   if (threadIdx.x < T::R) s_sc[threadIdx.x] = kSplit;
   __syncthreads();
   {
@@ -307,7 +333,7 @@ __global__ void __launch_bounds__(256) compress_values_kernel(ValArgs a) {
   }
   __syncthreads();
   float4v acc[T::TPW];
-  stage_gemm<D, true, true>(A, s_sc, a.pi, acc);
+  stage_gemm<D, true, true>(A, s_sc, a.pi, d, acc);
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g = lane >> 4;
@@ -320,16 +346,18 @@ __global__ void __launch_bounds__(256) compress_values_kernel(ValArgs a) {
       const float y = acc[t][e] * kUnsplit2;
       idx[row * D + col + e] = static_cast<uint8_t>(searchsorted_left(y, s_bnd, nb));
       const int64_t gr = row0 + row;
-      if (a.y_out && gr < a.n) a.y_out[gr * D + col + e] = y;
+      if (a.y_out && gr < a.n && col + e < d) a.y_out[gr * d + col + e] = y;
     }
   }
   __syncthreads();
-  const int kw = D * a.b / 32;
+  const int kbytes = d * a.b / 8, kw = (kbytes + 3) / 4;
   for (int e = threadIdx.x; e < T::R * kw; e += T::NT) {
     const int r = e / kw, w = e % kw;
     const int64_t gr = row0 + r;
-    if (gr < a.n)
-      reinterpret_cast<uint32_t*>(a.codes + gr * (D * a.b / 8))[w] = pack_word(idx + r * D, D, a.b, w);
+    if (gr >= a.n) continue;
+    const uint32_t word = pack_word(idx + r * D, d, a.b, w);
+    if (kbytes % 4 == 0) reinterpret_cast<uint32_t*>(a.codes + gr * kbytes)[w] = word;
+    else store_word_bytes(a.codes + gr * kbytes, w, kbytes, word);
   }
 }
 
@@ -342,6 +370,7 @@ struct DecArgs {
   int b;
   void* out;
   int64_t ld_out;
+  int d;  // head dim, d <= D, d % 8 == 0
 };
 
 template <int D, int DT>
@@ -353,15 +382,16 @@ __global__ void __launch_bounds__(256) decompress_values_kernel(DecArgs a) {
   if (threadIdx.x < T::R) s_sc[threadIdx.x] = kSplit;
   __syncthreads();
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * T::R;
-  const int kc = D * a.b / 8;
+  const int d = a.d;
+  const int kc = d * a.b / 8;
   for (int e = threadIdx.x; e < T::R * D; e += T::NT) {
     const int r = e / D, i = e % D;
     const int64_t gr = row0 + r;
-    A[r * T::LDA + i] = (gr < a.n) ? s_cent[read_code(a.codes + gr * kc, i, a.b)] : 0.f;
+    A[r * T::LDA + i] = (gr < a.n && i < d) ? s_cent[read_code(a.codes + gr * kc, i, a.b)] : 0.f;
   }
   __syncthreads();
   float4v acc[T::TPW];
-  stage_gemm<D, true, true>(A, s_sc, a.pit, acc);
+  stage_gemm<D, true, true>(A, s_sc, a.pit, d, acc);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g = lane >> 4;
 #pragma unroll
@@ -372,7 +402,8 @@ __global__ void __launch_bounds__(256) decompress_values_kernel(DecArgs a) {
     if (gr >= a.n) continue;
     const float vn = h2f(a.vn[gr]);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) store_act<DT>(a.out, gr * a.ld_out + col + e, (acc[t][e] * kUnsplit2) * vn);
+    for (int e = 0; e < 4; ++e)
+      if (col + e < d) store_act<DT>(a.out, gr * a.ld_out + col + e, (acc[t][e] * kUnsplit2) * vn);
   }
 }
 
@@ -383,6 +414,7 @@ struct PrepArgs {
   const uint16_t *pi, *seff;
   uint16_t* q_rot;
   float* q_proj;
+  int d;  // head dim, d <= D, d % 8 == 0
 };
 
 template <int D, int DT>
@@ -392,11 +424,12 @@ __global__ void __launch_bounds__(256) query_prep_kernel(PrepArgs a) {
   __shared__ float s_sc[T::R], s_inv[T::R];
   const int64_t n = static_cast<int64_t>(a.B) * a.Hq * a.Sq;
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * T::R;
+  const int d = a.d;
   for (int e = threadIdx.x; e < T::R * D; e += T::NT) {
     const int r = e / D, i = e % D;
     const int64_t gr = row0 + r;
     float v = 0.f;
-    if (gr < n) {
+    if (gr < n && i < d) {
       const int64_t s = gr % a.Sq, bh = gr / a.Sq;
       const int64_t h = bh % a.Hq, b = bh / a.Hq;
       v = load_act<DT>(a.q, b * a.sqb + h * a.sqh + s * a.sqs + i);
@@ -424,7 +457,7 @@ __global__ void __launch_bounds__(256) query_prep_kernel(PrepArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g = lane >> 4;
   // q_rot = f16(q Pi^T)   (compressors.py:186)
-  stage_gemm<D, true, true>(A, s_sc, a.pi, acc);
+  stage_gemm<D, true, true>(A, s_sc, a.pi, d, acc);
   __syncthreads();
 #pragma unroll
   for (int t = 0; t < T::TPW; ++t) {
@@ -436,7 +469,7 @@ __global__ void __launch_bounds__(256) query_prep_kernel(PrepArgs a) {
     for (int e = 0; e < 4; ++e) {
       const _Float16 h = static_cast<_Float16>(acc[t][e] * inv);
       A[row * T::LDA + col + e] = static_cast<float>(h);
-      if (gr < n) a.q_rot[gr * D + col + e] = __builtin_bit_cast(uint16_t, h);
+      if (gr < n && col + e < d) a.q_rot[gr * d + col + e] = __builtin_bit_cast(uint16_t, h);
     }
   }
   __syncthreads();
@@ -460,7 +493,7 @@ __global__ void __launch_bounds__(256) query_prep_kernel(PrepArgs a) {
   // q_proj = q_rot S_eff^T in f32: f32 accumulation of exact f16 products, as the reference's
   // fp32 q_rot.float() @ S_eff.float().T (kernels/attention.py:158-167, :453); S_eff is used
   // unscaled, hi part only
-  stage_gemm<D, false, false>(A, s_sc, a.seff, acc);
+  stage_gemm<D, false, false>(A, s_sc, a.seff, d, acc);
 #pragma unroll
   for (int t = 0; t < T::TPW; ++t) {
     const int tile = wave * T::TPW + t;
@@ -469,7 +502,8 @@ __global__ void __launch_bounds__(256) query_prep_kernel(PrepArgs a) {
     if (gr >= n) continue;
     const float inv = s_inv[row];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) a.q_proj[gr * D + col + e] = acc[t][e] * inv;
+    for (int e = 0; e < 4; ++e)
+      if (col + e < d) a.q_proj[gr * d + col + e] = acc[t][e] * inv;
   }
 }
 
@@ -1191,21 +1225,24 @@ TQ_DEFINE_LAUNCH(launch_values, compress_values_kernel, ValArgs)
 TQ_DEFINE_LAUNCH(launch_decomp, decompress_values_kernel, DecArgs)
 TQ_DEFINE_LAUNCH(launch_prep, query_prep_kernel, PrepArgs)
 
-#define TQ_SWITCH_DD(FN, d, dt, ...)                                    \
-  switch ((d) * 4 + (dt)) {                                              \
-    case 32 * 4 + TQ_F32: FN<32, TQ_F32>(__VA_ARGS__); break;            \
-    case 32 * 4 + TQ_F16: FN<32, TQ_F16>(__VA_ARGS__); break;            \
-    case 32 * 4 + TQ_BF16: FN<32, TQ_BF16>(__VA_ARGS__); break;          \
-    case 64 * 4 + TQ_F32: FN<64, TQ_F32>(__VA_ARGS__); break;            \
-    case 64 * 4 + TQ_F16: FN<64, TQ_F16>(__VA_ARGS__); break;            \
-    case 64 * 4 + TQ_BF16: FN<64, TQ_BF16>(__VA_ARGS__); break;          \
-    case 128 * 4 + TQ_F32: FN<128, TQ_F32>(__VA_ARGS__); break;          \
-    case 128 * 4 + TQ_F16: FN<128, TQ_F16>(__VA_ARGS__); break;          \
-    case 128 * 4 + TQ_BF16: FN<128, TQ_BF16>(__VA_ARGS__); break;        \
-    case 256 * 4 + TQ_F32: FN<256, TQ_F32>(__VA_ARGS__); break;          \
-    case 256 * 4 + TQ_F16: FN<256, TQ_F16>(__VA_ARGS__); break;          \
-    case 256 * 4 + TQ_BF16: FN<256, TQ_BF16>(__VA_ARGS__); break;        \
-    default: break;                                                      \
+// The tile kernel for head dim d: D = d rounded up to a multiple of 32.
+#define TQ_CASE_D(FN, DD, dt, ...)                                                \
+  case DD:                                                                        \
+    if ((dt) == TQ_F32) FN<DD, TQ_F32>(__VA_ARGS__);                              \
+    else if ((dt) == TQ_F16) FN<DD, TQ_F16>(__VA_ARGS__);                         \
+    else FN<DD, TQ_BF16>(__VA_ARGS__);                                            \
+    break;
+#define TQ_SWITCH_DD(FN, d, dt, ...)                                              \
+  switch (pad_dim(d)) {                                                           \
+    TQ_CASE_D(FN, 32, dt, __VA_ARGS__)                                            \
+    TQ_CASE_D(FN, 64, dt, __VA_ARGS__)                                            \
+    TQ_CASE_D(FN, 96, dt, __VA_ARGS__)                                            \
+    TQ_CASE_D(FN, 128, dt, __VA_ARGS__)                                           \
+    TQ_CASE_D(FN, 160, dt, __VA_ARGS__)                                           \
+    TQ_CASE_D(FN, 192, dt, __VA_ARGS__)                                           \
+    TQ_CASE_D(FN, 224, dt, __VA_ARGS__)                                           \
+    TQ_CASE_D(FN, 256, dt, __VA_ARGS__)                                           \
+    default: break;                                                               \
   }
 
 }  // namespace tq
@@ -1215,7 +1252,7 @@ using namespace tq;
 #define TQ_CHECK_DD(what, d, dtype)                                                              \
   do {                                                                                           \
     if (!supported_dim(d)) {                                                                     \
-      set_error("%s: head_dim %d not built (supported: 32, 64, 128, 256)", what, (int)(d));     \
+      set_error("%s: head_dim %d not supported (multiples of 8 from 8 to 256)", what, (int)(d));  \
       return TQ_EUNSUPPORTED;                                                                    \
     }                                                                                            \
     TQ_REQUIRE((dtype) == TQ_F32 || (dtype) == TQ_F16 || (dtype) == TQ_BF16,                     \
@@ -1248,7 +1285,7 @@ int tq_compress_keys(const void* x, int32_t dtype, int32_t B, int32_t H, int32_t
     return launch_status("tq_compress_keys");
   }
   KeyArgs a{x, n, Rows4{H, S, sxb, sxh, sxs}, pi_split, seff_split, centroids, bounds, b_eff, codes, signs, rn, vn,
-            y_out, proj_out};
+            y_out, proj_out, d};
   TQ_SWITCH_DD(launch_keys, d, dtype, a, n, as_stream(stream));
   return launch_status("tq_compress_keys");
 }
@@ -1271,7 +1308,7 @@ int tq_compress_values(const void* x, int32_t dtype, int32_t B, int32_t H, int32
     dispatch_tile<TM_VALUES>(t, d, dtype, b, as_stream(stream));
     return launch_status("tq_compress_values");
   }
-  ValArgs a{x, n, Rows4{H, S, sxb, sxh, sxs}, pi_split, bounds, b, codes, vn, y_out};
+  ValArgs a{x, n, Rows4{H, S, sxb, sxh, sxs}, pi_split, bounds, b, codes, vn, y_out, d};
   TQ_SWITCH_DD(launch_values, d, dtype, a, n, as_stream(stream));
   return launch_status("tq_compress_values");
 }
@@ -1284,7 +1321,7 @@ int tq_decompress_values(const uint8_t* codes, const uint16_t* vn, int64_t n, in
   TQ_REQUIRE(n >= 0 && ld_out >= d, "tq_decompress_values: bad shape");
   if (n == 0) return TQ_OK;
   TQ_REQUIRE(codes && vn && pit_split && centroids && out, "tq_decompress_values: null pointer");
-  DecArgs a{codes, vn, n, pit_split, centroids, b, out, ld_out};
+  DecArgs a{codes, vn, n, pit_split, centroids, b, out, ld_out, d};
   TQ_SWITCH_DD(launch_decomp, d, out_dtype, a, n, as_stream(stream));
   return launch_status("tq_decompress_values");
 }
@@ -1306,7 +1343,7 @@ int tq_query_prep(const void* q, int32_t dtype, int32_t B, int32_t Hq, int32_t S
     dispatch_tile<TM_QUERY>(t, d, dtype, 1, as_stream(stream));
     return launch_status("tq_query_prep");
   }
-  PrepArgs a{q, B, Hq, Sq, sqb, sqh, sqs, pi_split, s_eff_f16, q_rot, q_proj};
+  PrepArgs a{q, B, Hq, Sq, sqb, sqh, sqs, pi_split, s_eff_f16, q_rot, q_proj, d};
   TQ_SWITCH_DD(launch_prep, d, dtype, a, n, as_stream(stream));
   return launch_status("tq_query_prep");
 }
