@@ -13,10 +13,12 @@ through the fused decode attention (softmax . V).
 Secondary legs in the same line: BASELINE.json configs[1] (the same layer shape
 at 8192 tokens, bf16 Q/K/V ~ N(0,1) with 4 outlier channels x20 on K): compress
 tokens/s and the causal prefill (scores + online softmax + P.V for every query
-row, MFMA roofline); and one layer's eager decode step through the product path
-(torch.ops.tq) at B = 1 with 4096 cached tokens, host and device time.  CPU
-baselines: the build's torch CPU branch of the reference's PyTorch path on
-bounded samples.  Prints one JSON line.  With --gpus N > 1 it exits: this build
+row, MFMA roofline); one layer's eager decode step through the product path
+(torch.ops.tq) at B = 1 with 4096 cached tokens, host and device time; the HBM
+stream ceilings; compression at the north-star scale (1M key + 1M value rows);
+the head_dim-64 (GPT-2) tiled path; and configs[2]'s 36-layer model forward
+with its per-layer attention time.  CPU baselines: the build's torch CPU branch
+of the reference's PyTorch path on bounded samples.  Prints one JSON line.  With --gpus N > 1 it exits: this build
 runs on one GPU.
 """
 
@@ -576,43 +578,176 @@ def compress_leg(kc, vc, steps: int, warmup: int) -> dict:
             "tokens_per_s": 4 * 32768 / (both * 1e-6), **out}
 
 
-def decode_step_leg(kc, vc, cached: int = 4096, steps: int = 200) -> dict:
-    """One attention layer's eager decode step through the product path (torch.ops.tq): compress the
-    new token's K and V (8 kv heads), prepare the 32 query heads' query, split-K attention over the
-    cached planes.  B = 1, bits 3.  Host time per step (wall clock over `steps` back-to-back steps,
-    synchronised at the end) against device time (HIP events around the same steps)."""
+def decode_step_leg(kc, vc, steps: int = 200) -> dict:
+    """One attention layer's decode step on the cached serving path (TurboQuantCache, as a patched
+    layer runs it under generate): tq::cache_append compresses the new token's K and V (8 kv heads)
+    straight into the cache planes and prepares the 32 query heads' query in one launch, then the
+    split-K attention over every cached position (attention + merge).  bits 3, B = 1 and 16, with
+    4096 and 32768 cached tokens; the cache is sized beforehand so that no step grows it.  Host time
+    per step (wall clock over `steps` back-to-back steps, synchronised at the end) and device time
+    (HIP events around the same steps)."""
     import torch
 
-    from turboquant_pytorch import compressed_attention
+    from transformers_turboquant import TurboQuantCache
+    from turboquant_pytorch.fused import attention_from_prepared
 
     dev = "cuda"
-    g = torch.Generator(device=dev).manual_seed(5)
-    ck = kc.compress(torch.randn(1, HKV, cached, D, device=dev, generator=g).to(torch.bfloat16))
-    cv = vc.compress(torch.randn(1, HKV, cached, D, device=dev, generator=g).to(torch.bfloat16))
-    k1 = torch.randn(1, HKV, 1, D, device=dev, generator=g).to(torch.bfloat16)
-    v1 = torch.randn(1, HKV, 1, D, device=dev, generator=g).to(torch.bfloat16)
-    q1 = torch.randn(1, HQ, 1, D, device=dev, generator=g).to(torch.bfloat16)
+    out = {}
+    warm = 20
+    for b_, cached in ((1, 4096), (1, 32768), (16, 4096), (16, 32768)):
+        g = torch.Generator(device=dev).manual_seed(5 + b_ + cached)
+        cache = TurboQuantCache()
+        total = cached + warm + steps
+        for lo in range(0, total, 8192):  # prefill in chunks; then keep `cached` positions
+            n = min(8192, total - lo)
+            cache.append(0, kc, vc, torch.randn(b_, HKV, n, D, device=dev, generator=g).to(torch.bfloat16),
+                         torch.randn(b_, HKV, n, D, device=dev, generator=g).to(torch.bfloat16))
+        cache.layer(0).crop(cached)
+        k1 = torch.randn(b_, HKV, 1, D, device=dev, generator=g).to(torch.bfloat16)
+        v1 = torch.randn(b_, HKV, 1, D, device=dev, generator=g).to(torch.bfloat16)
+        q1 = torch.randn(b_, HQ, 1, D, device=dev, generator=g).to(torch.bfloat16)
 
-    def step():
-        kc.compress(k1)
-        vc.compress(v1)
-        return compressed_attention(q1, kc, vc, ck, cv, out_dtype=torch.bfloat16)
+        def step():
+            ck, cv, q_rot, q_proj = cache.append_prepare(0, kc, vc, k1, v1, q1)
+            return attention_from_prepared(q_rot, q_proj, kc, vc, ck, cv, out_dtype=torch.bfloat16)
 
-    for _ in range(20):
-        step()
-    torch.cuda.synchronize()
-    RANGES.push("decode_step", steps)
-    e0, e1 = _events(2)
-    t0 = time.perf_counter()
-    e0.record()
-    for _ in range(steps):
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    host_us = (time.perf_counter() - t0) / steps * 1e6
-    RANGES.pop()
-    return {"workload": f"B1 Hq{HQ} Hkv{HKV} d{D} bits{BITS}, {cached} cached tokens, one new token per step",
-            "host_us_per_step": host_us, "device_us_per_step": e0.elapsed_time(e1) / steps * 1e3}
+        for _ in range(warm):
+            step()
+        cache.layer(0).crop(cached)
+        torch.cuda.synchronize()
+        RANGES.push(f"decode_step_B{b_}_S{cached}", steps)
+        e0, e1 = _events(2)
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        host_us = (time.perf_counter() - t0) / steps * 1e6
+        RANGES.pop()
+        out[f"B{b_}_S{cached}"] = {"host_us_per_step": host_us, "device_us_per_step": e0.elapsed_time(e1) / steps * 1e3}
+        del cache
+        torch.cuda.empty_cache()
+    return {"workload": (f"Hq{HQ} Hkv{HKV} d{D} bits{BITS}: one new token per step appended to a TurboQuantCache "
+                         "(one launch: K, V and query preparation) + split-K attention over every cached position"),
+            **out}
+
+
+def head_dim64_leg(steps: int, warmup: int) -> dict:
+    """The head_dim-64 path (GPT-2's attention, BASELINE.json configs[0]'s shape: 12 heads, bits 3)
+    through the tiled kernel: one layer's compress K / V + query prep + fused attention per step,
+    at configs[0]'s 512 tokens and at 8192 tokens (causal), HIP events around the attention call
+    and around the whole step."""
+    import torch
+
+    from turboquant_pytorch.compressors import TurboQuantCompressorMSE, TurboQuantCompressorV2
+    from turboquant_pytorch.fused import attention_from_prepared
+
+    d, h = 64, 12
+    kc = TurboQuantCompressorV2(d, BITS, seed=42, device="cuda")
+    vc = TurboQuantCompressorMSE(d, BITS, seed=10042, device="cuda")
+    out = {}
+    for S_ in (512, 8192):
+        g = torch.Generator(device="cuda").manual_seed(S_)
+        q, k, v = (torch.randn(1, h, S_, d, device="cuda", generator=g).to(torch.bfloat16) for _ in range(3))
+        marks = []
+
+        def step(record):
+            e = _events(3) if record else None
+            if record:
+                e[0].record()
+            ck, cv = kc.compress(k), vc.compress(v)
+            q_rot, q_proj = kc.prepare_queries(q)
+            if record:
+                e[1].record()
+            attention_from_prepared(q_rot, q_proj, kc, vc, ck, cv, causal=True, out_dtype=torch.bfloat16)
+            if record:
+                e[2].record()
+                marks.append(e)
+
+        for _ in range(warmup + 1):
+            step(False)
+        torch.cuda.synchronize()
+        RANGES.push(f"head_dim64_S{S_}", steps)
+        for _ in range(steps):
+            step(True)
+        torch.cuda.synchronize()
+        RANGES.pop()
+        attn_ms = sorted(m[1].elapsed_time(m[2]) for m in marks)[len(marks) // 2]
+        step_ms = sorted(m[0].elapsed_time(m[2]) for m in marks)[len(marks) // 2]
+        key_heads = h * S_ * (S_ + 1) // 2
+        tflops = key_heads * 6 * d / (attn_ms * 1e-3) / 1e12
+        out[f"S{S_}"] = {"step_ms": step_ms, "attention_ms": attn_ms, "attention_tflops": tflops,
+                         "mfma_frac": tflops / MFMA_F16_PEAK_TFLOPS}
+    return {"workload": f"GPT-2 attention shape: B1 x {h} heads x d{d}, bits {BITS}, causal; tiled kernel "
+                        "tq::attn_kernel<64, 2, false, false>", **out}
+
+
+def model_leg(steps: int = 3, S_model: int = 8192, bits: int = BITS) -> dict:
+    """the 36-layer Qwen2.5-3B-shaped random-init model (hidden 2048, 16 / 2
+    heads, head_dim 128, bf16) patched by apply_turboquant (bits 3, seed 42, the reference's
+    defaults), one full-sequence forward of 8192 uniform-random token ids with logits_to_keep=1.
+    Whole-forward time (HIP events around each forward) and the time of every patched attention
+    module (events in forward pre / post hooks: q/k/v projections, rotary, K / V compression,
+    query preparation, fused attention, o_proj), summed over the layers."""
+    import torch
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    from transformers_turboquant import apply_turboquant
+
+    cfg = Qwen2Config(vocab_size=151936, hidden_size=2048, intermediate_size=11008, num_hidden_layers=36,
+                      num_attention_heads=16, num_key_value_heads=2, max_position_embeddings=32768,
+                      tie_word_embeddings=True)
+    torch.manual_seed(0)
+    with torch.device("cuda"):
+        model = Qwen2ForCausalLM(cfg)
+    model = model.to(torch.bfloat16).eval()
+    apply_turboquant(model, bits=bits, seed=42)
+    ids = torch.randint(0, cfg.vocab_size, (1, S_model), generator=torch.Generator().manual_seed(0)).to("cuda")
+    marks = []
+
+    record = [False]
+
+    def pre(mod, args, kwargs):
+        if record[0]:
+            e = _events(2)
+            e[0].record()
+            marks.append(e)
+
+    def post(mod, args, kwargs, out):
+        if record[0]:
+            marks[-1][1].record()
+
+    handles = []
+    for layer in model.model.layers:
+        handles.append(layer.self_attn.register_forward_pre_hook(pre, with_kwargs=True))
+        handles.append(layer.self_attn.register_forward_hook(post, with_kwargs=True))
+    with torch.no_grad():
+        model(input_ids=ids, logits_to_keep=1)
+        torch.cuda.synchronize()
+        record[0] = True
+        fwd = []
+        RANGES.push("model_forward", steps)
+        for _ in range(steps):
+            e = _events(2)
+            e[0].record()
+            model(input_ids=ids, logits_to_keep=1)
+            e[1].record()
+            fwd.append(e)
+        torch.cuda.synchronize()
+        RANGES.pop()
+    for h in handles:
+        h.remove()
+    fwd_ms = sorted(e[0].elapsed_time(e[1]) for e in fwd)[len(fwd) // 2]
+    n_layers = cfg.num_hidden_layers
+    attn_ms = sum(m[0].elapsed_time(m[1]) for m in marks) / steps
+    del model
+    torch.cuda.empty_cache()
+    return {"workload": (f"configs[2]: Qwen2.5-3B-shaped random-init model, 36 layers, bf16, B1 x {S_model} tokens, "
+                         f"bits {bits}, apply_turboquant defaults (non-causal as the reference), logits_to_keep=1"),
+            "forward_ms": fwd_ms, "tokens_per_s": S_model / (fwd_ms * 1e-3),
+            "attention_modules_ms": attn_ms, "attention_ms_per_layer": attn_ms / n_layers,
+            "attention_share": attn_ms / fwd_ms}
 
 
 def prefill_leg(kc, vc, q, k, v, steps: int, warmup: int) -> dict:
@@ -687,6 +822,7 @@ def main() -> None:
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-prefill", action="store_true", help="skip the causal prefill / compress leg")
     ap.add_argument("--no-ceiling", action="store_true", help="skip the HBM stream-ceiling leg")
+    ap.add_argument("--no-model", action="store_true", help="skip the whole-model forward leg")
     ap.add_argument("--compress-only", action="store_true",
                     help="run only the north-star compression leg (1M key + 1M value rows) and print its record")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -773,6 +909,8 @@ def main() -> None:
         "prefill": prefill,
         "decode_step": None if args.no_prefill else decode_step_leg(kc, vc),
         "compress_north_star": None if args.no_prefill else compress_leg(kc, vc, 5, 2),
+        "head_dim64": None if args.no_prefill else head_dim64_leg(args.steps, args.warmup),
+        "model_forward": None if (args.no_prefill or args.no_model) else model_leg(),
     }
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline_decode(args.cpu_seconds / 2)

@@ -22,6 +22,8 @@
  *   - A "split" d x d matrix W is f16 [2][d][d] row-major: hi = f16(1024*W),
  *     lo = f16(1024*W - hi).  The kernels run d x d products on f16 MFMA and
  *     recover f32 accuracy from the (hi, lo) pair.
+ *   - Head dims d: every multiple of 8 from 8 to 256 (packed rows of d*b/8
+ *     bytes, not dword aligned in general); others return TQ_EUNSUPPORTED.
  *
  * Reference: SrzStephen/transformers-turboquant, Python package
  * src/turboquant_pytorch (file:line citations below are relative to it).
@@ -164,8 +166,8 @@ int tq_attention_scores(const uint16_t* q_rot, const float* q_proj,
                         int32_t bits, float coeff, float* out, void* stream);
 
 /* Fused compressed-domain attention (one attention layer's tail).  q_proj f32 as in
- * tq_attention_scores; the split-K decode kernels use it at f32 grade (hi + lo), the
- * many-query kernels use its f16 rounding:
+ * tq_attention_scores; the split-K decode kernels and the tiled kernel (head dims other than
+ * 128) use it at f32 grade (hi + lo), the head_dim-128 prefill kernel its f16 rounding:
  *   s   = (vn*<q_rot,Ck[codes]> + coeff*rn*<q_proj, 2*sign-1>) * scale
  *         (+ mask[b, h, i, j] if mask != NULL) (causal: key j > i + Sk - Sq dropped)
  *   p   = softmax_j(s)                    (f32, online)
@@ -219,6 +221,32 @@ int tq_attention_fwd_kv(const uint16_t* q_rot, const float* q_proj,
                         int64_t smk, void* out, int32_t out_dtype, int64_t sob,
                         int64_t soh, int64_t sos, void* workspace,
                         int64_t workspace_bytes, void* stream);
+
+/* Compressed-cache append: compress the S new keys and values of each (batch, kv head),
+ * k / v [B, H, S, d] (element strides; unit stride on d), into rows [pos, pos + S) of
+ * cache planes that hold `capacity` positions per (batch, kv head) -- key_codes
+ * u8 [B, H, capacity, ceil(d*key_code_bits/8)], key_signs u8 [.., d/8], key_rn / key_vn
+ * f16 [B, H, capacity], val_codes u8 [.., ceil(d*val_bits/8)], val_vn f16 [B, H, capacity],
+ * the layout tq_attention_fwd_kv reads with kv_stride = capacity -- and, when q is not
+ * NULL, prepare the S new query rows q [B, Hq, S, d] as tq_query_prep does (q_rot f16 /
+ * q_proj f32 [B, Hq, S, d]).  Operands as in tq_compress_keys / tq_compress_values /
+ * tq_query_prep (key_code_bits = bits - 1 for bits-bit keys); every written row equals
+ * those entry points' output for the same input row bit for bit.  At head_dim 64 / 128 with
+ * key_code_bits = val_bits - 1 (val_bits 2-4) the three run in one launch.
+ * No counterpart in the reference, which disables the KV cache and recompresses the whole
+ * sequence every step (patch.py:81); a decoding step calls this once per layer. */
+int tq_cache_append(const void* k, const void* v, int32_t dtype, int32_t B,
+                    int32_t H, int32_t S, int32_t d, int64_t skb, int64_t skh,
+                    int64_t sks, int64_t svb, int64_t svh, int64_t svs,
+                    const uint16_t* key_pi_split, const uint16_t* key_seff_split,
+                    const float* key_centroids, const float* key_bounds,
+                    int32_t key_code_bits, const uint16_t* val_pi_split,
+                    const float* val_bounds, int32_t val_bits, uint8_t* key_codes,
+                    uint8_t* key_signs, uint16_t* key_rn, uint16_t* key_vn,
+                    uint8_t* val_codes, uint16_t* val_vn, int64_t capacity,
+                    int64_t pos, const void* q, int32_t Hq, int64_t sqb,
+                    int64_t sqh, int64_t sqs, const uint16_t* key_s_eff_f16,
+                    uint16_t* q_rot, float* q_proj, void* stream);
 
 /* Bytes of caller-provided device workspace tq_attention_fwd uses for the
  * split-K decode path at this shape (head_dim 128, bits 2-4, at most 16

@@ -131,3 +131,93 @@ def test_cached_generate_matches_recompute_gpu(dtype):
     cos = [O.cosine(a.float().cpu().numpy(), b.float().cpu().numpy()) for a, b in zip(got.logits, ref.logits)]
     assert min(cos) > (0.9999 if dtype == torch.float32 else 0.999), cos
     assert (got.sequences == ref.sequences).float().mean() > 0.95
+
+
+@pytest.mark.parametrize("d,bits,dt,B,H,Hq,S,cap,pos", [
+    (128, 3, torch.bfloat16, 1, 8, 32, 1, 4096, 4095),   # one decode step (one launch: K, V and Q)
+    (128, 2, torch.float32, 2, 3, 6, 37, 300, 17),
+    (128, 4, torch.float16, 2, 2, 8, 5, 256, 100),
+    (64, 3, torch.bfloat16, 2, 12, 12, 19, 64, 45),
+    (128, 3, torch.bfloat16, 2, 8, 32, 3000, 3500, 311),  # more blocks than the device holds: shared
+    (96, 3, torch.bfloat16, 2, 2, 4, 9, 40, 3),           # tile kernels: other head dims
+    (80, 2, torch.float32, 1, 3, 3, 7, 20, 13),
+])
+def test_cache_append_writes_the_compressors_rows(d, bits, dt, B, H, Hq, S, cap, pos):
+    """tq::cache_append (tq_cache_append) writes rows [pos, pos + S) of each (batch, kv head) of
+    the capacity planes exactly as compress() packs those rows, leaves every other row alone, and
+    prepares the queries exactly as prepare_queries() does."""
+    print(f"case: cache_append d={d} bits={bits} dt={dt} B={B} H={H} Hq={Hq} S={S} cap={cap} pos={pos}", flush=True)
+    from turboquant_pytorch._ops import ops
+
+    dev = "cuda"
+    kc = TurboQuantCompressorV2(d, bits, seed=42, device=dev)
+    vc = TurboQuantCompressorMSE(d, bits, seed=10042, device=dev)
+    g = torch.Generator(device=dev).manual_seed(S + d)
+    k = torch.randn(B, S, H, d, device=dev, generator=g).to(dt).transpose(1, 2)  # strided, as the families pass
+    v = torch.randn(B, H, S, d, device=dev, generator=g).to(dt)
+    q = torch.randn(B, Hq, S, d, device=dev, generator=g).to(dt)
+    fk, fv = kc.compress(k), vc.compress(v)
+    q_rot_ref, q_proj_ref = kc.prepare_queries(q)
+    kw, vw = fk["packed_key_indices"].shape[-1], fv["packed_indices"].shape[-1]
+    fill = 0xA5
+    planes = {
+        "kcodes": torch.full((B, H, cap, kw), fill, dtype=torch.uint8, device=dev),
+        "ksigns": torch.full((B, H, cap, d // 8), fill, dtype=torch.uint8, device=dev),
+        "krn": torch.full((B, H, cap), 7.0, dtype=torch.float16, device=dev),
+        "kvn": torch.full((B, H, cap), 7.0, dtype=torch.float16, device=dev),
+        "vcodes": torch.full((B, H, cap, vw), fill, dtype=torch.uint8, device=dev),
+        "vvn": torch.full((B, H, cap), 7.0, dtype=torch.float16, device=dev),
+    }
+    before = {n: t.clone() for n, t in planes.items()}
+    tk, tv = _tables(kc, dev, with_qjl=True), _tables(vc, dev, with_qjl=False)
+    q_rot, q_proj = ops().cache_append(k, v, q, tk.pi_split, tk.seff_split, tk.cent32, tk.bounds32, kc.mse_bits,
+                                       tv.pi_split, tv.bounds32, vc.bits, tk.s_eff16, planes["kcodes"],
+                                       planes["ksigns"], planes["krn"], planes["kvn"], planes["vcodes"],
+                                       planes["vvn"], pos)
+    torch.cuda.synchronize()
+    sl = slice(pos, pos + S)
+    want = {
+        "kcodes": fk["packed_key_indices"].reshape(B, H, S, kw), "ksigns": fk["packed_qjl_signs"].reshape(B, H, S, -1),
+        "krn": fk["residual_norm"].reshape(B, H, S), "kvn": fk["vec_norms"].reshape(B, H, S),
+        "vcodes": fv["packed_indices"].reshape(B, H, S, vw), "vvn": fv["vec_norms"].reshape(B, H, S),
+    }
+    for name, t in planes.items():
+        assert torch.equal(t[:, :, sl], want[name]), name
+        rest = torch.ones(cap, dtype=torch.bool, device=dev)
+        rest[sl] = False
+        assert torch.equal(t[:, :, rest], before[name][:, :, rest]), name
+    assert torch.equal(q_rot, q_rot_ref) and torch.equal(q_proj, q_proj_ref)
+    # without queries: the same rows, and empty query outputs
+    for name, t in planes.items():
+        t.copy_(before[name])
+    e_rot, e_proj = ops().cache_append(k, v, None, tk.pi_split, tk.seff_split, tk.cent32, tk.bounds32, kc.mse_bits,
+                                       tv.pi_split, tv.bounds32, vc.bits, tk.s_eff16, planes["kcodes"],
+                                       planes["ksigns"], planes["krn"], planes["kvn"], planes["vcodes"],
+                                       planes["vvn"], pos)
+    torch.cuda.synchronize()
+    assert e_rot.numel() == 0 and e_proj.numel() == 0
+    for name, t in planes.items():
+        assert torch.equal(t[:, :, sl], want[name]), name
+
+
+def test_cached_decode_step_uses_one_append_launch():
+    """A patched layer's decode step with a TurboQuantCache: the appended planes equal a one-shot
+    compression and the output equals compressed_attention on the compact planes."""
+    print("case: decode step through the cache", flush=True)
+    dev, d, B, Hkv, G, bits = "cuda", 128, 1, 8, 4, 3
+    kc = TurboQuantCompressorV2(d, bits, seed=42, device=dev)
+    vc = TurboQuantCompressorMSE(d, bits, seed=10042, device=dev)
+    g = torch.Generator(device=dev).manual_seed(3)
+    total = 600
+    k = torch.randn(B, Hkv, total, d, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, total, d, device=dev, generator=g).to(torch.bfloat16)
+    cache = TurboQuantCache()
+    cache.append(0, kc, vc, k[:, :, :599], v[:, :, :599])
+    q = torch.randn(B, Hkv * G, 1, d, device=dev, generator=g).to(torch.bfloat16)
+    ck, cv, q_rot, q_proj = cache.append_prepare(0, kc, vc, k[:, :, 599:], v[:, :, 599:], q)
+    from turboquant_pytorch.fused import attention_from_prepared
+    got = attention_from_prepared(q_rot, q_proj, kc, vc, ck, cv, out_dtype=torch.float32)
+    fk, fv = kc.compress(k), vc.compress(v)
+    ref = compressed_attention(q, kc, vc, fk, fv, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)

@@ -19,6 +19,7 @@
 //   memory, L2 resident) is the MFMA A operand and the LDS row tile is the B
 //   operand; the accumulator layout (4 consecutive output columns of one row per
 //   lane) is written straight back into the row tile.
+#include <algorithm>
 #include <type_traits>
 
 #include "tq_common.h"
@@ -161,7 +162,14 @@ struct KeyArgs {
   uint16_t *rn, *vn;
   float *y_out, *proj_out;
   int d;  // head dim, d <= D, d % 8 == 0
+  // output rows: input row (b, h, s) of S_in positions goes to (b * H + h) * ldo + off + s;
+  // ldo = 0 writes it to row (b, h, s)
+  int64_t S_in, ldo, off;
 };
+
+__device__ __forceinline__ int64_t map_row(int64_t gr, int64_t S_in, int64_t ldo, int64_t off) {
+  return ldo == 0 ? gr : (gr / S_in) * ldo + off + gr % S_in;
+}
 
 template <int D, int DT>
 __global__ void __launch_bounds__(256) compress_keys_kernel(KeyArgs a) {
@@ -243,8 +251,9 @@ __global__ void __launch_bounds__(256) compress_keys_kernel(KeyArgs a) {
       s_sc[r] = ldexpf(kSplit, -e2);  // residual scaled to norm in [0.5, 1)
       const int64_t gr = row0 + r;
       if (gr < a.n) {
-        a.rn[gr] = f2h(rn);
-        a.vn[gr] = f2h(s_vn[r]);
+        const int64_t orow = map_row(gr, a.S_in, a.ldo, a.off);
+        a.rn[orow] = f2h(rn);
+        a.vn[orow] = f2h(s_vn[r]);
       }
     }
   }
@@ -272,16 +281,17 @@ __global__ void __launch_bounds__(256) compress_keys_kernel(KeyArgs a) {
     const int r = e / (kw + sw), w = e % (kw + sw);
     const int64_t gr = row0 + r;
     if (gr >= a.n) continue;
+    const int64_t orow = map_row(gr, a.S_in, a.ldo, a.off);
     if (w < kw) {
       const uint32_t word = pack_word(idx + r * D, d, a.b, w);
-      if (whole) reinterpret_cast<uint32_t*>(a.codes + gr * kbytes)[w] = word;
-      else store_word_bytes(a.codes + gr * kbytes, w, kbytes, word);
+      if (whole) reinterpret_cast<uint32_t*>(a.codes + orow * kbytes)[w] = word;
+      else store_word_bytes(a.codes + orow * kbytes, w, kbytes, word);
     } else {
       const int ws = w - kw;
       uint32_t bits = 0;
       for (int k = 0; k < 32; ++k) bits |= (Bm[r * T::LDA + ws * 32 + k] >= 0.f ? 1u : 0u) << k;
-      if (whole) reinterpret_cast<uint32_t*>(a.signs + gr * sbytes)[ws] = bits;
-      else store_word_bytes(a.signs + gr * sbytes, ws, sbytes, bits);
+      if (whole) reinterpret_cast<uint32_t*>(a.signs + orow * sbytes)[ws] = bits;
+      else store_word_bytes(a.signs + orow * sbytes, ws, sbytes, bits);
     }
   }
   if (a.proj_out) {
@@ -304,6 +314,7 @@ struct ValArgs {
   uint16_t* vn;
   float* y_out;
   int d;  // head dim, d <= D, d % 8 == 0
+  int64_t S_in, ldo, off;  // output rows as in KeyArgs
 };
 
 template <int D, int DT>
@@ -324,7 +335,7 @@ __global__ void __launch_bounds__(256) compress_values_kernel(ValArgs a) {
     const int r = threadIdx.x / T::TPR;
     const float vn = sqrtf(ss);
     const int64_t gr = row0 + r;
-    if (threadIdx.x % T::TPR == 0 && gr < a.n) a.vn[gr] = f2h(vn);
+    if (threadIdx.x % T::TPR == 0 && gr < a.n) a.vn[map_row(gr, a.S_in, a.ldo, a.off)] = f2h(vn);
     const DivBy div(vn + 1e-8f);
     constexpr int PER = D / T::TPR;
     const int part = threadIdx.x % T::TPR;
@@ -355,9 +366,10 @@ __global__ void __launch_bounds__(256) compress_values_kernel(ValArgs a) {
     const int r = e / kw, w = e % kw;
     const int64_t gr = row0 + r;
     if (gr >= a.n) continue;
+    const int64_t orow = map_row(gr, a.S_in, a.ldo, a.off);
     const uint32_t word = pack_word(idx + r * D, d, a.b, w);
-    if (kbytes % 4 == 0) reinterpret_cast<uint32_t*>(a.codes + gr * kbytes)[w] = word;
-    else store_word_bytes(a.codes + gr * kbytes, w, kbytes, word);
+    if (kbytes % 4 == 0) reinterpret_cast<uint32_t*>(a.codes + orow * kbytes)[w] = word;
+    else store_word_bytes(a.codes + orow * kbytes, w, kbytes, word);
   }
 }
 
@@ -549,7 +561,20 @@ struct TileArgs {
   float *y_out, *proj_out;
   uint16_t* q_rot;
   float* q_proj;
+  // output rows: row (b, h, s) of the input goes to (b * H + h) * ldo + off + s of the packed and
+  // norm planes (a cache of ldo positions per (batch, head), filled from position off); ldo = 0
+  // writes row (b, h, s) to (b * H + h) * S + s
+  int64_t ldo, off;
 };
+
+// packed / norm plane row of input row gr (< 2^31); MAP = false: the kernel ignores ldo / off
+template <bool MAP>
+__device__ __forceinline__ int64_t out_row(const TileArgs& a, int64_t gr) {
+  if (!MAP || a.ldo == 0) return gr;
+  const uint32_t r32 = static_cast<uint32_t>(gr);
+  const uint32_t bh = a.S.div(r32);
+  return static_cast<int64_t>(bh) * a.ldo + a.off + (r32 - bh * a.S.d);
+}
 
 template <int D, int NW_ = 8>
 struct RT {
@@ -691,27 +716,47 @@ constexpr int row_waves() {
   return MODE == TM_VALUES && DT != TQ_F32 ? 16 : 8;
 }
 
-template <int D, int DT, int MODE, int BB>
-__global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(TileArgs a) {
-  using T = RT<D, row_waves<MODE, DT>()>;
-  constexpr bool DBUF = row_waves<MODE, DT>() <= 8;  // weight fragments double-buffered
+// LDS of one row-kernel block: the weight planes, each wave's output staging, centroids,
+// boundaries and the quantiser table.  Kernels declare it as raw bytes (a union of the three
+// modes' layouts in the fused append kernel).
+template <int D, int MODE, int BB, int NW>
+struct RowsSmem {
+  static constexpr int KC = D * BB / 8;                                         // packed code bytes per row
+  static constexpr int SC = D / 8;                                              // sign bytes per row
+  static constexpr int NPL = MODE == TM_KEYS ? 4 : (MODE == TM_VALUES ? 2 : 3);  // weight planes resident at once
+  static constexpr int STG = MODE == TM_QUERY ? 16 : 16 * (KC + (MODE == TM_KEYS ? SC : 0));  // wave staging bytes
+  static constexpr bool QTAB = MODE != TM_QUERY && BB >= 3;  // quantiser table built (3-4 code bits)
+  alignas(16) _Float16 wsm[NPL * D * D];
+  alignas(16) uint8_t stg_all[NW * STG];
+  alignas(16) float s_cent[MODE == TM_KEYS ? 16 : 1];
+  alignas(16) float s_bnd[MODE == TM_QUERY ? 1 : 16];
+  alignas(16) uint32_t s_qt[QTAB ? 512 : 2];  // (boundary bits, count) pairs
+};
+
+// One block of the row-owned kernels: block `block` of `nblocks` blocks that share the rows.
+// MAP: outputs go to the rows out_row<true> names (a cache append); the plain form keeps the
+// registers that mapping needs free for the tile loop.
+template <int D, int DT, int MODE, int BB, int NW_, bool MAP>
+__device__ __forceinline__ void rows_body(const TileArgs& a, RowsSmem<D, MODE, BB, NW_>& sm, int block,
+                                          int nblocks) {
+  using T = RT<D, NW_>;
+  using SM = RowsSmem<D, MODE, BB, NW_>;
+  constexpr bool DBUF = NW_ <= 8;  // weight fragments double-buffered
   constexpr int KS = T::KS, MB = T::MB, NW = T::NW;
-  constexpr int KC = D * BB / 8;                                         // packed code bytes per row
-  constexpr int SC = D / 8;                                              // sign bytes per row
-  constexpr int NPL = MODE == TM_KEYS ? 4 : (MODE == TM_VALUES ? 2 : 3);  // weight planes resident at once
-  constexpr int STG = MODE == TM_QUERY ? 16 : 16 * (KC + (MODE == TM_KEYS ? SC : 0));  // wave staging bytes
-  __shared__ __attribute__((aligned(16))) _Float16 wsm[NPL * D * D];
-  __shared__ __attribute__((aligned(16))) uint8_t stg_all[NW * STG];
-  __shared__ float s_cent[MODE == TM_KEYS ? 16 : 1], s_bnd[MODE == TM_QUERY ? 1 : 16];
-  constexpr bool QTAB = MODE != TM_QUERY && BB >= 3;  // quantiser table built (3-4 code bits)
-  __shared__ uint2 s_qt[QTAB ? 256 : 1];
+  constexpr int KC = SM::KC, SC = SM::SC, NPL = SM::NPL, STG = SM::STG;
+  constexpr bool QTAB = SM::QTAB;
+  _Float16* const wsm = sm.wsm;
+  uint8_t* const stg_all = sm.stg_all;
+  float* const s_cent = sm.s_cent;
+  float* const s_bnd = sm.s_bnd;
+  uint2* const s_qt = reinterpret_cast<uint2*>(sm.s_qt);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, g = lane >> 4;
   uint8_t* const stg = stg_all + wave * STG;  // this wave's 16 packed rows: codes, then signs
   const int64_t ntiles = (a.n + 15) / 16;
-  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * NW;
-  const int64_t gw = static_cast<int64_t>(blockIdx.x) * NW + wave;  // this wave's tiles: gw, gw + nwaves, ...
+  const int64_t nwaves = static_cast<int64_t>(nblocks) * NW;
+  const int64_t gw = static_cast<int64_t>(block) * NW + wave;  // this wave's tiles: gw, gw + nwaves, ...
   float br[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};  // BB <= 2: the boundaries in registers
   if constexpr (MODE != TM_QUERY) {
     constexpr int NC = 1 << BB;
@@ -850,12 +895,22 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
-  // copy `bytes`-byte rows of this wave's 16 staged rows at `src` to out + row0 * bytes
+  // copy `bytes`-byte rows of this wave's 16 staged rows at `src` to their output rows (one
+  // contiguous run when the output rows are the input rows)
   auto store_rows = [&](const uint8_t* src, uint8_t* out, int64_t row0, int bytes) {
     const int64_t nr = a.n - row0 < 16 ? a.n - row0 : 16;
     const int nd = static_cast<int>(nr) * bytes / 4;
-    uint32_t* dst = reinterpret_cast<uint32_t*>(out + row0 * bytes);
-    for (int i = lane; i < nd; i += 64) dst[i] = reinterpret_cast<const uint32_t*>(src)[i];
+    if (!MAP || a.ldo == 0) {
+      uint32_t* dst = reinterpret_cast<uint32_t*>(out + row0 * bytes);
+      for (int i = lane; i < nd; i += 64) dst[i] = reinterpret_cast<const uint32_t*>(src)[i];
+    } else {
+      const int wpr = bytes / 4;  // dwords per row (rows of d * b / 8 bytes, d = 64 or 128)
+      for (int i = lane; i < nd; i += 64) {
+        const int r = i / wpr;
+        reinterpret_cast<uint32_t*>(out + out_row<MAP>(a, row0 + r) * bytes)[i - r * wpr] =
+            reinterpret_cast<const uint32_t*>(src)[i];
+      }
+    }
   };
   // y = acc * ysc -> codes of this lane's 8 columns of k-step ks, staged at the row's packed
   // position; each(ks, j, acc value, code) sees every element
@@ -1024,7 +1079,7 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
       float vn_p = 0.f;
       auto flush = [&]() {
         const int64_t grp = tp * 16 + l16;
-        if (g == 0 && grp < a.n) a.vn[grp] = f2h(vn_p);
+        if (g == 0 && grp < a.n) a.vn[out_row<MAP>(a, grp)] = f2h(vn_p);
         wave_sync();
         store_rows(stg, a.codes, tp * 16, KC);
         wave_sync();
@@ -1076,8 +1131,9 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
       auto flush = [&]() {
         const int64_t grp = tp * 16 + l16;
         if (g == 0 && grp < a.n) {
-          a.vn[grp] = f2h(vn_p);
-          a.rn[grp] = f2h(rn_p);
+          const int64_t orow = out_row<MAP>(a, grp);
+          a.vn[orow] = f2h(vn_p);
+          a.rn[orow] = f2h(rn_p);
         }
         wave_sync();
         store_rows(stg, a.codes, tp * 16, KC);
@@ -1164,6 +1220,31 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
   }
 }
 
+template <int D, int DT, int MODE, int BB>
+__global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(TileArgs a) {
+  using SM = RowsSmem<D, MODE, BB, row_waves<MODE, DT>()>;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[sizeof(SM)];
+  rows_body<D, DT, MODE, BB, row_waves<MODE, DT>(), false>(a, *reinterpret_cast<SM*>(smem), blockIdx.x, gridDim.x);
+}
+
+// A cache append in one launch: blocks [0, nbk) compress the new keys, [nbk, nbk + nbv) the
+// new values, the rest prepare the new queries (nbq blocks, 0 without queries).  Every block
+// has 8 waves; the LDS holds one mode's layout at a time.
+template <int D, int DT, int KBB, int VB>
+__global__ void __launch_bounds__(512) append_kernel(TileArgs ka, TileArgs va, TileArgs qa, int nbk, int nbv,
+                                                     int nbq) {
+  using SK = RowsSmem<D, TM_KEYS, KBB, 8>;
+  using SV = RowsSmem<D, TM_VALUES, VB, 8>;
+  using SQ = RowsSmem<D, TM_QUERY, 1, 8>;
+  constexpr size_t BYTES = sizeof(SK) > sizeof(SV) ? (sizeof(SK) > sizeof(SQ) ? sizeof(SK) : sizeof(SQ))
+                                                   : (sizeof(SV) > sizeof(SQ) ? sizeof(SV) : sizeof(SQ));
+  __shared__ __attribute__((aligned(16))) uint8_t smem[BYTES];
+  const int blk = static_cast<int>(blockIdx.x);
+  if (blk < nbk) rows_body<D, DT, TM_KEYS, KBB, 8, true>(ka, *reinterpret_cast<SK*>(smem), blk, nbk);
+  else if (blk < nbk + nbv) rows_body<D, DT, TM_VALUES, VB, 8, true>(va, *reinterpret_cast<SV*>(smem), blk - nbk, nbv);
+  else rows_body<D, DT, TM_QUERY, 1, 8, false>(qa, *reinterpret_cast<SQ*>(smem), blk - nbk - nbv, nbq);
+}
+
 // Blocks of `kernel` the device holds at once (occupancy x compute units), per device.
 template <int D, int DT, int MODE, int BB>
 static void launch_tile(const TileArgs& a, hipStream_t s) {
@@ -1211,6 +1292,46 @@ template <>
 void dispatch_tile<TM_QUERY>(const TileArgs& a, int d, int dtype, int, hipStream_t s) {
   if (d == 64) launch_tile_dt<64, TM_QUERY, 1>(a, dtype, s);
   else launch_tile_dt<128, TM_QUERY, 1>(a, dtype, s);
+}
+
+// ---------------------------------------------------------------- cache append (one launch)
+template <int D, int DT, int KBB, int VB>
+static void launch_append(const TileArgs& ka, const TileArgs& va, const TileArgs& qa, hipStream_t s) {
+  static int cache[16] = {};
+  const int64_t res = resident_blocks(reinterpret_cast<const void*>(&append_kernel<D, DT, KBB, VB>), 512, cache);
+  // a block takes rounds of 128 rows; when the three modes need more blocks than the device holds
+  // at once, they share the resident blocks by work (a key row costs about two value or query rows)
+  auto rounds = [](int64_t n) { return (n + 127) / 128; };
+  int64_t nk = rounds(ka.n), nv = rounds(va.n), nq = rounds(qa.n);
+  if (nk + nv + nq > res) {
+    const double wk = 2.0 * static_cast<double>(ka.n), wv = static_cast<double>(va.n);
+    const double wq = static_cast<double>(qa.n), w = wk + wv + wq;
+    nk = std::max<int64_t>(1, std::min<int64_t>(nk, static_cast<int64_t>(res * wk / w)));
+    nv = std::max<int64_t>(1, std::min<int64_t>(nv, static_cast<int64_t>(res * wv / w)));
+    nq = qa.n > 0 ? std::max<int64_t>(1, std::min<int64_t>(nq, res - nk - nv)) : 0;
+  }
+  append_kernel<D, DT, KBB, VB><<<static_cast<unsigned>(nk + nv + nq), 512, 0, s>>>(
+      ka, va, qa, static_cast<int>(nk), static_cast<int>(nv), static_cast<int>(nq));
+}
+
+template <int D, int KBB, int VB>
+static void launch_append_dt(const TileArgs& ka, const TileArgs& va, const TileArgs& qa, int dtype, hipStream_t s) {
+  if (dtype == TQ_F32) launch_append<D, TQ_F32, KBB, VB>(ka, va, qa, s);
+  else if (dtype == TQ_F16) launch_append<D, TQ_F16, KBB, VB>(ka, va, qa, s);
+  else launch_append<D, TQ_BF16, KBB, VB>(ka, va, qa, s);
+}
+
+// head_dim 64 / 128, value bits 2-4 with key code bits one fewer (a compressor pair of one bit width)
+static void dispatch_append(const TileArgs& ka, const TileArgs& va, const TileArgs& qa, int d, int dtype, int vb,
+                            hipStream_t s) {
+  switch (d * 8 + vb) {
+    case 64 * 8 + 2: launch_append_dt<64, 1, 2>(ka, va, qa, dtype, s); break;
+    case 64 * 8 + 3: launch_append_dt<64, 2, 3>(ka, va, qa, dtype, s); break;
+    case 64 * 8 + 4: launch_append_dt<64, 3, 4>(ka, va, qa, dtype, s); break;
+    case 128 * 8 + 2: launch_append_dt<128, 1, 2>(ka, va, qa, dtype, s); break;
+    case 128 * 8 + 3: launch_append_dt<128, 2, 3>(ka, va, qa, dtype, s); break;
+    default: launch_append_dt<128, 3, 4>(ka, va, qa, dtype, s); break;
+  }
 }
 
 // ---------------------------------------------------------------- dispatch
@@ -1285,7 +1406,7 @@ int tq_compress_keys(const void* x, int32_t dtype, int32_t B, int32_t H, int32_t
     return launch_status("tq_compress_keys");
   }
   KeyArgs a{x, n, Rows4{H, S, sxb, sxh, sxs}, pi_split, seff_split, centroids, bounds, b_eff, codes, signs, rn, vn,
-            y_out, proj_out, d};
+            y_out, proj_out, d, S, 0, 0};
   TQ_SWITCH_DD(launch_keys, d, dtype, a, n, as_stream(stream));
   return launch_status("tq_compress_keys");
 }
@@ -1308,7 +1429,7 @@ int tq_compress_values(const void* x, int32_t dtype, int32_t B, int32_t H, int32
     dispatch_tile<TM_VALUES>(t, d, dtype, b, as_stream(stream));
     return launch_status("tq_compress_values");
   }
-  ValArgs a{x, n, Rows4{H, S, sxb, sxh, sxs}, pi_split, bounds, b, codes, vn, y_out, d};
+  ValArgs a{x, n, Rows4{H, S, sxb, sxh, sxs}, pi_split, bounds, b, codes, vn, y_out, d, S, 0, 0};
   TQ_SWITCH_DD(launch_values, d, dtype, a, n, as_stream(stream));
   return launch_status("tq_compress_values");
 }
@@ -1346,6 +1467,67 @@ int tq_query_prep(const void* q, int32_t dtype, int32_t B, int32_t Hq, int32_t S
   PrepArgs a{q, B, Hq, Sq, sqb, sqh, sqs, pi_split, s_eff_f16, q_rot, q_proj, d};
   TQ_SWITCH_DD(launch_prep, d, dtype, a, n, as_stream(stream));
   return launch_status("tq_query_prep");
+}
+
+int tq_cache_append(const void* k, const void* v, int32_t dtype, int32_t B, int32_t H, int32_t S, int32_t d,
+                    int64_t skb, int64_t skh, int64_t sks, int64_t svb, int64_t svh, int64_t svs,
+                    const uint16_t* key_pi_split, const uint16_t* key_seff_split, const float* key_centroids,
+                    const float* key_bounds, int32_t key_code_bits, const uint16_t* val_pi_split,
+                    const float* val_bounds, int32_t val_bits, uint8_t* key_codes, uint8_t* key_signs,
+                    uint16_t* key_rn, uint16_t* key_vn, uint8_t* val_codes, uint16_t* val_vn, int64_t capacity,
+                    int64_t pos, const void* q, int32_t Hq, int64_t sqb, int64_t sqh, int64_t sqs,
+                    const uint16_t* key_s_eff_f16, uint16_t* q_rot, float* q_proj, void* stream) {
+  TQ_CHECK_DD("tq_cache_append", d, dtype);
+  TQ_REQUIRE(key_code_bits >= 1 && key_code_bits <= 8 && val_bits >= 1 && val_bits <= 8,
+             "tq_cache_append: bits must be in [1, 8], got key code bits %d, value bits %d", key_code_bits, val_bits);
+  TQ_REQUIRE(B >= 0 && H >= 0 && S >= 0 && (!q || Hq >= 0), "tq_cache_append: bad shape");
+  TQ_REQUIRE(pos >= 0 && capacity >= pos + S, "tq_cache_append: rows [%lld, %lld) do not fit a capacity of %lld",
+             (long long)pos, (long long)(pos + S), (long long)capacity);
+  const int64_t n = static_cast<int64_t>(B) * H * S;
+  const int64_t nq = q ? static_cast<int64_t>(B) * Hq * S : 0;
+  if (n == 0 && nq == 0) return TQ_OK;
+  TQ_REQUIRE(n == 0 || (k && v && key_pi_split && key_seff_split && key_centroids && key_bounds && val_pi_split &&
+                        val_bounds && key_codes && key_signs && key_rn && key_vn && val_codes && val_vn),
+             "tq_cache_append: null pointer");
+  TQ_REQUIRE(nq == 0 || (key_pi_split && key_s_eff_f16 && q_rot && q_proj), "tq_cache_append: null query pointer");
+  hipStream_t st = as_stream(stream);
+  const bool aligned = reinterpret_cast<uintptr_t>(key_codes) % 4 == 0 && reinterpret_cast<uintptr_t>(key_signs) % 4 == 0 &&
+                       reinterpret_cast<uintptr_t>(val_codes) % 4 == 0 &&
+                       (nq == 0 || (reinterpret_cast<uintptr_t>(q_rot) % 8 == 0 && reinterpret_cast<uintptr_t>(q_proj) % 16 == 0));
+  if ((d == 64 || d == 128) && val_bits >= 2 && val_bits <= 4 && key_code_bits == val_bits - 1 && aligned &&
+      n < (int64_t(1) << 31) && nq < (int64_t(1) << 31) && (B * static_cast<int64_t>(H) * capacity) < (int64_t(1) << 40)) {
+    const uint32_t s1 = static_cast<uint32_t>(S > 0 ? S : 1);
+    TileArgs ka{}, va{}, qa{};
+    ka.x = k; ka.n = n; ka.H = make_div(static_cast<uint32_t>(H > 0 ? H : 1)); ka.S = make_div(s1);
+    ka.sb = skb; ka.sh = skh; ka.ss = sks; ka.vec = tile_vec(k, dtype, skb, skh, sks);
+    ka.w1 = key_pi_split; ka.w3 = key_seff_split; ka.cent = key_centroids; ka.bounds = key_bounds;
+    ka.codes = key_codes; ka.signs = key_signs; ka.rn = key_rn; ka.vn = key_vn; ka.ldo = capacity; ka.off = pos;
+    va.x = v; va.n = n; va.H = ka.H; va.S = ka.S;
+    va.sb = svb; va.sh = svh; va.ss = svs; va.vec = tile_vec(v, dtype, svb, svh, svs);
+    va.w1 = val_pi_split; va.bounds = val_bounds; va.codes = val_codes; va.vn = val_vn; va.ldo = capacity; va.off = pos;
+    qa.n = nq;
+    if (nq > 0) {
+      qa.x = q; qa.H = make_div(static_cast<uint32_t>(Hq)); qa.S = make_div(s1);
+      qa.sb = sqb; qa.sh = sqh; qa.ss = sqs; qa.vec = tile_vec(q, dtype, sqb, sqh, sqs);
+      qa.w1 = key_pi_split; qa.w2 = key_s_eff_f16; qa.q_rot = q_rot; qa.q_proj = q_proj;
+    }
+    dispatch_append(ka, va, qa, d, dtype, val_bits, st);
+    return launch_status("tq_cache_append");
+  }
+  // other head dims and bit widths: the tile kernels, writing the same mapped rows
+  if (n > 0) {
+    KeyArgs ka{k, n, Rows4{H, S, skb, skh, sks}, key_pi_split, key_seff_split, key_centroids, key_bounds,
+               key_code_bits, key_codes, key_signs, key_rn, key_vn, nullptr, nullptr, d, S, capacity, pos};
+    TQ_SWITCH_DD(launch_keys, d, dtype, ka, n, st);
+    ValArgs va{v, n, Rows4{H, S, svb, svh, svs}, val_pi_split, val_bounds, val_bits, val_codes, val_vn, nullptr, d,
+               S, capacity, pos};
+    TQ_SWITCH_DD(launch_values, d, dtype, va, n, st);
+    const int e = launch_status("tq_cache_append");
+    if (e != TQ_OK) return e;
+  }
+  if (nq > 0)
+    return tq_query_prep(q, dtype, B, Hq, S, d, sqb, sqh, sqs, key_pi_split, key_s_eff_f16, q_rot, q_proj, stream);
+  return TQ_OK;
 }
 
 }  // extern "C"

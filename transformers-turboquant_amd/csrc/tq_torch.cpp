@@ -373,6 +373,88 @@ std::tuple<Tensor, Tensor> query_prep(const Tensor& queries, const Tensor& pi_sp
   return {q_rot, q_proj};
 }
 
+// ---------------------------------------------------------------- compressed-cache append
+// New keys / values [B, H, S, D] compressed straight into rows [pos, pos + S) of a cache's
+// capacity planes ([B, H, capacity, ...], written in place), and the new queries [B, Hq, S, D]
+// prepared (empty outputs when no queries are given).  No reference counterpart: the reference
+// disables the KV cache (patch.py:81).
+std::tuple<Tensor, Tensor> cache_append_meta(const Tensor& k, const Tensor& v, const c10::optional<Tensor>& q,
+                                             const Tensor& kpi, const Tensor& kseff, const Tensor& kcent,
+                                             const Tensor& kbounds, int64_t key_code_bits, const Tensor& vpi,
+                                             const Tensor& vbounds, int64_t val_bits, const Tensor& kseff16,
+                                             const Tensor& kcodes, const Tensor& ksigns, const Tensor& krn,
+                                             const Tensor& kvn, const Tensor& vcodes, const Tensor& vvn, int64_t pos) {
+  const Checker c{"tq::cache_append", k.device()};
+  TORCH_CHECK(k.dim() == 4 && v.sizes() == k.sizes(), c.op, ": k and v must be [B, H, S, D] of one shape, got ",
+              k.sizes(), " and ", v.sizes());
+  c.same_device(v, "v");
+  TORCH_CHECK(key_code_bits >= 1 && key_code_bits <= 8 && val_bits >= 1 && val_bits <= 8, c.op,
+              ": bits must be 1..8");
+  const int64_t B = k.size(0), H = k.size(1), S = k.size(2), D = k.size(3);
+  TORCH_CHECK(kcodes.dim() == 4 && kcodes.size(0) == B && kcodes.size(1) == H, c.op,
+              ": key_codes must be [B, H, capacity, width] with B, H of the new keys, got ", kcodes.sizes());
+  const int64_t cap = kcodes.size(2), rows = B * H * cap;
+  TORCH_CHECK(pos >= 0 && pos + S <= cap, c.op, ": rows [", pos, ", ", pos + S, ") exceed the capacity ", cap);
+  c.plane(kcodes, "key_codes", at::kByte, rows, out_cols(D, key_code_bits));
+  c.plane(ksigns, "key_signs", at::kByte, rows, out_cols(D, 1));
+  c.plane(krn, "key residual norms", at::kHalf, rows);
+  c.plane(kvn, "key norms", at::kHalf, rows);
+  c.plane(vcodes, "value codes", at::kByte, rows, out_cols(D, val_bits));
+  c.plane(vvn, "value norms", at::kHalf, rows);
+  for (const Tensor* t : {&ksigns, &krn, &kvn, &vcodes, &vvn})
+    TORCH_CHECK(t->dim() >= 3 && t->size(0) == B && t->size(1) == H && t->size(2) == cap, c.op,
+                ": every cache plane must be [B, H, capacity, ...], got ", t->sizes());
+  c.table(kpi, "key split Pi", at::kHalf, 2 * D * D);
+  c.table(kseff, "key split S_eff", at::kHalf, 2 * D * D);
+  c.table(kcent, "key centroids", at::kFloat, int64_t{1} << key_code_bits);
+  c.table(kbounds, "key boundaries", at::kFloat, (int64_t{1} << key_code_bits) - 1);
+  c.table(vpi, "value split Pi", at::kHalf, 2 * D * D);
+  c.table(vbounds, "value boundaries", at::kFloat, (int64_t{1} << val_bits) - 1);
+  if (q.has_value() && q->defined()) {
+    c.same_device(*q, "q");
+    TORCH_CHECK(q->dim() == 4 && q->size(0) == B && q->size(2) == S && q->size(3) == D, c.op,
+                ": q must be [B, Hq, S, D] with B, S, D of the new keys, got ", q->sizes());
+    c.table(kseff16, "key f16 S_eff", at::kHalf, D * D);
+    return {at::empty({B, q->size(1), S, D}, q->options().dtype(at::kHalf)),
+            at::empty({B, q->size(1), S, D}, q->options().dtype(at::kFloat))};
+  }
+  return {at::empty({0}, k.options().dtype(at::kHalf)), at::empty({0}, k.options().dtype(at::kFloat))};
+}
+
+std::tuple<Tensor, Tensor> cache_append(const Tensor& k_in, const Tensor& v_in, const c10::optional<Tensor>& q_in,
+                                        const Tensor& kpi, const Tensor& kseff, const Tensor& kcent,
+                                        const Tensor& kbounds, int64_t key_code_bits, const Tensor& vpi,
+                                        const Tensor& vbounds, int64_t val_bits, const Tensor& kseff16,
+                                        const Tensor& kcodes, const Tensor& ksigns, const Tensor& krn,
+                                        const Tensor& kvn, const Tensor& vcodes, const Tensor& vvn, int64_t pos) {
+  cache_append_meta(k_in, v_in, q_in, kpi, kseff, kcent, kbounds, key_code_bits, vpi, vbounds, val_bits, kseff16,
+                    kcodes, ksigns, krn, kvn, vcodes, vvn, pos);
+  const c10::DeviceGuard g(k_in.device());
+  Tensor k = activation(k_in);
+  Tensor v = v_in.scalar_type() == k.scalar_type() && v_in.stride(-1) == 1 ? v_in : v_in.to(k.scalar_type()).contiguous();
+  const bool has_q = q_in.has_value() && q_in->defined();
+  Tensor q = has_q ? (q_in->scalar_type() == k.scalar_type() && q_in->stride(-1) == 1
+                          ? *q_in : q_in->to(k.scalar_type()).contiguous())
+                   : Tensor();
+  const int64_t B = k.size(0), H = k.size(1), S = k.size(2), D = k.size(3), cap = kcodes.size(2);
+  const int64_t Hq = has_q ? q.size(1) : 0;
+  Tensor q_rot = at::empty({has_q ? B : 0, Hq, S, D}, k.options().dtype(at::kHalf));
+  Tensor q_proj = at::empty({has_q ? B : 0, Hq, S, D}, k.options().dtype(at::kFloat));
+  check_status(tq_cache_append(k.data_ptr(), v.data_ptr(), dtype_code(k.scalar_type()), static_cast<int32_t>(B),
+                               static_cast<int32_t>(H), static_cast<int32_t>(S), static_cast<int32_t>(D), k.stride(0),
+                               k.stride(1), k.stride(2), v.stride(0), v.stride(1), v.stride(2), ptr<uint16_t>(kpi),
+                               ptr<uint16_t>(kseff), ptr<float>(kcent), ptr<float>(kbounds),
+                               static_cast<int32_t>(key_code_bits), ptr<uint16_t>(vpi), ptr<float>(vbounds),
+                               static_cast<int32_t>(val_bits), ptr<uint8_t>(kcodes), ptr<uint8_t>(ksigns),
+                               ptr<uint16_t>(krn), ptr<uint16_t>(kvn), ptr<uint8_t>(vcodes), ptr<uint16_t>(vvn), cap,
+                               pos, has_q ? q.data_ptr() : nullptr, static_cast<int32_t>(Hq),
+                               has_q ? q.stride(0) : 0, has_q ? q.stride(1) : 0, has_q ? q.stride(2) : 0,
+                               has_q ? ptr<uint16_t>(kseff16) : nullptr, has_q ? ptr<uint16_t>(q_rot) : nullptr,
+                               has_q ? ptr<float>(q_proj) : nullptr, stream_of(k)),
+               "TurboQuantCache.append");
+  return {q_rot, q_proj};
+}
+
 // ---------------------------------------------------------------- scores and attention
 Tensor scores_meta(const Tensor& q_rot, const Tensor& q_proj, const Tensor& codes, const Tensor& signs, const Tensor& rn,
                    const Tensor& vn, const Tensor& cent16, int64_t bits, int64_t hkv, int64_t sk, int64_t kv_stride,
@@ -484,6 +566,10 @@ TORCH_LIBRARY(tq, m) {
   m.def("decompress_values(Tensor codes, Tensor vn, Tensor pit_split, Tensor centroids, int bits, int[] shape) "
         "-> Tensor");
   m.def("query_prep(Tensor queries, Tensor pi_split, Tensor s_eff) -> (Tensor, Tensor)");
+  m.def("cache_append(Tensor k, Tensor v, Tensor? q, Tensor kpi, Tensor kseff, Tensor kcent, Tensor kbounds, "
+        "int key_code_bits, Tensor vpi, Tensor vbounds, int val_bits, Tensor kseff16, Tensor(a!) kcodes, "
+        "Tensor(b!) ksigns, Tensor(c!) krn, Tensor(d!) kvn, Tensor(e!) vcodes, Tensor(f!) vvn, int pos) "
+        "-> (Tensor, Tensor)");
   m.def("scores(Tensor q_rot, Tensor q_proj, Tensor codes, Tensor signs, Tensor rn, Tensor vn, Tensor centroids, "
         "int bits, int hkv, int sk, int kv_stride, float coeff) -> Tensor");
   m.def("attention(Tensor q_rot, Tensor q_proj, Tensor kcodes, Tensor ksigns, Tensor krn, Tensor kvn, "
@@ -502,6 +588,7 @@ TORCH_LIBRARY_IMPL(tq, CUDA, m) {
   m.impl("compress_values", &compress_values);
   m.impl("decompress_values", &decompress_values);
   m.impl("query_prep", &query_prep);
+  m.impl("cache_append", &cache_append);
   m.impl("scores", &scores);
   m.impl("attention", &attention);
 }
@@ -516,6 +603,7 @@ TORCH_LIBRARY_IMPL(tq, Meta, m) {
   m.impl("compress_values", &compress_values_meta);
   m.impl("decompress_values", &decompress_values_meta);
   m.impl("query_prep", &query_prep_meta);
+  m.impl("cache_append", &cache_append_meta);
   m.impl("scores", &scores_meta);
   m.impl("attention", &attention_meta);
 }

@@ -94,6 +94,15 @@ class TurboQuantCacheLayer(CacheLayerMixin):
     # ------------------------------------------------------------------ compressed storage
     def append(self, key_compressor, val_compressor, k: torch.Tensor, v: torch.Tensor) -> tuple[dict, dict]:
         """Compress k, v [B, Hkv, S, D], append them, and return dicts covering every cached position."""
+        ck, cv, _, _ = self.append_prepare(key_compressor, val_compressor, k, v)
+        return ck, cv
+
+    def append_prepare(self, key_compressor, val_compressor, k: torch.Tensor, v: torch.Tensor,
+                       q: torch.Tensor | None = None):
+        """append(), and on the GPU also the new queries q [B, Hq, S, D] prepared for scoring
+        (key_compressor.prepare_queries): (keys, values, q_rot, q_proj), the last two None on the
+        CPU or without q.  On the GPU the new rows are compressed straight into the capacity
+        planes and the queries prepared in the same launch (tq_cache_append)."""
         B, H, S, D = k.shape
         if self.shape is not None and self.length > 0 and self.shape != (B, H, D):
             raise ValueError(f"cache holds [B, Hkv, D] = {self.shape}, got {(B, H, D)}")
@@ -110,21 +119,31 @@ class TurboQuantCacheLayer(CacheLayerMixin):
         self.shape = (B, H, D)
         self.codec = codec
         if k.device.type != "cuda":
-            return self._append_cpu(key_compressor, val_compressor, k, v)
-        ck = key_compressor.compress(k)
-        cv = val_compressor.compress(v)
+            return (*self._append_cpu(key_compressor, val_compressor, k, v), None, None)
+        from turboquant_pytorch._ops import ops
+        from turboquant_pytorch.compressors import _tables
+
         need = self.length + S
-        if self.kp is None or need > self.capacity or self.kp["vec_norms"].shape[:2] != (B, H):
-            self._grow(need, ck, cv, B, H, S)
-        lo, hi = self.length, need
-        for name in _KEY_PLANES:
-            src = ck[name]
-            self.kp[name][:, :, lo:hi] = src.reshape(B, H, S, *src.shape[1:]) if src.dim() == 2 else src.reshape(B, H, S)
-        vi = cv["packed_indices"]
-        self.vp["packed_indices"][:, :, lo:hi] = vi.reshape(B, H, S, vi.shape[-1])
-        self.vp["vec_norms"][:, :, lo:hi] = cv["vec_norms"].reshape(B, H, S)
+        widths = (_cols(D, key_compressor.mse_bits), _cols(D, 1), _cols(D, val_compressor.bits))
+        if self.kp is None or need > self.capacity or self.kp["vec_norms"].shape[:2] != (B, H) or \
+                self._widths() != widths:
+            self._grow(need, B, H, widths, k.device)
+        tk = _tables(key_compressor, k.device, with_qjl=True)
+        tv = _tables(val_compressor, k.device, with_qjl=False)
+        q_rot, q_proj = ops().cache_append(
+            k, v, q, tk.pi_split, tk.seff_split, tk.cent32, tk.bounds32, key_compressor.mse_bits, tv.pi_split,
+            tv.bounds32, val_compressor.bits, tk.s_eff16, self.kp["packed_key_indices"], self.kp["packed_qjl_signs"],
+            self.kp["residual_norm"], self.kp["vec_norms"], self.vp["packed_indices"], self.vp["vec_norms"],
+            self.length)
         self.length = need
-        return self.strided()
+        ck, cv = self.strided()
+        return (ck, cv, q_rot, q_proj) if q is not None else (ck, cv, None, None)
+
+    def _widths(self) -> tuple | None:
+        if self.kp is None:
+            return None
+        return (self.kp["packed_key_indices"].shape[-1], self.kp["packed_qjl_signs"].shape[-1],
+                self.vp["packed_indices"].shape[-1])
 
     def strided(self) -> tuple[dict, dict]:
         """GPU dicts over the capacity planes: attend the first `length` rows (kv_stride = capacity)."""
@@ -170,7 +189,8 @@ class TurboQuantCacheLayer(CacheLayerMixin):
             self.cpu_k, self.cpu_v = keys, values
             self.length = S
             return
-        self._grow(S, keys, values, B, H, S)
+        self._grow(S, B, H, (keys["packed_key_indices"].shape[-1], keys["packed_qjl_signs"].shape[-1],
+                             values["packed_indices"].shape[-1]), dev)
         n = B * H * S
         for name in _KEY_PLANES:
             src = keys[name]
@@ -181,18 +201,20 @@ class TurboQuantCacheLayer(CacheLayerMixin):
         self.vp["vec_norms"][:, :, :S] = values["vec_norms"].reshape(B, H, S)
         self.length = S
 
-    def _grow(self, need: int, ck: dict, cv: dict, B: int, H: int, S: int) -> None:
+    def _grow(self, need: int, B: int, H: int, widths: tuple, dev) -> None:
+        """Capacity planes for at least `need` positions (row widths: key codes, signs, value
+        codes), keeping the cached rows."""
         cap = max(need, 2 * self.capacity, _ROUND)
         cap = (cap + _ROUND - 1) // _ROUND * _ROUND
-        dev = ck["vec_norms"].device
+        kw, sw, vw = widths
         kp = {
-            "packed_key_indices": torch.zeros(B, H, cap, ck["packed_key_indices"].shape[-1], dtype=torch.uint8, device=dev),
-            "packed_qjl_signs": torch.zeros(B, H, cap, ck["packed_qjl_signs"].shape[-1], dtype=torch.uint8, device=dev),
+            "packed_key_indices": torch.zeros(B, H, cap, kw, dtype=torch.uint8, device=dev),
+            "packed_qjl_signs": torch.zeros(B, H, cap, sw, dtype=torch.uint8, device=dev),
             "residual_norm": torch.zeros(B, H, cap, dtype=torch.float16, device=dev),
             "vec_norms": torch.zeros(B, H, cap, dtype=torch.float16, device=dev),
         }
         vp = {
-            "packed_indices": torch.zeros(B, H, cap, cv["packed_indices"].shape[-1], dtype=torch.uint8, device=dev),
+            "packed_indices": torch.zeros(B, H, cap, vw, dtype=torch.uint8, device=dev),
             "vec_norms": torch.zeros(B, H, cap, dtype=torch.float16, device=dev),
         }
         if self.kp is not None and self.length > 0:
@@ -226,6 +248,11 @@ class TurboQuantCacheLayer(CacheLayerMixin):
             self.cpu_k = _select_cpu(self.cpu_k, idx)
             self.cpu_v = _select_cpu(self.cpu_v, idx)
             self.shape = (int(idx.numel()),) + self.shape[1:]
+
+
+def _cols(d: int, b: int) -> int:
+    """Bytes of a packed row of d b-bit codes (bit_ops.py:162-164)."""
+    return (d * b + 7) // 8
 
 
 def _cat_cpu(a: dict, b: dict) -> dict:
@@ -291,6 +318,14 @@ class TurboQuantCache(Cache):
         if layer_idx is None:
             raise ValueError("TurboQuantCache needs attention modules with a layer_idx")
         return self.layer(layer_idx).append(key_compressor, val_compressor, k, v)
+
+    def append_prepare(self, layer_idx: int, key_compressor, val_compressor, k: torch.Tensor, v: torch.Tensor,
+                       q: torch.Tensor | None = None):
+        """append() plus the new queries prepared in the same launch on the GPU:
+        (keys, values, q_rot, q_proj) (see TurboQuantCacheLayer.append_prepare)."""
+        if layer_idx is None:
+            raise ValueError("TurboQuantCache needs attention modules with a layer_idx")
+        return self.layer(layer_idx).append_prepare(key_compressor, val_compressor, k, v, q)
 
     def save(self, path, metadata: dict | None = None) -> None:
         """Write every non-empty layer's cached positions to `path` (format turboquant-kv, one

@@ -23,7 +23,7 @@ import math
 import torch
 import torch.nn.functional as F
 
-from turboquant_pytorch.fused import compressed_attention
+from turboquant_pytorch.fused import attention_from_prepared, compressed_attention
 
 from ..cache import TurboQuantCache
 
@@ -62,16 +62,23 @@ def attention_tail(module, q, k, v, attention_mask, output_attentions: bool = Fa
     drop_active = dropout is not None and module.training and dropout.p > 0
     kc, vc = module.key_compressor, module.val_compressor
 
+    fused = q.device.type == "cuda" and not output_attentions and not drop_active
     cached = None  # (compressed keys, compressed values) of every cached position
     if isinstance(cache, TurboQuantCache):
+        if fused:
+            # one launch compresses the new keys / values into the cache and prepares the queries
+            ck, cv, q_rot, q_proj = cache.append_prepare(module.layer_idx, kc, vc, k, v, q)
+            out = attention_from_prepared(q_rot, q_proj, kc, vc, ck, cv, attention_mask=mask, causal=causal,
+                                          scale=1.0 / math.sqrt(D), out_dtype=q.dtype)
+            return out.reshape(B, T, Hq * D), None
         cached = cache.append(module.layer_idx, kc, vc, k, v)
         lay = cache.layer(module.layer_idx)
     elif cache is not None:
         k, v = cache.update(k, v, module.layer_idx)
     S = cached[0]["shape"][2] if cached is not None else k.shape[2]
 
-    if q.device.type == "cuda" and not output_attentions and not drop_active:
-        ck, cv = cached if cached is not None else (kc.compress(k), vc.compress(v))
+    if fused:
+        ck, cv = kc.compress(k), vc.compress(v)
         out = compressed_attention(q, kc, vc, ck, cv, attention_mask=mask, causal=causal,
                                    scale=1.0 / math.sqrt(D), out_dtype=q.dtype)
         return out.reshape(B, T, Hq * D), None

@@ -43,6 +43,9 @@ _SIGNATURES = {
                            _p, _p, _i32, _p, _p, _p, _p],
     "tq_decompress_values": [_p, _p, _i64, _i32, _p, _p, _i32, _p, _i32, _i64, _p],
     "tq_query_prep": [_p, _i32, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _p, _p, _p, _p, _p],
+    "tq_cache_append": [_p, _p, _i32, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _i64, _i64,
+                        _p, _p, _p, _p, _i32, _p, _p, _i32, _p, _p, _p, _p, _p, _p, _i64, _i64,
+                        _p, _i32, _i64, _i64, _i64, _p, _p, _p, _p],
     "tq_attention_scores": [_p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32,
                             _i32, _f32, _p, _p],
     "tq_attention_fwd": [_p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _p, _i32, _p,
