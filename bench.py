@@ -635,7 +635,7 @@ def decode_step_leg(kc, vc, steps: int = 200) -> dict:
 
 def head_dim64_leg(steps: int, warmup: int) -> dict:
     """The head_dim-64 path (GPT-2's attention, BASELINE.json configs[0]'s shape: 12 heads, bits 3)
-    through the tiled kernel: one layer's compress K / V + query prep + fused attention per step,
+    through the prefill kernel at head_dim 64: one layer's compress K / V + query prep + fused attention per step,
     at configs[0]'s 512 tokens and at 8192 tokens (causal), HIP events around the attention call
     and around the whole step."""
     import torch
@@ -679,8 +679,8 @@ def head_dim64_leg(steps: int, warmup: int) -> dict:
         tflops = key_heads * 6 * d / (attn_ms * 1e-3) / 1e12
         out[f"S{S_}"] = {"step_ms": step_ms, "attention_ms": attn_ms, "attention_tflops": tflops,
                          "mfma_frac": tflops / MFMA_F16_PEAK_TFLOPS}
-    return {"workload": f"GPT-2 attention shape: B1 x {h} heads x d{d}, bits {BITS}, causal; tiled kernel "
-                        "tq::attn_kernel<64, 2, false, false>", **out}
+    return {"workload": f"GPT-2 attention shape: B1 x {h} heads x d{d}, bits {BITS}, causal; "
+                        "tq::prefill_kernel<64, 3, false> (q_proj as f16 hi + lo)", **out}
 
 
 def model_leg(steps: int = 3, S_model: int = 8192, bits: int = BITS) -> dict:

@@ -562,7 +562,7 @@ bool prefill_applies(int Hq, int Hkv, int d, int bits, int val_bits, bool masked
 int prefill_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, const uint8_t* kcodes,
                       const uint8_t* ksigns, const uint16_t* krn, const uint16_t* kvn, const uint16_t* kcent,
                       int bits, const uint8_t* vcodes, const uint16_t* vvn, const float* vcent,
-                      const uint16_t* vpit, int B, int Hq, int Hkv, int Sq, int Sk, float coeff, float scale,
+                      const uint16_t* vpit, int B, int Hq, int Hkv, int Sq, int Sk, int d, float coeff, float scale,
                       int causal, const float* mask, int64_t smb, int64_t smh, int64_t smq, int64_t smk, void* out,
                       int out_dtype, int64_t sob, int64_t soh, int64_t sos, hipStream_t s);
 int decode_scores(int64_t ldk, const uint16_t* q_rot, const float* q_proj, const uint8_t* kcodes,
@@ -683,7 +683,7 @@ int tq_attention_fwd_kv(const uint16_t* q_rot, const float* q_proj, const uint8_
                             workspace, as_stream(stream));
   if (prefill_applies(Hq, Hkv, d, bits, val_bits, mask != nullptr))
     return prefill_attention(ldk, q_rot, q_proj, key_codes, key_signs, key_rn, key_vn, key_centroids_f16, bits,
-                             val_codes, val_vn, val_centroids, val_pit_split, B, Hq, Hkv, Sq, Sk, coeff, scale,
+                             val_codes, val_vn, val_centroids, val_pit_split, B, Hq, Hkv, Sq, Sk, d, coeff, scale,
                              causal, mask, smb, smh, smq, smk, out, out_dtype, sob, soh, sos, as_stream(stream));
   st = check_group("tq_attention_fwd", Hq, Hkv, d, false);
   if (st != TQ_OK) return st;

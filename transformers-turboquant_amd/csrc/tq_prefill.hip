@@ -1,4 +1,4 @@
-// Fused compressed-domain attention for many query rows (prefill), head_dim 128.
+// Fused compressed-domain attention for many query rows (prefill), head_dim 64 and 128.
 //
 // Same estimator and output as tq_attn.hip's tiled kernel (scores from packed
 // keys, online softmax, P.V over packed values, Pi_v applied once per output
@@ -26,6 +26,9 @@
 //    out of v_mfma_f32_16x16x32_f16 with 4 consecutive keys of one column per
 //    lane, the P^T operand layout of O^T += V^T P^T, so P stays in registers.
 //    P = f16(2^(s - m)) enters the P.V product (one f16 rounding, P <= 2^TAU).
+//  * q_proj enters the QJL term as f16 hi + lo (two MFMAs against the exact +-1 signs, f32
+//    grade) at head_dim 64; at head_dim 128 the lo fragments do not fit the registers of two
+//    column blocks per wave and q_proj is rounded once to f16.
 #include "tq_common.h"
 #include "tq_stream.h"
 
@@ -39,10 +42,13 @@ constexpr int kPfWaves = 4;  // waves per block, each with two 16-column blocks:
 // 16-column MFMA blocks per wave: 2, or 1 with an additive mask
 template <bool MASK>
 constexpr int pf_nbw() { return MASK ? 1 : 2; }
+// q_proj as an f16 (hi, lo) pair: where the lo fragments fit the registers
+template <int D>
+constexpr bool pf_qlo() { return D <= 64; }
 
 struct PrefillArgs {
   const uint16_t* q_rot;
-  const float* q_proj;  // f32; this kernel's term-2 operand is its f16 rounding
+  const float* q_proj;  // f32: f16 hi + lo operands at head_dim 64, its f16 rounding at 128
   const uint8_t *kcodes, *ksigns;
   const uint16_t *krn, *kvn, *kcent;  // f16 key centroids
   const uint8_t* vcodes;
@@ -59,9 +65,10 @@ struct PrefillArgs {
   int64_t sob, soh, sos;
 };
 
-template <int BITS>
+template <int D_, int BITS>
 struct PfCfg {
-  static constexpr int D = 128, KT = 32, R = kPfRing, NW = kPfWaves, NT = 64 * NW;
+  static constexpr int D = D_, KT = 32, R = kPfRing, NW = kPfWaves, NT = 64 * NW;
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
   static_assert(NW == 4 || NW == 8, "4 or 8 waves per block");
   static constexpr int KB = BITS - 1, VB = BITS;
   static constexpr int KC = D * KB / 8, SC = D / 8, VC = D * VB / 8;  // bytes per packed row
@@ -80,7 +87,8 @@ struct PfCfg {
   static constexpr int T_SGN = 0, T_KEY = 128;
   static constexpr int T_VAL = T_KEY + (KB == 1 ? 128 : (KB == 2 ? 64 : 256));
   static constexpr int T_BYTES = T_VAL + (VB == 2 ? 64 : (VB == 3 ? 256 : 1024));
-  static_assert(KT * SC == 512, "sign plane is half a DMA round");
+  static_assert((KT * KC) % 256 == 0 && (KT * SC) % 256 == 0 && (KT * VC) % 256 == 0,
+                "planes of whole 16-byte chunks per lane");
 };
 
 // 32 bits of a packed row from byte `off` on: the dword pair around it, byte-aligned
@@ -96,10 +104,11 @@ constexpr uint32_t odd_fields() {
   return VB == 2 ? 0xCCCCu : (VB == 3 ? 0xE38E38u : 0xF0F0F0F0u);
 }
 
-template <int BITS, bool MASK>
+template <int D_, int BITS, bool MASK>
 __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2))) prefill_kernel(PrefillArgs a) {
-  using C = PfCfg<BITS>;
+  using C = PfCfg<D_, BITS>;
   constexpr int D = C::D, KT = C::KT, R = C::R, KB = C::KB, VB = C::VB;
+  constexpr bool QLO = pf_qlo<D>();
   constexpr int KC = C::KC, SC = C::SC, VC = C::VC, LDK = C::LDK, LDV = C::LDV;
   constexpr int KS = D / 32, DB = D / 16, NT = C::NT, NBW = pf_nbw<MASK>();  // 16 columns per block
   constexpr float LOG2E = 1.4426950408889634f;
@@ -161,6 +170,7 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
   int col_i[NBW], col_h[NBW];
   bool col_ok[NBW];
   half8 qr[KS][NBW], qp[KS][NBW];
+  [[maybe_unused]] half8 qlo[QLO ? KS : 1][NBW];
 #pragma unroll
   for (int nb = 0; nb < NBW; ++nb) {
     const int r = (wave * NBW + nb) * 16 + l16;
@@ -173,7 +183,14 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
     for (int ks = 0; ks < KS; ++ks) {
       const int d0 = ks * 32 + lg * 8;
       qr[ks][nb] = col_ok[nb] ? *reinterpret_cast<const half8*>(a.q_rot + qrow + d0) : half8{};
-      qp[ks][nb] = col_ok[nb] ? round8(a.q_proj + qrow + d0) : half8{};
+      if constexpr (QLO) {
+        half8 hi = half8{}, lo = half8{};
+        if (col_ok[nb]) split8(a.q_proj + qrow + d0, hi, lo);
+        qp[ks][nb] = hi;
+        qlo[ks][nb] = lo;
+      } else {
+        qp[ks][nb] = col_ok[nb] ? round8(a.q_proj + qrow + d0) : half8{};
+      }
     }
   }
   // additive-mask rows of this lane's columns (row 0 for padding columns, whose scores are
@@ -214,7 +231,8 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       if (c >= nrounds) break;
-      if ((c + 1) * 1024 <= bytes || lane < 32) dma16(r, dst + c * 1024, lo + c * 1024);
+      // whole rounds need no lane test; a partial round's lanes cover its remaining bytes
+      if ((c + 1) * 1024 <= bytes || lane * 16 < bytes - c * 1024) dma16(r, dst + c * 1024, lo + c * 1024);
     }
   };
   auto issue = [&](int j) __attribute__((always_inline)) {  // wave 0 only
@@ -241,9 +259,10 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
   // slot past the last tile decodes stale bytes into a buffer nobody reads)
   auto decode_ks = [&](int j, _Float16* dK, _Float16* dS) __attribute__((always_inline)) {  // item (key, 8-dim group)
     const uint8_t* raw = ring + (j % R) * C::SLOT;
+    constexpr int NG = D / 8;  // 8-dim groups per row
 #pragma unroll
-    for (int rep = 0; rep < 512 / NT; ++rep) {
-      const int i = tid + rep * NT, key = i >> 4, g = i & 15;
+    for (int rep = 0; rep < KT * NG / NT; ++rep) {
+      const int i = tid + rep * NT, key = i / NG, g = i % NG;  // NG a power of two: shifts
       half8 kv;
       if constexpr (KB == 1) {
         kv = nib2x4<0>(tK, raw[C::OFF_K + key * KC + g]);
@@ -259,12 +278,15 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
   };
   auto decode_v = [&](int j, _Float16* dV, float (*dF)[KT]) __attribute__((always_inline)) {
     const uint8_t* raw = ring + (j % R) * C::SLOT;
+    constexpr int NG = D / 8;  // 8-dim groups per row
 #pragma unroll
-    for (int rep = 0; rep < 512 / NT; ++rep) {
+    for (int rep = 0; rep < 2 * (KT / 2) * NG / NT; ++rep) {
       // values: item (key pair kp, 8-dim group dg, parity par) -> dwords (C[code 2kp], C[code 2kp+1])
       // of the even (par 0) or odd (par 1) dims of the group
-      static_assert(NT == 256, "item (kp, dg, par) = (tid & 15, tid >> 4, rep)");
-      const int kp = tid & 15, dg = tid >> 4, par = rep;
+      static_assert(NT == 256, "items i = tid + 256 rep: kp = i % 16, dg = (i / 16) % NG, par = i / (16 NG)");
+      const int i = tid + rep * NT;
+      // (tid < 256: at head_dim 128 the item is (tid & 15, tid >> 4, rep))
+      const int kp = tid & 15, dg = NG == 16 ? (tid >> 4) : ((i >> 4) % NG), par = NG == 16 ? rep : ((i >> 4) / NG);
       const uint8_t* r0 = raw + C::OFF_V + (2 * kp) * VC;
       const uint32_t w0 = field32(r0, dg * VB), w1 = field32(r0 + VC, dg * VB);
       constexpr uint32_t M = odd_fields<VB>();
@@ -338,6 +360,7 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
       for (int nb = 0; nb < NBW; ++nb) {
         sacc[mb][nb] = mfma16x16x32(ka[c], qr[ks][nb], sacc[mb][nb]);
         tacc[mb][nb] = mfma16x16x32(sa[c], qp[ks][nb], tacc[mb][nb]);
+        if constexpr (QLO) tacc[mb][nb] = mfma16x16x32(sa[c], qlo[ks][nb], tacc[mb][nb]);
       }
     }
   };
@@ -590,13 +613,13 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
 // Used by tq_attn.hip's entry points.
 bool prefill_applies(int Hq, int Hkv, int d, int bits, int val_bits, bool masked) {
   const int cols = kPfWaves * 16 * (masked ? pf_nbw<true>() : pf_nbw<false>());
-  return d == 128 && bits >= 2 && bits <= 4 && val_bits == bits && Hq / Hkv <= cols;
+  return (d == 64 || d == 128) && bits >= 2 && bits <= 4 && val_bits == bits && Hq / Hkv <= cols;
 }
 
 int prefill_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, const uint8_t* kcodes,
                       const uint8_t* ksigns, const uint16_t* krn, const uint16_t* kvn, const uint16_t* kcent,
                       int bits, const uint8_t* vcodes, const uint16_t* vvn, const float* vcent,
-                      const uint16_t* vpit, int B, int Hq, int Hkv, int Sq, int Sk, float coeff, float scale,
+                      const uint16_t* vpit, int B, int Hq, int Hkv, int Sq, int Sk, int d, float coeff, float scale,
                       int causal, const float* mask, int64_t smb, int64_t smh, int64_t smq, int64_t smk, void* out,
                       int out_dtype, int64_t sob, int64_t soh, int64_t sos, hipStream_t s) {
   PrefillArgs a{};
@@ -617,7 +640,7 @@ int prefill_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, c
   a.Sq = Sq;
   a.Sk = Sk;
   a.G = Hq / Hkv;
-  a.QT = PfCfg<3>::NW * 16 * (mask ? pf_nbw<true>() : pf_nbw<false>()) / a.G;  // query rows per block
+  a.QT = kPfWaves * 16 * (mask ? pf_nbw<true>() : pf_nbw<false>()) / a.G;  // query rows per block
   a.nqb = (Sq + a.QT - 1) / a.QT;
   a.ldk = ldk;
   a.coeff = coeff;
@@ -634,12 +657,18 @@ int prefill_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, c
   a.soh = soh;
   a.sos = sos;
   const dim3 grid(a.nqb, Hkv, B);
-#define TQ_PF_LAUNCH(BB)                                                   \
-  if (mask) prefill_kernel<BB, true><<<grid, PfCfg<BB>::NT, 0, s>>>(a);  \
-  else prefill_kernel<BB, false><<<grid, PfCfg<BB>::NT, 0, s>>>(a);
-  if (bits == 2) { TQ_PF_LAUNCH(2) }
-  else if (bits == 3) { TQ_PF_LAUNCH(3) }
-  else { TQ_PF_LAUNCH(4) }
+#define TQ_PF_LAUNCH(DD, BB)                                                       \
+  if (mask) prefill_kernel<DD, BB, true><<<grid, PfCfg<DD, BB>::NT, 0, s>>>(a);  \
+  else prefill_kernel<DD, BB, false><<<grid, PfCfg<DD, BB>::NT, 0, s>>>(a);
+  if (d == 64) {
+    if (bits == 2) { TQ_PF_LAUNCH(64, 2) }
+    else if (bits == 3) { TQ_PF_LAUNCH(64, 3) }
+    else { TQ_PF_LAUNCH(64, 4) }
+  } else {
+    if (bits == 2) { TQ_PF_LAUNCH(128, 2) }
+    else if (bits == 3) { TQ_PF_LAUNCH(128, 3) }
+    else { TQ_PF_LAUNCH(128, 4) }
+  }
 #undef TQ_PF_LAUNCH
   return launch_status("tq_attention_fwd (prefill)");
 }
