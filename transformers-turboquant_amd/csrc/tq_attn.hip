@@ -55,10 +55,12 @@ struct ATile {
   static constexpr int DB = D / 16;              // 16-dim blocks
   static constexpr int LDK = D + 8;              // f16 row stride of decoded key / sign tiles
   static constexpr int LDV = KT + 8;             // f16 row stride of the V^T tile
-  // raw planes of a tile as a byte stream (rows of d*b/8 bytes, not dword aligned in
-  // general), staged from the dword-aligned address at or below the tile's first byte;
-  // 8 bytes of slack cover that shift and the dword-pair reads of the last row
-  static constexpr int KRAW = KT * D * 3 / 8 + 8, SRAW = KT * D / 8 + 8, VRAW = KT * D * 4 / 8 + 8;
+  // raw planes of a tile in LDS, either as rows padded by one dword (head dims that are a
+  // multiple of 32: dword-aligned rows, and the pad spreads the decode's row-strided reads
+  // over the banks) or as a byte stream (other head dims: rows of d*b/8 bytes, staged from
+  // the dword at or below the tile's first byte); slack covers the stream's shift and the
+  // dword-pair reads of the last row
+  static constexpr int KRAW = KT * (D * 3 / 8 + 4) + 8, SRAW = KT * (D / 8 + 4) + 8, VRAW = KT * (D * 4 / 8 + 4) + 8;
   static constexpr int KREG = (KRAW / 4 + NT - 1) / NT;  // per-thread dwords of a tile
   static constexpr int SREG = (SRAW / 4 + NT - 1) / NT;
   static constexpr int VREG = (VRAW / 4 + NT - 1) / NT;
@@ -104,7 +106,9 @@ __device__ __forceinline__ void store4(void* out, int64_t o, float4v v, int n) {
     if (e < n) store_act<DT>(out, o + e, v[e]);
 }
 
-template <int D, int KB, bool SCORES, bool MASK>
+// STREAM: head dims that are not a multiple of 32 (byte-stream staging, run-time d); otherwise
+// d = D and rows are staged padded
+template <int D, int KB, bool SCORES, bool MASK, bool STREAM>
 __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
   using T = ATile<D, SCORES>;
   constexpr int KT = T::KT, NBW = T::NBW, KS = T::KS, MBK = T::MBK, DB = T::DB, NT = T::NT;
@@ -131,7 +135,7 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
   const int qblk = a.nqb - 1 - static_cast<int>(blockIdx.x);  // heavy causal blocks first
   const int hkv = blockIdx.y, b = blockIdx.z;
   const int q0 = qblk * a.QT;
-  const int d = a.d;
+  const int d = STREAM ? a.d : D;
   const int KC = d * KB / 8, SC = d / 8, vc = d * a.vb / 8;  // bytes per packed row
   const int ng = d / 8;                                       // real 8-dim groups
   const int64_t bh_kv = static_cast<int64_t>(b) * a.Hkv + hkv;
@@ -197,12 +201,28 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
   uint32_t rk[T::KREG], rs[T::SREG], rv[SCORES ? 1 : T::VREG];
   float r_a = 0.f, r_b = 0.f, r_v = 0.f;
   auto fetch_stream = [&](const uint8_t* plane, int k0, int rowbytes, int bytes, uint32_t* regs, int nreg) {
-    const int shift = shift_of(plane, k0, rowbytes);
+    // STREAM: from the dword holding the tile's first byte; otherwise rows are whole dwords
+    const int shift = STREAM ? shift_of(plane, k0, rowbytes) : 0;
     const uint32_t* g = reinterpret_cast<const uint32_t*>(plane + (plane_off(k0, rowbytes) - shift));
     const int ndw = (shift + bytes + 3) >> 2;  // dwords holding the tile's bytes
     for (int j = 0; j < nreg; ++j) {
       const int w = tid + j * NT;
       regs[j] = (w < ndw) ? g[w] : 0u;
+    }
+  };
+  // staged dwords -> LDS: contiguous (STREAM) or rows of `rowbytes` padded to rowbytes + 4
+  auto stash_stream = [&](uint8_t* dst, int rowbytes, int raw_bytes, const uint32_t* regs, int nreg) {
+    for (int j = 0; j < nreg; ++j) {
+      const int w = tid + j * NT;
+      if constexpr (STREAM) {
+        if (w < raw_bytes / 4) reinterpret_cast<uint32_t*>(dst)[w] = regs[j];
+      } else {
+        const int wpr = rowbytes / 4;
+        if (w < KT * wpr) {
+          const int row = w / wpr, col = w - row * wpr;
+          *reinterpret_cast<uint32_t*>(dst + row * (rowbytes + 4) + col * 4) = regs[j];
+        }
+      }
     }
   };
   auto fetch = [&](int k0) {
@@ -221,23 +241,9 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
     }
   };
   auto stash = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < T::KREG; ++j) {
-      const int w = tid + j * NT;
-      if (w < T::KRAW / 4) reinterpret_cast<uint32_t*>(rawK[buf])[w] = rk[j];
-    }
-#pragma unroll
-    for (int j = 0; j < T::SREG; ++j) {
-      const int w = tid + j * NT;
-      if (w < T::SRAW / 4) reinterpret_cast<uint32_t*>(rawS[buf])[w] = rs[j];
-    }
-    if constexpr (!SCORES) {
-#pragma unroll
-      for (int j = 0; j < T::VREG; ++j) {
-        const int w = tid + j * NT;
-        if (w < T::VRAW / 4) reinterpret_cast<uint32_t*>(rawV[buf])[w] = rv[j];
-      }
-    }
+    stash_stream(rawK[buf], KC, T::KRAW, rk, T::KREG);
+    stash_stream(rawS[buf], SC, T::SRAW, rs, T::SREG);
+    if constexpr (!SCORES) stash_stream(rawV[buf], vc, T::VRAW, rv, T::VREG);
     if (tid < KT) {
       skA[buf][tid] = r_a;
       skB[buf][tid] = r_b;
@@ -266,27 +272,31 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
     __syncthreads();  // tile k0 staged in buffer `cur`; previous tile's decoded tiles consumed
     // ---- decode this tile once per block: K^ and sign tiles [key][dim], V^T [dim][key];
     // groups past d decode to zeros
-    const int shk = shift_of(a.kcodes, k0, KC);
-    const int shs = shift_of(a.ksigns, k0, SC);
+    // row r of a plane starts at byte sh + r * rp of its staged copy
+    const int shk = STREAM ? shift_of(a.kcodes, k0, KC) : 0, rpk = STREAM ? KC : KC + 4;
+    const int shs = STREAM ? shift_of(a.ksigns, k0, SC) : 0, rps = STREAM ? SC : SC + 4;
 #pragma unroll
     for (int j = 0; j < (KITEMS + NT - 1) / NT; ++j) {
       const int it = tid + j * NT;
       if (KITEMS % NT == 0 || it < KITEMS) {
         const int key = it / (D / 8), dg = it % (D / 8);
         half8 kv = half8{}, sv = half8{};
-        if (dg < ng) {
-          const int ko = shk + key * KC + dg * KB;  // the group's KB bytes
+        if (!STREAM || dg < ng) {
+          const int ko = shk + key * rpk + dg * KB;  // the group's KB bytes
           if constexpr (KB == 1) {
             kv = *reinterpret_cast<const half8*>(&lutK[rawK[cur][ko] * 8]);
           } else if constexpr (KB == 2) {
-            kv = cat8(*reinterpret_cast<const half4*>(&lutK[rawK[cur][ko] * 4]),
-                      *reinterpret_cast<const half4*>(&lutK[rawK[cur][ko + 1] * 4]));
+            uint32_t two;  // the group's two code bytes (an aligned u16 in the padded rows)
+            if constexpr (STREAM) two = rawK[cur][ko] | (static_cast<uint32_t>(rawK[cur][ko + 1]) << 8);
+            else two = *reinterpret_cast<const uint16_t*>(&rawK[cur][ko]);
+            kv = cat8(*reinterpret_cast<const half4*>(&lutK[(two & 0xffu) * 4]),
+                      *reinterpret_cast<const half4*>(&lutK[(two >> 8) * 4]));
           } else {
             const uint32_t w = bits32_at(rawK[cur], ko);
 #pragma unroll
             for (int e = 0; e < 8; ++e) kv[e] = lutK[(w >> (e * 3)) & 7u];
           }
-          sv = *reinterpret_cast<const half8*>(&lutS[rawS[cur][shs + key * SC + dg] * 8]);
+          sv = *reinterpret_cast<const half8*>(&lutS[rawS[cur][shs + key * rps + dg] * 8]);
         }
         *reinterpret_cast<half8*>(&sK[key * T::LDK + dg * 8]) = kv;
         *reinterpret_cast<half8*>(&sS[key * T::LDK + dg * 8]) = sv;
@@ -295,7 +305,7 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
     if constexpr (!SCORES) {
       // V^ = f16(Cv[code] * vn_v); item = (8-dim group dg, 4-key quad kq)
       const uint32_t mv = (1u << a.vb) - 1u;
-      const int shv = shift_of(a.vcodes, k0, vc);
+      const int shv = STREAM ? shift_of(a.vcodes, k0, vc) : 0, rpv = STREAM ? vc : vc + 4;
 #pragma unroll
       for (int j = 0; j < (VITEMS + NT - 1) / NT; ++j) {
         const int it = tid + j * NT;
@@ -305,11 +315,12 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
           half4 col[8];
 #pragma unroll
           for (int kk = 0; kk < 4; ++kk) {
-            const uint32_t w = dg < ng ? bits32_at(rawV[cur], shv + (kq * 4 + kk) * vc + dg * a.vb) : 0u;
+            const bool real = !STREAM || dg < ng;
+            const uint32_t w = real ? bits32_at(rawV[cur], shv + (kq * 4 + kk) * rpv + dg * a.vb) : 0u;
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-              col[e][kk] = dg < ng ? static_cast<_Float16>(lutV[(w >> (e * a.vb)) & mv] * vn4[kk])
-                                   : static_cast<_Float16>(0.f);
+              col[e][kk] = real ? static_cast<_Float16>(lutV[(w >> (e * a.vb)) & mv] * vn4[kk])
+                                : static_cast<_Float16>(0.f);
           }
 #pragma unroll
           for (int e = 0; e < 8; ++e)
@@ -508,11 +519,16 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
   }
 }
 
+template <int D, int KB, bool SCORES, bool STREAM>
+static void launch_attn_st(const AttnArgs& a, hipStream_t s) {
+  dim3 grid(a.nqb, a.Hkv, a.B);
+  if (!SCORES && a.mask) attn_kernel<D, KB, SCORES, !SCORES, STREAM><<<grid, ATile<D, SCORES>::NT, 0, s>>>(a);
+  else attn_kernel<D, KB, SCORES, false, STREAM><<<grid, ATile<D, SCORES>::NT, 0, s>>>(a);
+}
 template <int D, int KB, bool SCORES>
 static void launch_attn(const AttnArgs& a, hipStream_t s) {
-  dim3 grid(a.nqb, a.Hkv, a.B);
-  if (!SCORES && a.mask) attn_kernel<D, KB, SCORES, !SCORES><<<grid, ATile<D, SCORES>::NT, 0, s>>>(a);
-  else attn_kernel<D, KB, SCORES, false><<<grid, ATile<D, SCORES>::NT, 0, s>>>(a);
+  if (a.d == D) launch_attn_st<D, KB, SCORES, false>(a, s);
+  else launch_attn_st<D, KB, SCORES, true>(a, s);
 }
 
 // the tiled kernel for head dim d: D = d rounded up to a multiple of 32
