@@ -91,9 +91,20 @@ def test_gpt2_config1_gpu_against_reference_logits(impl, fixture):
     passes no mask and, as in the reference (gpt2.py:99-101), every position is attended."""
     import os
 
+    from turboquant_pytorch.codebook import clear_pinned_rotations, load_rotations, pin_rotations
+
     print("case: gpt2 reference logits", impl, flush=True)
-    g = np.load(os.path.join(os.path.dirname(__file__), "golden", fixture))
-    gpu = apply_turboquant(_gpt2(impl), bits=3, seed=42).to("cuda")
+    golden = os.path.join(os.path.dirname(__file__), "golden")
+    g = np.load(os.path.join(golden, fixture))
+    # the reference's own rotations (this host's LAPACK may round the QR differently), so that
+    # the CPU path below reproduces the reference's logits and the GPU path differs from them
+    # only by the packed format
+    pin_rotations(load_rotations(os.path.join(golden, "rotations.npz")))
+    try:
+        gpu = apply_turboquant(_gpt2(impl), bits=3, seed=42).to("cuda")
+        cpu = apply_turboquant(_gpt2(impl), bits=3, seed=42)
+    finally:
+        clear_pinned_rotations()
     with torch.no_grad():
         lg = gpu(input_ids=torch.from_numpy(g["input_ids"]).long().cuda()).logits[0].float().cpu().numpy()
     # packed GPU format vs the reference's unpacked CPU format: same estimator, f16 vs f32
@@ -102,4 +113,24 @@ def test_gpt2_config1_gpu_against_reference_logits(impl, fixture):
     # path, which reproduces these fixtures bit for bit, is test_gpt2_small_gpu_matches_cpu)
     assert O.cosine(lg[:8, :16], g["logits_head"]) > 0.998
     assert O.cosine(lg[-8:, -16:], g["logits_tail"]) > 0.998
-    assert (lg.argmax(-1) == g["argmax"]).mean() > 0.9
+    # argmax: the CPU path (the reference's unpacked format) must give the reference's argmax
+    # wherever its top-1 / top-2 margin is above this host's f32 BLAS drift (1e-3; on the box
+    # they differed only at margins below 6e-4); the GPU path must agree with the CPU path
+    # wherever that margin exceeds twice the largest logit difference between the two formats at
+    # that position (there the packed-vs-unpacked difference cannot reorder them), and those
+    # positions must be most of the sequence (69% under eager, 95% under sdpa on the box)
+    with torch.no_grad():
+        lc = cpu(input_ids=torch.from_numpy(g["input_ids"]).long()).logits[0].numpy()
+    top2 = np.sort(lc, axis=-1)[:, -2:]
+    margin = top2[:, 1] - top2[:, 0]
+    cpu_ref = lc.argmax(-1) == g["argmax"]
+    dev = np.abs(lg - lc).max(-1)
+    decided = margin > 2 * dev
+    agree = lg.argmax(-1) == lc.argmax(-1)
+    print(f"CPU path vs reference argmax: {cpu_ref.mean():.4f} (smallest margin where they differ "
+          f"{margin[~cpu_ref].max() if (~cpu_ref).any() else 0:.2e}); positions decided by their margin: "
+          f"{decided.mean():.3f}; GPU/CPU argmax agreement there {agree[decided].mean():.3f}, overall "
+          f"{agree.mean():.3f}; GPU vs reference overall {(lg.argmax(-1) == g['argmax']).mean():.3f}", flush=True)
+    assert cpu_ref[margin > 1e-3].all()
+    assert agree[decided].all()
+    assert decided.mean() > 0.5
