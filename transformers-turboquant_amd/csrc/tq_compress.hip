@@ -1227,22 +1227,36 @@ __global__ void __launch_bounds__((64 * row_waves<MODE, DT>())) rows_kernel(Tile
   rows_body<D, DT, MODE, BB, row_waves<MODE, DT>(), false>(a, *reinterpret_cast<SM*>(smem), blockIdx.x, gridDim.x);
 }
 
+// Few rows (a decode step's queries): blocks of 4 waves, one per SIMD, so that the rows'
+// 16-row tiles spread over more compute units instead of pairing up on the SIMDs of a few
+// 8-wave blocks
+constexpr int kFewWaves = 4;
+template <int D, int DT, int MODE, int BB>
+__global__ void __launch_bounds__(64 * kFewWaves) rows_few_kernel(TileArgs a) {
+  using SM = RowsSmem<D, MODE, BB, kFewWaves>;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[sizeof(SM)];
+  rows_body<D, DT, MODE, BB, kFewWaves, false>(a, *reinterpret_cast<SM*>(smem), blockIdx.x, gridDim.x);
+}
+
 // A cache append in one launch: blocks [0, nbk) compress the new keys, [nbk, nbk + nbv) the
 // new values, the rest prepare the new queries (nbq blocks, 0 without queries).  Every block
-// has 8 waves; the LDS holds one mode's layout at a time.
+// has 4 waves (one per SIMD: a step's few tiles spread over compute units); the LDS holds one
+// mode's layout at a time.
+constexpr int kAppendWaves = 4;
 template <int D, int DT, int KBB, int VB>
-__global__ void __launch_bounds__(512) append_kernel(TileArgs ka, TileArgs va, TileArgs qa, int nbk, int nbv,
-                                                     int nbq) {
-  using SK = RowsSmem<D, TM_KEYS, KBB, 8>;
-  using SV = RowsSmem<D, TM_VALUES, VB, 8>;
-  using SQ = RowsSmem<D, TM_QUERY, 1, 8>;
+__global__ void __launch_bounds__(64 * kAppendWaves) append_kernel(TileArgs ka, TileArgs va, TileArgs qa, int nbk,
+                                                                   int nbv, int nbq) {
+  constexpr int NW = kAppendWaves;
+  using SK = RowsSmem<D, TM_KEYS, KBB, NW>;
+  using SV = RowsSmem<D, TM_VALUES, VB, NW>;
+  using SQ = RowsSmem<D, TM_QUERY, 1, NW>;
   constexpr size_t BYTES = sizeof(SK) > sizeof(SV) ? (sizeof(SK) > sizeof(SQ) ? sizeof(SK) : sizeof(SQ))
                                                    : (sizeof(SV) > sizeof(SQ) ? sizeof(SV) : sizeof(SQ));
   __shared__ __attribute__((aligned(16))) uint8_t smem[BYTES];
   const int blk = static_cast<int>(blockIdx.x);
-  if (blk < nbk) rows_body<D, DT, TM_KEYS, KBB, 8, true>(ka, *reinterpret_cast<SK*>(smem), blk, nbk);
-  else if (blk < nbk + nbv) rows_body<D, DT, TM_VALUES, VB, 8, true>(va, *reinterpret_cast<SV*>(smem), blk - nbk, nbv);
-  else rows_body<D, DT, TM_QUERY, 1, 8, false>(qa, *reinterpret_cast<SQ*>(smem), blk - nbk - nbv, nbq);
+  if (blk < nbk) rows_body<D, DT, TM_KEYS, KBB, NW, true>(ka, *reinterpret_cast<SK*>(smem), blk, nbk);
+  else if (blk < nbk + nbv) rows_body<D, DT, TM_VALUES, VB, NW, true>(va, *reinterpret_cast<SV*>(smem), blk - nbk, nbv);
+  else rows_body<D, DT, TM_QUERY, 1, NW, false>(qa, *reinterpret_cast<SQ*>(smem), blk - nbk - nbv, nbq);
 }
 
 // Blocks of `kernel` the device holds at once (occupancy x compute units), per device.
@@ -1250,6 +1264,16 @@ template <int D, int DT, int MODE, int BB>
 static void launch_tile(const TileArgs& a, hipStream_t s) {
   static int cache[16] = {};
   using T = RT<D, row_waves<MODE, DT>()>;
+  if constexpr (MODE == TM_QUERY) {
+    static int cache_few[16] = {};
+    const int64_t blocks = (a.n + 16 * kFewWaves - 1) / (16 * kFewWaves);  // one tile per wave
+    const int64_t res = resident_blocks(reinterpret_cast<const void*>(&rows_few_kernel<D, DT, MODE, BB>),
+                                        64 * kFewWaves, cache_few);
+    if (blocks > 1 && blocks <= res) {  // all resident at once, one tile per SIMD
+      rows_few_kernel<D, DT, MODE, BB><<<static_cast<unsigned>(blocks), 64 * kFewWaves, 0, s>>>(a);
+      return;
+    }
+  }
   const int64_t blocks = (a.n + T::R - 1) / T::R;  // one 16-row tile per wave
   const int64_t res = resident_blocks(reinterpret_cast<const void*>(&rows_kernel<D, DT, MODE, BB>), T::NT, cache);
   const unsigned grid = static_cast<unsigned>(blocks < res ? blocks : res);
@@ -1298,10 +1322,12 @@ void dispatch_tile<TM_QUERY>(const TileArgs& a, int d, int dtype, int, hipStream
 template <int D, int DT, int KBB, int VB>
 static void launch_append(const TileArgs& ka, const TileArgs& va, const TileArgs& qa, hipStream_t s) {
   static int cache[16] = {};
-  const int64_t res = resident_blocks(reinterpret_cast<const void*>(&append_kernel<D, DT, KBB, VB>), 512, cache);
-  // a block takes rounds of 128 rows; when the three modes need more blocks than the device holds
-  // at once, they share the resident blocks by work (a key row costs about two value or query rows)
-  auto rounds = [](int64_t n) { return (n + 127) / 128; };
+  constexpr int NT = 64 * kAppendWaves, RROWS = 16 * kAppendWaves;
+  const int64_t res = resident_blocks(reinterpret_cast<const void*>(&append_kernel<D, DT, KBB, VB>), NT, cache);
+  // a block takes rounds of RROWS rows; when the three modes need more blocks than the device
+  // holds at once, they share the resident blocks by work (a key row costs about two value or
+  // query rows)
+  auto rounds = [](int64_t n) { return (n + RROWS - 1) / RROWS; };
   int64_t nk = rounds(ka.n), nv = rounds(va.n), nq = rounds(qa.n);
   if (nk + nv + nq > res) {
     const double wk = 2.0 * static_cast<double>(ka.n), wv = static_cast<double>(va.n);
@@ -1310,7 +1336,7 @@ static void launch_append(const TileArgs& ka, const TileArgs& va, const TileArgs
     nv = std::max<int64_t>(1, std::min<int64_t>(nv, static_cast<int64_t>(res * wv / w)));
     nq = qa.n > 0 ? std::max<int64_t>(1, std::min<int64_t>(nq, res - nk - nv)) : 0;
   }
-  append_kernel<D, DT, KBB, VB><<<static_cast<unsigned>(nk + nv + nq), 512, 0, s>>>(
+  append_kernel<D, DT, KBB, VB><<<static_cast<unsigned>(nk + nv + nq), NT, 0, s>>>(
       ka, va, qa, static_cast<int>(nk), static_cast<int>(nv), static_cast<int>(nq));
 }
 
