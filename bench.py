@@ -187,17 +187,23 @@ def trace_summary(kernel_csv: str, marker_csv: str) -> str:
                 int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"]))
             kernels.append((short(r["Kernel_Name"]), grid, int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
     kernels.sort(key=lambda k: k[2])
-    lines = ["| timed range (steps) | kernel | grid (work-items) | launches | avg us | min us | max us |",
-             "|---|---|---|---|---|---|---|"]
+    lines = ["| timed range (steps) | kernel | grid (work-items) | launches per step | avg us | min us | max us | "
+             "us per step |", "|---|---|---|---|---|---|---|---|"]
     for leg, steps, t0, t1 in sorted(ranges, key=lambda r: r[2]):
         groups: dict = {}
         for name, grid, k0, k1 in kernels:
             if t0 <= k0 and k1 <= t1:
                 groups.setdefault((name, grid), []).append((k1 - k0) / 1e3)
-        for (name, grid), us in sorted(groups.items(), key=lambda g: -sum(g[1][-steps:])):
-            us = us[-steps:]
-            lines.append(f"| {leg} ({steps}) | `{name}` | {grid} | {len(us)} | {sum(us) / len(us):.1f} | "
-                         f"{min(us):.1f} | {max(us):.1f} |")
+        rows = []
+        for (name, grid), us in groups.items():
+            per_step = max(1, round(len(us) / steps))  # lead-in launches aside
+            last = us[-steps * per_step:]
+            avg = sum(last) / len(last)
+            rows.append((avg * per_step, name, grid, per_step, avg, min(last), max(last)))
+        for tot, name, grid, per_step, avg, lo, hi in sorted(rows, reverse=True)[:12]:
+            short = name if len(name) <= 72 else name[:69] + "..."
+            lines.append(f"| {leg} ({steps}) | `{short}` | {grid} | {per_step} | {avg:.1f} | {lo:.1f} | {hi:.1f} | "
+                         f"{tot:.1f} |")
     return "\n".join(lines)
 
 
