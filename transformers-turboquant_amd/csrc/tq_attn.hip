@@ -132,8 +132,16 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
-  const int qblk = a.nqb - 1 - static_cast<int>(blockIdx.x);  // heavy causal blocks first
-  const int hkv = blockIdx.y, b = blockIdx.z;
+  // blocks in order of decreasing causal work across every (batch, kv head): block i takes query
+  // block nqb - 1 - i / (B Hkv) of group i % (B Hkv), so the longest blocks of all groups start
+  // first and the grid's tail is short ones (the per-group order, all of one group's query
+  // blocks before the next group's, left a 23% longer schedule at 8 kv heads); consecutive
+  // blocks are different groups, so each XCD (blocks dealt round-robin) keeps to a fixed set of
+  // groups and their K / V planes in its L2
+  const int nbh = a.B * a.Hkv;
+  const int qblk = a.nqb - 1 - static_cast<int>(blockIdx.x) / nbh;
+  const int bhi = static_cast<int>(blockIdx.x) % nbh;
+  const int hkv = bhi % a.Hkv, b = bhi / a.Hkv;
   const int q0 = qblk * a.QT;
   const int d = STREAM ? a.d : D;
   const int KC = d * KB / 8, SC = d / 8, vc = d * a.vb / 8;  // bytes per packed row
@@ -521,7 +529,7 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
 
 template <int D, int KB, bool SCORES, bool STREAM>
 static void launch_attn_st(const AttnArgs& a, hipStream_t s) {
-  dim3 grid(a.nqb, a.Hkv, a.B);
+  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.nqb) * a.Hkv * a.B));  // see the kernel
   if (!SCORES && a.mask) attn_kernel<D, KB, SCORES, !SCORES, STREAM><<<grid, ATile<D, SCORES>::NT, 0, s>>>(a);
   else attn_kernel<D, KB, SCORES, false, STREAM><<<grid, ATile<D, SCORES>::NT, 0, s>>>(a);
 }
@@ -661,6 +669,8 @@ int tq_attention_scores_kv(const uint16_t* q_rot, const float* q_proj, const uin
   a.kcent = centroids_f16;
   a.vb = 1;
   fill_common(a, B, Hq, Hkv, Sq, Sk, ldk, d, true);
+  TQ_REQUIRE(static_cast<int64_t>(a.nqb) * Hkv * B < (int64_t(1) << 31), "%s: %lld query blocks exceed one grid",
+             "tq_attention", (long long)(static_cast<int64_t>(a.nqb) * Hkv * B));
   a.coeff = coeff;
   a.scale = 1.f;
   a.scores = out;
@@ -717,6 +727,8 @@ int tq_attention_fwd_kv(const uint16_t* q_rot, const float* q_proj, const uint8_
   a.vpit = val_pit_split;
   a.vb = val_bits;
   fill_common(a, B, Hq, Hkv, Sq, Sk, ldk, d, false);
+  TQ_REQUIRE(static_cast<int64_t>(a.nqb) * Hkv * B < (int64_t(1) << 31), "%s: %lld query blocks exceed one grid",
+             "tq_attention", (long long)(static_cast<int64_t>(a.nqb) * Hkv * B));
   a.coeff = coeff;
   a.scale = scale;
   a.causal = causal;
