@@ -27,8 +27,13 @@
 //    lane, the P^T operand layout of O^T += V^T P^T, so P stays in registers.
 //    P = f16(2^(s - m)) enters the P.V product (one f16 rounding, P <= 2^TAU).
 //  * q_proj enters the QJL term as f16 hi + lo (two MFMAs against the exact +-1 signs, f32
-//    grade) at head_dim 64; at head_dim 128 the lo fragments do not fit the registers of two
-//    column blocks per wave and q_proj is rounded once to f16.
+//    grade).  The hi fragments stay in registers.  The lo fragments stay in registers where
+//    they fit (head_dim 64, or one column block per wave).  At head_dim 128 with two column
+//    blocks per wave they live in LDS: each wave holds its own 8 KB of them and reads each one
+//    once per tile.  Their LDS comes from the +-1 sign tiles, which that form does not decode:
+//    its sign operands come straight from the raw sign bits through a 16-entry table, and the
+//    QJL term's k-slots are permuted so that one dword of a key's sign row serves all four
+//    k-steps.
 #include "tq_common.h"
 #include "tq_stream.h"
 
@@ -42,13 +47,14 @@ constexpr int kPfWaves = 4;  // waves per block, each with two 16-column blocks:
 // 16-column MFMA blocks per wave: 2, or 1 with an additive mask
 template <bool MASK>
 constexpr int pf_nbw() { return MASK ? 1 : 2; }
-// q_proj as an f16 (hi, lo) pair: where the lo fragments fit the registers
-template <int D>
-constexpr bool pf_qlo() { return D <= 64; }
+// where q_proj's lo fragments live: registers where they fit, otherwise LDS (two column
+// blocks per wave at head_dim 128)
+template <int D, bool MASK>
+constexpr bool pf_qlo_lds() { return D > 64 && pf_nbw<MASK>() > 1; }
 
 struct PrefillArgs {
   const uint16_t* q_rot;
-  const float* q_proj;  // f32: f16 hi + lo operands at head_dim 64, its f16 rounding at 128
+  const float* q_proj;  // f32, taken as f16 hi + lo operands
   const uint8_t *kcodes, *ksigns;
   const uint16_t *krn, *kvn, *kcent;  // f16 key centroids
   const uint8_t* vcodes;
@@ -108,7 +114,7 @@ template <int D_, int BITS, bool MASK>
 __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2))) prefill_kernel(PrefillArgs a) {
   using C = PfCfg<D_, BITS>;
   constexpr int D = C::D, KT = C::KT, R = C::R, KB = C::KB, VB = C::VB;
-  constexpr bool QLO = pf_qlo<D>();
+  constexpr bool QLDS = pf_qlo_lds<D_, MASK>();  // lo fragments in LDS, signs from the raw bits
   constexpr int KC = C::KC, SC = C::SC, VC = C::VC, LDK = C::LDK, LDV = C::LDV;
   constexpr int KS = D / 32, DB = D / 16, NT = C::NT, NBW = pf_nbw<MASK>();  // 16 columns per block
   constexpr float LOG2E = 1.4426950408889634f;
@@ -117,7 +123,9 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
   __shared__ __attribute__((aligned(16))) uint8_t luts[C::T_BYTES];
   __shared__ __attribute__((aligned(16))) uint8_t ring[R * C::SLOT];
   __shared__ __attribute__((aligned(16))) _Float16 sK0[KT * LDK], sK1[KT * LDK];
-  __shared__ __attribute__((aligned(16))) _Float16 sS0[KT * LDK], sS1[KT * LDK];
+  __shared__ __attribute__((aligned(16))) _Float16 sS0[QLDS ? 8 : KT * LDK], sS1[QLDS ? 8 : KT * LDK];
+  // lo fragments of q_proj, per wave [k-step][column block][lane] (QLDS only)
+  __shared__ __attribute__((aligned(16))) half8 sQlo[QLDS ? kPfWaves * KS * NBW * 64 : 1];
   __shared__ __attribute__((aligned(16))) _Float16 sV0[D * LDV], sV1[D * LDV];
   __shared__ __attribute__((aligned(16))) float fac0[3][KT], fac1[3][KT];  // fa*vn_k, fa*coeff*rn_k, unused
   const uint8_t* tS = luts + C::T_SGN;
@@ -178,7 +186,8 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
   int col_i[NBW], col_h[NBW];
   bool col_ok[NBW];
   half8 qr[KS][NBW], qp[KS][NBW];
-  [[maybe_unused]] half8 qlo[QLO ? KS : 1][NBW];
+  [[maybe_unused]] half8 qlo[QLDS ? 1 : KS][NBW];
+  half8* const wlo = sQlo + wave * (KS * NBW * 64) + lane;  // this lane's lo fragments (QLDS)
 #pragma unroll
   for (int nb = 0; nb < NBW; ++nb) {
     const int r = (wave * NBW + nb) * 16 + l16;
@@ -191,14 +200,14 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
     for (int ks = 0; ks < KS; ++ks) {
       const int d0 = ks * 32 + lg * 8;
       qr[ks][nb] = col_ok[nb] ? *reinterpret_cast<const half8*>(a.q_rot + qrow + d0) : half8{};
-      if constexpr (QLO) {
-        half8 hi = half8{}, lo = half8{};
-        if (col_ok[nb]) split8(a.q_proj + qrow + d0, hi, lo);
-        qp[ks][nb] = hi;
-        qlo[ks][nb] = lo;
-      } else {
-        qp[ks][nb] = col_ok[nb] ? round8(a.q_proj + qrow + d0) : half8{};
-      }
+      // the QJL term's k-slots: lane group lg, k-step ks <-> dims 32 lg + 8 ks + 0..7 where the
+      // sign operands come from the raw bits (byte 4 lg + ks of the key's sign row)
+      const int dp = QLDS ? lg * 32 + ks * 8 : d0;
+      half8 hi = half8{}, lo = half8{};
+      if (col_ok[nb]) split8(a.q_proj + qrow + dp, hi, lo);
+      qp[ks][nb] = hi;
+      if constexpr (QLDS) wlo[(ks * NBW + nb) * 64] = lo;
+      else qlo[ks][nb] = lo;
     }
   }
   // additive-mask rows of this lane's columns (row 0 for padding columns, whose scores are
@@ -279,9 +288,11 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
       } else {
         kv = six4x2(tK, field32(raw + C::OFF_K + key * KC, 3 * g));
       }
-      const half8 sv = nib2x4<0>(tS, raw[C::OFF_S + key * SC + g]);
       *reinterpret_cast<half8*>(dK + key * LDK + 8 * g) = kv;
-      *reinterpret_cast<half8*>(dS + key * LDK + 8 * g) = sv;
+      if constexpr (!QLDS) {
+        const half8 sv = nib2x4<0>(tS, raw[C::OFF_S + key * SC + g]);
+        *reinterpret_cast<half8*>(dS + key * LDK + 8 * g) = sv;
+      }
     }
   };
   auto decode_v = [&](int j, _Float16* dV, float (*dF)[KT]) __attribute__((always_inline)) {
@@ -342,8 +353,10 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
     for (int db = 0; db < DB; ++db) oacc[db][nb] = float4v{0.f, 0.f, 0.f, 0.f};
   }
 
-  // ---- scores of tile j: S^T = K^ Q_rot^T (term 1) and Sign Q_proj^T (term 2)
-  auto scores = [&](const _Float16* cK, const _Float16* cS, float4v (&sacc)[2][NBW], float4v (&tacc)[2][NBW]) __attribute__((always_inline)) {
+  // ---- scores of tile j: S^T = K^ Q_rot^T (term 1) and Sign Q_proj^T (term 2).  `sw` (QLDS):
+  // sign dword lg of the rows of keys l16 and 16 + l16 (raw bits of the tile)
+  auto scores = [&](const _Float16* cK, const _Float16* cS, const uint32_t (&sw)[2], float4v (&sacc)[2][NBW],
+                    float4v (&tacc)[2][NBW]) __attribute__((always_inline)) {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
@@ -351,26 +364,37 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
         sacc[mb][nb] = float4v{0.f, 0.f, 0.f, 0.f};
         tacc[mb][nb] = float4v{0.f, 0.f, 0.f, 0.f};
       }
-    // K^ and sign fragments one (k-step, key block) step ahead of their MFMAs
+    // K^ and sign fragments one (k-step, key block) step ahead of their MFMAs; lo fragments
+    // (QLDS) one k-step ahead
     half8 ka[2], sa[2];
-    auto frag = [&](int i, int slot) {
+    [[maybe_unused]] half8 la[2][NBW];
+    auto frag = [&](auto I, int slot) __attribute__((always_inline)) {
+      constexpr int i = decltype(I)::value;
       const int off = ((i & 1) * 16 + l16) * LDK + (i >> 1) * 32 + lg * 8;
       ka[slot] = *reinterpret_cast<const half8*>(cK + off);
-      sa[slot] = *reinterpret_cast<const half8*>(cS + off);
+      if constexpr (QLDS) sa[slot] = nib2x4<(i >> 1)>(tS, sw[i & 1]);
+      else sa[slot] = *reinterpret_cast<const half8*>(cS + off);
     };
-    frag(0, 0);
+    auto lofrag = [&](int ks) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 2 * KS; ++i) {
-      const int ks = i >> 1, mb = i & 1, c = i & 1;
-      if (i + 1 < 2 * KS) frag(i + 1, c ^ 1);
+      for (int nb = 0; nb < NBW; ++nb) la[ks & 1][nb] = wlo[(ks * NBW + nb) * 64];
+    };
+    frag(std::integral_constant<int, 0>{}, 0);
+    if constexpr (QLDS) lofrag(0);
+    static_for<2 * KS>([&](auto I) __attribute__((always_inline)) {
+      constexpr int i = decltype(I)::value;
+      constexpr int ks = i >> 1, mb = i & 1, c = i & 1;
+      if constexpr (i + 1 < 2 * KS) frag(std::integral_constant<int, i + 1>{}, c ^ 1);
+      if constexpr (QLDS && mb == 0 && ks + 1 < KS) lofrag(ks + 1);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int nb = 0; nb < NBW; ++nb) {
         sacc[mb][nb] = mfma16x16x32(ka[c], qr[ks][nb], sacc[mb][nb]);
         tacc[mb][nb] = mfma16x16x32(sa[c], qp[ks][nb], tacc[mb][nb]);
-        if constexpr (QLO) tacc[mb][nb] = mfma16x16x32(sa[c], qlo[ks][nb], tacc[mb][nb]);
+        if constexpr (QLDS) tacc[mb][nb] = mfma16x16x32(sa[c], la[ks & 1][nb], tacc[mb][nb]);
+        else tacc[mb][nb] = mfma16x16x32(sa[c], qlo[ks][nb], tacc[mb][nb]);
       }
-    }
+    });
   };
   // ---- log2-domain scores with masking, column maxima, lazy rescale (one rare branch per tile)
   auto softmax_max = [&](int j, const float (*cF)[KT], const float4v (&sacc)[2][NBW],
@@ -510,6 +534,14 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
     }
   };
 
+  // sign dword lg of keys l16 and 16 + l16 of raw tile j (QLDS)
+  uint32_t swc[2] = {0u, 0u}, swn[2] = {0u, 0u};
+  auto sign_words = [&](int j, uint32_t (&w)[2]) __attribute__((always_inline)) {
+    const uint8_t* raw = ring + (j % R) * C::SLOT + C::OFF_S + lg * 4;
+    w[0] = *reinterpret_cast<const uint32_t*>(raw + l16 * SC);
+    w[1] = *reinterpret_cast<const uint32_t*>(raw + (16 + l16) * SC);
+  };
+
   // ---- pipeline: tiles 0..R-1 in flight, tile 0 decoded, then one barrier per tile
   __builtin_amdgcn_s_waitcnt(0);  // q fragments landed: the ring's vmcnt waits count DMAs only
   if (nt > 0) {
@@ -522,6 +554,7 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
     __syncthreads();  // tables and raw tile 0 visible
     decode_ks(0, sK0, sS0);
     decode_v(0, sV0, fac0);
+    if constexpr (QLDS) sign_words(0, swc);
   }
   auto iter = [&](int t, const _Float16* cK, const _Float16* cS, const _Float16* cV, const float (*cF)[KT],
                   _Float16* nK, _Float16* nS, _Float16* nV, float (*nF)[KT]) __attribute__((always_inline)) {
@@ -532,14 +565,19 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
     float sc[NBW][2][4];
     // the wave's priority is raised while it issues MFMAs
     decode_ks(t + 1, nK, nS);  // overlaps the score MFMAs
+    if constexpr (QLDS) sign_words(t + 1, swn);  // raw tile t + 1 is overwritten at the next barrier
     __builtin_amdgcn_s_setprio(1);
-    scores(cK, cS, sacc, tacc);
+    scores(cK, cS, swc, sacc, tacc);
     __builtin_amdgcn_s_setprio(0);
     softmax_max(t, cF, sacc, tacc, sc);
     __builtin_amdgcn_s_setprio(1);
     pv_tile(cV, sc);
     __builtin_amdgcn_s_setprio(0);
     decode_v(t + 1, nV, nF);   // overlaps the P.V MFMAs
+    if constexpr (QLDS) {
+      swc[0] = swn[0];
+      swc[1] = swn[1];
+    }
   };
   for (int t = 0; t < nt; t += 2) {
     iter(t, sK0, sS0, sV0, fac0, sK1, sS1, sV1, fac1);
