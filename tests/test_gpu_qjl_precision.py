@@ -17,7 +17,9 @@ also checks that it is sensitive: the oracle with q_proj rounded to f16 misses t
 least 10x.  Kernels covered, by shape: the head_dim-128 prefill kernel (unmasked, whose lo
 fragments live in LDS, and masked), the head_dim-64 prefill kernel, the tiled kernel (head dim
 96, scores mode), the bit-plane decode kernels (bits 3, at most 4 columns), and the table
-decode kernels (bits 4, and 12 columns).
+decode kernels (bits 4, and 12 columns).  With q_proj scaled by 8 and by 2^-30 the prefill,
+tiled and bit-plane kernels are held to the oracle where an unscaled f16 split would overflow or
+lose its lo part.
 """
 
 import math
@@ -65,10 +67,11 @@ def _planes(d, bits, B, hkv, sk, seed):
     return x, codes, sign_bits
 
 
-def _setup(d, bits, B, hq, hkv, sq, sk, seed=0):
+def _setup(d, bits, B, hq, hkv, sq, sk, seed=0, qscale=1.0):
     kc = TurboQuantCompressorV2(d, bits, seed=42, device=DEV)
     vc = TurboQuantCompressorMSE(d, bits, seed=10042, device=DEV)
     x, codes, sign_bits = _planes(d, bits, B, hkv, sk, seed)
+    x = x * qscale  # a power of two: still exact in f32
     g = hq // hkv
     rng = np.random.default_rng(seed + 1)
     q_rot16 = rng.standard_normal((B, hkv, d)).astype(np.float16)
@@ -164,3 +167,48 @@ def test_attention_qjl_term_f32_grade(d, bits, hq, hkv, sq, sk, masked):
     print(f"attention: rel-err {err:.2e}; f16 q_proj would give {err16:.2e}")
     assert err16 > 10 * REL  # the case is sensitive to an f16 q_proj
     assert err < REL and O.cosine(got.reshape(-1), ref.reshape(-1)) > 0.9999
+
+
+# q_proj outside f16's range: scaled by 8 its largest values reach ~2^17 (f16 ends at 65504);
+# scaled by 2^-30 (values ~2^-17..2^-15) an unscaled split would leave hi subnormal and round lo
+# away (~2^-9 relative).  The prefill and tiled kernels split q_proj after a power-of-two scale
+# of their own and the bit-plane decode kernels take it as per-column fixed point, so all stay
+# at f32 grade.  (Much larger scales make the scores themselves too large for f32 to resolve
+# attention weights: at 2^12 they reach ~6.6e6 in log2 units, whose f32 ulp is 0.5.)  The table
+# decode kernels (bits 4, or more than 4 columns) split q_proj unscaled and are not held to this.
+KERNEL_CASES = [
+    (128, 3, 32, 8, 64, 48, False),  # head_dim-128 prefill
+    (128, 3, 32, 8, 64, 48, True),   # masked prefill
+    (64, 3, 12, 12, 40, 48, False),  # head_dim-64 prefill
+    (96, 3, 8, 2, 40, 48, False),    # tiled kernel
+    (128, 3, 32, 8, 1, 64, False),   # bit-plane decode
+    (128, 2, 8, 2, 1, 64, False),    # bit-plane decode, bits 2
+]
+
+
+@pytest.mark.parametrize("qscale", [8.0, 2.0 ** -30])
+@pytest.mark.parametrize("d,bits,hq,hkv,sq,sk,masked", KERNEL_CASES)
+def test_qjl_term_extreme_query_magnitudes(d, bits, hq, hkv, sq, sk, masked, qscale):
+    _case(d=d, bits=bits, hq=hq, hkv=hkv, sq=sq, sk=sk, masked=masked, qscale=qscale)
+    B = 2
+    kc, vc, q_rot, q_proj, ck, cv, x, oracle_scores, vals = _setup(d, bits, B, hq, hkv, sq, sk,
+                                                                   seed=d + 5 * bits + sq, qscale=qscale)
+    g = hq // hkv
+    ref_s = oracle_scores(x)
+    if not masked:
+        t = _tables(kc, q_rot.device, with_qjl=True)
+        got_s = scores_from_prepared(q_rot, q_proj, ck["packed_key_indices"], ck["packed_qjl_signs"],
+                                     ck["residual_norm"], ck["vec_norms"], t.cent16, bits, O.COEFF(d), hkv, sk,
+                                     sk).cpu().numpy().astype(np.float64)
+        err_s = np.abs(got_s - ref_s).max() / np.abs(ref_s).max()
+        print(f"scores: max err {err_s:.2e} of the score scale")
+        assert np.isfinite(got_s).all() and err_s < 1e-6
+    mask = torch.zeros(B, 1, sq, sk, device=DEV) if masked else None
+    got = attention_from_prepared(q_rot, q_proj, kc, vc, ck, cv, mask, False, None, torch.float32).cpu().numpy()
+    ref = np.zeros((B, sq, hq, d))
+    for b in range(B):
+        for h in range(hq):
+            ref[b, :, h] = O.attention(ref_s[b, h], vals[b, h // g], 1 / math.sqrt(d))
+    err = O.rel_err(got, ref)
+    print(f"attention: rel-err {err:.2e}")
+    assert np.isfinite(got).all() and err < REL

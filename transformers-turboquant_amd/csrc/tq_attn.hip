@@ -167,6 +167,8 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
   int col_i[NBW], col_h[NBW];
   bool col_ok[NBW];
   half8 qr[KS][NBW], qp[KS][NBW], qlo[KS][NBW];
+  int64_t qrow[NBW];
+  float qmax = 0.f;  // largest |q_proj| of the block's columns: the scale of its (hi, lo) split
 #pragma unroll
   for (int nb = 0; nb < NBW; ++nb) {
     const int r = (wave * NBW + nb) * 16 + l16;
@@ -174,18 +176,32 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
     col_i[nb] = q0 + ql;
     col_h[nb] = hkv * a.G + gi;
     col_ok[nb] = (ql < a.QT) && (col_i[nb] < a.Sq);
-    const int64_t qrow = ((static_cast<int64_t>(b) * a.Hq + col_h[nb]) * a.Sq + col_i[nb]) * d;
+    qrow[nb] = ((static_cast<int64_t>(b) * a.Hq + col_h[nb]) * a.Sq + col_i[nb]) * d;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      if (col_ok[nb] && ks * 32 + lg * 8 < d) qmax = fmaxf(qmax, absmax8(a.q_proj + qrow[nb] + ks * 32 + lg * 8));
+  }
+  __shared__ float s_qmax[T::NW];
+  qmax = wave_max(qmax);
+  if (lane == 0) s_qmax[wave] = qmax;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < T::NW; ++w) qmax = fmaxf(qmax, s_qmax[w]);
+  const float qs = qproj_split_scale(qmax);
+#pragma unroll
+  for (int nb = 0; nb < NBW; ++nb) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int d0 = ks * 32 + lg * 8;
       const bool ok = col_ok[nb] && d0 < d;  // d % 8 == 0: the 8 dims from d0 are all real or all padding
-      qr[ks][nb] = ok ? *reinterpret_cast<const half8*>(a.q_rot + qrow + d0) : half8{};
+      qr[ks][nb] = ok ? *reinterpret_cast<const half8*>(a.q_rot + qrow[nb] + d0) : half8{};
       half8 hi = half8{}, lo = half8{};
-      if (ok) split8(a.q_proj + qrow + d0, hi, lo);
+      if (ok) split8s(a.q_proj + qrow[nb] + d0, qs, hi, lo);
       qp[ks][nb] = hi;
       qlo[ks][nb] = lo;
     }
   }
+  const float coeff_q = a.coeff * (1.f / qs);  // q_proj's operands carry qs
 
   // key range this block needs; tiles past `kfull` need per-element masking
   int kend = a.Sk;
@@ -244,7 +260,7 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
       const float vn = ok ? h2f(a.kvn[kr]) : 0.f;
       const float rn = ok ? h2f(a.krn[kr]) : 0.f;
       r_a = fa * vn;
-      r_b = fa * a.coeff * rn;
+      r_b = fa * coeff_q * rn;
       if constexpr (!SCORES) r_v = ok ? h2f(a.vvn[kr]) : 0.f;
     }
   };

@@ -118,6 +118,46 @@ __device__ __forceinline__ void split8(const float* p, half8& hi, half8& lo) {
     lo[j] = static_cast<_Float16>(x - static_cast<float>(hi[j]));
   }
 }
+// split8 of the eight values p[j] * qs
+__device__ __forceinline__ void split8s(const float* p, float qs, half8& hi, half8& lo) {
+  const float4v a = *reinterpret_cast<const float4v*>(p);
+  const float4v b = *reinterpret_cast<const float4v*>(p + 4);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float x = (j < 4 ? a[j] : b[j - 4]) * qs;
+    hi[j] = static_cast<_Float16>(x);
+    lo[j] = static_cast<_Float16>(x - static_cast<float>(hi[j]));
+  }
+}
+// largest |p[j]| of eight values.  Non-temporal loads: the compiler does not merge them with
+// the loads of the split that follows, which would hold every value of a lane in registers
+// until the maximum is known
+__device__ __forceinline__ float absmax8(const float* p) {
+  const float4v a = __builtin_nontemporal_load(reinterpret_cast<const float4v*>(p));
+  const float4v b = __builtin_nontemporal_load(reinterpret_cast<const float4v*>(p + 4));
+  float m = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) m = fmaxf(m, fmaxf(fabsf(a[j]), fabsf(b[j])));
+  return m;
+}
+// Power-of-two scale for q_proj's f16 (hi, lo) split: with m the largest |q_proj| the operands
+// hold, m * qs lies in [2^13, 2^14), so hi stays finite (f16 ends at 65504, the reference keeps
+// q_proj in f32) and lo stays a normal f16 for every value down to ~2^-17 of m.  The QJL
+// term's factor takes 1 / qs; both products are exact.  m = 0 (or not finite) gives 1.
+__device__ __forceinline__ float qproj_split_scale(float m) {
+  int e;
+  frexpf(m, &e);  // m < 2^e
+  const float qs = (!(m > 0.f) || m > 3.0e38f) ? 1.f : ldexpf(1.f, 14 - e);
+  // wave-uniform: kept in a scalar register (the loops around it sit at their VGPR caps)
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, qs)));
+}
+// maximum over the wave, as a wave-uniform (scalar) value
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int sh = 32; sh >= 1; sh >>= 1) v = fmaxf(v, __shfl_xor(v, sh, 64));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+
 __device__ __forceinline__ half8 round8(const float* p) {
   half8 hi, lo;
   split8(p, hi, lo);

@@ -188,6 +188,8 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
   half8 qr[KS][NBW], qp[KS][NBW];
   [[maybe_unused]] half8 qlo[QLDS ? 1 : KS][NBW];
   half8* const wlo = sQlo + wave * (KS * NBW * 64) + lane;  // this lane's lo fragments (QLDS)
+  int64_t qrow[NBW];
+  float qmax = 0.f;  // largest |q_proj| of the block's columns: the scale of its (hi, lo) split
 #pragma unroll
   for (int nb = 0; nb < NBW; ++nb) {
     const int r = (wave * NBW + nb) * 16 + l16;
@@ -195,16 +197,29 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
     col_i[nb] = q0 + ql;
     col_h[nb] = hkv * a.G + gi;
     col_ok[nb] = (ql < a.QT) && (col_i[nb] < a.Sq);
-    const int64_t qrow = ((static_cast<int64_t>(b) * a.Hq + col_h[nb]) * a.Sq + (col_ok[nb] ? col_i[nb] : 0)) * D;
+    qrow[nb] = ((static_cast<int64_t>(b) * a.Hq + col_h[nb]) * a.Sq + (col_ok[nb] ? col_i[nb] : 0)) * D;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      if (col_ok[nb]) qmax = fmaxf(qmax, absmax8(a.q_proj + qrow[nb] + ks * 32 + lg * 8));
+  }
+  __shared__ float s_qmax[kPfWaves];
+  qmax = wave_max(qmax);
+  if (lane == 0) s_qmax[wave] = qmax;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kPfWaves; ++w) qmax = fmaxf(qmax, s_qmax[w]);
+  const float qs = qproj_split_scale(qmax);
+#pragma unroll
+  for (int nb = 0; nb < NBW; ++nb) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int d0 = ks * 32 + lg * 8;
-      qr[ks][nb] = col_ok[nb] ? *reinterpret_cast<const half8*>(a.q_rot + qrow + d0) : half8{};
+      qr[ks][nb] = col_ok[nb] ? *reinterpret_cast<const half8*>(a.q_rot + qrow[nb] + d0) : half8{};
       // the QJL term's k-slots: lane group lg, k-step ks <-> dims 32 lg + 8 ks + 0..7 where the
       // sign operands come from the raw bits (byte 4 lg + ks of the key's sign row)
       const int dp = QLDS ? lg * 32 + ks * 8 : d0;
       half8 hi = half8{}, lo = half8{};
-      if (col_ok[nb]) split8(a.q_proj + qrow + dp, hi, lo);
+      if (col_ok[nb]) split8s(a.q_proj + qrow[nb] + dp, qs, hi, lo);
       qp[ks][nb] = hi;
       if constexpr (QLDS) wlo[(ks * NBW + nb) * 64] = lo;
       else qlo[ks][nb] = lo;
@@ -232,7 +247,7 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
   }
   const int nt = (kend + KT - 1) / KT;
   const float fa = a.scale * LOG2E;  // scores kept in log2 units
-  const float fb = fa * a.coeff;
+  const float fb = fa * a.coeff * (1.f / qs);  // q_proj's operands carry qs
 
   // ---- raw ring: wave 0 copies tile j's planes into slot j % R
   const int64_t g0 = bh * a.ldk;
