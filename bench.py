@@ -812,9 +812,9 @@ def prefill_leg(kc, vc, q, k, v, steps: int, warmup: int) -> dict:
         "query_prep_ms": prep_ms,
         "attention_ms": attn_ms,
         "roofline": {
-            "kernel": "tq::prefill_kernel<3, false> (fused scores + softmax + P.V)",
+            "kernel": "tq::prefill_kernel<128, 3, false> (fused scores + softmax + P.V; q_proj as f16 hi + lo)",
             "bound": "mfma", "achieved": tflops, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": tflops / MFMA_F16_PEAK_TFLOPS, "traffic": measured_traffic("tq::prefill_kernel<3, false>"),
+            "frac": tflops / MFMA_F16_PEAK_TFLOPS, "traffic": measured_traffic("tq::prefill_kernel<128, 3, false>"),
         },
     }
 
