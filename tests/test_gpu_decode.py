@@ -94,14 +94,16 @@ def test_decode_scores_any_codebook(bits, cb, qmul):
 
 @pytest.mark.parametrize("bits", [2, 3])
 @pytest.mark.parametrize("cb", ["nonaffine", "shifted"])
-def test_decode_attention_any_codebook(bits, cb):
+@pytest.mark.parametrize("hq", [8, 16])
+def test_decode_attention_any_codebook(bits, cb, hq):
     """Fused decode attention with key codebooks that are not odd (and, for 2-bit codes, not
-    affine in the code bits) against the oracle evaluated with the same f16 codebook."""
-    _case(bits=bits, cb=cb)
+    affine in the code bits) against the oracle evaluated with the same f16 codebook; 4 and 8
+    columns per kv head (one and two column groups of the bit-plane kernel)."""
+    _case(bits=bits, cb=cb, hq=hq)
     from turboquant_pytorch._ops import ops
     from turboquant_pytorch.compressors import _tables
 
-    B, hq, hkv, sq, sk, d = 2, 8, 2, 1, 2000, 128
+    B, hkv, sq, sk, d = 2, 2, 1, 2000, 128
     assert _on_decode_path(B, hq, hkv, sq, sk, bits)
     torch.manual_seed(11 * bits + len(cb))
     q = torch.randn(B, hq, sq, d, device=DEV, dtype=torch.bfloat16)
@@ -145,6 +147,10 @@ def test_decode_attention_any_codebook(bits, cb):
     (8, 4, 2, 1025, True, 1.0, 1.0),     # 4 columns (2 heads x 2 rows), causal
     (12, 4, 1, 3001, False, 8.0, 3000.0),
     (6, 2, 1, 2048, True, 1.0, 0.01),
+    (16, 2, 1, 5000, False, 1.0, 1.0),   # 8 columns: two column groups of the bit-plane kernel
+    (8, 2, 2, 1025, True, 1.0, 1.0),     # 8 columns (4 heads x 2 rows), causal
+    (5, 1, 1, 777, False, 8.0, 1.0),     # 5 columns: the second group holds one
+    (12, 2, 1, 3001, True, 1.0, 3000.0), # 6 columns, value norms ~3e4
 ])
 def test_decode_attention_matches_oracle_and_tiled(bits, hq, hkv, sq, sk, causal, qmul, vmul):
     _case(bits=bits, hq=hq, hkv=hkv, sq=sq, sk=sk, causal=causal, qmul=qmul, vmul=vmul)
@@ -259,8 +265,9 @@ def test_decode_attention_left_padding(bits, sq, npad):
     """Left padding with finfo.min on the first `npad` keys of batch row 0: whole 32-key slabs,
     and at npad = 1000 whole splits, see only masked keys before the first real one.  Batch row
     1 masks one key with a moderate bias, batch row 2 masks every key (the reference's softmax
-    of equal scores gives every key the same weight).  Sq = 1 takes the bit-plane kernels at
-    bits 2-3 (4 columns), Sq = 2 the table kernels (8 columns).  Against the float64 oracle."""
+    of equal scores gives every key the same weight).  At bits 2-3, Sq = 1 takes the bit-plane
+    kernel's one-group form (4 columns) and Sq = 2 its two-group form (8 columns); bits 4 the
+    table kernel.  Against the float64 oracle."""
     _case(what="decode left padding", bits=bits, sq=sq, npad=npad)
     B, hq, hkv, sk, d = 3, 16, 4, 1500, 128
     assert _on_decode_path(B, hq, hkv, sq, sk, bits)

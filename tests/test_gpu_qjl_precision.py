@@ -143,6 +143,8 @@ def test_scores_qjl_term_f32_grade(d, bits, hq, hkv, sq, sk):
     (64, 3, 12, 12, 40, 48, False),  # head_dim-64 prefill
     (96, 3, 8, 2, 40, 48, False),    # tiled kernel
     (128, 3, 32, 8, 1, 64, False),   # bit-plane decode attention
+    (128, 3, 16, 2, 1, 64, False),   # bit-plane decode attention, two column groups
+    (128, 2, 6, 1, 1, 64, True),     # bit-plane decode attention, bits 2, 6 columns, masked
     (128, 4, 32, 8, 1, 64, False),   # table decode attention
     (128, 3, 32, 8, 3, 64, False),   # table decode attention, 12 columns
 ])

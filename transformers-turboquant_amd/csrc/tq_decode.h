@@ -206,29 +206,39 @@ __device__ __forceinline__ float digits_f32(i32x4v acc) {
   return fmaf(static_cast<float>(hi), 65536.f, static_cast<float>(lo));
 }
 
-// The query side of a block: column c of the block's kv head is MFMA row group c (rows
-// 4c + t, t = digit), so a lane of group lg holds column lg's digits in its A fragments and,
-// after the MFMAs over a 16-key block on the N side, the digit sums of column lg against
-// its own key (lane l16).  STAGE_BYTES of LDS serve as staging during setup().
-template <int KB>
+// The query side of a block: column c of the block's kv head is MFMA row group c & 3 (rows
+// 4 (c & 3) + t, t = digit) of column group c >> 2, so a lane of group lg holds the digits of
+// columns lg, lg + 4, ... (one set of A fragments per column group) and, after the MFMAs over
+// a 16-key block on the N side, the digit sums of those columns against its own key (lane
+// l16).  The key-side plane operands are built once per key and serve every column group.
+// STAGE_BYTES of LDS serve as staging during setup().
+template <int KB, int NCG = 1>
 struct PlaneQuery {
   static_assert(KB == 1 || KB == 2, "1- or 2-bit key codes");
+  static_assert(NCG == 1 || NCG == 2, "4 or 8 columns");
   static constexpr int D = 128;
+  static constexpr int NC = 4 * NCG;           // columns served
   static constexpr int NT1 = 2 * KB;           // code-plane fragments (MFMAs per 16 keys)
   static constexpr int NFM = NT1 + 2;          // then the two sign-plane fragments
   static constexpr int NDL = KB == 2 ? 2 : 0;  // interaction-plane fragments
   static constexpr int NF = NFM + NDL;
-  static constexpr int STAGE_BYTES = (4 * 2 * D * 4 > NFM * 1024) ? 4 * 2 * D * 4 : NFM * 1024;
-  i32x4v A[NF];
-  int x1, x2;      // column lg: dot = 2^x digits_f32(acc)
-  float k1, k2;    // column lg: c0 sum(q_rot), sum(q_proj)
-  bool inter;      // the codebook needs the interaction plane (block-uniform)
+  static constexpr int STAGE_BYTES =
+      (NC * 2 * D * 4 > NCG * NFM * 1024) ? NC * 2 * D * 4 : NCG * NFM * 1024;
+  // with two column groups the interaction-plane fragments (used only by codebooks that are
+  // not affine in their bits) stay in LDS instead of registers
+  static constexpr bool INTER_LDS = NCG > 1 && NDL > 0;
+  i32x4v A[NCG][INTER_LDS ? NFM : NF];
+  const i32x4v* aint;      // INTER_LDS: this lane's interaction fragments, [g * NDL + w] * 64
+  int x1[NCG], x2[NCG];    // column lg + 4g: dot = 2^x digits_f32(acc)
+  float k1[NCG], k2[NCG];  // column lg + 4g: c0 sum(q_rot), sum(q_proj)
+  bool inter;              // the codebook needs the interaction plane (block-uniform)
 
   // Every thread of the block calls this (it holds barriers); the staging area may be
   // reused once the caller has passed another barrier.
   __device__ __forceinline__ void setup(const DecodeArgs& a, int b, int hkv, uint8_t* stg, int tid) {
-    __shared__ float st_k1[4], st_k2[4];
-    __shared__ int st_f1[4], st_f2[4];
+    __shared__ float st_k1[NC], st_k2[NC];
+    __shared__ int st_f1[NC], st_f2[NC];
+    __shared__ i32x4v s_int[INTER_LDS ? NCG * NDL * 64 : 1];
     const int lane = tid & 63, wave = tid >> 6, lg = lane >> 4;
     // codebook in plane form: c(b0, b1) = c0 + alo b0 + ahi b1 + adl b0 b1
     const float c0 = h2f(a.kcent[0]), alo = h2f(a.kcent[1]) - c0;
@@ -236,11 +246,12 @@ struct PlaneQuery {
     const float adl = KB == 2 ? (h2f(a.kcent[3]) - h2f(a.kcent[2])) - alo : 0.f;
     inter = adl != 0.f;
 
-    // phase 1: wave c stages column c (f32) and finds its scales
-    float* const qst = reinterpret_cast<float*>(stg);  // [4][2][D]: q_rot, q_proj
+    // phase 1: wave w stages columns w, w + 4, ... (f32) and finds their scales
+    float* const qst = reinterpret_cast<float*>(stg);  // [NC][2][D]: q_rot, q_proj
     const float cmax = fmaxf(fabsf(alo), fmaxf(fabsf(ahi), fabsf(adl)));
-    {
-      const int c = wave;
+#pragma unroll
+    for (int g = 0; g < NCG; ++g) {
+      const int c = wave + 4 * g;
       float r0 = 0.f, r1 = 0.f, p0 = 0.f, p1 = 0.f;
       if (c < a.C) {
         const int qi = c / a.G, h = hkv * a.G + c % a.G;
@@ -275,16 +286,18 @@ struct PlaneQuery {
     }
     __syncthreads();
 
-    // phase 2: each thread builds dword groups (fragment f, column cq, lane group lg',
-    // element e): 4 A values (bytes j = 0..3) -> one dword per digit row 4 cq + t
-    constexpr int PER = (NF * 64 + 255) / 256;
+    // phase 2: each thread builds dword groups (column group g, fragment f, column 4 g + cq,
+    // lane group lg', element e): 4 A values (bytes j = 0..3) -> one dword per digit row
+    // 4 cq + t
+    constexpr int PER = (NCG * NF * 64 + 255) / 256;
     uint32_t outw[PER][4];
     int oaddr[PER], ofrag[PER];
 #pragma unroll
     for (int r = 0; r < PER; ++r) {
       const int gi = tid + 256 * r;
-      const int e = gi & 3, lgp = (gi >> 2) & 3, cq = (gi >> 4) & 3, f = gi >> 6;
-      ofrag[r] = f;
+      const int e = gi & 3, lgp = (gi >> 2) & 3, cq = (gi >> 4) & 3, gf = gi >> 6;
+      const int g = gf / NF, f = gf % NF;
+      ofrag[r] = g < NCG ? f : NF;
       int i = 0, m0 = 0, mstep = 8, term = 1;  // slot bit i; dims m0 + j * mstep
       float coef = 0.f;
       if (f < NT1) {
@@ -299,19 +312,20 @@ struct PlaneQuery {
         m0 = 32 * lgp + i;
         coef = 2.f;
         term = 2;
-      } else if (f < NF) {
+      } else {
         const int w = f - NFM;
         i = 2 * e;
         m0 = 32 * lgp + 16 * w + e;
         mstep = 4;
         coef = adl;
       }
-      const int F = term == 1 ? st_f1[cq] : st_f2[cq];
-      const float* qv = qst + (cq * 2 + (term - 1)) * D;
+      const int c = 4 * (g < NCG ? g : 0) + cq;
+      const int F = term == 1 ? st_f1[c] : st_f2[c];
+      const float* qv = qst + (c * 2 + (term - 1)) * D;
       uint32_t u[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int wv = f < NF ? __float2int_rn(ldexpf(coef * qv[m0 + j * mstep], F)) : 0;
+        const int wv = g < NCG ? __float2int_rn(ldexpf(coef * qv[m0 + j * mstep], F)) : 0;
         const int av = i < 7 ? wv * (1 << (7 - i)) : -wv;
         u[j] = (static_cast<uint32_t>(av) + 0x808080u) ^ 0x808080u;
       }
@@ -319,80 +333,65 @@ struct PlaneQuery {
       for (int t = 0; t < 4; ++t)
         outw[r][t] = ((u[0] >> (8 * t)) & 0xFFu) | (((u[1] >> (8 * t)) & 0xFFu) << 8) |
                      (((u[2] >> (8 * t)) & 0xFFu) << 16) | (((u[3] >> (8 * t)) & 0xFFu) << 24);
-      oaddr[r] = (((f < NFM ? f : f - NFM) * 64 + 4 * cq + 16 * lgp) * 4 + e) * 4;
+      const int slot = f < NFM ? g * NFM + f : g * NDL + (f - NFM);
+      oaddr[r] = ((slot * 64 + 4 * cq + 16 * lgp) * 4 + e) * 4;
     }
     // the staged queries are read; fragments overwrite them (row 4 cq + t = lane + t)
-    auto put = [&](bool second) {
+    auto put = [&](bool second, uint8_t* dst) {
 #pragma unroll
       for (int r = 0; r < PER; ++r) {
         if (ofrag[r] < NF && (ofrag[r] >= NFM) == second) {
 #pragma unroll
-          for (int t = 0; t < 4; ++t) *reinterpret_cast<uint32_t*>(stg + oaddr[r] + t * 16) = outw[r][t];
+          for (int t = 0; t < 4; ++t) *reinterpret_cast<uint32_t*>(dst + oaddr[r] + t * 16) = outw[r][t];
         }
       }
     };
     __syncthreads();
-    put(false);
+    put(false, stg);
+    if constexpr (INTER_LDS) {
+      if (inter) put(true, reinterpret_cast<uint8_t*>(s_int));
+    }
+    aint = s_int + lane;
     __syncthreads();
 
-    // phase 3: the lane's fragments and its column's constants
+    // phase 3: the lane's fragments and its columns' constants
 #pragma unroll
-    for (int f = 0; f < NFM; ++f) A[f] = *reinterpret_cast<const i32x4v*>(stg + (f * 64 + lane) * 16);
-    if constexpr (NDL > 0) {
+    for (int g = 0; g < NCG; ++g)
+#pragma unroll
+      for (int f = 0; f < NFM; ++f) A[g][f] = *reinterpret_cast<const i32x4v*>(stg + ((g * NFM + f) * 64 + lane) * 16);
+    if constexpr (NDL > 0 && !INTER_LDS) {
       if (inter) {
         __syncthreads();
-        put(true);
+        put(true, stg);
         __syncthreads();
 #pragma unroll
-        for (int f = NFM; f < NF; ++f) A[f] = *reinterpret_cast<const i32x4v*>(stg + ((f - NFM) * 64 + lane) * 16);
+        for (int g = 0; g < NCG; ++g)
+#pragma unroll
+          for (int f = NFM; f < NF; ++f)
+            A[g][f] = *reinterpret_cast<const i32x4v*>(stg + ((g * NDL + f - NFM) * 64 + lane) * 16);
       } else {
 #pragma unroll
-        for (int f = NFM; f < NF; ++f) A[f] = i32x4v{0, 0, 0, 0};
+        for (int g = 0; g < NCG; ++g)
+#pragma unroll
+          for (int f = NFM; f < NF; ++f) A[g][f] = i32x4v{0, 0, 0, 0};
       }
     }
-    x1 = -7 - st_f1[lg];
-    x2 = -7 - st_f2[lg];
-    k1 = st_k1[lg];
-    k2 = st_k2[lg];
+#pragma unroll
+    for (int g = 0; g < NCG; ++g) {
+      x1[g] = -7 - st_f1[lg + 4 * g];
+      x2[g] = -7 - st_f2[lg + 4 * g];
+      k1[g] = st_k1[lg + 4 * g];
+      k2[g] = st_k2[lg + 4 * g];
+    }
   }
 
-  // term 1 (q_rot . f16(C)[codes]) and term 2 (q_proj . (2 s - 1)) of column lg against the
-  // key whose code field (KB dwords) and sign field (one dword) this lane reads from LDS
-  __device__ __forceinline__ void dots(const uint8_t* kp, const uint8_t* sp, float& t1, float& t2) const {
-    uint32_t kw[KB];
-    if constexpr (KB == 2) {
-      const u32x2 t = *reinterpret_cast<const u32x2*>(kp);
-      kw[0] = t[0];
-      kw[1] = t[1];
-    } else {
-      kw[0] = *reinterpret_cast<const uint32_t*>(kp);
-    }
-    const uint32_t sw = *reinterpret_cast<const uint32_t*>(sp);
-    i32x4v s1 = i32x4v{0, 0, 0, 0}, s2 = i32x4v{0, 0, 0, 0};
-    static_for<NT1>([&](auto ff) {
-      constexpr int f = decltype(ff)::value;
-      s1 = mfma_i8(A[f], planes4<4 * (f & 1)>(kw[f >> 1]), s1);
-    });
-    static_for<2>([&](auto ff) {
-      constexpr int f = decltype(ff)::value;
-      s2 = mfma_i8(A[NT1 + f], planes4<4 * f>(sw), s2);
-    });
-    if constexpr (NDL > 0) {
-      if (inter) {
-        static_for<NDL>([&](auto ff) {
-          constexpr int w = decltype(ff)::value;
-          s1 = mfma_i8(A[NFM + w], planes_even(kw[w] & (kw[w] >> 1)), s1);
-        });
-      }
-    }
-    t1 = ldexpf(digits_f32(s1), x1) + k1;
-    t2 = ldexpf(digits_f32(s2), x2) - k2;
-  }
-  // dots() of two keys: both keys' fields are read before any MFMA, and the (block-uniform,
-  // rare) interaction-plane branch is taken once for both, so that it does not split the
-  // keys' work into separate basic blocks
+  // term 1 (q_rot . f16(C)[codes]) and term 2 (q_proj . (2 s - 1)) of columns lg + 4g against
+  // two keys, whose code fields (KB dwords each) and sign fields (one dword each) this lane
+  // reads from LDS.  Both keys' fields are read before any MFMA, and the (block-uniform, rare)
+  // interaction-plane branch is taken once for both, so that it does not split the keys'
+  // work into separate basic blocks; each plane operand feeds the MFMAs of every column group.
   __device__ __forceinline__ void dots2(const uint8_t* kp0, const uint8_t* sp0, const uint8_t* kp1,
-                                        const uint8_t* sp1, float (&t1)[2], float (&t2)[2]) const {
+                                        const uint8_t* sp1, float (&t1)[2][NCG], float (&t2)[2][NCG]) const {
     uint32_t kw[2][KB], sw[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -406,34 +405,75 @@ struct PlaneQuery {
       }
       sw[j] = *reinterpret_cast<const uint32_t*>(j ? sp1 : sp0);
     }
-    i32x4v s1[2], s2[2];
+    if constexpr (NCG == 1) {
+      i32x4v s1[2], s2[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      s1[j] = i32x4v{0, 0, 0, 0};
-      s2[j] = i32x4v{0, 0, 0, 0};
-      static_for<NT1>([&](auto ff) {
-        constexpr int f = decltype(ff)::value;
-        s1[j] = mfma_i8(A[f], planes4<4 * (f & 1)>(kw[j][f >> 1]), s1[j]);
-      });
-      static_for<2>([&](auto ff) {
-        constexpr int f = decltype(ff)::value;
-        s2[j] = mfma_i8(A[NT1 + f], planes4<4 * f>(sw[j]), s2[j]);
-      });
-    }
-    if constexpr (NDL > 0) {
-      if (inter) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          static_for<NDL>([&](auto ff) {
-            constexpr int w = decltype(ff)::value;
-            s1[j] = mfma_i8(A[NFM + w], planes_even(kw[j][w] & (kw[j][w] >> 1)), s1[j]);
-          });
+      for (int j = 0; j < 2; ++j) {
+        s1[j] = i32x4v{0, 0, 0, 0};
+        s2[j] = i32x4v{0, 0, 0, 0};
+        static_for<NT1>([&](auto ff) {
+          constexpr int f = decltype(ff)::value;
+          s1[j] = mfma_i8(A[0][f], planes4<4 * (f & 1)>(kw[j][f >> 1]), s1[j]);
+        });
+        static_for<2>([&](auto ff) {
+          constexpr int f = decltype(ff)::value;
+          s2[j] = mfma_i8(A[0][NT1 + f], planes4<4 * f>(sw[j]), s2[j]);
+        });
       }
-    }
+      if constexpr (NDL > 0) {
+        if (inter) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      t1[j] = ldexpf(digits_f32(s1[j]), x1) + k1;
-      t2[j] = ldexpf(digits_f32(s2[j]), x2) - k2;
+          for (int j = 0; j < 2; ++j)
+            static_for<NDL>([&](auto ff) {
+              constexpr int w = decltype(ff)::value;
+              s1[j] = mfma_i8(A[0][NFM + w], planes_even(kw[j][w] & (kw[j][w] >> 1)), s1[j]);
+            });
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        t1[j][0] = ldexpf(digits_f32(s1[j]), x1[0]) + k1[0];
+        t2[j][0] = ldexpf(digits_f32(s2[j]), x2[0]) - k2[0];
+      }
+    } else {
+      // one key at a time (its accumulators die at its conversion); each plane operand feeds
+      // the MFMAs of both column groups
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        i32x4v s1[NCG], s2[NCG];
+#pragma unroll
+        for (int g = 0; g < NCG; ++g) {
+          s1[g] = i32x4v{0, 0, 0, 0};
+          s2[g] = i32x4v{0, 0, 0, 0};
+        }
+        static_for<NT1>([&](auto ff) {
+          constexpr int f = decltype(ff)::value;
+          const i32x4v op = planes4<4 * (f & 1)>(kw[j][f >> 1]);
+#pragma unroll
+          for (int g = 0; g < NCG; ++g) s1[g] = mfma_i8(A[g][f], op, s1[g]);
+        });
+        static_for<2>([&](auto ff) {
+          constexpr int f = decltype(ff)::value;
+          const i32x4v op = planes4<4 * f>(sw[j]);
+#pragma unroll
+          for (int g = 0; g < NCG; ++g) s2[g] = mfma_i8(A[g][NT1 + f], op, s2[g]);
+        });
+        if constexpr (NDL > 0) {
+          if (inter) {
+            static_for<NDL>([&](auto ff) {
+              constexpr int w = decltype(ff)::value;
+              const i32x4v op = planes_even(kw[j][w] & (kw[j][w] >> 1));
+#pragma unroll
+              for (int g = 0; g < NCG; ++g) s1[g] = mfma_i8(aint[(g * NDL + w) * 64], op, s1[g]);
+            });
+          }
+        }
+#pragma unroll
+        for (int g = 0; g < NCG; ++g) {
+          t1[j][g] = ldexpf(digits_f32(s1[g]), x1[g]) + k1[g];
+          t2[j][g] = ldexpf(digits_f32(s2[g]), x2[g]) - k2[g];
+        }
+      }
     }
   }
 };

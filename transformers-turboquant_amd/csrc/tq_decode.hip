@@ -438,7 +438,7 @@ __global__ void __launch_bounds__(256) decode_scores_i8_kernel(DecodeArgs a) {
   if (k0w + (R - 1) * SLAB < kend) issue(k0w + (R - 1) * SLAB, R - 1);
 
   auto slab = [&](const uint8_t* src, int ks0) {
-    float sc[2], t1[2], t2[2];
+    float sc[2], t1[2][1], t2[2][1];
     pq.dots2(src + OFF_K + (2 * l16) * KC + lg * KLANE, src + OFF_S + (2 * l16) * SC + lg * 4,
              src + OFF_K + (2 * l16 + 1) * KC + lg * KLANE, src + OFF_S + (2 * l16 + 1) * SC + lg * 4, t1, t2);
 #pragma unroll
@@ -446,7 +446,7 @@ __global__ void __launch_bounds__(256) decode_scores_i8_kernel(DecodeArgs a) {
       const int row = 2 * l16 + u;
       const float kn = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + row * 4)));
       const float rn = fb * h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + NRM + row * 4)));
-      sc[u] = fmaf(t1[u], kn, t2[u] * rn);
+      sc[u] = fmaf(t1[u][0], kn, t2[u][0] * rn);
     }
     const int key = ks0 + 2 * l16;
     if (key < kend) {
@@ -483,24 +483,26 @@ void launch_scores_planes(const DecodeArgs& a, int bits, hipStream_t s) {
   else decode_scores_i8_kernel<2, 3><<<grid, 256, 0, s>>>(a);
 }
 
-// Fused decode attention for 1- and 2-bit key codes and at most 4 columns, scores on the
+// Fused decode attention for 1- and 2-bit key codes and at most 8 columns, scores on the
 // integer MFMA in bit-plane form (PlaneQuery, tq_decode.h) with the keys on the N side:
-// lane (key n, group g) scores key n of each 16-key block for column g, so the softmax
-// runs once per (column, key) instead of once per MFMA column.  P goes through a small
-// per-wave LDS tile into the P^T operand of the value MFMA (the same O^T += V^T P^T step
-// as decode_attn_lds_kernel, with column n of O^T serving column n & 3).
+// lane (key n, group g) scores key n of each 16-key block for columns g, g + 4 (NCG column
+// groups of 4), so the softmax runs once per (column, key) instead of once per MFMA column.
+// P goes through a small per-wave LDS tile into the P^T operand of the value MFMA (the same
+// O^T += V^T P^T step as decode_attn_lds_kernel, with column n of O^T serving column
+// n & (4 NCG - 1)); the value decode is shared by all of a kv head's columns.
 //
 // MASK (an additive mask is applied): scores stay absolute until the column maximum is
 // settled and are made relative to it after the rescale test.  The unmasked form folds the
 // reference into the score fmas (s - mref), which is exact only while mref is of the order
 // of real scores: a leading slab masked with finfo.min (clamped to -3e38) would set mref to
 // -3e38, and s - mref would then round every later real score to the same value.
-template <int KB, int R, bool MASK>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+template <int KB, int R, bool MASK, int NCG>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NCG == 1 ? 4 : 3)))
 decode_attn_i8_kernel(DecodeArgs a) {
   constexpr int D = 128, BITS = KB + 1;
   using L = SmallLuts<BITS>;
-  using PQ = PlaneQuery<KB>;
+  using PQ = PlaneQuery<KB, NCG>;
+  constexpr int NC = PQ::NC;
   constexpr int VB = L::VB;
   constexpr int DB = D / 16;
   constexpr int KC = D * KB / 8, SC = D / 8, VC = D * VB / 8;
@@ -512,7 +514,7 @@ decode_attn_i8_kernel(DecodeArgs a) {
   constexpr int NRM = NK * 4;
   constexpr int SLOT = OFF_N + 3 * NRM;
   constexpr int STG = 4 * SLOT;  // slot r of the four waves; slot R - 1 first stages the set-up
-  constexpr int MERGE = 4 * 4 * (D + 2) * 4;
+  constexpr int MERGE = 4 * NC * (D + 2) * 4;
   constexpr int STAGE = R * STG > MERGE ? R * STG : MERGE;
   static_assert(STG >= PQ::STAGE_BYTES, "set-up staging fits in one ring slot per wave");
   static_assert(R >= 2 && R <= 3, "ring of 2 or 3 slots");
@@ -522,7 +524,7 @@ decode_attn_i8_kernel(DecodeArgs a) {
 
   __shared__ __attribute__((aligned(16))) uint8_t luts[L::BYTES];
   __shared__ __attribute__((aligned(16))) uint8_t stage[STAGE];
-  __shared__ __attribute__((aligned(16))) _Float16 ptile[4][4][NK];  // per wave: P [column][key]
+  __shared__ __attribute__((aligned(16))) _Float16 ptile[4][NC][NK];  // per wave: P [column][key]
   const uint8_t* tV = luts + L::VAL_OFF;
   uint8_t* const stg = stage + (R - 1) * STG;
 
@@ -533,12 +535,20 @@ decode_attn_i8_kernel(DecodeArgs a) {
 
   build_small_luts<BITS, true>(a, luts, tid);
 
-  // this lane's score column lg
-  const bool c_ok = lg < a.C;
-  const int qi = c_ok ? lg / a.G : 0, h = hkv * a.G + (c_ok ? lg % a.G : 0);
+  // this lane's score columns lg + 4g
+  bool c_ok[NCG];
+  int lim[NCG];
+  const float* mrow[NCG];  // MASK: the column's mask row (key 0)
+#pragma unroll
+  for (int g = 0; g < NCG; ++g) {
+    const int c = lg + 4 * g;
+    c_ok[g] = c < a.C;
+    const int qi = c_ok[g] ? c / a.G : 0, h = hkv * a.G + (c_ok[g] ? c % a.G : 0);
+    lim[g] = a.causal ? qi + (a.Sk - a.Sq) : 0x7fffffff;
+    mrow[g] = MASK ? a.mask + (b * a.smb + h * a.smh + static_cast<int64_t>(qi) * a.smq) : nullptr;
+  }
   const float fa = a.scale * LOG2E;
   const float fb = a.coeff * fa;
-  const int lim = a.causal ? qi + (a.Sk - a.Sq) : 0x7fffffff;
   const int causal_from = a.causal ? a.Sk - a.Sq : 0x7fffffff;
   const int kbeg = split * a.chunk;
   const int kend = min(a.Sk, kbeg + a.chunk);
@@ -593,9 +603,15 @@ decode_attn_i8_kernel(DecodeArgs a) {
   __syncthreads();  // fragments held (and tables built): the staging slot joins the ring
   if (k0w + (R - 1) * SLAB < kend) issue(k0w + (R - 1) * SLAB, R - 1);
 
-  // column lg: reference mref = m - PUP (0 until the column has a maximum m) and the threshold
-  // a score relative to mref must exceed to move it (-inf until then, TAU + PUP after)
-  float mref = 0.f, thr = -INFINITY, l_run = 0.f;
+  // column lg + 4g: reference mref = m - PUP (0 until the column has a maximum m) and the
+  // threshold a score relative to mref must exceed to move it (-inf until then, TAU + PUP after)
+  float mref[NCG], thr[NCG], l_run[NCG];
+#pragma unroll
+  for (int g = 0; g < NCG; ++g) {
+    mref[g] = 0.f;
+    thr[g] = -INFINITY;
+    l_run[g] = 0.f;
+  }
   float vcap = 0x1p-24f, inv_vcap = 0x1p24f;
   float4v oacc[DB];
 #pragma unroll
@@ -603,8 +619,8 @@ decode_attn_i8_kernel(DecodeArgs a) {
   _Float16* const pt = &ptile[wave][0][0];
 
   auto slab = [&](const uint8_t* src, int ks0) {
-    // ---- scores of keys ks0 + 16j + l16 (j = 0, 1) for column lg, log2 domain
-    float sc[2], nv[2], t1[2], t2[2];
+    // ---- scores of keys ks0 + 16j + l16 (j = 0, 1) for columns lg + 4g, log2 domain
+    float sc[NCG][2], nv[2], t1[2][NCG], t2[2][NCG];
     pq.dots2(src + OFF_K + l16 * KC + lg * KLANE, src + OFF_S + l16 * SC + lg * 4,
              src + OFF_K + (16 + l16) * KC + lg * KLANE, src + OFF_S + (16 + l16) * SC + lg * 4, t1, t2);
 #pragma unroll
@@ -613,8 +629,11 @@ decode_attn_i8_kernel(DecodeArgs a) {
       const float kn = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + row * 4)));
       const float rn = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + NRM + row * 4)));
       nv[j] = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + 2 * NRM + row * 4)));
+      const float ka = fa * kn, kb = fb * rn;
       // s - mref; absolute s under a mask (made relative after the rescale test)
-      sc[j] = fmaf(t1[j], fa * kn, MASK ? t2[j] * (fb * rn) : fmaf(t2[j], fb * rn, -mref));
+#pragma unroll
+      for (int g = 0; g < NCG; ++g)
+        sc[g][j] = fmaf(t1[j][g], ka, MASK ? t2[j][g] * kb : fmaf(t2[j][g], kb, -mref[g]));
     }
     // ---- value norms enter P as vn / vcap <= 1; vcap is a power of two that only grows
     {
@@ -638,55 +657,78 @@ decode_attn_i8_kernel(DecodeArgs a) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int key = ks0 + 16 * j + l16;
-        if (MASK && c_ok && key < kend)
-          sc[j] += fmaxf(a.mask[b * a.smb + h * a.smh + static_cast<int64_t>(qi) * a.smq +
-                                static_cast<int64_t>(key) * a.smk] * LOG2E,
-                         -3.0e38f);
-        if (key >= kend || key > lim) sc[j] = -INFINITY;
+#pragma unroll
+        for (int g = 0; g < NCG; ++g) {
+          if (MASK && c_ok[g] && key < kend)
+            sc[g][j] += fmaxf(mrow[g][static_cast<int64_t>(key) * a.smk] * LOG2E, -3.0e38f);
+          if (key >= kend || key > lim[g]) sc[g][j] = -INFINITY;
+        }
       }
     }
-    // ---- lazy online softmax: column lg's maximum m (uniform over the 16 lanes of the column)
+    // ---- lazy online softmax: column c's maximum m (uniform over the 16 lanes of the column)
     // moves only when a score exceeds it by more than TAU; p = 2^(s - m + PUP) = 2^sc
-    const float lmax = max_raw(sc[0], sc[1]);
-    if (__any((MASK ? lmax - mref : lmax) > thr)) {
-      float t = lmax;
+    float lmax[NCG];
+    bool hit = false;
 #pragma unroll
-      for (int sh = 8; sh >= 1; sh >>= 1) t = fmaxf(t, __shfl_xor(t, sh, 64));
-      float alpha = 1.f;
-      if ((MASK ? t - mref : t) > thr) {
-        const float mref_new = (MASK ? t : t + mref) - PUP;
-        alpha = (thr == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mref - mref_new);
-        if constexpr (!MASK) {
-          const float shift = mref_new - mref;
-          sc[0] -= shift;
-          sc[1] -= shift;
+    for (int g = 0; g < NCG; ++g) {
+      lmax[g] = max_raw(sc[g][0], sc[g][1]);
+      hit = hit || (MASK ? lmax[g] - mref[g] : lmax[g]) > thr[g];
+    }
+    if (__any(hit)) {
+      float alpha[NCG];
+#pragma unroll
+      for (int g = 0; g < NCG; ++g) {
+        float t = lmax[g];
+#pragma unroll
+        for (int sh = 8; sh >= 1; sh >>= 1) t = fmaxf(t, __shfl_xor(t, sh, 64));
+        alpha[g] = 1.f;
+        if ((MASK ? t - mref[g] : t) > thr[g]) {
+          const float mref_new = (MASK ? t : t + mref[g]) - PUP;
+          alpha[g] = (thr[g] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mref[g] - mref_new);
+          if constexpr (!MASK) {
+            const float shift = mref_new - mref[g];
+            sc[g][0] -= shift;
+            sc[g][1] -= shift;
+          }
+          mref[g] = mref_new;
+          thr[g] = TAU + PUP;
+          l_run[g] *= alpha[g];
         }
-        mref = mref_new;
-        thr = TAU + PUP;
-        l_run *= alpha;
       }
-      const float ac = __shfl(alpha, 16 * (l16 & 3), 64);  // O^T column l16 serves column l16 & 3
+      // O^T column l16 serves column l16 & (NC - 1), held by lane group l16 & 3
+      float ac = __shfl(alpha[0], 16 * (l16 & 3), 64);
+      if constexpr (NCG == 2) {
+        const float a1 = __shfl(alpha[1], 16 * (l16 & 3), 64);
+        ac = (l16 & 4) ? a1 : ac;
+      }
 #pragma unroll
       for (int db = 0; db < DB; ++db) oacc[db] *= ac;
     }
     if constexpr (MASK) {
       // relative to the settled reference: a column that has seen only masked keys (all at
       // -3e38) gives them equal weights, as the reference's softmax of equal scores does
-      sc[0] -= mref;
-      sc[1] -= mref;
+#pragma unroll
+      for (int g = 0; g < NCG; ++g) {
+        sc[g][0] -= mref[g];
+        sc[g][1] -= mref[g];
+      }
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const float p = __builtin_amdgcn_exp2f(sc[j]);
-      l_run += p;
-      pt[lg * NK + 16 * j + l16] = static_cast<_Float16>(p * (nv[j] * inv_vcap));
+      const float vs = nv[j] * inv_vcap;
+#pragma unroll
+      for (int g = 0; g < NCG; ++g) {
+        const float p = __builtin_amdgcn_exp2f(sc[g][j]);
+        l_run[g] += p;
+        pt[(lg + 4 * g) * NK + 16 * j + l16] = static_cast<_Float16>(p * vs);
+      }
     }
     // ---- values: O^T += V^T (P * vn)^T over the slab's 32 keys in one 16x16x32 MFMA per row
     // block: K-slot 8lg + 4j + e is key 16j + 4lg + e; the B operand (column l16) reads
-    // column l16 & 3 of the P tile
+    // column l16 & (NC - 1) of the P tile
     half8 pb;
     {
-      const _Float16* pr = pt + (l16 & 3) * NK + 4 * lg;
+      const _Float16* pr = pt + (l16 & (NC - 1)) * NK + 4 * lg;
       const u32x2 p0 = *reinterpret_cast<const u32x2*>(pr);
       const u32x2 p1 = *reinterpret_cast<const u32x2*>(pr + 16);
       pb = __builtin_bit_cast(half8, u32x4{p0[0], p0[1], p1[0], p1[1]});
@@ -759,21 +801,28 @@ decode_attn_i8_kernel(DecodeArgs a) {
 
   // ---- merge the 4 waves of the block in LDS (reusing the staging area)
   __syncthreads();
-  float* mrg = reinterpret_cast<float*>(stage);  // [wave][column < 4][D + 2]
-  float l = l_run;
+  float* mrg = reinterpret_cast<float*>(stage);  // [wave][column < NC][D + 2]
+  float l[NCG];
 #pragma unroll
-  for (int sh = 8; sh >= 1; sh >>= 1) l += __shfl_xor(l, sh, 64);
-  if (l16 < 4) {
-    float* my = mrg + (wave * 4 + l16) * (D + 2);
+  for (int g = 0; g < NCG; ++g) {
+    l[g] = l_run[g];
+#pragma unroll
+    for (int sh = 8; sh >= 1; sh >>= 1) l[g] += __shfl_xor(l[g], sh, 64);
+  }
+  if (l16 < NC) {
+    float* my = mrg + (wave * NC + l16) * (D + 2);
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
       for (int e = 0; e < 4; ++e) my[(lg * 4 + e) * (D / 16) + db] = oacc[db][e] * vcap;
   }
   if (l16 == 0) {
-    float* my = mrg + (wave * 4 + lg) * (D + 2);
-    my[D] = (thr == -INFINITY) ? -INFINITY : mref;
-    my[D + 1] = l;
+#pragma unroll
+    for (int g = 0; g < NCG; ++g) {
+      float* my = mrg + (wave * NC + lg + 4 * g) * (D + 2);
+      my[D] = (thr[g] == -INFINITY) ? -INFINITY : mref[g];
+      my[D + 1] = l[g];
+    }
   }
   __syncthreads();
   const int64_t pbase = (bh * a.nsplit + split) * a.C;
@@ -781,11 +830,11 @@ decode_attn_i8_kernel(DecodeArgs a) {
     const int c = it / D, d = it % D;
     float mx = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, mrg[(w * 4 + c) * (D + 2) + D]);
+    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, mrg[(w * NC + c) * (D + 2) + D]);
     float o = 0.f, ls = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const float* srcm = mrg + (w * 4 + c) * (D + 2);
+      const float* srcm = mrg + (w * NC + c) * (D + 2);
       const float scw = (srcm[D] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(srcm[D] - mx);
       o += scw * srcm[d];
       ls += scw * srcm[D + 1];
@@ -807,23 +856,24 @@ struct MergeArgs {
   int64_t sob, soh, sos;
 };
 
-// One block per (batch, kv head): combine the splits of its C columns with
+// One block per (batch, kv head, group of 4 columns): combine the splits of its columns with
 // log-sum-exp weights into o[c][:] (LDS), then out^T = Pi_v^T o^T on MFMA with
 // Pi_v^T as the split-f16 A operand (rows i = output dim) and o^T as split-f16 B
 // operand (columns c, scaled per column by a power of two), hi.hi + lo.hi + hi.lo.
 // The kernel is latency-bound (a few KB per block), so it is laid out as few dependent
 // round trips as possible: each wave first issues the loads of its Pi_v^T fragments,
-// then combines whole columns (c = wave, wave + 4, ...) on its own: split maxima and
+// then combines one whole column (c = 4 blockIdx.z + wave) on its own: split maxima and
 // weights by wave reductions, and 2 dims per lane summed over all splits with the loads
-// of a batch issued together; one block barrier precedes the Pi_v product.
+// of a batch issued together; one block barrier precedes the Pi_v product.  Columns beyond
+// the first 4 of a kv head go to further blocks rather than further rounds of a wave.
 template <int D>
 __global__ void __launch_bounds__(256) decode_merge_kernel(MergeArgs a) {
   static_assert(D == 128, "merge is built for head_dim 128");
   constexpr int SW = 64;  // splits per weight batch (one per lane)
-  __shared__ float o_s[16 * D];
+  __shared__ float o_s[4 * D];
   __shared__ float s_w[4][SW];
-  __shared__ float s_up[16];
-  const int hkv = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  __shared__ float s_up[4];
+  const int hkv = blockIdx.x, b = blockIdx.y, c0 = blockIdx.z * 4, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6, l16 = lane & 15, lg = lane >> 4;
   const int C = a.C, ns = a.nsplit;
   const int64_t base = (static_cast<int64_t>(b) * a.Hkv + hkv) * ns;  // first split record
@@ -842,13 +892,13 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeArgs a) {
     }
   }
 
-  // ---- columns c = wave, wave + 4, ...: o[c] = sum_s w_s o_s / sum_s w_s l_s
-  for (int c = wave; c < 16; c += 4) {
-    float* oc = o_s + c * D;
+  // ---- column c = c0 + wave: o[c] = sum_s w_s o_s / sum_s w_s l_s
+  for (int c = c0 + wave; c < c0 + 4; c += 4) {
+    float* oc = o_s + (c - c0) * D;
     if (c >= C) {
       oc[2 * lane] = 0.f;
       oc[2 * lane + 1] = 0.f;
-      if (lane == 0) s_up[c] = 1.f;
+      if (lane == 0) s_up[c - c0] = 1.f;
       continue;
     }
     auto ml = [&](int s, int k) { return a.part_ml[((base + s) * C + c) * 2 + k]; };
@@ -922,17 +972,18 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeArgs a) {
     if (lane == 0) {
       int ex;
       frexpf(m, &ex);
-      s_up[c] = ldexpf(kSplit, -ex);  // scaled |o| < kSplit
+      s_up[c - c0] = ldexpf(kSplit, -ex);  // scaled |o| < kSplit
     }
   }
   __syncthreads();
 
-  // ---- out^T[i][c] = sum_j Pi_v^T[i][j] o[c][j]; wave w owns output rows 32w .. 32w+31
-  const float up = s_up[l16];
+  // ---- out^T[i][c] = sum_j Pi_v^T[i][j] o[c][j]; wave w owns output rows 32w .. 32w+31;
+  // MFMA column l16 < 4 is column c0 + l16 (the other 12 repeat them and are not stored)
+  const float up = s_up[l16 & 3];
   half8 bh[D / 32], bl[D / 32];
 #pragma unroll
   for (int ks = 0; ks < D / 32; ++ks) {
-    const float* src = o_s + l16 * D + ks * 32 + lg * 8;
+    const float* src = o_s + (l16 & 3) * D + ks * 32 + lg * 8;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       _Float16 h, lo;
@@ -941,8 +992,8 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeArgs a) {
       bl[ks][e] = lo;
     }
   }
-  const bool col_ok = l16 < C;
-  const int qi = col_ok ? l16 / a.G : 0, h = hkv * a.G + (col_ok ? l16 % a.G : 0);
+  const bool col_ok = l16 < 4 && c0 + l16 < C;
+  const int qi = col_ok ? (c0 + l16) / a.G : 0, h = hkv * a.G + (col_ok ? (c0 + l16) % a.G : 0);
   const float down = kUnsplit2 / up;  // 1/(kSplit * up) * (1/kSplit) for Pi_v^T's scale
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
@@ -967,17 +1018,23 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeArgs a) {
   }
 }
 
-// bit-plane kernel for 1- and 2-bit key codes and at most 4 columns
-static bool attn_planes(int bits, int C) { return bits <= 3 && C <= 4; }
+// bit-plane kernel for 1- and 2-bit key codes and at most 8 columns (one or two groups of 4)
+static bool attn_planes(int bits, int C) { return bits <= 3 && C <= 8; }
 constexpr int kAttnPlaneRing = 2;
+
+template <int KB, int NCG>
+static const void* attn_i8_kernel() {
+  return reinterpret_cast<const void*>(&decode_attn_i8_kernel<KB, kAttnPlaneRing, false, NCG>);
+}
 
 // grid target of the fused decode attention: one round of resident blocks
 static int attn_target_blocks(int bits, int C) {
-  static int cache[5][16] = {};
+  static int cache[7][16] = {};
   if (attn_planes(bits, C)) {
-    const void* k = bits == 2 ? reinterpret_cast<const void*>(&decode_attn_i8_kernel<1, kAttnPlaneRing, false>)
-                              : reinterpret_cast<const void*>(&decode_attn_i8_kernel<2, kAttnPlaneRing, false>);
-    return resident_blocks(k, 256, cache[bits + 1]);
+    const bool two = C > 4;
+    const void* k = bits == 2 ? (two ? attn_i8_kernel<1, 2>() : attn_i8_kernel<1, 1>())
+                              : (two ? attn_i8_kernel<2, 2>() : attn_i8_kernel<2, 1>());
+    return resident_blocks(k, 256, cache[bits + 1 + (two ? 2 : 0)]);
   }
   const void* k = bits == 2 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 2, kAttnNbs, kAttnRing, true>)
                 : bits == 3 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 3, kAttnNbs, kAttnRing, true>)
@@ -1014,8 +1071,13 @@ static void launch_decode_attn(const DecodeArgs& a, hipStream_t s) {
   dim3 grid(a.nsplit, a.Hkv, a.B);
   if constexpr (BITS <= 3) {
     if (attn_planes(BITS, a.C)) {
-      if (a.mask) decode_attn_i8_kernel<BITS - 1, kAttnPlaneRing, true><<<grid, 256, 0, s>>>(a);
-      else decode_attn_i8_kernel<BITS - 1, kAttnPlaneRing, false><<<grid, 256, 0, s>>>(a);
+      if (a.C > 4) {
+        if (a.mask) decode_attn_i8_kernel<BITS - 1, kAttnPlaneRing, true, 2><<<grid, 256, 0, s>>>(a);
+        else decode_attn_i8_kernel<BITS - 1, kAttnPlaneRing, false, 2><<<grid, 256, 0, s>>>(a);
+      } else {
+        if (a.mask) decode_attn_i8_kernel<BITS - 1, kAttnPlaneRing, true, 1><<<grid, 256, 0, s>>>(a);
+        else decode_attn_i8_kernel<BITS - 1, kAttnPlaneRing, false, 1><<<grid, 256, 0, s>>>(a);
+      }
       return;
     }
   }
@@ -1085,7 +1147,7 @@ int decode_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, co
   m.sob = sob;
   m.soh = soh;
   m.sos = sos;
-  dim3 grid(Hkv, B);
+  dim3 grid(Hkv, B, (a.C + 3) / 4);
   decode_merge_kernel<128><<<grid, 256, 0, s>>>(m);
   return launch_status("tq_attention_fwd (decode merge)");
 }
