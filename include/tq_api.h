@@ -151,8 +151,9 @@ int tq_query_prep(const void* q, int32_t dtype, int32_t B, int32_t Hq,
 
 /* Materialised asymmetric scores out f32 [B, Hq, Sq, Sk] (contiguous):
  *   out = vn * <q_rot, C[codes]> + coeff * rn * <q_proj, 2*sign - 1>
- * from q_rot f16 / q_proj f32 [B, Hq, Sq, d] (tq_query_prep; q_proj enters as
- * f16 hi + lo, i.e. at f32 grade) and key planes of
+ * from q_rot f16 / q_proj f32 [B, Hq, Sq, d] (tq_query_prep; q_proj enters at f32
+ * grade: as 24-bit fixed point per query in the bit-plane decode kernels, as f16
+ * hi + lo elsewhere) and key planes of
  * [B, Hkv, Sk] rows; query head h reads kv head h / (Hq / Hkv).
  * centroids_f16 holds the 2^(bits-1) key centroids.  bits is the total key
  * bit budget (codes use bits-1 bits), as in the reference.
@@ -166,8 +167,7 @@ int tq_attention_scores(const uint16_t* q_rot, const float* q_proj,
                         int32_t bits, float coeff, float* out, void* stream);
 
 /* Fused compressed-domain attention (one attention layer's tail).  q_proj f32 as in
- * tq_attention_scores; the split-K decode kernels and the tiled kernel (head dims other than
- * 128) use it at f32 grade (hi + lo), the head_dim-128 prefill kernel its f16 rounding:
+ * tq_attention_scores, taken at f32 grade by every kernel:
  *   s   = (vn*<q_rot,Ck[codes]> + coeff*rn*<q_proj, 2*sign-1>) * scale
  *         (+ mask[b, h, i, j] if mask != NULL) (causal: key j > i + Sk - Sq dropped)
  *   p   = softmax_j(s)                    (f32, online)

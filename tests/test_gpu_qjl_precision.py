@@ -16,8 +16,8 @@ score scale, and attention outputs within the usual rel-err 1e-3 / cosine 0.9999
 also checks that it is sensitive: the oracle with q_proj rounded to f16 misses the bar by at
 least 10x.  Kernels covered, by shape: the head_dim-128 prefill kernel (unmasked, whose lo
 fragments live in LDS, and masked), the head_dim-64 prefill kernel, the tiled kernel (head dim
-96, scores mode), the bit-plane decode kernels (bits 3, at most 4 columns), and the table
-decode kernels (bits 4, and 12 columns).  With q_proj scaled by 8 and by 2^-30 the prefill,
+96, scores mode), the bit-plane decode kernels (bits 2-3, one and two groups of 4 columns), and
+the table decode kernels (bits 4, and 12 columns).  With q_proj scaled by 8 and by 2^-30 the prefill,
 tiled and bit-plane kernels are held to the oracle where an unscaled f16 split would overflow or
 lose its lo part.
 """
@@ -113,6 +113,7 @@ def _setup(d, bits, B, hq, hkv, sq, sk, seed=0, qscale=1.0):
 
 @pytest.mark.parametrize("d,bits,hq,hkv,sq,sk", [
     (128, 3, 32, 8, 1, 64),    # bit-plane decode scores kernel
+    (128, 3, 16, 2, 1, 64),    # bit-plane decode scores kernel, two column groups
     (128, 4, 32, 8, 1, 64),    # table decode scores kernel (bits 4)
     (128, 3, 32, 8, 3, 64),    # table decode scores kernel (12 columns)
     (128, 3, 8, 2, 40, 48),    # tiled kernel, scores mode
@@ -177,7 +178,7 @@ def test_attention_qjl_term_f32_grade(d, bits, hq, hkv, sq, sk, masked):
 # of their own and the bit-plane decode kernels take it as per-column fixed point, so all stay
 # at f32 grade.  (Much larger scales make the scores themselves too large for f32 to resolve
 # attention weights: at 2^12 they reach ~6.6e6 in log2 units, whose f32 ulp is 0.5.)  The table
-# decode kernels (bits 4, or more than 4 columns) split q_proj unscaled and are not held to this.
+# decode kernels (bits 4, or more than 8 columns) split q_proj unscaled and are not held to this.
 KERNEL_CASES = [
     (128, 3, 32, 8, 64, 48, False),  # head_dim-128 prefill
     (128, 3, 32, 8, 64, 48, True),   # masked prefill
@@ -185,6 +186,8 @@ KERNEL_CASES = [
     (96, 3, 8, 2, 40, 48, False),    # tiled kernel
     (128, 3, 32, 8, 1, 64, False),   # bit-plane decode
     (128, 2, 8, 2, 1, 64, False),    # bit-plane decode, bits 2
+    (128, 3, 16, 2, 1, 64, False),   # bit-plane decode, two column groups
+    (128, 2, 6, 1, 1, 64, True),     # bit-plane decode, bits 2, 6 columns, masked attention
 ]
 
 

@@ -42,6 +42,7 @@
 namespace tq {
 
 constexpr int kScoreBlocks = 4096;
+constexpr int kScoreBlocks2 = 512;  // the bit-plane kernel's two-column-group form
 constexpr int kAttnNbs = 2;
 constexpr int kAttnRing = 2;
 constexpr int score_ring(int bits) { return bits == 2 ? 2 : 3; }
@@ -165,7 +166,7 @@ __device__ __forceinline__ half8 key_operand(const uint8_t* t, const uint32_t (&
 }
 
 // ---------------------------------------------------------------- bit-plane scores
-// Scores on the integer MFMA for 1- and 2-bit key codes and at most 4 columns.
+// Scores on the integer MFMA for 1- and 2-bit key codes and at most 8 columns.
 // Both terms are sums of query values over the set bits of key bit-planes:
 //   term 1: f16(C)[code] = c0 + (c1 - c0) b0 [+ (c2 - c0) b1 + (c3 - c2 - c1 + c0) b0 b1]
 //           (b0, b1: low / high code bit), so q_rot . f16(C)[codes] =
@@ -478,7 +479,7 @@ struct PlaneQuery {
   }
 };
 
-// materialised scores for bits 2-3 and at most 4 columns (tq_decode.hip), on a plan of
+// materialised scores for bits 2-3 and at most 8 columns (tq_decode.hip), on a plan of
 // tq_decode_scores.hip
 void launch_scores_planes(const DecodeArgs& a, int bits, hipStream_t s);
 

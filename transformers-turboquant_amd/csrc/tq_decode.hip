@@ -361,13 +361,14 @@ decode_attn_lds_kernel(DecodeArgs a) {
 }
 
 // Materialised scores on the integer MFMA (bit-plane form, PlaneQuery in tq_decode.h), with
-// the MFMA accumulators in VGPRs like every kernel of this file: one column per lane group,
-// keys on the N side; unit u of a 32-key slab scores keys 2n + u (n = l16), so each lane ends
-// with two adjacent keys of its column and a score row's 32 values leave as one 128-byte run.
-template <int KB, int R>
+// the MFMA accumulators in VGPRs like every kernel of this file: columns lg + 4g (NCG groups
+// of 4) per lane group, keys on the N side; unit u of a 32-key slab scores keys 2n + u
+// (n = l16), so each lane ends with two adjacent keys of its columns and a score row's 32
+// values leave as one 128-byte run.
+template <int KB, int R, int NCG>
 __global__ void __launch_bounds__(256) decode_scores_i8_kernel(DecodeArgs a) {
   static_assert(R >= 2 && R <= 4, "ring of 2 to 4 slots");
-  using PQ = PlaneQuery<KB>;
+  using PQ = PlaneQuery<KB, NCG>;
   constexpr int D = 128, NK = 32;
   constexpr int KC = D * KB / 8, SC = D / 8;
   constexpr int KLANE = KC / 4;
@@ -375,13 +376,14 @@ __global__ void __launch_bounds__(256) decode_scores_i8_kernel(DecodeArgs a) {
   constexpr int OFF_K = 0, OFF_S = NK * KC, OFF_N = OFF_S + NK * SC;
   constexpr int NRM = NK * 4;
   constexpr int SLOT = OFF_N + 2 * NRM;
-  // ring slot r of wave w at (r * 4 + w) * SLOT; slot R - 1 of the four waves (issued after
-  // the query set-up) first serves as the set-up's staging area
+  // ring slot r of wave w at (r * 4 + w) * SLOT; the last NSTG slots of the four waves
+  // (issued after the query set-up) first serve as the set-up's staging area
   constexpr int STG = 4 * SLOT;
-  static_assert(STG >= PQ::STAGE_BYTES, "set-up staging fits in one ring slot per wave");
+  constexpr int NSTG = (PQ::STAGE_BYTES + STG - 1) / STG;
+  static_assert(NSTG < R, "set-up staging fits in the ring and leaves a slot to prefetch");
 
   __shared__ __attribute__((aligned(16))) uint8_t stage[R * STG];
-  uint8_t* const stg = stage + (R - 1) * STG;
+  uint8_t* const stg = stage + (R - NSTG) * STG;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lg = lane >> 4;
@@ -422,23 +424,30 @@ __global__ void __launch_bounds__(256) decode_scores_i8_kernel(DecodeArgs a) {
     else if (later == 1) wait_vm<NDMA>();
     else wait_vm<0>();
   };
-  // slots 0 .. R-2 stream while the queries are set up
+  // slots 0 .. R-NSTG-1 stream while the queries are set up
   const int k0w = kbeg + wave * NK;
 #pragma unroll
-  for (int r = 0; r < R - 1; ++r)
+  for (int r = 0; r < R - NSTG; ++r)
     if (k0w + r * SLAB < kend) issue(k0w + r * SLAB, r);
 
   PQ pq;
   pq.setup(a, b, hkv, stg, tid);
   const float* pout = a.scores + (static_cast<int64_t>(b) * a.Hq + hkv * a.G) * a.Sq * a.Sk;
   const uint32_t out_bytes = static_cast<uint32_t>(a.C) * a.Sk * 4;
-  const uint32_t oo = lg < a.C ? static_cast<uint32_t>((lg % a.G) * a.Sq + lg / a.G) * a.Sk * 4 + 8 * l16 : kOutOfRange;
+  uint32_t oo[NCG];
+#pragma unroll
+  for (int g = 0; g < NCG; ++g) {
+    const int c = lg + 4 * g;
+    oo[g] = c < a.C ? static_cast<uint32_t>((c % a.G) * a.Sq + c / a.G) * a.Sk * 4 + 8 * l16 : kOutOfRange;
+  }
   const float fb = a.coeff;
-  __syncthreads();  // every wave holds its fragments: the staging slot joins the ring
-  if (k0w + (R - 1) * SLAB < kend) issue(k0w + (R - 1) * SLAB, R - 1);
+  __syncthreads();  // every wave holds its fragments: the staging slots join the ring
+#pragma unroll
+  for (int r = R - NSTG; r < R; ++r)
+    if (k0w + r * SLAB < kend) issue(k0w + r * SLAB, r);
 
   auto slab = [&](const uint8_t* src, int ks0) {
-    float sc[2], t1[2][1], t2[2][1];
+    float sc[NCG][2], t1[2][NCG], t2[2][NCG];
     pq.dots2(src + OFF_K + (2 * l16) * KC + lg * KLANE, src + OFF_S + (2 * l16) * SC + lg * 4,
              src + OFF_K + (2 * l16 + 1) * KC + lg * KLANE, src + OFF_S + (2 * l16 + 1) * SC + lg * 4, t1, t2);
 #pragma unroll
@@ -446,16 +455,20 @@ __global__ void __launch_bounds__(256) decode_scores_i8_kernel(DecodeArgs a) {
       const int row = 2 * l16 + u;
       const float kn = h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + row * 4)));
       const float rn = fb * h2f(static_cast<uint16_t>(*reinterpret_cast<const uint32_t*>(src + OFF_N + NRM + row * 4)));
-      sc[u] = fmaf(t1[u][0], kn, t2[u][0] * rn);
+#pragma unroll
+      for (int g = 0; g < NCG; ++g) sc[g][u] = fmaf(t1[u][g], kn, t2[u][g] * rn);
     }
     const int key = ks0 + 2 * l16;
     if (key < kend) {
       const rsrc_t ro = make_rsrc(pout + ks0, out_bytes - static_cast<uint32_t>(ks0) * 4);
-      if (key + 1 < kend)
-        __builtin_amdgcn_raw_buffer_store_b64(u32x2{__builtin_bit_cast(uint32_t, sc[0]), __builtin_bit_cast(uint32_t, sc[1])},
-                                              ro, oo, 0, 2);
-      else
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sc[0]), ro, oo, 0, 2);
+#pragma unroll
+      for (int g = 0; g < NCG; ++g) {
+        if (key + 1 < kend)
+          __builtin_amdgcn_raw_buffer_store_b64(
+              u32x2{__builtin_bit_cast(uint32_t, sc[g][0]), __builtin_bit_cast(uint32_t, sc[g][1])}, ro, oo[g], 0, 2);
+        else
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sc[g][0]), ro, oo[g], 0, 2);
+      }
     }
   };
 
@@ -479,8 +492,13 @@ __global__ void __launch_bounds__(256) decode_scores_i8_kernel(DecodeArgs a) {
 
 void launch_scores_planes(const DecodeArgs& a, int bits, hipStream_t s) {
   const dim3 grid(a.nsplit, a.Hkv, a.B);
-  if (bits == 2) decode_scores_i8_kernel<1, 3><<<grid, 256, 0, s>>>(a);
-  else decode_scores_i8_kernel<2, 3><<<grid, 256, 0, s>>>(a);
+  if (a.C > 4) {
+    if (bits == 2) decode_scores_i8_kernel<1, 3, 2><<<grid, 256, 0, s>>>(a);
+    else decode_scores_i8_kernel<2, 3, 2><<<grid, 256, 0, s>>>(a);
+  } else {
+    if (bits == 2) decode_scores_i8_kernel<1, 3, 1><<<grid, 256, 0, s>>>(a);
+    else decode_scores_i8_kernel<2, 3, 1><<<grid, 256, 0, s>>>(a);
+  }
 }
 
 // Fused decode attention for 1- and 2-bit key codes and at most 8 columns, scores on the

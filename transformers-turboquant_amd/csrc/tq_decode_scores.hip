@@ -1,5 +1,5 @@
 // Decode-shaped materialised scores (split-K over keys) through lookup tables, for bits 4
-// and 5-16 columns (the bit-plane kernel for bits 2-3 and at most 4 columns is in
+// and 9-16 columns (the bit-plane kernel for bits 2-3 and at most 8 columns is in
 // tq_decode.hip); the shared argument block, lookup tables and split planning are in
 // tq_decode.h.  Built without -amdgpu-mfma-vgpr-form: with MFMA accumulators in VGPRs the
 // compiler gave wrong scores from the second ring slot on when part of an accumulator is
@@ -192,7 +192,11 @@ __global__ void __launch_bounds__(256) decode_scores_kernel(DecodeArgs a) {
 static DecodePlan plan_scores(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
   if (!decode_shape(Hq, Hkv, Sq, Sk, d, bits)) return DecodePlan{false, 0, 0, 0};
   const int slab = 4 * score_slab_keys(bits);
-  return plan_split(B, Hkv, Sk, kScoreBlocks, slab, 2 * slab);
+  // the two-column-group bit-plane kernel (5-8 columns) costs more per block to set up:
+  // fewer, longer splits (measured: 512 blocks against 4096, B16 x 32k keys, 16/2 heads,
+  // bits 3: 22.0 vs 39.4 us)
+  const int C = (Hq / Hkv) * Sq;
+  return plan_split(B, Hkv, Sk, (bits <= 3 && C > 4) ? kScoreBlocks2 : kScoreBlocks, slab, 2 * slab);
 }
 
 
@@ -223,7 +227,7 @@ int decode_scores(int64_t ldk, const uint16_t* q_rot, const float* q_proj, const
   a.scale = 1.f;
   a.scores = out;
   dim3 grid(a.nsplit, a.Hkv, a.B);
-  if (bits <= 3 && a.C <= 4) {
+  if (bits <= 3 && a.C <= 8) {
     launch_scores_planes(a, bits, s);  // tq_decode.hip
     return launch_status("tq_attention_scores (decode, bit planes)");
   }
