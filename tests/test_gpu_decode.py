@@ -55,13 +55,15 @@ def test_decode_scores_match_oracle(bits, hq, hkv, sq, sk):
 @pytest.mark.parametrize("bits", [2, 3, 4])
 @pytest.mark.parametrize("cb", ["nonaffine", "shifted", "reference"])
 @pytest.mark.parametrize("qmul", [1.0, 300.0, 1e-5])
-def test_decode_scores_any_codebook(bits, cb, qmul):
+@pytest.mark.parametrize("hq", [12, 8])
+def test_decode_scores_any_codebook(bits, cb, qmul, hq):
     """Decode scores with key codebooks that are not odd (shifted, and for 2-bit codes
     not affine in the code bits: c3 - c2 != c1 - c0), and queries scaled far from 1,
     against the oracle evaluated with the same f16 codebook.  One query column is all
-    zero."""
-    _case(bits=bits, cb=cb, qmul=qmul)
-    B, hq, hkv, sq, sk, d = 2, 12, 2, 1, 1500, 128
+    zero.  6 and 4 columns per kv head (at bits 2-3 the bit-plane kernel's two- and
+    one-group forms)."""
+    _case(bits=bits, cb=cb, qmul=qmul, hq=hq)
+    B, hkv, sq, sk, d = 2, 2, 1, 1500, 128
     assert _on_decode_path(B, hq, hkv, sq, sk, bits)
     torch.manual_seed(7 * bits + len(cb))
     k = torch.randn(B, hkv, sk, d, device=DEV, dtype=torch.bfloat16)
