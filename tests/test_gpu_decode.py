@@ -153,6 +153,7 @@ def test_decode_attention_any_codebook(bits, cb, hq):
     (8, 2, 2, 1025, True, 1.0, 1.0),     # 8 columns (4 heads x 2 rows), causal
     (5, 1, 1, 777, False, 8.0, 1.0),     # 5 columns: the second group holds one
     (12, 2, 1, 3001, True, 1.0, 3000.0), # 6 columns, value norms ~3e4
+    (16, 2, 1, 20000, True, 1.0, 1.0),   # 8 columns, 79 splits: the merge with one block per column
 ])
 def test_decode_attention_matches_oracle_and_tiled(bits, hq, hkv, sq, sk, causal, qmul, vmul):
     _case(bits=bits, hq=hq, hkv=hkv, sq=sq, sk=sk, causal=causal, qmul=qmul, vmul=vmul)

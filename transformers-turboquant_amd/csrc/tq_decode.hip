@@ -865,6 +865,12 @@ decode_attn_i8_kernel(DecodeArgs a) {
   }
 }
 
+// splits the one-wave-per-column merge loads in its first round trip; shapes with more take
+// decode_merge_split_kernel (measured, C ABI, bits 3: 32/8 heads B1 x 32k keys, 128 splits,
+// 25.7 -> 21.9 us for attention + merge; at 8 splits, B16 x 32k, the per-column blocks'
+// extra Pi_v fragment reads made it 4% slower)
+constexpr int kMergeSplitsPerWave = 16;
+
 struct MergeArgs {
   const float *part_o, *part_ml;
   const uint16_t* vpit;  // split Pi_v^T
@@ -925,7 +931,7 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeArgs a) {
     // one memory round trip for up to NB0 splits (the decode shapes: 8 at 16 sequences x 32k
     // keys, 16 at one sequence x 4k): the first NB0 splits' partial o and this lane's split
     // maximum and sum are all issued before any is used
-    constexpr int NB0 = 16;
+    constexpr int NB0 = kMergeSplitsPerWave;
     float2 v0[NB0];
 #pragma unroll
     for (int u = 0; u < NB0; ++u)
@@ -1023,6 +1029,173 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeArgs a) {
       f = mfma16x16x32(ah[rb][ks], bl[ks], f);
     }
     if (col_ok) {
+      const int64_t off = static_cast<int64_t>(b) * a.sob + static_cast<int64_t>(h) * a.soh +
+                          static_cast<int64_t>(qi) * a.sos + wave * 32 + rb * 16 + lg * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float v = f[e] * (down * kSplit);
+        if (a.out_dtype == TQ_BF16) store_act<TQ_BF16>(a.out, off + e, v);
+        else if (a.out_dtype == TQ_F16) store_act<TQ_F16>(a.out, off + e, v);
+        else store_act<TQ_F32>(a.out, off + e, v);
+      }
+    }
+  }
+}
+
+// The same merge for many splits (decode_merge_kernel walks a column's splits in one wave,
+// a batch of 16 per memory round trip): one block per (column, kv head, batch) combines the
+// column's splits with log-sum-exp
+// weights into o[:], then out = Pi_v^T o on MFMA with Pi_v^T as the split-f16 A operand
+// (rows i = output dim) and o as split-f16 B operand (scaled by a power of two; every MFMA
+// column holds it, column 0 is stored), hi.hi + lo.hi + hi.lo.  The kernel is latency-bound
+// (a few KB per block), so it is laid out as few dependent round trips as possible: each wave
+// issues the loads of its Pi_v^T fragments, of the partial o of its splits (wave w takes
+// splits w, w + 4, ..., up to NB of them per batch) and of their maxima and sums together;
+// the block maximum crosses one barrier, each wave sums its splits (2 dims per lane), and
+// the waves' partial sums cross a second barrier before the Pi_v product.
+template <int D>
+__global__ void __launch_bounds__(256) decode_merge_split_kernel(MergeArgs a) {
+  static_assert(D == 128, "merge is built for head_dim 128");
+  constexpr int NB = 16;  // splits per wave per load batch
+  __shared__ float s_m[4], s_l[4];
+  __shared__ __attribute__((aligned(16))) float s_o[4][D];
+  const int c = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6, l16 = lane & 15, lg = lane >> 4;
+  const int C = a.C, ns = a.nsplit;
+  const int64_t base = (static_cast<int64_t>(b) * a.Hkv + hkv) * ns;  // first split record
+
+  // ---- Pi_v^T fragments of this wave's output rows 32w .. 32w+31 (in flight meanwhile)
+  const _Float16* Ph = reinterpret_cast<const _Float16*>(a.vpit);
+  const _Float16* Pl = Ph + D * D;
+  half8 ah[2][D / 32], al[2][D / 32];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const int i = wave * 32 + rb * 16 + l16;
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) {
+      ah[rb][ks] = *reinterpret_cast<const half8*>(Ph + i * D + ks * 32 + lg * 8);
+      al[rb][ks] = *reinterpret_cast<const half8*>(Pl + i * D + ks * 32 + lg * 8);
+    }
+  }
+
+  // ---- this wave's splits w + 4u, u < nw: partial o (first batch), maxima and sums
+  const int nw = ns > wave ? (ns - wave + 3) / 4 : 0;
+  const int64_t ostep = 4 * static_cast<int64_t>(C) * D;  // floats between the wave's splits
+  const int64_t mstep = 4 * 2 * static_cast<int64_t>(C);
+  const float* src0 = a.part_o + ((base + wave) * C + c) * D + 2 * lane;
+  const float* ml0 = a.part_ml + ((base + wave) * C + c) * 2;
+  float2 v0[NB];
+#pragma unroll
+  for (int u = 0; u < NB; ++u) v0[u] = u < nw ? *reinterpret_cast<const float2*>(src0 + u * ostep) : float2{0.f, 0.f};
+  const float m_first = lane < nw ? ml0[lane * mstep] : -INFINITY;
+  const float l_first = lane < nw ? ml0[lane * mstep + 1] : 0.f;
+  float mx = m_first;
+  for (int u = lane + 64; u < nw; u += 64) mx = fmaxf(mx, ml0[u * mstep]);
+#pragma unroll
+  for (int sh = 32; sh >= 1; sh >>= 1) mx = fmaxf(mx, __shfl_xor(mx, sh, 64));
+  if (lane == 0) s_m[wave] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+
+  // ---- o_w = sum_u wt_u o_u, l_w = sum_u wt_u l_u, wt_u = 2^(m_u - M); lane u holds wt_u of
+  // its batch of 64 and every lane reads it back with v_readlane
+  float o0 = 0.f, o1 = 0.f, lsum = 0.f;
+  for (int s0 = 0; s0 < nw; s0 += 64) {
+    const int u = s0 + lane;
+    float w = 0.f;
+    if (u < nw) {
+      const float m = s0 == 0 ? m_first : ml0[u * mstep];
+      w = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - M);
+      lsum += w * (s0 == 0 ? l_first : ml0[u * mstep + 1]);
+    }
+    const int nb = min(64, nw - s0);
+    int k = 0;
+    if (s0 == 0) {
+      // the first batch, loaded above (splits past nw hold zeros and weight 0)
+#pragma unroll
+      for (int uu = 0; uu < NB; ++uu) {
+        const float ww = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), uu));
+        o0 = fmaf(ww, v0[uu].x, o0);
+        o1 = fmaf(ww, v0[uu].y, o1);
+      }
+      k = NB;
+    }
+    for (; k < nb; k += NB) {
+      float2 v[NB];
+#pragma unroll
+      for (int uu = 0; uu < NB; ++uu)
+        v[uu] = k + uu < nb ? *reinterpret_cast<const float2*>(src0 + (s0 + k + uu) * ostep) : float2{0.f, 0.f};
+#pragma unroll
+      for (int uu = 0; uu < NB; ++uu) {
+        const float ww = k + uu < 64 ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), k + uu)) : 0.f;
+        o0 = fmaf(ww, v[uu].x, o0);
+        o1 = fmaf(ww, v[uu].y, o1);
+      }
+    }
+  }
+#pragma unroll
+  for (int sh = 32; sh >= 1; sh >>= 1) lsum += __shfl_xor(lsum, sh, 64);
+  *reinterpret_cast<float2*>(&s_o[wave][2 * lane]) = float2{o0, o1};
+  if (lane == 0) s_l[wave] = lsum;
+  __syncthreads();
+
+  // ---- o = sum_w o_w / sum_w l_w as this lane's B operand dims ks*32 + lg*8 + e, scaled so
+  // that |o| < kSplit (the same scale in every wave: every wave builds the same operand)
+  const float L = (s_l[0] + s_l[1]) + (s_l[2] + s_l[3]);
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  float ov[D / 32][8];
+  float om = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < D / 32; ++ks) {
+    const int d0 = ks * 32 + lg * 8;
+#pragma unroll
+    for (int h4 = 0; h4 < 2; ++h4) {
+      float4 t = *reinterpret_cast<const float4*>(&s_o[0][d0 + 4 * h4]);
+#pragma unroll
+      for (int w = 1; w < 4; ++w) {
+        const float4 x = *reinterpret_cast<const float4*>(&s_o[w][d0 + 4 * h4]);
+        t.x += x.x;
+        t.y += x.y;
+        t.z += x.z;
+        t.w += x.w;
+      }
+      ov[ks][4 * h4 + 0] = t.x * inv;
+      ov[ks][4 * h4 + 1] = t.y * inv;
+      ov[ks][4 * h4 + 2] = t.z * inv;
+      ov[ks][4 * h4 + 3] = t.w * inv;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) om = fmaxf(om, fabsf(ov[ks][e]));
+  }
+#pragma unroll
+  for (int sh = 32; sh >= 16; sh >>= 1) om = fmaxf(om, __shfl_xor(om, sh, 64));  // over lane groups
+  int ex;
+  frexpf(om, &ex);
+  const float up = ldexpf(kSplit, -ex);  // scaled |o| < kSplit
+  half8 bh[D / 32], bl[D / 32];
+#pragma unroll
+  for (int ks = 0; ks < D / 32; ++ks) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      _Float16 hh, lo;
+      split_f16(ov[ks][e] * up, hh, lo);
+      bh[ks][e] = hh;
+      bl[ks][e] = lo;
+    }
+  }
+  // ---- out[i] = sum_j Pi_v^T[i][j] o[j]; wave w owns output rows 32w .. 32w+31
+  const int qi = c / a.G, h = hkv * a.G + c % a.G;
+  const float down = kUnsplit2 / up;  // 1/(kSplit * up) * (1/kSplit) for Pi_v^T's scale
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    float4v f = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) {
+      f = mfma16x16x32(ah[rb][ks], bh[ks], f);
+      f = mfma16x16x32(al[rb][ks], bh[ks], f);
+      f = mfma16x16x32(ah[rb][ks], bl[ks], f);
+    }
+    if (l16 == 0) {
       const int64_t off = static_cast<int64_t>(b) * a.sob + static_cast<int64_t>(h) * a.soh +
                           static_cast<int64_t>(qi) * a.sos + wave * 32 + rb * 16 + lg * 4;
 #pragma unroll
@@ -1165,8 +1338,11 @@ int decode_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, co
   m.sob = sob;
   m.soh = soh;
   m.sos = sos;
-  dim3 grid(Hkv, B, (a.C + 3) / 4);
-  decode_merge_kernel<128><<<grid, 256, 0, s>>>(m);
+  if (p.nsplit > kMergeSplitsPerWave) {
+    decode_merge_split_kernel<128><<<dim3(a.C, Hkv, B), 256, 0, s>>>(m);
+  } else {
+    decode_merge_kernel<128><<<dim3(Hkv, B, (a.C + 3) / 4), 256, 0, s>>>(m);
+  }
   return launch_status("tq_attention_fwd (decode merge)");
 }
 
