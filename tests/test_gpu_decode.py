@@ -293,3 +293,42 @@ def test_decode_attention_left_padding(bits, sq, npad):
         err = O.rel_err(got[b], ref[b])
         print(f"batch row {b}: rel-err {err:.2e}", flush=True)
         assert err < REL, (b, err)
+
+
+@pytest.mark.parametrize("bits", [2, 3])
+@pytest.mark.parametrize("hq,hkv,sq,sk,causal,masked", [
+    (5, 1, 1, 2000, False, False),   # 5 columns: one lane group of the second column group
+    (7, 1, 1, 9000, False, True),    # 7 columns, padding mask, 36 splits (merge by column blocks)
+    (3, 1, 2, 1500, True, False),    # 6 columns from 3 heads x 2 rows, causal
+    (14, 2, 1, 20000, True, False),  # 7 columns per kv head over 2 kv heads, many splits
+])
+def test_decode_two_column_groups_scores_and_attention(bits, hq, hkv, sq, sk, causal, masked):
+    """Bit-plane decode kernels with 5-8 columns per kv head (the second column group partly
+    filled), scores and fused attention against the float64 oracle, with the merge of few and
+    of many splits."""
+    _case(bits=bits, hq=hq, hkv=hkv, sq=sq, sk=sk, causal=causal, masked=masked)
+    B, d = 2, 128
+    assert _on_decode_path(B, hq, hkv, sq, sk, bits)
+    torch.manual_seed(17 * bits + hq + sk)
+    q = torch.randn(B, hq, sq, d, device=DEV, dtype=torch.bfloat16)
+    k = torch.randn(B, hkv, sk, d, device=DEV, dtype=torch.bfloat16)
+    v = torch.randn(B, hkv, sk, d, device=DEV, dtype=torch.bfloat16)
+    kc = TurboQuantCompressorV2(d, bits, seed=42, device=DEV)
+    vc = TurboQuantCompressorMSE(d, bits, seed=10042, device=DEV)
+    ck, cv = kc.compress(k), vc.compress(v)
+    got_s = _np(kc.asymmetric_attention_scores(q, ck))
+    ref_s = _oracle_scores(kc, q, ck, hq, hkv)
+    assert O.rel_err(got_s, ref_s) < REL
+    mask = None
+    if masked:
+        mask = torch.zeros(B, 1, sq, sk)
+        mask[0, 0, :, : sk // 3] = torch.finfo(torch.float32).min  # left padding on batch row 0
+        mask[1, 0, :, 7] = -4.0
+    ref = _oracle_attention(kc, vc, q, ck, cv, hq, hkv, causal=causal,
+                            mask=mask.numpy() if mask is not None else None)
+    got = _np(compressed_attention(q, kc, vc, ck, cv, causal=causal, out_dtype=torch.float32,
+                                   attention_mask=mask.to(DEV) if mask is not None else None))
+    assert np.isfinite(got).all()
+    err = O.rel_err(got, ref)
+    print(f"scores rel-err {O.rel_err(got_s, ref_s):.2e}, attention rel-err {err:.2e}", flush=True)
+    assert err < REL and O.cosine(got, ref) > 0.9999
