@@ -213,3 +213,46 @@ def test_unsupported_head_dim_raises():
     kc = TurboQuantCompressorV2(100, 3, seed=42, device=DEV)
     with pytest.raises(RuntimeError, match="100"):
         kc.compress(torch.randn(1, 1, 4, 100, device=DEV))
+
+
+@pytest.mark.parametrize("d,bits,vbits,hq,hkv,sq,sk,causal,masked", [
+    (64, 3, 3, 32, 8, 1, 5000, False, False),    # Llama-3.2-1B-shaped decode step
+    (64, 2, 2, 12, 12, 1, 9000, False, True),    # GPT-2-shaped decode, padding mask
+    (64, 4, 4, 16, 2, 2, 3000, True, False),     # two query rows, causal
+    (80, 3, 3, 8, 2, 1, 4000, False, False),     # 10-byte sign rows (byte-stream staging)
+    (96, 2, 2, 4, 4, 3, 2500, True, False),
+    (256, 3, 3, 8, 2, 1, 3000, False, False),    # partial rows of 256 floats
+    (40, 3, 3, 4, 1, 1, 2100, False, False),     # head dim padded to 64
+    (128, 3, 2, 32, 8, 1, 6000, False, False),   # value bits below the key bits (no decode kernels)
+    (128, 3, 3, 64, 2, 1, 4000, False, False),   # 32 columns per kv head (beyond the decode kernels)
+])
+def test_attention_split_keys_any_dim(d, bits, vbits, hq, hkv, sq, sk, causal, masked):
+    """The tiled kernel split over keys (few query rows per kv head, long key ranges) and its
+    merge, against the float64 oracle and against the unsplit tiled kernel."""
+    _case(d=d, bits=bits, vbits=vbits, hq=hq, hkv=hkv, sq=sq, sk=sk, causal=causal, masked=masked)
+    from turboquant_pytorch import _native
+    B = 2
+    assert _native.lib().tq_attention_workspace_size(B, hq, hkv, sq, sk, d, bits) > 0
+    torch.manual_seed(d + 3 * sk + sq)
+    q = torch.randn(B, hq, sq, d, device=DEV, dtype=torch.bfloat16)
+    k = torch.randn(B, hkv, sk, d, device=DEV, dtype=torch.bfloat16)
+    v = torch.randn(B, hkv, sk, d, device=DEV, dtype=torch.bfloat16)
+    kc = TurboQuantCompressorV2(d, bits, seed=42, device=DEV)
+    vc = TurboQuantCompressorMSE(d, vbits, seed=10042, device=DEV)
+    ck, cv = kc.compress(k), vc.compress(v)
+    mask = None
+    if masked:
+        mask = torch.zeros(B, 1, sq, sk)
+        mask[0, 0, :, : sk // 4] = torch.finfo(torch.float32).min  # left padding on batch row 0
+        mask[1, 0, :, 11] = -2.5
+    mdev = mask.to(DEV) if mask is not None else None
+    got = _np(compressed_attention(q, kc, vc, ck, cv, attention_mask=mdev, causal=causal, out_dtype=torch.float32))
+    unsplit = _np(compressed_attention(q, kc, vc, ck, cv, attention_mask=mdev, causal=causal,
+                                       out_dtype=torch.float32, split_k=False))
+    ref = _oracle_attention(kc, vc, q, ck, cv, hq, hkv, mask=mask.numpy() if mask is not None else None,
+                            causal=causal)
+    err, err_u = O.rel_err(got, ref), O.rel_err(unsplit, ref)
+    print(f"split rel-err {err:.2e}, unsplit {err_u:.2e}", flush=True)
+    assert np.isfinite(got).all()
+    assert err < REL and O.cosine(got, ref) > 0.9999
+    assert err_u < REL

@@ -86,6 +86,11 @@ struct AttnArgs {
   int out_dtype;
   int64_t sob, soh, sos;
   float* scores;  // scores-only mode output f32 [B, Hq, Sq, Sk]
+  // split-K (part_o != nullptr, attention mode): block (x, split) attends keys
+  // [split * chunk, (split + 1) * chunk) and writes its columns' partial O (unnormalised,
+  // rotated value domain, rows of dp floats), reference maximum and sum for attn_merge_kernel
+  float *part_o, *part_ml;
+  int nsplit, chunk, C, dp;
 };
 
 __device__ __forceinline__ half8 cat8(half4 a, half4 b) {
@@ -143,6 +148,8 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
   const int bhi = static_cast<int>(blockIdx.x) % nbh;
   const int hkv = bhi % a.Hkv, b = bhi / a.Hkv;
   const int q0 = qblk * a.QT;
+  const bool split_k = !SCORES && a.part_o != nullptr;
+  const int split = split_k ? static_cast<int>(blockIdx.y) : 0;
   const int d = STREAM ? a.d : D;
   const int KC = d * KB / 8, SC = d / 8, vc = d * a.vb / 8;  // bytes per packed row
   const int ng = d / 8;                                       // real 8-dim groups
@@ -203,13 +210,19 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
   }
   const float coeff_q = a.coeff * (1.f / qs);  // q_proj's operands carry qs
 
-  // key range this block needs; tiles past `kfull` need per-element masking
+  // key range this block needs; tiles past `kfull` need per-element masking.  A split ends
+  // on a tile boundary (chunk is a multiple of KT), so only the keys' own end needs masking.
   int kend = a.Sk;
   int kfull = a.Sk;
   if (a.causal) {
     const int imax = min(q0 + a.QT - 1, a.Sq - 1);
     kend = min(a.Sk, imax + (a.Sk - a.Sq) + 1);
     kfull = min(kfull, q0 + (a.Sk - a.Sq) + 1);
+  }
+  int kbeg = 0;
+  if (split_k) {
+    kbeg = split * a.chunk;
+    kend = min(kend, kbeg + a.chunk);
   }
   constexpr float LOG2E = 1.4426950408889634f;
   const float fa = SCORES ? 1.f : a.scale * LOG2E;  // scores kept in log2 units
@@ -287,12 +300,12 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
     }
   }
 
-  if (kend > 0) {
-    fetch(0);
+  if (kend > kbeg) {
+    fetch(kbeg);
     stash(0);
   }
   int cur = 0;
-  for (int k0 = 0; k0 < kend; k0 += KT) {
+  for (int k0 = kbeg; k0 < kend; k0 += KT) {
     __syncthreads();  // tile k0 staged in buffer `cur`; previous tile's decoded tiles consumed
     // ---- decode this tile once per block: K^ and sign tiles [key][dim], V^T [dim][key];
     // groups past d decode to zeros
@@ -475,6 +488,28 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
   }
 
   if constexpr (!SCORES) {
+    if (split_k) {
+      // ---- split-K partial of each column: O (dims 16 db + 4 lg + e), the reference maximum
+      // its weights are relative to (-inf when the split saw no finite score) and their sum
+#pragma unroll
+      for (int nb = 0; nb < NBW; ++nb) {
+        float l = l_run[nb];
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        if (col_ok[nb]) {
+          const int c = col_i[nb] * a.G + (col_h[nb] - hkv * a.G);
+          const int64_t rec = (bh_kv * a.nsplit + split) * a.C + c;
+          float* po = a.part_o + rec * a.dp;
+#pragma unroll
+          for (int db = 0; db < DB; ++db) *reinterpret_cast<float4v*>(po + db * 16 + lg * 4) = oacc[db][nb];
+          if (lg == 0) {
+            a.part_ml[rec * 2] = m_run[nb];
+            a.part_ml[rec * 2 + 1] = l;
+          }
+        }
+      }
+      return;
+    }
     // ---- normalise and rotate back: out = (O^T / l)^T Pi_v, Pi_v^T [2][d][d] as A operand
     // (rows and columns past d read as zero)
     const half4* Ph = reinterpret_cast<const half4*>(a.vpit);
@@ -545,7 +580,8 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
 
 template <int D, int KB, bool SCORES, bool STREAM>
 static void launch_attn_st(const AttnArgs& a, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.nqb) * a.Hkv * a.B));  // see the kernel
+  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.nqb) * a.Hkv * a.B),  // see the kernel
+                  static_cast<unsigned>(!SCORES && a.part_o ? a.nsplit : 1));
   if (!SCORES && a.mask) attn_kernel<D, KB, SCORES, !SCORES, STREAM><<<grid, ATile<D, SCORES>::NT, 0, s>>>(a);
   else attn_kernel<D, KB, SCORES, false, STREAM><<<grid, ATile<D, SCORES>::NT, 0, s>>>(a);
 }
@@ -591,6 +627,232 @@ static int block_rows(int d, bool scores) {
   }
 }
 
+// ---------------------------------------------------------------- split-K merge, any head dim
+// Combines the tiled kernel's split-K partials (rows of DP floats, DP = 64, 128 or 256 >= the
+// padded head dim) with log-sum-exp weights and applies Pi_v (Pi_v^T [2][d][d] split f16,
+// rows and columns past d read as zero) on MFMA, hi.hi + lo.hi + hi.lo.  One block per (kv
+// head, batch, group of 4 columns); wave w combines column 4 blockIdx.z + w (PL = DP / 64 dims
+// per lane, the loads of 16 splits issued together), then owns output row blocks
+// NRB w .. NRB w + NRB - 1 of the product.  Latency-bound like the head_dim-128 merge.
+struct SplitMergeArgs {
+  const float *part_o, *part_ml;
+  const uint16_t* vpit;
+  int B, Hq, Hkv, Sq, G, C, nsplit, d, dpad;
+  void* out;
+  int out_dtype;
+  int64_t sob, soh, sos;
+};
+
+template <int DP>
+__global__ void __launch_bounds__(256) attn_merge_kernel(SplitMergeArgs a) {
+  static_assert(DP == 64 || DP == 128 || DP == 256, "partial rows of 64, 128 or 256 floats");
+  constexpr int PL = DP / 64;    // dims per lane in the combine
+  constexpr int NRB = DP / 64;   // 16-row output blocks per wave
+  constexpr int KS = DP / 32;    // k-steps of the product
+  constexpr int NB = 16;         // splits per load batch
+  constexpr int SW = 64;         // splits per weight batch (one per lane)
+  __shared__ __attribute__((aligned(16))) float o_s[4][DP];
+  __shared__ float s_w[4][SW];
+  __shared__ float s_up[4];
+  const int hkv = blockIdx.x, b = blockIdx.y, c0 = blockIdx.z * 4, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6, l16 = lane & 15, lg = lane >> 4;
+  const int C = a.C, ns = a.nsplit, d = a.d;
+  const int64_t base = (static_cast<int64_t>(b) * a.Hkv + hkv) * ns;
+  typedef float floatPL __attribute__((ext_vector_type(PL)));
+
+  // ---- column c = c0 + wave: o = sum_s w_s o_s / sum_s w_s l_s
+  {
+    const int c = c0 + wave;
+    float* oc = o_s[wave];
+    if (c >= C) {
+#pragma unroll
+      for (int e = 0; e < PL; ++e) oc[PL * lane + e] = 0.f;
+      if (lane == 0) s_up[wave] = 1.f;
+    } else {
+      auto ml = [&](int sp, int k) { return a.part_ml[((base + sp) * C + c) * 2 + k]; };
+      const int64_t step = static_cast<int64_t>(C) * DP;
+      const float* src0 = a.part_o + (base * C + c) * DP + PL * lane;
+      const bool real = PL * lane < a.dpad;  // dims past the padded head dim are not written
+      auto load = [&](int sp) {
+        floatPL v;
+        if (real) {
+          v = *reinterpret_cast<const floatPL*>(src0 + sp * step);
+        } else {
+#pragma unroll
+          for (int e = 0; e < PL; ++e) v[e] = 0.f;
+        }
+        return v;
+      };
+      floatPL v0[NB];
+#pragma unroll
+      for (int u = 0; u < NB; ++u) {
+        if (u < ns) {
+          v0[u] = load(u);
+        } else {
+#pragma unroll
+          for (int e = 0; e < PL; ++e) v0[u][e] = 0.f;
+        }
+      }
+      const float m_first = lane < ns ? ml(lane, 0) : -INFINITY;
+      const float l_first = lane < ns ? ml(lane, 1) : 0.f;
+      float mx = m_first;
+      for (int sp = lane + SW; sp < ns; sp += SW) mx = fmaxf(mx, ml(sp, 0));
+#pragma unroll
+      for (int sh = 32; sh >= 1; sh >>= 1) mx = fmaxf(mx, __shfl_xor(mx, sh, 64));
+      float lsum = 0.f;
+      float o[PL];
+#pragma unroll
+      for (int e = 0; e < PL; ++e) o[e] = 0.f;
+      for (int s0 = 0; s0 < ns; s0 += SW) {
+        const int sp = s0 + lane;
+        float w = 0.f;
+        if (sp < ns) {
+          const float m = s0 == 0 ? m_first : ml(sp, 0);
+          w = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - mx);
+          lsum += w * (s0 == 0 ? l_first : ml(sp, 1));
+        }
+        s_w[wave][lane] = w;  // read back by the same wave only: LDS order suffices
+        const int nb = min(SW, ns - s0);
+        int k = 0;
+        if (s0 == 0) {
+#pragma unroll
+          for (int u = 0; u < NB; ++u) {
+            const float ww = u < nb ? s_w[wave][u] : 0.f;
+#pragma unroll
+            for (int e = 0; e < PL; ++e) o[e] = fmaf(ww, v0[u][e], o[e]);
+          }
+          k = min(NB, nb);
+        }
+        for (; k < nb; k += NB) {
+          floatPL v[NB];
+#pragma unroll
+          for (int u = 0; u < NB; ++u) {
+            if (k + u < nb) {
+              v[u] = load(s0 + k + u);
+            } else {
+#pragma unroll
+              for (int e = 0; e < PL; ++e) v[u][e] = 0.f;
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < NB; ++u) {
+            const float ww = k + u < nb ? s_w[wave][k + u] : 0.f;
+#pragma unroll
+            for (int e = 0; e < PL; ++e) o[e] = fmaf(ww, v[u][e], o[e]);
+          }
+        }
+      }
+#pragma unroll
+      for (int sh = 32; sh >= 1; sh >>= 1) lsum += __shfl_xor(lsum, sh, 64);
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+      float m = 0.f;
+#pragma unroll
+      for (int e = 0; e < PL; ++e) {
+        o[e] *= inv;
+        oc[PL * lane + e] = o[e];
+        m = fmaxf(m, fabsf(o[e]));
+      }
+#pragma unroll
+      for (int sh = 32; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh, 64));
+      if (lane == 0) {
+        int ex;
+        frexpf(m, &ex);
+        s_up[wave] = ldexpf(kSplit, -ex);  // scaled |o| < kSplit
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- out^T[i][c] = sum_j Pi_v^T[i][j] o[c][j]; MFMA column l16 < 4 is column c0 + l16
+  const float up = s_up[l16 & 3];
+  half8 bh[KS], bl[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const float* src = o_s[l16 & 3] + ks * 32 + lg * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      _Float16 hh, lo;
+      split_f16(src[e] * up, hh, lo);
+      bh[ks][e] = hh;
+      bl[ks][e] = lo;
+    }
+  }
+  const bool col_ok = l16 < 4 && c0 + l16 < C;
+  const int qi = col_ok ? (c0 + l16) / a.G : 0, h = hkv * a.G + (col_ok ? (c0 + l16) % a.G : 0);
+  const float down = kUnsplit2 / up;
+  const _Float16* Ph = reinterpret_cast<const _Float16*>(a.vpit);
+  const _Float16* Pl = Ph + static_cast<int64_t>(d) * d;
+#pragma unroll
+  for (int r = 0; r < NRB; ++r) {
+    const int i = (wave * NRB + r) * 16 + l16;
+    float4v f = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int j0 = ks * 32 + lg * 8;
+      const bool ok = i < d && j0 < d;  // d % 8 == 0: the 8 columns from j0 are all real or all padding
+      const int64_t pofs = static_cast<int64_t>(i) * d + j0;
+      const half8 ah = ok ? *reinterpret_cast<const half8*>(Ph + pofs) : half8{};
+      const half8 al = ok ? *reinterpret_cast<const half8*>(Pl + pofs) : half8{};
+      f = mfma16x16x32(ah, bh[ks], f);
+      f = mfma16x16x32(al, bh[ks], f);
+      f = mfma16x16x32(ah, bl[ks], f);
+    }
+    const int row0 = (wave * NRB + r) * 16 + lg * 4;
+    if (col_ok && row0 < d) {
+      const int64_t off = static_cast<int64_t>(b) * a.sob + static_cast<int64_t>(h) * a.soh +
+                          static_cast<int64_t>(qi) * a.sos + row0;
+      const float4v fo = f * (down * kSplit);
+      const int n = min(4, d - row0);
+      if (a.out_dtype == TQ_BF16) store4<TQ_BF16>(a.out, off, fo, n);
+      else if (a.out_dtype == TQ_F16) store4<TQ_F16>(a.out, off, fo, n);
+      else store4<TQ_F32>(a.out, off, fo, n);
+    }
+  }
+}
+
+// Split-K plan of the tiled kernel for few query rows per kv head (one query block) over long
+// key ranges: about kSplitBlocks blocks (two resident per CU), splits of whole 32-key tiles and
+// at least kSplitMinKeys keys each.  Not used when the split-K decode kernels apply.
+constexpr int kSplitBlocks = 512;
+constexpr int kSplitMinKeys = 256;
+struct SplitPlan {
+  int nsplit = 0, chunk = 0, dp = 0;
+  int64_t bytes = 0;
+};
+static int split_row_floats(int d) {
+  const int dpad = pad_dim(d);
+  return dpad <= 64 ? 64 : (dpad <= 128 ? 128 : 256);
+}
+static SplitPlan tiled_split_plan(int B, int Hq, int Hkv, int Sq, int Sk, int d) {
+  SplitPlan p;
+  if (!supported_dim(d) || Hkv <= 0 || Hq % Hkv || B <= 0 || Sq <= 0) return p;
+  const int G = Hq / Hkv;
+  if (G * Sq > block_rows(d, false) || G > block_rows(d, false)) return p;  // one query block per kv head
+  if (Sk < 2 * kSplitMinKeys) return p;
+  const int64_t groups = static_cast<int64_t>(B) * Hkv;
+  int64_t ns = (kSplitBlocks + groups - 1) / groups;
+  const int64_t max_split = Sk / kSplitMinKeys;
+  if (ns > max_split) ns = max_split;
+  if (ns > 1024) ns = 1024;
+  if (ns < 2) return p;
+  int chunk = static_cast<int>((Sk + ns - 1) / ns);
+  chunk = (chunk + kAttnKeys - 1) / kAttnKeys * kAttnKeys;
+  p.nsplit = (Sk + chunk - 1) / chunk;
+  if (p.nsplit < 2) return SplitPlan{};
+  p.chunk = chunk;
+  p.dp = split_row_floats(d);
+  const int64_t C = static_cast<int64_t>(G) * Sq;
+  p.bytes = groups * p.nsplit * C * (p.dp + 2) * 4;
+  return p;
+}
+
+static void launch_split_merge(const SplitMergeArgs& m, int dp, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(m.Hkv), static_cast<unsigned>(m.B), static_cast<unsigned>((m.C + 3) / 4));
+  if (dp == 64) attn_merge_kernel<64><<<grid, 256, 0, s>>>(m);
+  else if (dp == 128) attn_merge_kernel<128><<<grid, 256, 0, s>>>(m);
+  else attn_merge_kernel<256><<<grid, 256, 0, s>>>(m);
+}
+
 }  // namespace tq
 
 using namespace tq;
@@ -599,12 +861,14 @@ namespace tq {
 int64_t decode_workspace_bytes(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits);
 bool decode_applies(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits);
 bool prefill_applies(int Hq, int Hkv, int d, int bits, int val_bits, bool masked);
+bool prefill_split_applies(int Hq, int Hkv, int Sq, int d, int bits, int val_bits, bool masked);
 int prefill_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, const uint8_t* kcodes,
                       const uint8_t* ksigns, const uint16_t* krn, const uint16_t* kvn, const uint16_t* kcent,
                       int bits, const uint8_t* vcodes, const uint16_t* vvn, const float* vcent,
                       const uint16_t* vpit, int B, int Hq, int Hkv, int Sq, int Sk, int d, float coeff, float scale,
                       int causal, const float* mask, int64_t smb, int64_t smh, int64_t smq, int64_t smk, void* out,
-                      int out_dtype, int64_t sob, int64_t soh, int64_t sos, hipStream_t s);
+                      int out_dtype, int64_t sob, int64_t soh, int64_t sos, hipStream_t s, float* part_o = nullptr,
+                      float* part_ml = nullptr, int nsplit = 0, int chunk = 0, int C = 0, int dp = 0);
 int decode_scores(int64_t ldk, const uint16_t* q_rot, const float* q_proj, const uint8_t* kcodes,
                   const uint8_t* ksigns, const uint16_t* krn, const uint16_t* kvn, const uint16_t* kcent,
                   int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits, float coeff, float* out,
@@ -655,7 +919,11 @@ extern "C" {
 
 int64_t tq_attention_workspace_size(int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq, int32_t Sk, int32_t d,
                                     int32_t bits) {
-  return decode_workspace_bytes(B, Hq, Hkv, Sq, Sk, d, bits);
+  // the split-K decode kernels' partials, or the tiled kernel's split over keys (value bits
+  // other than the key bits, head dims other than 128, larger groups): enough for either
+  const int64_t dec = decode_workspace_bytes(B, Hq, Hkv, Sq, Sk, d, bits);
+  const int64_t til = tiled_split_plan(B, Hq, Hkv, Sq, Sk, d).bytes;
+  return dec > til ? dec : til;
 }
 
 int tq_attention_scores_kv(const uint16_t* q_rot, const float* q_proj, const uint8_t* key_codes,
@@ -723,7 +991,46 @@ int tq_attention_fwd_kv(const uint16_t* q_rot, const float* q_proj, const uint8_
                             val_codes, val_vn, val_centroids, val_pit_split, B, Hq, Hkv, Sq, Sk, d, coeff,
                             scale, causal, mask, smb, smh, smq, smk, out, out_dtype, sob, soh, sos,
                             workspace, as_stream(stream));
-  if (prefill_applies(Hq, Hkv, d, bits, val_bits, mask != nullptr))
+  // few query rows per kv head over a long key range: the tiled kernel split over keys, then a
+  // merge (the decode kernels above take head_dim 128 with key bits = value bits)
+  const SplitPlan sp = tiled_split_plan(B, Hq, Hkv, Sq, Sk, d);
+  const bool split = sp.nsplit > 0 && workspace && workspace_bytes >= sp.bytes &&
+                     reinterpret_cast<uintptr_t>(workspace) % 16 == 0;
+  auto merge_split = [&](float* part_o, float* part_ml, int C) {
+    SplitMergeArgs m{};
+    m.part_o = part_o;
+    m.part_ml = part_ml;
+    m.vpit = val_pit_split;
+    m.B = B;
+    m.Hq = Hq;
+    m.Hkv = Hkv;
+    m.Sq = Sq;
+    m.G = Hq / Hkv;
+    m.C = C;
+    m.nsplit = sp.nsplit;
+    m.d = d;
+    m.dpad = pad_dim(d);
+    m.out = out;
+    m.out_dtype = out_dtype;
+    m.sob = sob;
+    m.soh = soh;
+    m.sos = sos;
+    launch_split_merge(m, sp.dp, as_stream(stream));
+    return launch_status("tq_attention_fwd (split merge)");
+  };
+  if (split && prefill_split_applies(Hq, Hkv, Sq, d, bits, val_bits, mask != nullptr)) {
+    // head_dim 64 / 128: the prefill kernel split over keys
+    const int C = (Hq / Hkv) * Sq;
+    float* part_o = static_cast<float*>(workspace);
+    float* part_ml = part_o + static_cast<int64_t>(B) * Hkv * sp.nsplit * C * sp.dp;
+    st = prefill_attention(ldk, q_rot, q_proj, key_codes, key_signs, key_rn, key_vn, key_centroids_f16, bits,
+                           val_codes, val_vn, val_centroids, val_pit_split, B, Hq, Hkv, Sq, Sk, d, coeff, scale,
+                           causal, mask, smb, smh, smq, smk, out, out_dtype, sob, soh, sos, as_stream(stream), part_o,
+                           part_ml, sp.nsplit, sp.chunk, C, sp.dp);
+    if (st != TQ_OK) return st;
+    return merge_split(part_o, part_ml, C);
+  }
+  if (!split && prefill_applies(Hq, Hkv, d, bits, val_bits, mask != nullptr))
     return prefill_attention(ldk, q_rot, q_proj, key_codes, key_signs, key_rn, key_vn, key_centroids_f16, bits,
                              val_codes, val_vn, val_centroids, val_pit_split, B, Hq, Hkv, Sq, Sk, d, coeff, scale,
                              causal, mask, smb, smh, smq, smk, out, out_dtype, sob, soh, sos, as_stream(stream));
@@ -758,8 +1065,21 @@ int tq_attention_fwd_kv(const uint16_t* q_rot, const float* q_proj, const uint8_
   a.sob = sob;
   a.soh = soh;
   a.sos = sos;
+  if (split) {
+    const int C = (Hq / Hkv) * Sq;
+    const int64_t n_part = static_cast<int64_t>(B) * Hkv * sp.nsplit * C;
+    a.part_o = static_cast<float*>(workspace);
+    a.part_ml = a.part_o + n_part * sp.dp;
+    a.nsplit = sp.nsplit;
+    a.chunk = sp.chunk;
+    a.C = C;
+    a.dp = sp.dp;
+  }
   dispatch_attn<false>(d, bits - 1, a, as_stream(stream));
-  return launch_status("tq_attention_fwd");
+  if (!split) return launch_status("tq_attention_fwd");
+  st = launch_status("tq_attention_fwd (keys split)");
+  if (st != TQ_OK) return st;
+  return merge_split(a.part_o, a.part_ml, a.C);
 }
 
 }  // extern "C"
@@ -816,16 +1136,24 @@ int tq_attention_fwd_kv_noalloc(const uint16_t* q_rot, const float* q_proj, cons
   if (st != TQ_OK) return st;
   void* ws = nullptr;
   int64_t ws_bytes = 0;
-  if (val_bits == bits && static_cast<int64_t>(B) * Hq * Sq > 0) {
-    const int64_t need = decode_workspace_bytes(B, Hq, Hkv, Sq, Sk, d, bits);
-    TQ_REQUIRE(need <= kScratchBytes,
+  const int64_t dec = (val_bits == bits && static_cast<int64_t>(B) * Hq * Sq > 0)
+                          ? decode_workspace_bytes(B, Hq, Hkv, Sq, Sk, d, bits) : 0;
+  if (dec > 0) {
+    TQ_REQUIRE(dec <= kScratchBytes,
                "tq_attention_fwd_kv_noalloc: this shape's split-K partials need %lld bytes, more than the "
                "%lld-byte scratch array; use tq_attention_fwd_kv with a caller workspace",
-               (long long)need, (long long)kScratchBytes);
-    if (need > 0) {
+               (long long)dec, (long long)kScratchBytes);
+    ws = device_scratch();
+    if (!ws) return TQ_EHIP;
+    ws_bytes = dec;
+  } else if (static_cast<int64_t>(B) * Hq * Sq > 0) {
+    // the tiled kernel's split over keys when its partials fit the array; otherwise it runs
+    // unsplit (no workspace), which needs none
+    const int64_t til = tiled_split_plan(B, Hq, Hkv, Sq, Sk, d).bytes;
+    if (til > 0 && til <= kScratchBytes) {
       ws = device_scratch();
       if (!ws) return TQ_EHIP;
-      ws_bytes = need;
+      ws_bytes = til;
     }
   }
   // every split record is written in full before the merge reads it: nothing to clear

@@ -69,6 +69,11 @@ struct PrefillArgs {
   void* out;
   int out_dtype;
   int64_t sob, soh, sos;
+  // split-K (part_o != nullptr, one query block per kv head): block (x, split) attends keys
+  // [split * chunk, (split + 1) * chunk) and writes its columns' partial O (unnormalised,
+  // rotated value domain, rows of dp floats), reference maximum and sum for a merge
+  float *part_o, *part_ml;
+  int nsplit, chunk, C, dp;
 };
 
 template <int D_, int BITS>
@@ -238,14 +243,22 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
     mvec = a.smk == 1 && (reinterpret_cast<uintptr_t>(a.mask) & 15) == 0 && ((a.smb | a.smh | a.smq) & 3) == 0;
   }
 
-  // keys this block needs; tiles past `kfull` need per-element masking
+  // keys this block needs; tiles past `kfull` need per-element masking.  A split starts and
+  // ends on tile boundaries (chunk is a multiple of KT); tb is its first tile.
+  const bool split_k = a.part_o != nullptr;
+  const int split = split_k ? static_cast<int>(blockIdx.y) : 0;
   int kend = a.Sk, kfull = a.Sk;
   if (a.causal) {
     const int imax = min(q0 + a.QT - 1, a.Sq - 1);
     kend = min(a.Sk, imax + (a.Sk - a.Sq) + 1);
     kfull = min(kfull, q0 + (a.Sk - a.Sq) + 1);
   }
-  const int nt = (kend + KT - 1) / KT;
+  int tb = 0;
+  if (split_k) {
+    tb = split * (a.chunk / KT);
+    kend = min(kend, (tb * KT) + a.chunk);
+  }
+  const int nt = kend > tb * KT ? (kend - tb * KT + KT - 1) / KT : 0;  // tiles tb .. tb + nt - 1
   const float fa = a.scale * LOG2E;  // scores kept in log2 units
   const float fb = fa * a.coeff * (1.f / qs);  // q_proj's operands carry qs
 
@@ -268,7 +281,7 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
     }
   };
   auto issue = [&](int j) __attribute__((always_inline)) {  // wave 0 only
-    const int kb = j * KT;
+    const int kb = (tb + j) * KT;
     const uint32_t dst = ring_lds + (j % R) * C::SLOT;
     copy_plane(rows_desc(pk, KC, kb, kend), dst + C::OFF_K, KT * KC, C::NKD);
     copy_plane(rows_desc(ps, SC, kb, kend), dst + C::OFF_S, KT * SC, C::NSD);
@@ -414,7 +427,7 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
   // ---- log2-domain scores with masking, column maxima, lazy rescale (one rare branch per tile)
   auto softmax_max = [&](int j, const float (*cF)[KT], const float4v (&sacc)[2][NBW],
                          const float4v (&tacc)[2][NBW], float (&sc)[NBW][2][4]) __attribute__((always_inline)) {
-    const int k0 = j * KT;
+    const int k0 = (tb + j) * KT;
     const float4v fA0 = *reinterpret_cast<const float4v*>(&cF[0][4 * lg]);
     const float4v fA1 = *reinterpret_cast<const float4v*>(&cF[0][16 + 4 * lg]);
     const float4v fB0 = *reinterpret_cast<const float4v*>(&cF[1][4 * lg]);
@@ -599,6 +612,30 @@ __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per
     if (t + 1 < nt) iter(t + 1, sK1, sS1, sV1, fac1, sK0, sS0, sV0, fac0);
   }
 
+  if (split_k) {
+    // ---- split-K partial of each column: O in dim order (O^T row 16 db + 4 lg + e holds dim
+    // 32 (db >> 1) + 8 lg + 4 (db & 1) + e), the reference its weights are relative to (-inf
+    // while the column has none) and their sum
+#pragma unroll
+    for (int nb = 0; nb < NBW; ++nb) {
+      float l = l_run[nb];
+      l += __shfl_xor(l, 16, 64);
+      l += __shfl_xor(l, 32, 64);
+      if (col_ok[nb]) {
+        const int c = col_i[nb] * a.G + (col_h[nb] - hkv * a.G);
+        const int64_t rec = (bh * a.nsplit + split) * a.C + c;
+        float* po = a.part_o + rec * a.dp;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+          *reinterpret_cast<float4v*>(po + 32 * (db >> 1) + 8 * lg + 4 * (db & 1)) = oacc[db][nb];
+        if (lg == 0) {
+          a.part_ml[rec * 2] = (thr[nb] == -INFINITY) ? -INFINITY : mref[nb];
+          a.part_ml[rec * 2 + 1] = l;
+        }
+      }
+    }
+    return;
+  }
   // ---- normalise and rotate back: out = (O^T / l)^T Pi_v, Pi_v^T as split-f16 A operand.
   // Lane group g of O^T blocks 2c, 2c+1 holds dims 32c + 8g + 0..7 (the V^T row order), so
   // each A fragment is one 16-byte run of a Pi_v^T row, read once for both column blocks.
@@ -676,13 +713,19 @@ bool prefill_applies(int Hq, int Hkv, int d, int bits, int val_bits, bool masked
   const int cols = kPfWaves * 16 * (masked ? pf_nbw<true>() : pf_nbw<false>());
   return (d == 64 || d == 128) && bits >= 2 && bits <= 4 && val_bits == bits && Hq / Hkv <= cols;
 }
+// the split-K form: the kv head's columns (query rows x group) in one block
+bool prefill_split_applies(int Hq, int Hkv, int Sq, int d, int bits, int val_bits, bool masked) {
+  const int cols = kPfWaves * 16 * (masked ? pf_nbw<true>() : pf_nbw<false>());
+  return prefill_applies(Hq, Hkv, d, bits, val_bits, masked) && static_cast<int64_t>(Hq / Hkv) * Sq <= cols;
+}
 
 int prefill_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, const uint8_t* kcodes,
                       const uint8_t* ksigns, const uint16_t* krn, const uint16_t* kvn, const uint16_t* kcent,
                       int bits, const uint8_t* vcodes, const uint16_t* vvn, const float* vcent,
                       const uint16_t* vpit, int B, int Hq, int Hkv, int Sq, int Sk, int d, float coeff, float scale,
                       int causal, const float* mask, int64_t smb, int64_t smh, int64_t smq, int64_t smk, void* out,
-                      int out_dtype, int64_t sob, int64_t soh, int64_t sos, hipStream_t s) {
+                      int out_dtype, int64_t sob, int64_t soh, int64_t sos, hipStream_t s, float* part_o,
+                      float* part_ml, int nsplit, int chunk, int C, int dp) {
   PrefillArgs a{};
   a.q_rot = q_rot;
   a.q_proj = q_proj;
@@ -717,11 +760,21 @@ int prefill_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, c
   a.sob = sob;
   a.soh = soh;
   a.sos = sos;
-  // one block per (query block, batch, kv head), query blocks heavy first across all groups
+  // one block per (query block, batch, kv head), query blocks heavy first across all groups;
+  // split-K: one query block, grid.y = splits
+  if (part_o) {
+    a.part_o = part_o;
+    a.part_ml = part_ml;
+    a.nsplit = nsplit;
+    a.chunk = chunk;
+    a.C = C;
+    a.dp = dp;
+  }
   const int64_t nblocks = static_cast<int64_t>(a.nqb) * Hkv * B;
   TQ_REQUIRE(nblocks < (int64_t(1) << 31), "tq_attention_fwd: %lld query blocks exceed one grid",
              (long long)nblocks);
-  const dim3 grid(static_cast<unsigned>(nblocks));
+  TQ_REQUIRE(!part_o || (a.nqb == 1 && chunk % PfCfg<128, 3>::KT == 0), "tq_attention_fwd: bad split plan");
+  const dim3 grid(static_cast<unsigned>(nblocks), static_cast<unsigned>(part_o ? nsplit : 1));
 #define TQ_PF_LAUNCH(DD, BB)                                                       \
   if (mask) prefill_kernel<DD, BB, true><<<grid, PfCfg<DD, BB>::NT, 0, s>>>(a);  \
   else prefill_kernel<DD, BB, false><<<grid, PfCfg<DD, BB>::NT, 0, s>>>(a);

@@ -530,7 +530,7 @@ Tensor attention(const Tensor& q_rot, const Tensor& q_proj, const Tensor& kcodes
   }
   Tensor ws;
   int64_t ws_bytes = 0;
-  if (workspace == 1 && val_bits == bits) {
+  if (workspace == 1) {
     ws_bytes = tq_attention_workspace_size(B32, Hq32, Hkv32, Sq32, Sk32, D32, b32);
     if (ws_bytes > 0) ws = at::empty({ws_bytes}, q_rot.options().dtype(at::kByte));
   }
