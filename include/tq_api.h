@@ -174,7 +174,7 @@ int tq_attention_scores(const uint16_t* q_rot, const float* q_proj,
  *   o   = (sum_j p_j * vnv_j * Cv[vcodes_j]) Pi_v    (Cv: f32 value centroids)
  * out[b, i, h, :] in out_dtype with element strides (sob, soh, sos).
  * workspace / workspace_bytes: scratch of at least tq_attention_workspace_size
- * bytes enables the split-K decode kernels for few-query shapes.
+ * bytes (16-byte aligned) enables the split-K paths for few-query shapes.
  * mask: f32 additive, element strides (smb, smh, smq, smk) (0 = broadcast).
  * val_pi_split: the value compressor's Pi^T split as in tq_compress_keys.
  * Replaces the family forward tail families/qwen2.py:105-117 (same in
@@ -248,12 +248,14 @@ int tq_cache_append(const void* k, const void* v, int32_t dtype, int32_t B,
                     int64_t sqh, int64_t sqs, const uint16_t* key_s_eff_f16,
                     uint16_t* q_rot, float* q_proj, void* stream);
 
-/* Bytes of caller-provided device workspace tq_attention_fwd uses for the
- * split-K decode path at this shape (head_dim 128, bits 2-4, at most 16
- * (query row, query head) pairs per kv head, value bits == key bits); 0 when
- * that path does not apply.  With a smaller or NULL workspace
- * tq_attention_fwd runs its tiled path instead.  No counterpart in the
- * reference, whose attention is never split over keys. */
+/* Bytes of caller-provided device workspace tq_attention_fwd uses to split the keys of a
+ * few-query shape: the split-K decode kernels (head_dim 128, bits 2-4, at most 16
+ * (query row, query head) pairs per kv head, value bits == key bits) or, for other
+ * few-query shapes whose kv head's columns fit one block (any head dim, other value
+ * bits, larger groups) with at least 512 keys, the fused kernels split over keys plus a
+ * merge; the larger of the two, 0 when neither applies.  With a smaller or NULL
+ * workspace tq_attention_fwd runs unsplit.  No counterpart in the reference, whose
+ * attention is never split over keys. */
 int64_t tq_attention_workspace_size(int32_t B, int32_t Hq, int32_t Hkv,
                                     int32_t Sq, int32_t Sk, int32_t d,
                                     int32_t bits);
@@ -262,13 +264,13 @@ int64_t tq_attention_workspace_size(int32_t B, int32_t Hq, int32_t Hkv,
 #define TQ_NOALLOC_SCRATCH_BYTES (16LL << 20)
 
 /* tq_attention_fwd_kv with no caller workspace and no device allocation: the split-K
- * decode path keeps its per-split partials in a library-owned device array of
+ * paths keep their per-split partials in a library-owned device array of
  * TQ_NOALLOC_SCRATCH_BYTES (16 MiB) per GPU, held from the library's first use of that GPU
  * until the process ends.  Same arguments, results and error behaviour as
  * tq_attention_fwd_kv otherwise (bit-identical outputs for the same inputs).
- *   - Shapes whose partials need more than the array (tq_attention_workspace_size >
- *     tq_noalloc_scratch_bytes(), e.g. more than 16 MiB of (batch, kv head, split)
- *     records) fail with TQ_EINVAL and a message; shapes off the split-K path use none.
+ *   - Decode-kernel shapes whose partials need more than the array (more than 16 MiB of
+ *     (batch, kv head, split) records) fail with TQ_EINVAL and a message; the other split
+ *     path runs unsplit when its partials do not fit; shapes off both paths use none.
  *   - Every call on one GPU shares that GPU's array, which keeps the last call's contents:
  *     calls that overlap in time on one GPU (other streams, other host threads) race.
  *     Calls queued on one stream are ordered and safe.
