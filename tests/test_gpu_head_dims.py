@@ -256,3 +256,24 @@ def test_attention_split_keys_any_dim(d, bits, vbits, hq, hkv, sq, sk, causal, m
     assert np.isfinite(got).all()
     assert err < REL and O.cosine(got, ref) > 0.9999
     assert err_u < REL
+
+
+@pytest.mark.parametrize("d,bits,hq,hkv,sq,sk", [
+    (64, 3, 32, 8, 1, 5001),    # blocks split the keys; the last split ends inside a tile
+    (80, 2, 12, 12, 1, 3000),   # byte-stream rows
+    (256, 4, 8, 2, 2, 2600),
+    (128, 3, 64, 2, 1, 3000),   # 32 columns per kv head (beyond the decode kernels)
+])
+def test_scores_split_keys_any_dim(d, bits, hq, hkv, sq, sk):
+    """Materialised scores of few-query shapes over long key ranges, with the keys split over
+    blocks, against the float64 oracle."""
+    _case(d=d, bits=bits, hq=hq, hkv=hkv, sq=sq, sk=sk)
+    torch.manual_seed(d + bits + sk)
+    k = torch.randn(2, hkv, sk, d, device=DEV, dtype=torch.bfloat16)
+    q = torch.randn(2, hq, sq, d, device=DEV, dtype=torch.bfloat16)
+    kc = TurboQuantCompressorV2(d, bits, seed=42, device=DEV)
+    ck = kc.compress(k)
+    got = _np(kc.asymmetric_attention_scores(q, ck))
+    ref = _oracle_scores(kc, q, ck, hq, hkv)
+    assert got.shape == ref.shape and np.isfinite(got).all()
+    assert O.rel_err(got, ref) < REL

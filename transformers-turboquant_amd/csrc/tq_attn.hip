@@ -86,9 +86,10 @@ struct AttnArgs {
   int out_dtype;
   int64_t sob, soh, sos;
   float* scores;  // scores-only mode output f32 [B, Hq, Sq, Sk]
-  // split-K (part_o != nullptr, attention mode): block (x, split) attends keys
-  // [split * chunk, (split + 1) * chunk) and writes its columns' partial O (unnormalised,
-  // rotated value domain, rows of dp floats), reference maximum and sum for attn_merge_kernel
+  // split over keys (nsplit > 1): block (x, split) takes keys [split * chunk, (split + 1) *
+  // chunk); in scores mode it writes their scores, in attention mode (part_o) its columns'
+  // partial O (unnormalised, rotated value domain, rows of dp floats), reference maximum and
+  // sum for attn_merge_kernel
   float *part_o, *part_ml;
   int nsplit, chunk, C, dp;
 };
@@ -148,7 +149,7 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
   const int bhi = static_cast<int>(blockIdx.x) % nbh;
   const int hkv = bhi % a.Hkv, b = bhi / a.Hkv;
   const int q0 = qblk * a.QT;
-  const bool split_k = !SCORES && a.part_o != nullptr;
+  const bool split_k = a.nsplit > 1;
   const int split = split_k ? static_cast<int>(blockIdx.y) : 0;
   const int d = STREAM ? a.d : D;
   const int KC = d * KB / 8, SC = d / 8, vc = d * a.vb / 8;  // bytes per packed row
@@ -488,7 +489,7 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
   }
 
   if constexpr (!SCORES) {
-    if (split_k) {
+    if (split_k) {  // attention mode splits only with part_o set
       // ---- split-K partial of each column: O (dims 16 db + 4 lg + e), the reference maximum
       // its weights are relative to (-inf when the split saw no finite score) and their sum
 #pragma unroll
@@ -581,7 +582,7 @@ __global__ void __launch_bounds__(64 * kAttnWaves, 2) attn_kernel(AttnArgs a) {
 template <int D, int KB, bool SCORES, bool STREAM>
 static void launch_attn_st(const AttnArgs& a, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.nqb) * a.Hkv * a.B),  // see the kernel
-                  static_cast<unsigned>(!SCORES && a.part_o ? a.nsplit : 1));
+                  static_cast<unsigned>(a.nsplit > 1 ? a.nsplit : 1));
   if (!SCORES && a.mask) attn_kernel<D, KB, SCORES, !SCORES, STREAM><<<grid, ATile<D, SCORES>::NT, 0, s>>>(a);
   else attn_kernel<D, KB, SCORES, false, STREAM><<<grid, ATile<D, SCORES>::NT, 0, s>>>(a);
 }
@@ -823,11 +824,12 @@ static int split_row_floats(int d) {
   const int dpad = pad_dim(d);
   return dpad <= 64 ? 64 : (dpad <= 128 ? 128 : 256);
 }
-static SplitPlan tiled_split_plan(int B, int Hq, int Hkv, int Sq, int Sk, int d) {
+static SplitPlan tiled_split_plan(int B, int Hq, int Hkv, int Sq, int Sk, int d, bool scores = false) {
   SplitPlan p;
   if (!supported_dim(d) || Hkv <= 0 || Hq % Hkv || B <= 0 || Sq <= 0) return p;
   const int G = Hq / Hkv;
-  if (G * Sq > block_rows(d, false) || G > block_rows(d, false)) return p;  // one query block per kv head
+  const int64_t cols = block_rows(d, scores);
+  if (static_cast<int64_t>(G) * Sq > cols) return p;  // one query block per kv head
   if (Sk < 2 * kSplitMinKeys) return p;
   const int64_t groups = static_cast<int64_t>(B) * Hkv;
   int64_t ns = (kSplitBlocks + groups - 1) / groups;
@@ -958,6 +960,13 @@ int tq_attention_scores_kv(const uint16_t* q_rot, const float* q_proj, const uin
   a.coeff = coeff;
   a.scale = 1.f;
   a.scores = out;
+  // few query rows per kv head over a long key range: blocks split the keys (each writes its
+  // own keys' scores, nothing to merge)
+  const SplitPlan sp = tiled_split_plan(B, Hq, Hkv, Sq, Sk, d, true);
+  if (sp.nsplit > 1) {
+    a.nsplit = sp.nsplit;
+    a.chunk = sp.chunk;
+  }
   dispatch_attn<true>(d, bits - 1, a, as_stream(stream));
   return launch_status("tq_attention_scores");
 }
