@@ -685,8 +685,29 @@ def head_dim64_leg(steps: int, warmup: int) -> dict:
         tflops = key_heads * 6 * d / (attn_ms * 1e-3) / 1e12
         out[f"S{S_}"] = {"step_ms": step_ms, "attention_ms": attn_ms, "attention_tflops": tflops,
                          "mfma_frac": tflops / MFMA_F16_PEAK_TFLOPS}
+    # one decode step's attention over a compressed cache at this head dim (one query row per
+    # sequence): the prefill kernel split over keys + merge
+    for b_, sk in ((1, 4096), (1, 32768)):
+        g = torch.Generator(device="cuda").manual_seed(sk)
+        ck = kc.compress(torch.randn(b_, h, sk, d, device="cuda", generator=g).to(torch.bfloat16))
+        cv = vc.compress(torch.randn(b_, h, sk, d, device="cuda", generator=g).to(torch.bfloat16))
+        q_rot, q_proj = kc.prepare_queries(torch.randn(b_, h, 1, d, device="cuda", generator=g).to(torch.bfloat16))
+        for _ in range(warmup + 5):
+            attention_from_prepared(q_rot, q_proj, kc, vc, ck, cv, out_dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        RANGES.push(f"head_dim64_decode_B{b_}_S{sk}", steps)
+        e0, e1 = _events(2)
+        e0.record()
+        for _ in range(steps):
+            attention_from_prepared(q_rot, q_proj, kc, vc, ck, cv, out_dtype=torch.bfloat16)
+        e1.record()
+        torch.cuda.synchronize()
+        RANGES.pop()
+        out[f"decode_B{b_}_S{sk}"] = {"attention_us": e0.elapsed_time(e1) / steps * 1e3}
     return {"workload": f"GPT-2 attention shape: B1 x {h} heads x d{d}, bits {BITS}, causal; "
-                        "tq::prefill_kernel<64, 3, false> (q_proj as f16 hi + lo)", **out}
+                        "tq::prefill_kernel<64, 3, false> (q_proj as f16 hi + lo); decode steps (one query "
+                        "row over 4k / 32k cached keys) through the same kernel split over keys + merge",
+            **out}
 
 
 def model_leg(steps: int = 3, S_model: int = 8192, bits: int = BITS) -> dict:
