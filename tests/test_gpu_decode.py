@@ -1,5 +1,6 @@
-"""GPU parity of the split-K decode kernels (head_dim 128, at most 16 query
-(row, head) columns per kv head) against the CPU oracle and the tiled kernel.
+"""GPU parity of the split-K decode kernels (head_dim 128 with at most 16 query
+(row, head) columns per kv head; head_dim 64 with bits 2-3 and at most 8) against
+the CPU oracle and the tiled kernel.
 
 Same bars as the other kernel tests: scores and attention outputs within
 rel-err 1e-3 and cosine >= 0.9999 of the float64 oracle estimator evaluated on
@@ -97,16 +98,18 @@ def test_decode_scores_any_codebook(bits, cb, qmul, hq):
 @pytest.mark.parametrize("bits", [2, 3])
 @pytest.mark.parametrize("cb", ["nonaffine", "shifted"])
 @pytest.mark.parametrize("hq", [8, 16])
-def test_decode_attention_any_codebook(bits, cb, hq):
+@pytest.mark.parametrize("d", [128, 64])
+def test_decode_attention_any_codebook(bits, cb, hq, d):
     """Fused decode attention with key codebooks that are not odd (and, for 2-bit codes, not
     affine in the code bits) against the oracle evaluated with the same f16 codebook; 4 and 8
-    columns per kv head (one and two column groups of the bit-plane kernel)."""
-    _case(bits=bits, cb=cb, hq=hq)
+    columns per kv head (one and two column groups of the bit-plane kernel), head_dim 128
+    and 64."""
+    _case(bits=bits, cb=cb, hq=hq, d=d)
     from turboquant_pytorch._ops import ops
     from turboquant_pytorch.compressors import _tables
 
-    B, hkv, sq, sk, d = 2, 2, 1, 2000, 128
-    assert _on_decode_path(B, hq, hkv, sq, sk, bits)
+    B, hkv, sq, sk = 2, 2, 1, 2000
+    assert _on_decode_path(B, hq, hkv, sq, sk, bits, d)
     torch.manual_seed(11 * bits + len(cb))
     q = torch.randn(B, hq, sq, d, device=DEV, dtype=torch.bfloat16)
     k = torch.randn(B, hkv, sk, d, device=DEV, dtype=torch.bfloat16)
@@ -332,3 +335,52 @@ def test_decode_two_column_groups_scores_and_attention(bits, hq, hkv, sq, sk, ca
     err = O.rel_err(got, ref)
     print(f"scores rel-err {O.rel_err(got_s, ref_s):.2e}, attention rel-err {err:.2e}", flush=True)
     assert err < REL and O.cosine(got, ref) > 0.9999
+
+
+@pytest.mark.parametrize("bits", [2, 3])
+@pytest.mark.parametrize("hq,hkv,sq,sk,causal,masked", [
+    (32, 8, 1, 4097, False, False),   # 4 columns per kv head (a 32/8-head model)
+    (12, 12, 1, 3000, False, False),  # one column per kv head (multi-head attention)
+    (16, 2, 1, 20000, True, False),   # 8 columns, 79 splits
+    (8, 2, 2, 1025, True, True),      # 8 columns from 4 heads x 2 rows, causal, mask
+    (5, 1, 1, 777, False, False),     # 5 columns: the second group holds one
+    (4, 1, 1, 1, False, False),       # a single key
+    (6, 2, 1, 65, True, False),       # 3 columns, one partial slab
+    (7, 1, 1, 9000, False, True),     # 7 columns, padding mask
+])
+def test_decode_head_dim64_scores_and_attention(bits, hq, hkv, sq, sk, causal, masked):
+    """The bit-plane decode kernels at head_dim 64 (16-dim lane groups: 2-byte sign and 1-bit
+    code fields, 4 value dims per lane), scores and fused attention against the float64
+    oracle, and the tiled kernel on the same inputs."""
+    _case(what="decode d64", bits=bits, hq=hq, hkv=hkv, sq=sq, sk=sk, causal=causal, masked=masked)
+    B, d = 2, 64
+    assert _on_decode_path(B, hq, hkv, sq, sk, bits, d)
+    torch.manual_seed(29 * bits + hq + sk)
+    q = torch.randn(B, hq, sq, d, device=DEV, dtype=torch.bfloat16)
+    k = torch.randn(B, hkv, sk, d, device=DEV, dtype=torch.bfloat16)
+    v = torch.randn(B, hkv, sk, d, device=DEV, dtype=torch.bfloat16)
+    kc = TurboQuantCompressorV2(d, bits, seed=42, device=DEV)
+    vc = TurboQuantCompressorMSE(d, bits, seed=10042, device=DEV)
+    ck, cv = kc.compress(k), vc.compress(v)
+    got_s = _np(kc.asymmetric_attention_scores(q, ck))
+    ref_s = _oracle_scores(kc, q, ck, hq, hkv)
+    assert got_s.shape == ref_s.shape
+    assert O.rel_err(got_s, ref_s) < REL
+    mask = None
+    if masked:
+        mask = torch.zeros(B, 1, sq, sk)
+        mask[0, 0, :, : sk // 3] = torch.finfo(torch.float32).min  # left padding on batch row 0
+        mask[1, 0, :, 7] = -4.0
+    mask_dev = mask.to(DEV) if mask is not None else None
+    ref = _oracle_attention(kc, vc, q, ck, cv, hq, hkv, causal=causal,
+                            mask=mask.numpy() if mask is not None else None)
+    got = _np(compressed_attention(q, kc, vc, ck, cv, causal=causal, out_dtype=torch.float32,
+                                   attention_mask=mask_dev))
+    tiled = _np(compressed_attention(q, kc, vc, ck, cv, causal=causal, out_dtype=torch.float32,
+                                     attention_mask=mask_dev, split_k=False))
+    assert np.isfinite(got).all()
+    err = O.rel_err(got, ref)
+    print(f"scores rel-err {O.rel_err(got_s, ref_s):.2e}, attention rel-err {err:.2e}, "
+          f"tiled {O.rel_err(tiled, ref):.2e}", flush=True)
+    assert err < REL and O.cosine(got, ref) > 0.9999
+    assert O.rel_err(tiled, ref) < REL

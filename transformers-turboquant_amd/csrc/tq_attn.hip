@@ -855,6 +855,31 @@ static void launch_split_merge(const SplitMergeArgs& m, int dp, hipStream_t s) {
   else attn_merge_kernel<256><<<grid, 256, 0, s>>>(m);
 }
 
+int merge_key_splits(const float* part_o, const float* part_ml, const uint16_t* vpit, int B, int Hq, int Hkv,
+                     int Sq, int C, int nsplit, int d, void* out, int out_dtype, int64_t sob, int64_t soh,
+                     int64_t sos, hipStream_t s) {
+  SplitMergeArgs m{};
+  m.part_o = part_o;
+  m.part_ml = part_ml;
+  m.vpit = vpit;
+  m.B = B;
+  m.Hq = Hq;
+  m.Hkv = Hkv;
+  m.Sq = Sq;
+  m.G = Hq / Hkv;
+  m.C = C;
+  m.nsplit = nsplit;
+  m.d = d;
+  m.dpad = pad_dim(d);
+  m.out = out;
+  m.out_dtype = out_dtype;
+  m.sob = sob;
+  m.soh = soh;
+  m.sos = sos;
+  launch_split_merge(m, split_row_floats(d), s);
+  return launch_status("tq_attention_fwd (split merge)");
+}
+
 }  // namespace tq
 
 using namespace tq;
@@ -1001,31 +1026,14 @@ int tq_attention_fwd_kv(const uint16_t* q_rot, const float* q_proj, const uint8_
                             scale, causal, mask, smb, smh, smq, smk, out, out_dtype, sob, soh, sos,
                             workspace, as_stream(stream));
   // few query rows per kv head over a long key range: the tiled kernel split over keys, then a
-  // merge (the decode kernels above take head_dim 128 with key bits = value bits)
+  // merge (the decode kernels above take head_dim 128, and head_dim 64 at bits 2-3 with at most 8
+  // columns, with key bits = value bits)
   const SplitPlan sp = tiled_split_plan(B, Hq, Hkv, Sq, Sk, d);
   const bool split = sp.nsplit > 0 && workspace && workspace_bytes >= sp.bytes &&
                      reinterpret_cast<uintptr_t>(workspace) % 16 == 0;
   auto merge_split = [&](float* part_o, float* part_ml, int C) {
-    SplitMergeArgs m{};
-    m.part_o = part_o;
-    m.part_ml = part_ml;
-    m.vpit = val_pit_split;
-    m.B = B;
-    m.Hq = Hq;
-    m.Hkv = Hkv;
-    m.Sq = Sq;
-    m.G = Hq / Hkv;
-    m.C = C;
-    m.nsplit = sp.nsplit;
-    m.d = d;
-    m.dpad = pad_dim(d);
-    m.out = out;
-    m.out_dtype = out_dtype;
-    m.sob = sob;
-    m.soh = soh;
-    m.sos = sos;
-    launch_split_merge(m, sp.dp, as_stream(stream));
-    return launch_status("tq_attention_fwd (split merge)");
+    return merge_key_splits(part_o, part_ml, val_pit_split, B, Hq, Hkv, Sq, C, sp.nsplit, d, out, out_dtype, sob,
+                            soh, sos, as_stream(stream));
   };
   if (split && prefill_split_applies(Hq, Hkv, Sq, d, bits, val_bits, mask != nullptr)) {
     // head_dim 64 / 128: the prefill kernel split over keys

@@ -213,15 +213,18 @@ __device__ __forceinline__ float digits_f32(i32x4v acc) {
 // a 16-key block on the N side, the digit sums of those columns against its own key (lane
 // l16).  The key-side plane operands are built once per key and serve every column group.
 // STAGE_BYTES of LDS serve as staging during setup().
-template <int KB, int NCG = 1>
+template <int KB, int NCG = 1, int D_ = 128>
 struct PlaneQuery {
   static_assert(KB == 1 || KB == 2, "1- or 2-bit key codes");
   static_assert(NCG == 1 || NCG == 2, "4 or 8 columns");
-  static constexpr int D = 128;
-  static constexpr int NC = 4 * NCG;           // columns served
-  static constexpr int NT1 = 2 * KB;           // code-plane fragments (MFMAs per 16 keys)
-  static constexpr int NFM = NT1 + 2;          // then the two sign-plane fragments
-  static constexpr int NDL = KB == 2 ? 2 : 0;  // interaction-plane fragments
+  static_assert(D_ == 64 || D_ == 128, "head_dim 64 or 128");
+  static constexpr int D = D_;
+  static constexpr int LW = D / 4;                 // dims per lane group (a quarter of a key row)
+  static constexpr int KWD = (LW * KB + 31) / 32;  // code dwords per lane (head_dim 64, 1 bit: half a dword)
+  static constexpr int NC = 4 * NCG;               // columns served
+  static constexpr int NT1 = 2 * KWD;              // code-plane fragments (MFMAs per 16 keys)
+  static constexpr int NFM = NT1 + 2;              // then the two sign-plane fragments
+  static constexpr int NDL = KB == 2 ? KWD : 0;    // interaction-plane fragments
   static constexpr int NF = NFM + NDL;
   static constexpr int STAGE_BYTES =
       (NC * 2 * D * 4 > NCG * NFM * 1024) ? NC * 2 * D * 4 : NCG * NFM * 1024;
@@ -254,7 +257,8 @@ struct PlaneQuery {
     for (int g = 0; g < NCG; ++g) {
       const int c = wave + 4 * g;
       float r0 = 0.f, r1 = 0.f, p0 = 0.f, p1 = 0.f;
-      if (c < a.C) {
+      const bool dim_ok = 2 * lane < D;  // head_dim 64: lanes 0-31 hold the row
+      if (c < a.C && dim_ok) {
         const int qi = c / a.G, h = hkv * a.G + c % a.G;
         const int64_t qrow = ((static_cast<int64_t>(b) * a.Hq + h) * a.Sq + qi) * D + 2 * lane;
         const uint32_t rr = *reinterpret_cast<const uint32_t*>(a.q_rot + qrow);
@@ -264,8 +268,10 @@ struct PlaneQuery {
         p0 = pp.x;
         p1 = pp.y;
       }
-      *reinterpret_cast<float2*>(qst + (c * 2) * D + 2 * lane) = float2{r0, r1};
-      *reinterpret_cast<float2*>(qst + (c * 2 + 1) * D + 2 * lane) = float2{p0, p1};
+      if (dim_ok) {
+        *reinterpret_cast<float2*>(qst + (c * 2) * D + 2 * lane) = float2{r0, r1};
+        *reinterpret_cast<float2*>(qst + (c * 2 + 1) * D + 2 * lane) = float2{p0, p1};
+      }
       float mr = fmaxf(fabsf(r0), fabsf(r1)), mp = fmaxf(fabsf(p0), fabsf(p1));
       float sr = r0 + r1, sp = p0 + p1;
 #pragma unroll
@@ -299,34 +305,37 @@ struct PlaneQuery {
       const int e = gi & 3, lgp = (gi >> 2) & 3, cq = (gi >> 4) & 3, gf = gi >> 6;
       const int g = gf / NF, f = gf % NF;
       ofrag[r] = g < NCG ? f : NF;
-      int i = 0, m0 = 0, mstep = 8, term = 1;  // slot bit i; dims m0 + j * mstep
+      int i = 0, m0 = 0, mstep = 8, term = 1;  // slot bit i; lane-group dims m0 + j * mstep
       float coef = 0.f;
       if (f < NT1) {
         const int w = f >> 1;
         i = 4 * (f & 1) + e;
         const int p0 = 32 * w + i;  // + 8j
-        m0 = 32 * lgp + (KB == 1 ? p0 : (p0 >> 1));
+        m0 = KB == 1 ? p0 : (p0 >> 1);
         mstep = KB == 1 ? 8 : 4;
         coef = (KB == 2 && (i & 1)) ? ahi : alo;
       } else if (f < NFM) {
         i = 4 * (f - NT1) + e;
-        m0 = 32 * lgp + i;
+        m0 = i;
         coef = 2.f;
         term = 2;
       } else {
         const int w = f - NFM;
         i = 2 * e;
-        m0 = 32 * lgp + 16 * w + e;
+        m0 = 16 * w + e;
         mstep = 4;
         coef = adl;
       }
       const int c = 4 * (g < NCG ? g : 0) + cq;
       const int F = term == 1 ? st_f1[c] : st_f2[c];
-      const float* qv = qst + (c * 2 + (term - 1)) * D;
+      const float* qv = qst + (c * 2 + (term - 1)) * D + LW * lgp;
       uint32_t u[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int wv = g < NCG ? __float2int_rn(ldexpf(coef * qv[m0 + j * mstep], F)) : 0;
+        // slots past the lane group's dims (head_dim 64: the upper half of a 1-bit code or
+        // sign dword) carry zero, so the bits read there add nothing
+        const int m = m0 + j * mstep;
+        const int wv = (g < NCG && m < LW) ? __float2int_rn(ldexpf(coef * qv[m], F)) : 0;
         const int av = i < 7 ? wv * (1 << (7 - i)) : -wv;
         u[j] = (static_cast<uint32_t>(av) + 0x808080u) ^ 0x808080u;
       }
@@ -393,18 +402,22 @@ struct PlaneQuery {
   // work into separate basic blocks; each plane operand feeds the MFMAs of every column group.
   __device__ __forceinline__ void dots2(const uint8_t* kp0, const uint8_t* sp0, const uint8_t* kp1,
                                         const uint8_t* sp1, float (&t1)[2][NCG], float (&t2)[2][NCG]) const {
-    uint32_t kw[2][KB], sw[2];
+    uint32_t kw[2][KWD], sw[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const uint8_t* kp = j ? kp1 : kp0;
-      if constexpr (KB == 2) {
+      if constexpr (KWD == 2) {
         const u32x2 t = *reinterpret_cast<const u32x2*>(kp);
         kw[j][0] = t[0];
         kw[j][1] = t[1];
+      } else if constexpr (LW * KB == 16) {
+        kw[j][0] = *reinterpret_cast<const uint16_t*>(kp);  // a 2-byte field
       } else {
         kw[j][0] = *reinterpret_cast<const uint32_t*>(kp);
       }
-      sw[j] = *reinterpret_cast<const uint32_t*>(j ? sp1 : sp0);
+      const uint8_t* sp = j ? sp1 : sp0;
+      if constexpr (LW == 16) sw[j] = *reinterpret_cast<const uint16_t*>(sp);
+      else sw[j] = *reinterpret_cast<const uint32_t*>(sp);
     }
     if constexpr (NCG == 1) {
       i32x4v s1[2], s2[2];
@@ -479,9 +492,16 @@ struct PlaneQuery {
   }
 };
 
-// materialised scores for bits 2-3 and at most 8 columns (tq_decode.hip), on a plan of
-// tq_decode_scores.hip
-void launch_scores_planes(const DecodeArgs& a, int bits, hipStream_t s);
+// materialised scores for bits 2-3 and at most 8 columns, head_dim d = 64 or 128
+// (tq_decode.hip), on a plan of tq_decode_scores.hip
+void launch_scores_planes(const DecodeArgs& a, int bits, int d, hipStream_t s);
+
+// Log-sum-exp merge of per-split partial rows (unnormalised o in the rotated value domain,
+// d floats for d = 64, then [maximum (log2), sum] per row at part_ml) and the Pi_v product,
+// for any supported head dim (tq_attn.hip)
+int merge_key_splits(const float* part_o, const float* part_ml, const uint16_t* vpit, int B, int Hq, int Hkv,
+                     int Sq, int C, int nsplit, int d, void* out, int out_dtype, int64_t sob, int64_t soh,
+                     int64_t sos, hipStream_t s);
 
 // ---------------------------------------------------------------- planning
 struct DecodePlan {
@@ -508,11 +528,18 @@ inline DecodePlan plan_split(int B, int Hkv, int Sk, int target, int quantum, in
   return p;
 }
 
-// head_dim 128, bits 2-4, at most 16 query columns per kv head; S_k below 2^24
-// keeps every per-group byte offset of the planes and score rows under 2^31
+// head_dim 128 with bits 2-4 and at most 16 query columns per kv head, or head_dim 64 with
+// bits 2-3 and at most 8; S_k below 2^24 keeps every per-group byte offset of the planes and
+// score rows under 2^31
 inline bool decode_shape(int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
-  if (d != 128 || bits < 2 || bits > 4 || Hkv <= 0 || Hq % Hkv) return false;
-  return (Hq / Hkv) * Sq <= 16 && Sk >= 1 && Sk < (1 << 24);
+  if (bits < 2 || bits > 4 || Hkv <= 0 || Hq % Hkv) return false;
+  const int C = (Hq / Hkv) * Sq;
+  if (d == 64) {
+    if (bits > 3 || C > 8) return false;  // head_dim 64: the bit-plane kernels only
+  } else if (d != 128) {
+    return false;
+  }
+  return C <= 16 && Sk >= 1 && Sk < (1 << 24);
 }
 
 }  // namespace tq

@@ -365,13 +365,13 @@ decode_attn_lds_kernel(DecodeArgs a) {
 // of 4) per lane group, keys on the N side; unit u of a 32-key slab scores keys 2n + u
 // (n = l16), so each lane ends with two adjacent keys of its columns and a score row's 32
 // values leave as one 128-byte run.
-template <int KB, int R, int NCG>
+template <int KB, int R, int NCG, int D>
 __global__ void __launch_bounds__(256) decode_scores_i8_kernel(DecodeArgs a) {
   static_assert(R >= 2 && R <= 4, "ring of 2 to 4 slots");
-  using PQ = PlaneQuery<KB, NCG>;
-  constexpr int D = 128, NK = 32;
+  using PQ = PlaneQuery<KB, NCG, D>;
+  constexpr int NK = 32;
   constexpr int KC = D * KB / 8, SC = D / 8;
-  constexpr int KLANE = KC / 4;
+  constexpr int KLANE = KC / 4, SLANE = SC / 4;  // a lane group's quarter of a code / sign row
   constexpr int SLAB = 4 * NK;
   constexpr int OFF_K = 0, OFF_S = NK * KC, OFF_N = OFF_S + NK * SC;
   constexpr int NRM = NK * 4;
@@ -400,12 +400,13 @@ __global__ void __launch_bounds__(256) decode_scores_i8_kernel(DecodeArgs a) {
   const uint32_t ring_lds = lds_offset(stage) + wave * SLOT;
   constexpr int NKD = (NK * KC + 1023) / 1024, NSD = (NK * SC + 1023) / 1024;
   constexpr int NDMA = NKD + NSD + 2;
+  // 16 bytes per lane and round; the plane sizes (256 to 1536 bytes) are multiples of 16
   auto copy_plane = [&](const i32x4& r, uint32_t dst, int bytes, int nrounds) {
     const uint32_t lo = lane * 16;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       if (c >= nrounds) break;
-      if ((c + 1) * 1024 <= bytes || lane < 32) dma16(r, dst + c * 1024, lo + c * 1024);
+      if ((c + 1) * 1024 <= bytes || lane * 16 < bytes - c * 1024) dma16(r, dst + c * 1024, lo + c * 1024);
     }
   };
   auto issue = [&](int kb, int slot) {
@@ -448,8 +449,8 @@ __global__ void __launch_bounds__(256) decode_scores_i8_kernel(DecodeArgs a) {
 
   auto slab = [&](const uint8_t* src, int ks0) {
     float sc[NCG][2], t1[2][NCG], t2[2][NCG];
-    pq.dots2(src + OFF_K + (2 * l16) * KC + lg * KLANE, src + OFF_S + (2 * l16) * SC + lg * 4,
-             src + OFF_K + (2 * l16 + 1) * KC + lg * KLANE, src + OFF_S + (2 * l16 + 1) * SC + lg * 4, t1, t2);
+    pq.dots2(src + OFF_K + (2 * l16) * KC + lg * KLANE, src + OFF_S + (2 * l16) * SC + lg * SLANE,
+             src + OFF_K + (2 * l16 + 1) * KC + lg * KLANE, src + OFF_S + (2 * l16 + 1) * SC + lg * SLANE, t1, t2);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int row = 2 * l16 + u;
@@ -490,15 +491,23 @@ __global__ void __launch_bounds__(256) decode_scores_i8_kernel(DecodeArgs a) {
   }
 }
 
-void launch_scores_planes(const DecodeArgs& a, int bits, hipStream_t s) {
+template <int D>
+static void launch_scores_planes_d(const DecodeArgs& a, int bits, hipStream_t s) {
+  // head_dim 64 with 1-bit codes and two column groups stages its set-up over 3 ring slots
+  constexpr int R = D == 64 ? 4 : 3;
   const dim3 grid(a.nsplit, a.Hkv, a.B);
   if (a.C > 4) {
-    if (bits == 2) decode_scores_i8_kernel<1, 3, 2><<<grid, 256, 0, s>>>(a);
-    else decode_scores_i8_kernel<2, 3, 2><<<grid, 256, 0, s>>>(a);
+    if (bits == 2) decode_scores_i8_kernel<1, R, 2, D><<<grid, 256, 0, s>>>(a);
+    else decode_scores_i8_kernel<2, R, 2, D><<<grid, 256, 0, s>>>(a);
   } else {
-    if (bits == 2) decode_scores_i8_kernel<1, 3, 1><<<grid, 256, 0, s>>>(a);
-    else decode_scores_i8_kernel<2, 3, 1><<<grid, 256, 0, s>>>(a);
+    if (bits == 2) decode_scores_i8_kernel<1, R, 1, D><<<grid, 256, 0, s>>>(a);
+    else decode_scores_i8_kernel<2, R, 1, D><<<grid, 256, 0, s>>>(a);
   }
+}
+
+void launch_scores_planes(const DecodeArgs& a, int bits, int d, hipStream_t s) {
+  if (d == 64) launch_scores_planes_d<64>(a, bits, s);
+  else launch_scores_planes_d<128>(a, bits, s);
 }
 
 // Fused decode attention for 1- and 2-bit key codes and at most 8 columns, scores on the
@@ -514,27 +523,32 @@ void launch_scores_planes(const DecodeArgs& a, int bits, hipStream_t s) {
 // reference into the score fmas (s - mref), which is exact only while mref is of the order
 // of real scores: a leading slab masked with finfo.min (clamped to -3e38) would set mref to
 // -3e38, and s - mref would then round every later real score to the same value.
-template <int KB, int R, bool MASK, int NCG>
+template <int KB, int R, bool MASK, int NCG, int D>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NCG == 1 ? 4 : 3)))
 decode_attn_i8_kernel(DecodeArgs a) {
-  constexpr int D = 128, BITS = KB + 1;
+  constexpr int BITS = KB + 1;
   using L = SmallLuts<BITS>;
-  using PQ = PlaneQuery<KB, NCG>;
+  using PQ = PlaneQuery<KB, NCG, D>;
   constexpr int NC = PQ::NC;
   constexpr int VB = L::VB;
-  constexpr int DB = D / 16;
+  constexpr int DB = D / 16;    // value-MFMA row blocks: lane l16 holds dims DB l16 .. DB l16 + DB - 1
+  constexpr int NPAIR = D / 32; // pair-table groups per parity
   constexpr int KC = D * KB / 8, SC = D / 8, VC = D * VB / 8;
-  constexpr int KLANE = KC / 4;
-  constexpr int VW32 = (VB == 3) ? 2 : 1;
+  constexpr int KLANE = KC / 4, SLANE = SC / 4;
+  constexpr int VFB = DB * VB;  // value field bits of a lane
+  constexpr int VW32 = (VB == 3) ? 2 : 1;  // 3-bit fields may straddle a dword
   constexpr int NK = 32;
   constexpr int SLAB = 4 * NK;
   constexpr int OFF_K = 0, OFF_S = NK * KC, OFF_V = OFF_S + NK * SC, OFF_N = OFF_V + NK * VC;
   constexpr int NRM = NK * 4;
   constexpr int SLOT = OFF_N + 3 * NRM;
-  constexpr int STG = 4 * SLOT;  // slot r of the four waves; slot R - 1 first stages the set-up
+  // slot r of the four waves at r * STG; the last NSTG slots (issued after the query set-up)
+  // first serve as the set-up's staging area
+  constexpr int STG = 4 * SLOT;
+  constexpr int NSTG = (PQ::STAGE_BYTES + STG - 1) / STG;
   constexpr int MERGE = 4 * NC * (D + 2) * 4;
   constexpr int STAGE = R * STG > MERGE ? R * STG : MERGE;
-  static_assert(STG >= PQ::STAGE_BYTES, "set-up staging fits in one ring slot per wave");
+  static_assert(NSTG < R, "set-up staging fits in the ring and leaves a slot to prefetch");
   static_assert(R >= 2 && R <= 3, "ring of 2 or 3 slots");
   constexpr float LOG2E = 1.4426950408889634f;
   constexpr float TAU = 8.0f;
@@ -544,7 +558,7 @@ decode_attn_i8_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t stage[STAGE];
   __shared__ __attribute__((aligned(16))) _Float16 ptile[4][NC][NK];  // per wave: P [column][key]
   const uint8_t* tV = luts + L::VAL_OFF;
-  uint8_t* const stg = stage + (R - 1) * STG;
+  uint8_t* const stg = stage + (R - NSTG) * STG;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lg = lane >> 4;
@@ -571,10 +585,10 @@ decode_attn_i8_kernel(DecodeArgs a) {
   const int kbeg = split * a.chunk;
   const int kend = min(a.Sk, kbeg + a.chunk);
 
-  // value field of the lane (value-MFMA row l16): dims l16*8 .. l16*8+7
-  const int voff = l16 * VB;
-  const int vbase = voff & ~3;
-  const int vbyte = voff & 3;
+  // value field of the lane (value-MFMA row l16): VFB bits from bit l16 * VFB of the row
+  const int vbit = l16 * VFB;
+  const int vbase = (vbit >> 5) * 4;
+  const int vshift = vbit & 31;
 
   const int64_t g0 = bh * a.ldk;
   const uint8_t* pk = a.kcodes + g0 * KC;
@@ -586,12 +600,13 @@ decode_attn_i8_kernel(DecodeArgs a) {
   const uint32_t ring_lds = lds_offset(stage) + wave * SLOT;
   constexpr int NKD = (NK * KC + 1023) / 1024, NSD = (NK * SC + 1023) / 1024, NVD = (NK * VC + 1023) / 1024;
   constexpr int NDMA = NKD + NSD + NVD + 3;
+  // 16 bytes per lane and round; the plane sizes (256 to 1536 bytes) are multiples of 16
   auto copy_plane = [&](const i32x4& r, uint32_t dst, int bytes, int nrounds) {
     const uint32_t lo = lane * 16;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       if (c >= nrounds) break;
-      if ((c + 1) * 1024 <= bytes || lane < 32) dma16(r, dst + c * 1024, lo + c * 1024);
+      if ((c + 1) * 1024 <= bytes || lane * 16 < bytes - c * 1024) dma16(r, dst + c * 1024, lo + c * 1024);
     }
   };
   auto issue = [&](int kb, int slot) {
@@ -613,13 +628,15 @@ decode_attn_i8_kernel(DecodeArgs a) {
   };
   const int k0w = kbeg + wave * NK;
 #pragma unroll
-  for (int r = 0; r < R - 1; ++r)
+  for (int r = 0; r < R - NSTG; ++r)
     if (k0w + r * SLAB < kend) issue(k0w + r * SLAB, r);
 
   PQ pq;
   pq.setup(a, b, hkv, stg, tid);
-  __syncthreads();  // fragments held (and tables built): the staging slot joins the ring
-  if (k0w + (R - 1) * SLAB < kend) issue(k0w + (R - 1) * SLAB, R - 1);
+  __syncthreads();  // fragments held (and tables built): the staging slots join the ring
+#pragma unroll
+  for (int r = R - NSTG; r < R; ++r)
+    if (k0w + r * SLAB < kend) issue(k0w + r * SLAB, r);
 
   // column lg + 4g: reference mref = m - PUP (0 until the column has a maximum m) and the
   // threshold a score relative to mref must exceed to move it (-inf until then, TAU + PUP after)
@@ -639,8 +656,8 @@ decode_attn_i8_kernel(DecodeArgs a) {
   auto slab = [&](const uint8_t* src, int ks0) {
     // ---- scores of keys ks0 + 16j + l16 (j = 0, 1) for columns lg + 4g, log2 domain
     float sc[NCG][2], nv[2], t1[2][NCG], t2[2][NCG];
-    pq.dots2(src + OFF_K + l16 * KC + lg * KLANE, src + OFF_S + l16 * SC + lg * 4,
-             src + OFF_K + (16 + l16) * KC + lg * KLANE, src + OFF_S + (16 + l16) * SC + lg * 4, t1, t2);
+    pq.dots2(src + OFF_K + l16 * KC + lg * KLANE, src + OFF_S + l16 * SC + lg * SLANE,
+             src + OFF_K + (16 + l16) * KC + lg * KLANE, src + OFF_S + (16 + l16) * SC + lg * SLANE, t1, t2);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int row = 16 * j + l16;
@@ -770,9 +787,9 @@ decode_attn_i8_kernel(DecodeArgs a) {
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         if constexpr (VW32 == 2)
-          w[j][kk] = __builtin_amdgcn_alignbyte(r1[j][kk], r0[j][kk], vbyte);
+          w[j][kk] = __builtin_amdgcn_alignbit(r1[j][kk], r0[j][kk], vshift);
         else
-          w[j][kk] = r0[j][kk] >> (8 * vbyte);
+          w[j][kk] = r0[j][kk] >> vshift;
       }
 #pragma unroll
     for (int par = 0; par < 2; ++par) {
@@ -791,10 +808,10 @@ decode_attn_i8_kernel(DecodeArgs a) {
                                                value_pair<VB, i>(tV, f[1][0]), value_pair<VB, i>(tV, f[1][1])});
       };
       half8 va = look(std::integral_constant<int, 0>{});
-      static_for<4>([&](auto ic) {
+      static_for<NPAIR>([&](auto ic) {
         constexpr int i = decltype(ic)::value;
         half8 vn = va;
-        if constexpr (i + 1 < 4) vn = look(std::integral_constant<int, i + 1>{});
+        if constexpr (i + 1 < NPAIR) vn = look(std::integral_constant<int, i + 1>{});
         __builtin_amdgcn_sched_barrier(0);
         oacc[2 * i + par] = mfma16x16x32(va, pb, oacc[2 * i + par]);
         va = vn;
@@ -1211,21 +1228,31 @@ __global__ void __launch_bounds__(256) decode_merge_split_kernel(MergeArgs a) {
 
 // bit-plane kernel for 1- and 2-bit key codes and at most 8 columns (one or two groups of 4)
 static bool attn_planes(int bits, int C) { return bits <= 3 && C <= 8; }
-constexpr int kAttnPlaneRing = 2;
+// ring slots: head_dim 128 stages the query set-up in one slot, head_dim 64 (smaller slots)
+// in up to two
+template <int D>
+constexpr int attn_plane_ring() {
+  return D == 64 ? 3 : 2;
+}
 
-template <int KB, int NCG>
+template <int KB, int NCG, int D>
 static const void* attn_i8_kernel() {
-  return reinterpret_cast<const void*>(&decode_attn_i8_kernel<KB, kAttnPlaneRing, false, NCG>);
+  return reinterpret_cast<const void*>(&decode_attn_i8_kernel<KB, attn_plane_ring<D>(), false, NCG, D>);
 }
 
 // grid target of the fused decode attention: one round of resident blocks
-static int attn_target_blocks(int bits, int C) {
-  static int cache[7][16] = {};
+static int attn_target_blocks(int bits, int C, int d) {
+  static int cache[11][16] = {};
   if (attn_planes(bits, C)) {
     const bool two = C > 4;
-    const void* k = bits == 2 ? (two ? attn_i8_kernel<1, 2>() : attn_i8_kernel<1, 1>())
-                              : (two ? attn_i8_kernel<2, 2>() : attn_i8_kernel<2, 1>());
-    return resident_blocks(k, 256, cache[bits + 1 + (two ? 2 : 0)]);
+    const void* k;
+    if (d == 64)
+      k = bits == 2 ? (two ? attn_i8_kernel<1, 2, 64>() : attn_i8_kernel<1, 1, 64>())
+                    : (two ? attn_i8_kernel<2, 2, 64>() : attn_i8_kernel<2, 1, 64>());
+    else
+      k = bits == 2 ? (two ? attn_i8_kernel<1, 2, 128>() : attn_i8_kernel<1, 1, 128>())
+                    : (two ? attn_i8_kernel<2, 2, 128>() : attn_i8_kernel<2, 1, 128>());
+    return resident_blocks(k, 256, cache[bits + 1 + (two ? 2 : 0) + (d == 64 ? 4 : 0)]);
   }
   const void* k = bits == 2 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 2, kAttnNbs, kAttnRing, true>)
                 : bits == 3 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 3, kAttnNbs, kAttnRing, true>)
@@ -1237,7 +1264,7 @@ static DecodePlan plan_decode(int B, int Hq, int Hkv, int Sq, int Sk, int d, int
   if (!decode_shape(Hq, Hkv, Sq, Sk, d, bits)) return DecodePlan{false, 0, 0, 0};
   constexpr int slab = 64 * kAttnNbs;  // 4 waves x 32 keys for both kernels
   const int C = (Hq / Hkv) * Sq;
-  DecodePlan p = plan_split(B, Hkv, Sk, attn_target_blocks(bits, C), slab, 2 * slab);
+  DecodePlan p = plan_split(B, Hkv, Sk, attn_target_blocks(bits, C, d), slab, 2 * slab);
   p.ws_bytes = static_cast<int64_t>(B) * Hkv * p.nsplit * C * static_cast<int64_t>(d + 2) * 4;
   return p;
 }
@@ -1257,21 +1284,23 @@ bool decode_applies(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
   return plan_decode(B, Hq, Hkv, Sq, Sk, d, bits).use;
 }
 
-template <int BITS>
+template <int BITS, int D>
 static void launch_decode_attn(const DecodeArgs& a, hipStream_t s) {
   dim3 grid(a.nsplit, a.Hkv, a.B);
   if constexpr (BITS <= 3) {
     if (attn_planes(BITS, a.C)) {
+      constexpr int R = attn_plane_ring<D>();
       if (a.C > 4) {
-        if (a.mask) decode_attn_i8_kernel<BITS - 1, kAttnPlaneRing, true, 2><<<grid, 256, 0, s>>>(a);
-        else decode_attn_i8_kernel<BITS - 1, kAttnPlaneRing, false, 2><<<grid, 256, 0, s>>>(a);
+        if (a.mask) decode_attn_i8_kernel<BITS - 1, R, true, 2, D><<<grid, 256, 0, s>>>(a);
+        else decode_attn_i8_kernel<BITS - 1, R, false, 2, D><<<grid, 256, 0, s>>>(a);
       } else {
-        if (a.mask) decode_attn_i8_kernel<BITS - 1, kAttnPlaneRing, true, 1><<<grid, 256, 0, s>>>(a);
-        else decode_attn_i8_kernel<BITS - 1, kAttnPlaneRing, false, 1><<<grid, 256, 0, s>>>(a);
+        if (a.mask) decode_attn_i8_kernel<BITS - 1, R, true, 1, D><<<grid, 256, 0, s>>>(a);
+        else decode_attn_i8_kernel<BITS - 1, R, false, 1, D><<<grid, 256, 0, s>>>(a);
       }
       return;
     }
   }
+  if constexpr (D == 64) return;  // not planned: head_dim 64 takes the bit-plane kernels only
   if (a.C <= 8) decode_attn_lds_kernel<128, BITS, kAttnNbs, kAttnRing, true><<<grid, 256, 0, s>>>(a);
   else decode_attn_lds_kernel<128, BITS, kAttnNbs, kAttnRing, false><<<grid, 256, 0, s>>>(a);
 }
@@ -1317,9 +1346,18 @@ int decode_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, co
   const int64_t n_part = static_cast<int64_t>(B) * Hkv * p.nsplit * a.C;
   a.part_o = ws;
   a.part_ml = ws + n_part * d;
-  if (bits == 2) launch_decode_attn<2>(a, s);
-  else if (bits == 3) launch_decode_attn<3>(a, s);
-  else launch_decode_attn<4>(a, s);
+  if (d == 64) {
+    if (bits == 2) launch_decode_attn<2, 64>(a, s);
+    else launch_decode_attn<3, 64>(a, s);
+    const int st = launch_status("tq_attention_fwd (decode)");
+    if (st != TQ_OK) return st;
+    // partial rows of 64 floats: the split merge of any head dim (tq_attn.hip)
+    return merge_key_splits(a.part_o, a.part_ml, vpit, B, Hq, Hkv, Sq, a.C, p.nsplit, d, out, out_dtype, sob,
+                            soh, sos, s);
+  }
+  if (bits == 2) launch_decode_attn<2, 128>(a, s);
+  else if (bits == 3) launch_decode_attn<3, 128>(a, s);
+  else launch_decode_attn<4, 128>(a, s);
   int st = launch_status("tq_attention_fwd (decode)");
   if (st != TQ_OK) return st;
   MergeArgs m{};

@@ -228,7 +228,7 @@ int decode_scores(int64_t ldk, const uint16_t* q_rot, const float* q_proj, const
   a.scores = out;
   dim3 grid(a.nsplit, a.Hkv, a.B);
   if (bits <= 3 && a.C <= 8) {
-    launch_scores_planes(a, bits, s);  // tq_decode.hip
+    launch_scores_planes(a, bits, d, s);  // tq_decode.hip
     return launch_status("tq_attention_scores (decode, bit planes)");
   }
   if (a.C <= 8) {
