@@ -240,6 +240,37 @@ def test_reference_kernel_api_gpu_matches_cpu():
     assert (gpu.cpu() - cpu).abs().max().item() < 3e-2
 
 
+@pytest.mark.parametrize("d,m,per_head", [(128, 64, False), (128, 96, True), (128, 200, False),
+                                          (128, 256, False), (64, 100, True), (64, 20, False)])
+def test_reference_kernel_api_gpu_non_square_qjl(d, m, per_head):
+    """kernels.asymmetric_attention_scores on GPU with a QJL matrix of m != d rows (reference
+    attention.py:274-300 takes qjl_matrix [m, d] and m-bit sign rows), against the float64
+    oracle estimator on the same packed planes."""
+    _case(what="kernel api, non-square QJL", d=d, m=m, per_head=per_head)
+    rng = np.random.default_rng(d + m)
+    B, H, Sq, Sk, bits = 2, 4, 3, 300, 3
+    codes = rng.integers(0, 4, (B * H * Sk, d))
+    sb = rng.integers(0, 2, (B * H * Sk, m))
+    base = np.array([-0.2, -0.07, 0.07, 0.2])
+    cent = np.stack([base * (1.0 + 0.1 * h if per_head else 1.0) for h in range(H)]).astype(np.float16)
+    q = rng.standard_normal((B, H, Sq, d)).astype(np.float16)
+    s_eff = rng.standard_normal((m, d)).astype(np.float16)
+    rn = rng.random((B, H, Sk)).astype(np.float16)
+    vn = (rng.random((B, H, Sk)) * 8).astype(np.float16)
+    coeff = O.COEFF(d)
+    got = _np(asymmetric_attention_scores(
+        torch.from_numpy(q).to(DEV), torch.from_numpy(O.pack_bits(codes, 2)).view(B, H, Sk, -1).to(DEV),
+        torch.from_numpy(O.pack_bits(sb, 1)).view(B, H, Sk, -1).to(DEV), torch.from_numpy(rn).to(DEV),
+        torch.from_numpy(cent).to(DEV), torch.from_numpy(s_eff).to(DEV), torch.from_numpy(vn).to(DEV), bits, coeff))
+    assert got.shape == (B, H, Sq, Sk)
+    for bh in range(B * H):
+        b_, h_ = divmod(bh, H)
+        qp = q[b_, h_].astype(np.float64) @ s_eff.astype(np.float64).T
+        ref = O.scores_packed(q[b_, h_], qp, codes[bh * Sk:(bh + 1) * Sk], sb[bh * Sk:(bh + 1) * Sk],
+                              rn[b_, h_], vn[b_, h_], cent[h_], coeff)
+        assert O.rel_err(got[b_, h_], ref) < REL, (bh, O.rel_err(got[b_, h_], ref))
+
+
 # ---------------------------------------------------------------- fused attention
 
 def _oracle_attention(kc, vc, q, ck, cv, hq, hkv, mask=None, causal=False):

@@ -1072,8 +1072,11 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeArgs a) {
 // the waves' partial sums cross a second barrier before the Pi_v product.
 template <int D>
 __global__ void __launch_bounds__(256) decode_merge_split_kernel(MergeArgs a) {
-  static_assert(D == 128, "merge is built for head_dim 128");
-  constexpr int NB = 16;  // splits per wave per load batch
+  static_assert(D == 64 || D == 128, "merge is built for head_dim 64 or 128");
+  constexpr int NB = 16;       // splits per wave per load batch
+  constexpr int PL = D / 64;   // dims per lane in the combine
+  constexpr int RB = D / 64;   // 16-row output blocks per wave
+  typedef float floatPL __attribute__((ext_vector_type(PL)));
   __shared__ float s_m[4], s_l[4];
   __shared__ __attribute__((aligned(16))) float s_o[4][D];
   const int c = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
@@ -1081,13 +1084,14 @@ __global__ void __launch_bounds__(256) decode_merge_split_kernel(MergeArgs a) {
   const int C = a.C, ns = a.nsplit;
   const int64_t base = (static_cast<int64_t>(b) * a.Hkv + hkv) * ns;  // first split record
 
-  // ---- Pi_v^T fragments of this wave's output rows 32w .. 32w+31 (in flight meanwhile)
+  // ---- Pi_v^T fragments of this wave's output rows (D / 4) w .. (D / 4) w + D / 4 - 1 (in
+  // flight meanwhile)
   const _Float16* Ph = reinterpret_cast<const _Float16*>(a.vpit);
   const _Float16* Pl = Ph + D * D;
-  half8 ah[2][D / 32], al[2][D / 32];
+  half8 ah[RB][D / 32], al[RB][D / 32];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int i = wave * 32 + rb * 16 + l16;
+  for (int rb = 0; rb < RB; ++rb) {
+    const int i = wave * (D / 4) + rb * 16 + l16;
 #pragma unroll
     for (int ks = 0; ks < D / 32; ++ks) {
       ah[rb][ks] = *reinterpret_cast<const half8*>(Ph + i * D + ks * 32 + lg * 8);
@@ -1099,11 +1103,12 @@ __global__ void __launch_bounds__(256) decode_merge_split_kernel(MergeArgs a) {
   const int nw = ns > wave ? (ns - wave + 3) / 4 : 0;
   const int64_t ostep = 4 * static_cast<int64_t>(C) * D;  // floats between the wave's splits
   const int64_t mstep = 4 * 2 * static_cast<int64_t>(C);
-  const float* src0 = a.part_o + ((base + wave) * C + c) * D + 2 * lane;
+  const float* src0 = a.part_o + ((base + wave) * C + c) * D + PL * lane;
   const float* ml0 = a.part_ml + ((base + wave) * C + c) * 2;
-  float2 v0[NB];
+  auto load = [&](int64_t off) { return *reinterpret_cast<const floatPL*>(src0 + off); };
+  floatPL v0[NB];
 #pragma unroll
-  for (int u = 0; u < NB; ++u) v0[u] = u < nw ? *reinterpret_cast<const float2*>(src0 + u * ostep) : float2{0.f, 0.f};
+  for (int u = 0; u < NB; ++u) v0[u] = u < nw ? load(u * ostep) : floatPL{};
   const float m_first = lane < nw ? ml0[lane * mstep] : -INFINITY;
   const float l_first = lane < nw ? ml0[lane * mstep + 1] : 0.f;
   float mx = m_first;
@@ -1116,7 +1121,8 @@ __global__ void __launch_bounds__(256) decode_merge_split_kernel(MergeArgs a) {
 
   // ---- o_w = sum_u wt_u o_u, l_w = sum_u wt_u l_u, wt_u = 2^(m_u - M); lane u holds wt_u of
   // its batch of 64 and every lane reads it back with v_readlane
-  float o0 = 0.f, o1 = 0.f, lsum = 0.f;
+  floatPL o = floatPL{};
+  float lsum = 0.f;
   for (int s0 = 0; s0 < nw; s0 += 64) {
     const int u = s0 + lane;
     float w = 0.f;
@@ -1132,27 +1138,26 @@ __global__ void __launch_bounds__(256) decode_merge_split_kernel(MergeArgs a) {
 #pragma unroll
       for (int uu = 0; uu < NB; ++uu) {
         const float ww = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), uu));
-        o0 = fmaf(ww, v0[uu].x, o0);
-        o1 = fmaf(ww, v0[uu].y, o1);
+#pragma unroll
+        for (int e = 0; e < PL; ++e) o[e] = fmaf(ww, v0[uu][e], o[e]);
       }
       k = NB;
     }
     for (; k < nb; k += NB) {
-      float2 v[NB];
+      floatPL v[NB];
 #pragma unroll
-      for (int uu = 0; uu < NB; ++uu)
-        v[uu] = k + uu < nb ? *reinterpret_cast<const float2*>(src0 + (s0 + k + uu) * ostep) : float2{0.f, 0.f};
+      for (int uu = 0; uu < NB; ++uu) v[uu] = k + uu < nb ? load((s0 + k + uu) * ostep) : floatPL{};
 #pragma unroll
       for (int uu = 0; uu < NB; ++uu) {
         const float ww = k + uu < 64 ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), k + uu)) : 0.f;
-        o0 = fmaf(ww, v[uu].x, o0);
-        o1 = fmaf(ww, v[uu].y, o1);
+#pragma unroll
+        for (int e = 0; e < PL; ++e) o[e] = fmaf(ww, v[uu][e], o[e]);
       }
     }
   }
 #pragma unroll
   for (int sh = 32; sh >= 1; sh >>= 1) lsum += __shfl_xor(lsum, sh, 64);
-  *reinterpret_cast<float2*>(&s_o[wave][2 * lane]) = float2{o0, o1};
+  *reinterpret_cast<floatPL*>(&s_o[wave][PL * lane]) = o;
   if (lane == 0) s_l[wave] = lsum;
   __syncthreads();
 
@@ -1200,11 +1205,11 @@ __global__ void __launch_bounds__(256) decode_merge_split_kernel(MergeArgs a) {
       bl[ks][e] = lo;
     }
   }
-  // ---- out[i] = sum_j Pi_v^T[i][j] o[j]; wave w owns output rows 32w .. 32w+31
+  // ---- out[i] = sum_j Pi_v^T[i][j] o[j]; wave w owns output rows (D / 4) w .. (D / 4) w + D / 4 - 1
   const int qi = c / a.G, h = hkv * a.G + c % a.G;
   const float down = kUnsplit2 / up;  // 1/(kSplit * up) * (1/kSplit) for Pi_v^T's scale
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
+  for (int rb = 0; rb < RB; ++rb) {
     float4v f = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < D / 32; ++ks) {
@@ -1214,7 +1219,7 @@ __global__ void __launch_bounds__(256) decode_merge_split_kernel(MergeArgs a) {
     }
     if (l16 == 0) {
       const int64_t off = static_cast<int64_t>(b) * a.sob + static_cast<int64_t>(h) * a.soh +
-                          static_cast<int64_t>(qi) * a.sos + wave * 32 + rb * 16 + lg * 4;
+                          static_cast<int64_t>(qi) * a.sos + wave * (D / 4) + rb * 16 + lg * 4;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float v = f[e] * (down * kSplit);
@@ -1349,17 +1354,18 @@ int decode_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, co
   if (d == 64) {
     if (bits == 2) launch_decode_attn<2, 64>(a, s);
     else launch_decode_attn<3, 64>(a, s);
-    const int st = launch_status("tq_attention_fwd (decode)");
-    if (st != TQ_OK) return st;
-    // partial rows of 64 floats: the split merge of any head dim (tq_attn.hip)
-    return merge_key_splits(a.part_o, a.part_ml, vpit, B, Hq, Hkv, Sq, a.C, p.nsplit, d, out, out_dtype, sob,
-                            soh, sos, s);
+  } else {
+    if (bits == 2) launch_decode_attn<2, 128>(a, s);
+    else if (bits == 3) launch_decode_attn<3, 128>(a, s);
+    else launch_decode_attn<4, 128>(a, s);
   }
-  if (bits == 2) launch_decode_attn<2, 128>(a, s);
-  else if (bits == 3) launch_decode_attn<3, 128>(a, s);
-  else launch_decode_attn<4, 128>(a, s);
   int st = launch_status("tq_attention_fwd (decode)");
   if (st != TQ_OK) return st;
+  // head_dim 64, few splits: the split merge of any head dim (tq_attn.hip: a wave per column,
+  // partial rows of 64 floats)
+  if (d == 64 && p.nsplit <= kMergeSplitsPerWave)
+    return merge_key_splits(a.part_o, a.part_ml, vpit, B, Hq, Hkv, Sq, a.C, p.nsplit, d, out, out_dtype, sob, soh,
+                            sos, s);
   MergeArgs m{};
   m.part_o = a.part_o;
   m.part_ml = a.part_ml;
@@ -1377,7 +1383,8 @@ int decode_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, co
   m.soh = soh;
   m.sos = sos;
   if (p.nsplit > kMergeSplitsPerWave) {
-    decode_merge_split_kernel<128><<<dim3(a.C, Hkv, B), 256, 0, s>>>(m);
+    if (d == 64) decode_merge_split_kernel<64><<<dim3(a.C, Hkv, B), 256, 0, s>>>(m);
+    else decode_merge_split_kernel<128><<<dim3(a.C, Hkv, B), 256, 0, s>>>(m);
   } else {
     decode_merge_kernel<128><<<dim3(Hkv, B, (a.C + 3) / 4), 256, 0, s>>>(m);
   }

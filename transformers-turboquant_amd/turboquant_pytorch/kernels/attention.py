@@ -63,12 +63,9 @@ def asymmetric_attention_scores(query: torch.Tensor, packed_key_indices: torch.T
     m = qjl_matrix.shape[0]
     b_eff = b - 1
     if query.device.type == "cuda":
-        if m != d:
-            raise ValueError(f"GPU scores need a square QJL matrix (m == d); got m={m}, d={d}")
         dev = query.device
         q16 = query.to(torch.float16).contiguous()
         s_eff = qjl_matrix.to(dev, torch.float16).contiguous()
-        q_proj = project_queries(q16, s_eff)
         codes = packed_key_indices.to(dev).contiguous()
         signs = packed_qjl_signs.to(dev).contiguous()
         rn = residual_norms.to(dev, torch.float16).contiguous()
@@ -76,15 +73,38 @@ def asymmetric_attention_scores(query: torch.Tensor, packed_key_indices: torch.T
         cent = centroids.to(dev, torch.float16)
         if cent.dim() == 1:
             cent = cent.unsqueeze(0).expand(H, -1)
+        if m != d and signs.shape[-1] != (m + 7) // 8:
+            raise ValueError(f"packed_qjl_signs hold {signs.shape[-1]} bytes per key; m={m} needs {(m + 7) // 8}")
+        # the kernels take a sign plane of d bits against a q_proj of d values; a QJL matrix of
+        # m != d rows is scored as ceil(m / d) blocks of d rows (the last one zero-padded: a zero
+        # q_proj value adds nothing for any sign bit), the first block with the codebook and the
+        # others with a zero codebook (their term 1 is exactly 0), summed in f32
+        blocks = []
+        for r0 in range(0, m, d):
+            rows = min(d, m - r0)
+            s_blk = s_eff[r0:r0 + rows]
+            sg = signs if m == d else signs[..., r0 // 8:(r0 + rows + 7) // 8]
+            if rows < d:
+                s_blk = torch.nn.functional.pad(s_blk, (0, 0, 0, d - rows))
+                # bits past row m of the last byte meet zero q_proj values
+                sg = torch.nn.functional.pad(sg, (0, d // 8 - sg.shape[-1]))
+            blocks.append((project_queries(q16, s_blk.contiguous()), sg.contiguous(), r0 == 0))
+
+        def score(cent_row, sl):
+            out = None
+            for q_proj, sg, first in blocks:
+                c = cent_row if first else torch.zeros_like(cent_row)
+                sc = scores_from_prepared(q16[:, sl].contiguous(), q_proj[:, sl].contiguous(),
+                                          codes[:, sl].contiguous(), sg[:, sl].contiguous(),
+                                          rn[:, sl].contiguous(), vn[:, sl].contiguous(), c, b, coeff,
+                                          sl.stop - sl.start)
+                out = sc if out is None else out.add_(sc)
+            return out
+
         if bool((cent == cent[:1]).all()):
-            return scores_from_prepared(q16, q_proj, codes, signs, rn, vn, cent[0].contiguous(), b,
-                                        coeff, H)
+            return score(cent[0].contiguous(), slice(0, H))
         # per-head codebooks: one launch per head
-        outs = [scores_from_prepared(q16[:, h:h + 1].contiguous(), q_proj[:, h:h + 1].contiguous(),
-                                     codes[:, h:h + 1].contiguous(), signs[:, h:h + 1].contiguous(),
-                                     rn[:, h:h + 1].contiguous(), vn[:, h:h + 1].contiguous(),
-                                     cent[h].contiguous(), b, coeff, 1) for h in range(H)]
-        return torch.cat(outs, dim=1)
+        return torch.cat([score(cent[h].contiguous(), slice(h, h + 1)) for h in range(H)], dim=1)
 
     # CPU tensors: the same estimator in f32 from the f16 inputs
     idx = unpack_bits(packed_key_indices.reshape(B * H * Sk, -1), b_eff, d).reshape(B, H, Sk, d)
