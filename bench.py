@@ -148,7 +148,7 @@ def pmc_summary(paths: list[str], copy_mib: int) -> dict:
         fetch, write = mean[kf], mean[kw]
         kernels[name] = {"grid_size": kf[1], "dispatches": count[kf], "fetch_kib": fetch, "write_kib": write,
                          "traffic_bytes": int(round((fetch * cal["FETCH_SIZE"] + write * cal["WRITE_SIZE"]) * 1024))}
-    a, m = "tq::decode_attn_i8_kernel<2, 2, false, 1>", "tq::decode_merge_kernel<128>"
+    a, m = "tq::decode_attn_i8_kernel<2, 2, false, 1, 128>", "tq::decode_merge_kernel<128>"
     if a in kernels and m in kernels:
         kernels["decode_attention (attention + merge)"] = {
             "name": f"{a} + {m}", "traffic_bytes": kernels[a]["traffic_bytes"] + kernels[m]["traffic_bytes"]}
@@ -457,9 +457,9 @@ def decode_legs(kc, vc, outliers, steps: int, warmup: int) -> tuple[dict, dict]:
         "ms_per_launch": ms_scores,
         "key_heads_per_s": key_heads / (ms_scores * 1e-3),
         "roofline": {
-            "kernel": "tq::decode_scores_i8_kernel<2, 3, 1> (scores, f32 written)",
+            "kernel": "tq::decode_scores_i8_kernel<2, 3, 1, 128> (scores, f32 written)",
             "bound": "hbm", "achieved": gbs_s, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": gbs_s / HBM_PEAK_GBS, "traffic": measured_traffic("tq::decode_scores_i8_kernel<2, 3, 1>"),
+            "frac": gbs_s / HBM_PEAK_GBS, "traffic": measured_traffic("tq::decode_scores_i8_kernel<2, 3, 1, 128>"),
             "algorithmic_bytes_per_launch": score_bytes,
         },
         "api_step": {
@@ -476,7 +476,7 @@ def decode_legs(kc, vc, outliers, steps: int, warmup: int) -> tuple[dict, dict]:
         "ms_per_launch": ms_attn,
         "key_heads_per_s": key_heads / (ms_attn * 1e-3),
         "roofline": {
-            "kernel": "tq::decode_attn_i8_kernel<2, 2, false, 1> + tq::decode_merge_kernel<128>",
+            "kernel": "tq::decode_attn_i8_kernel<2, 2, false, 1, 128> + tq::decode_merge_kernel<128>",
             "bound": "hbm", "achieved": gbs_a, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": gbs_a / HBM_PEAK_GBS, "traffic": measured_traffic("decode_attention (attention + merge)"),
             "algorithmic_bytes_per_launch": attn_bytes,
