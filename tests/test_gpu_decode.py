@@ -337,7 +337,7 @@ def test_decode_two_column_groups_scores_and_attention(bits, hq, hkv, sq, sk, ca
     assert err < REL and O.cosine(got, ref) > 0.9999
 
 
-@pytest.mark.parametrize("bits", [2, 3])
+@pytest.mark.parametrize("bits", [2, 3, 4])
 @pytest.mark.parametrize("hq,hkv,sq,sk,causal,masked", [
     (32, 8, 1, 4097, False, False),   # 4 columns per kv head (a 32/8-head model)
     (12, 12, 1, 3000, False, False),  # one column per kv head (multi-head attention)
@@ -347,11 +347,15 @@ def test_decode_two_column_groups_scores_and_attention(bits, hq, hkv, sq, sk, ca
     (4, 1, 1, 1, False, False),       # a single key
     (6, 2, 1, 65, True, False),       # 3 columns, one partial slab
     (7, 1, 1, 9000, False, True),     # 7 columns, padding mask
+    (16, 1, 1, 3000, False, False),   # 16 columns: the table kernels at every width
+    (6, 2, 4, 1500, True, False),     # 12 columns from 3 heads x 4 rows, causal
+    (24, 2, 1, 20000, True, True),    # 12 columns, 79 splits, padding mask
 ])
 def test_decode_head_dim64_scores_and_attention(bits, hq, hkv, sq, sk, causal, masked):
-    """The bit-plane decode kernels at head_dim 64 (16-dim lane groups: 2-byte sign and 1-bit
-    code fields, 4 value dims per lane), scores and fused attention against the float64
-    oracle, and the tiled kernel on the same inputs."""
+    """The decode kernels at head_dim 64: the bit-plane kernels (bits 2-3, at most 8 columns;
+    16-dim lane groups: 2-byte sign and 1-bit code fields, 4 value dims per lane) and the
+    table kernels (bits 4, or 9-16 columns; 6-byte code fields at bits 4), scores and fused
+    attention against the float64 oracle, and the tiled kernel on the same inputs."""
     _case(what="decode d64", bits=bits, hq=hq, hkv=hkv, sq=sq, sk=sk, causal=causal, masked=masked)
     B, d = 2, 64
     assert _on_decode_path(B, hq, hkv, sq, sk, bits, d)

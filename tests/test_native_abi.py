@@ -47,8 +47,8 @@ def test_argument_validation_without_gpu():
     assert lib.tq_attention_fwd(*([None] * 7), 5, None, None, None, 3, None, 1, 8, 8, 1, 1, 128, 0.0, 1.0, 0,
                                 None, 0, 0, 0, 0, None, 0, 0, 0, 0, None, 0, None) == -1
     assert b"key bits" in lib.tq_last_error()
-    # split-K workspace: the decode kernels' partials (head_dim 128 with <= 16 columns per kv
-    # head, head_dim 64 with bits 2-3 and <= 8 columns), or the tiled kernel split over keys (any head dim, the kv head's columns in one query
+    # split-K workspace: the decode kernels' partials (head_dim 64 / 128, <= 16 columns per kv
+    # head), or the tiled kernel split over keys (any head dim, the kv head's columns in one query
     # block, at least 512 keys): B * Hkv * splits * columns * (row floats + 2) * 4 bytes, with
     # about 512 blocks of >= 256 keys (whole 32-key tiles) and rows of 64 / 128 / 256 floats
     assert lib.tq_attention_workspace_size(4, 32, 8, 1, 32768, 128, 3) > 0
@@ -62,8 +62,9 @@ def test_argument_validation_without_gpu():
         return groups * ns * (Hq // Hkv) * Sq * (rowf + 2) * 4
 
     assert lib.tq_attention_workspace_size(4, 32, 8, 8, 32768, 128, 3) == tiled(4, 32, 8, 8, 32768, 128)
-    assert lib.tq_attention_workspace_size(4, 32, 8, 3, 32768, 64, 3) == tiled(4, 32, 8, 3, 32768, 64)
-    assert lib.tq_attention_workspace_size(4, 32, 8, 1, 32768, 64, 4) == tiled(4, 32, 8, 1, 32768, 64)
+    assert lib.tq_attention_workspace_size(4, 32, 8, 1, 32768, 96, 3) == tiled(4, 32, 8, 1, 32768, 96)
+    assert lib.tq_attention_workspace_size(4, 32, 8, 5, 32768, 64, 3) == tiled(4, 32, 8, 5, 32768, 64)
+    assert lib.tq_attention_workspace_size(4, 32, 8, 3, 32768, 64, 4) >= tiled(4, 32, 8, 3, 32768, 64)
     assert lib.tq_attention_workspace_size(4, 32, 8, 1, 32768, 64, 3) >= tiled(4, 32, 8, 1, 32768, 64)
     assert lib.tq_attention_workspace_size(1, 12, 12, 1, 5000, 96, 2) == tiled(1, 12, 12, 1, 5000, 96)
     assert lib.tq_attention_workspace_size(2, 8, 2, 1, 400, 96, 3) == 0       # too few keys to split

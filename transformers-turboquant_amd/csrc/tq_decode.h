@@ -150,7 +150,36 @@ __device__ __forceinline__ void build_small_luts(const DecodeArgs& a, uint8_t* t
   }
 }
 
-// Key operand of k-step KS: dims KS*8 .. KS*8+7 of the lane's 32-dim field
+// A lane group's quarter of a packed key row (KLANE = D * KB / 32 bytes from byte
+// lg * KLANE) as dwords, LSB first.  Head_dim 64 gives fields that are not dword multiples
+// (2 bytes at 1 code bit, 6 at 3 bits), read as 2-byte pieces: their rows are only 2-byte
+// aligned.
+template <int KLANE>
+__device__ __forceinline__ void load_key_field(const uint8_t* kp, uint32_t (&kw)[(KLANE + 3) / 4]) {
+  if constexpr (KLANE == 2) {
+    kw[0] = *reinterpret_cast<const uint16_t*>(kp);
+  } else if constexpr (KLANE == 6) {
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(kp);
+    kw[0] = static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16);
+    kw[1] = h[2];
+  } else if constexpr (KLANE == 8) {
+    const u32x2 t = *reinterpret_cast<const u32x2*>(kp);
+    kw[0] = t[0];
+    kw[1] = t[1];
+  } else {
+    static_assert(KLANE % 4 == 0, "dword fields");
+#pragma unroll
+    for (int w = 0; w < KLANE / 4; ++w) kw[w] = reinterpret_cast<const uint32_t*>(kp)[w];
+  }
+}
+// a lane group's sign bits (D / 4 of them, from byte lg * D / 32 of the sign row)
+template <int D>
+__device__ __forceinline__ uint32_t load_sign_field(const uint8_t* sp) {
+  if constexpr (D == 64) return *reinterpret_cast<const uint16_t*>(sp);
+  else return *reinterpret_cast<const uint32_t*>(sp);
+}
+
+// Key operand of k-step KS: dims KS*8 .. KS*8+7 of the lane's field (D / 4 dims)
 template <int KB, int KW32, int KS>
 __device__ __forceinline__ half8 key_operand(const uint8_t* t, const uint32_t (&k)[KW32]) {
   if constexpr (KB == 1) {
@@ -528,18 +557,11 @@ inline DecodePlan plan_split(int B, int Hkv, int Sk, int target, int quantum, in
   return p;
 }
 
-// head_dim 128 with bits 2-4 and at most 16 query columns per kv head, or head_dim 64 with
-// bits 2-3 and at most 8; S_k below 2^24 keeps every per-group byte offset of the planes and
-// score rows under 2^31
+// head_dim 64 or 128, bits 2-4, at most 16 query columns per kv head; S_k below 2^24
+// keeps every per-group byte offset of the planes and score rows under 2^31
 inline bool decode_shape(int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
-  if (bits < 2 || bits > 4 || Hkv <= 0 || Hq % Hkv) return false;
-  const int C = (Hq / Hkv) * Sq;
-  if (d == 64) {
-    if (bits > 3 || C > 8) return false;  // head_dim 64: the bit-plane kernels only
-  } else if (d != 128) {
-    return false;
-  }
-  return C <= 16 && Sk >= 1 && Sk < (1 << 24);
+  if ((d != 64 && d != 128) || bits < 2 || bits > 4 || Hkv <= 0 || Hq % Hkv) return false;
+  return (Hq / Hkv) * Sq <= 16 && Sk >= 1 && Sk < (1 << 24);
 }
 
 }  // namespace tq

@@ -14,14 +14,17 @@ namespace tq {
 template <int D, int BITS, int NBS, int R, bool PACK>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PACK ? 4 : 3)))
 decode_attn_lds_kernel(DecodeArgs a) {
-  static_assert(D == 128, "decode kernel is built for head_dim 128");
+  static_assert(D == 64 || D == 128, "decode kernel is built for head_dim 64 or 128");
   using L = SmallLuts<BITS>;
   constexpr int KB = L::KB, VB = L::VB;
   constexpr int KS = D / 32;           // score k-steps
-  constexpr int DB = D / 16;           // value row blocks
+  constexpr int DB = D / 16;           // value row blocks: lane l16 holds dims DB l16 .. DB l16 + DB - 1
+  constexpr int NPAIR = D / 32;        // pair-table groups per parity
   constexpr int KC = D * KB / 8, SC = D / 8, VC = D * VB / 8;  // bytes per packed row
   constexpr int KLANE = KC / 4;        // key-code bytes per lane (4 lanes share a key row)
-  constexpr int KW32 = KLANE / 4;
+  constexpr int KW32 = (KLANE + 3) / 4;
+  constexpr int SLANE = SC / 4;        // sign bytes per lane
+  constexpr int VFB = DB * VB;         // value field bits of a lane
   constexpr int VW32 = (VB == 3) ? 2 : 1;  // dwords holding a lane's value field
   constexpr int NK = 16 * NBS;         // keys per wave slab
   constexpr int SLAB = 4 * NK;         // keys per block slab
@@ -89,12 +92,12 @@ decode_attn_lds_kernel(DecodeArgs a) {
   const int kbeg = split * a.chunk;
   const int kend = min(a.Sk, kbeg + a.chunk);
 
-  // this lane's value field: dims l16*8 .. l16*8+7 = VB bytes at byte voff of the row,
-  // read as the dword pair at vbase = voff & ~3 (the pair may run past the row end into
-  // the next row or the slot's norm area; those bytes are not used)
-  const int voff = l16 * VB;
-  const int vbase = voff & ~3;
-  const int vbyte = voff & 3;
+  // this lane's value field: VFB bits from bit l16 * VFB of the row, read as the dword (pair)
+  // from byte vbase (the pair may run past the row end into the next row or the slot's norm
+  // area; those bits are not used)
+  const int vbit = l16 * VFB;
+  const int vbase = (vbit >> 5) * 4;
+  const int vshift = vbit & 31;
 
   const int64_t g0 = bh * a.ldk;
   const uint8_t* pk = a.kcodes + g0 * KC;
@@ -108,14 +111,14 @@ decode_attn_lds_kernel(DecodeArgs a) {
   const uint32_t mine_lds = lds_offset(mine);
   constexpr int NKD = (NK * KC + 1023) / 1024, NSD = (NK * SC + 1023) / 1024, NVD = (NK * VC + 1023) / 1024;
   constexpr int NDMA = NKD + NSD + NVD + 3;  // DMA instructions per slot
-  // a plane of `bytes` (a multiple of 512) moves in 1 KB rounds of 64 lanes x 16 B;
-  // a final half round uses lanes 0-31 only
+  // a plane of `bytes` (a multiple of 16) moves in 1 KB rounds of 64 lanes x 16 B; a final
+  // partial round uses the lanes it needs
   auto copy_plane = [&](const i32x4& r, uint32_t dst, int bytes, int nrounds) {
     const uint32_t lo = lane * 16;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       if (c >= nrounds) break;
-      if ((c + 1) * 1024 <= bytes || lane < 32) dma16(r, dst + c * 1024, lo + c * 1024);
+      if ((c + 1) * 1024 <= bytes || lane * 16 < bytes - c * 1024) dma16(r, dst + c * 1024, lo + c * 1024);
     }
   };
   // DMA the wave's slab of keys [kb, kb + NK) into ring slot `slot`; rows past kend read zero
@@ -183,16 +186,8 @@ decode_attn_lds_kernel(DecodeArgs a) {
 #pragma unroll
     for (int j = 0; j < NBS; ++j) {
       uint32_t kw[KW32];
-      const uint8_t* kp = src + OFF_K + (16 * j + l16) * KC + lg * KLANE;
-      if constexpr (KW32 == 2) {
-        const u32x2 t = *reinterpret_cast<const u32x2*>(kp);
-        kw[0] = t[0];
-        kw[1] = t[1];
-      } else {
-#pragma unroll
-        for (int w = 0; w < KW32; ++w) kw[w] = reinterpret_cast<const uint32_t*>(kp)[w];
-      }
-      const uint32_t sw = *reinterpret_cast<const uint32_t*>(src + OFF_S + (16 * j + l16) * SC + lg * 4);
+      load_key_field<KLANE>(src + OFF_K + (16 * j + l16) * KC + lg * KLANE, kw);
+      const uint32_t sw = load_sign_field<D>(src + OFF_S + (16 * j + l16) * SC + lg * SLANE);
       s1[j] = float4v{0.f, 0.f, 0.f, 0.f};
       s2[j] = float4v{0.f, 0.f, 0.f, 0.f};
       static_for<KS>([&](auto cc) {
@@ -270,9 +265,9 @@ decode_attn_lds_kernel(DecodeArgs a) {
         for (int kk = 0; kk < 4; ++kk) {
           const uint32_t* vp = reinterpret_cast<const uint32_t*>(src + OFF_V + (16 * j + 4 * lg + kk) * VC + vbase);
           if constexpr (VW32 == 2)
-            w[h][kk] = __builtin_amdgcn_alignbyte(vp[1], vp[0], vbyte);
+            w[h][kk] = __builtin_amdgcn_alignbit(vp[1], vp[0], vshift);
           else
-            w[h][kk] = vp[0] >> (8 * vbyte);
+            w[h][kk] = vp[0] >> vshift;
         }
       }
       // parity 0: even dims (fields of key 2c, fields of key 2c + 1 shifted into the odd slots);
@@ -287,7 +282,7 @@ decode_attn_lds_kernel(DecodeArgs a) {
             const uint32_t wa = w[h][2 * c], wb = w[h][2 * c + 1];
             f[h][c] = par ? bfi32(M, wb, wa >> VB) : bfi32(M, wb << VB, wa);
           }
-        static_for<4>([&](auto ic) {
+        static_for<NPAIR>([&](auto ic) {
           constexpr int i = decltype(ic)::value;
           const int db = 2 * i + par;
           const half8 va = __builtin_bit_cast(half8, u32x4{value_pair<VB, i>(tV, f[0][0]), value_pair<VB, i>(tV, f[0][1]),
@@ -1247,7 +1242,7 @@ static const void* attn_i8_kernel() {
 
 // grid target of the fused decode attention: one round of resident blocks
 static int attn_target_blocks(int bits, int C, int d) {
-  static int cache[11][16] = {};
+  static int cache[14][16] = {};
   if (attn_planes(bits, C)) {
     const bool two = C > 4;
     const void* k;
@@ -1258,6 +1253,12 @@ static int attn_target_blocks(int bits, int C, int d) {
       k = bits == 2 ? (two ? attn_i8_kernel<1, 2, 128>() : attn_i8_kernel<1, 1, 128>())
                     : (two ? attn_i8_kernel<2, 2, 128>() : attn_i8_kernel<2, 1, 128>());
     return resident_blocks(k, 256, cache[bits + 1 + (two ? 2 : 0) + (d == 64 ? 4 : 0)]);
+  }
+  if (d == 64) {
+    const void* k = bits == 2 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<64, 2, kAttnNbs, kAttnRing, true>)
+                  : bits == 3 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<64, 3, kAttnNbs, kAttnRing, true>)
+                              : reinterpret_cast<const void*>(&decode_attn_lds_kernel<64, 4, kAttnNbs, kAttnRing, true>);
+    return resident_blocks(k, 256, cache[11 + bits - 2]);
   }
   const void* k = bits == 2 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 2, kAttnNbs, kAttnRing, true>)
                 : bits == 3 ? reinterpret_cast<const void*>(&decode_attn_lds_kernel<128, 3, kAttnNbs, kAttnRing, true>)
@@ -1305,9 +1306,8 @@ static void launch_decode_attn(const DecodeArgs& a, hipStream_t s) {
       return;
     }
   }
-  if constexpr (D == 64) return;  // not planned: head_dim 64 takes the bit-plane kernels only
-  if (a.C <= 8) decode_attn_lds_kernel<128, BITS, kAttnNbs, kAttnRing, true><<<grid, 256, 0, s>>>(a);
-  else decode_attn_lds_kernel<128, BITS, kAttnNbs, kAttnRing, false><<<grid, 256, 0, s>>>(a);
+  if (a.C <= 8) decode_attn_lds_kernel<D, BITS, kAttnNbs, kAttnRing, true><<<grid, 256, 0, s>>>(a);
+  else decode_attn_lds_kernel<D, BITS, kAttnNbs, kAttnRing, false><<<grid, 256, 0, s>>>(a);
 }
 
 int decode_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, const uint8_t* kcodes,
@@ -1353,7 +1353,8 @@ int decode_attention(int64_t ldk, const uint16_t* q_rot, const float* q_proj, co
   a.part_ml = ws + n_part * d;
   if (d == 64) {
     if (bits == 2) launch_decode_attn<2, 64>(a, s);
-    else launch_decode_attn<3, 64>(a, s);
+    else if (bits == 3) launch_decode_attn<3, 64>(a, s);
+    else launch_decode_attn<4, 64>(a, s);
   } else {
     if (bits == 2) launch_decode_attn<2, 128>(a, s);
     else if (bits == 3) launch_decode_attn<3, 128>(a, s);

@@ -15,7 +15,7 @@ namespace tq {
 // per-lane scalars and each column's 16 scores leave as one 64-byte run.
 template <int D, int BITS, int R, int NK, bool PACK>
 __global__ void __launch_bounds__(256) decode_scores_kernel(DecodeArgs a) {
-  static_assert(D == 128, "decode kernel is built for head_dim 128");
+  static_assert(D == 64 || D == 128, "decode kernel is built for head_dim 64 or 128");
   static_assert(R >= 2 && R <= 4, "ring of 2 to 4 slots");
   static_assert(NK == 32 || NK == 64, "slabs of 32 or 64 keys");
   using L = SmallLuts<BITS>;
@@ -23,7 +23,8 @@ __global__ void __launch_bounds__(256) decode_scores_kernel(DecodeArgs a) {
   constexpr int KS = D / 32;
   constexpr int KC = D * KB / 8, SC = D / 8;
   constexpr int KLANE = KC / 4;
-  constexpr int KW32 = KLANE / 4;
+  constexpr int KW32 = (KLANE + 3) / 4;
+  constexpr int SLANE = SC / 4;
   constexpr int NBS = NK / 16;
   constexpr int SLAB = 4 * NK;           // keys per block slab
   constexpr int OFF_K = 0, OFF_S = NK * KC, OFF_N = OFF_S + NK * SC;
@@ -97,14 +98,14 @@ __global__ void __launch_bounds__(256) decode_scores_kernel(DecodeArgs a) {
   const uint32_t mine_lds = lds_offset(mine);
   constexpr int NKD = (NK * KC + 1023) / 1024, NSD = (NK * SC + 1023) / 1024;
   constexpr int NDMA = NKD + NSD + 2;  // DMA instructions per slot
-  // a plane of `bytes` (a multiple of 512) moves in 1 KB rounds of 64 lanes x 16 B;
-  // a final half round uses lanes 0-31 only
+  // a plane of `bytes` (a multiple of 16) moves in 1 KB rounds of 64 lanes x 16 B; a final
+  // partial round uses the lanes it needs
   auto copy_plane = [&](const i32x4& r, uint32_t dst, int bytes, int nrounds) {
     const uint32_t lo = lane * 16;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       if (c >= nrounds) break;
-      if ((c + 1) * 1024 <= bytes || lane < 32) dma16(r, dst + c * 1024, lo + c * 1024);
+      if ((c + 1) * 1024 <= bytes || lane * 16 < bytes - c * 1024) dma16(r, dst + c * 1024, lo + c * 1024);
     }
   };
   // DMA the wave's slab of keys [kb, kb + NK) into ring slot `slot`; rows past kend read zero
@@ -131,16 +132,8 @@ __global__ void __launch_bounds__(256) decode_scores_kernel(DecodeArgs a) {
 #pragma unroll
     for (int j = 0; j < NBS; ++j) {
       uint32_t kw[KW32];
-      const uint8_t* kp = src + OFF_K + (16 * j + l16) * KC + lg * KLANE;
-      if constexpr (KW32 == 2) {
-        const u32x2 t = *reinterpret_cast<const u32x2*>(kp);
-        kw[0] = t[0];
-        kw[1] = t[1];
-      } else {
-#pragma unroll
-        for (int w = 0; w < KW32; ++w) kw[w] = reinterpret_cast<const uint32_t*>(kp)[w];
-      }
-      const uint32_t sw = *reinterpret_cast<const uint32_t*>(src + OFF_S + (16 * j + l16) * SC + lg * 4);
+      load_key_field<KLANE>(src + OFF_K + (16 * j + l16) * KC + lg * KLANE, kw);
+      const uint32_t sw = load_sign_field<D>(src + OFF_S + (16 * j + l16) * SC + lg * SLANE);
       float4v s1 = float4v{0.f, 0.f, 0.f, 0.f}, s2 = float4v{0.f, 0.f, 0.f, 0.f};
       static_for<KS>([&](auto c) {
         constexpr int ks = decltype(c)::value;
@@ -189,6 +182,20 @@ __global__ void __launch_bounds__(256) decode_scores_kernel(DecodeArgs a) {
   }
 }
 
+template <int D>
+static void launch_scores_tables(const DecodeArgs& a, int bits, hipStream_t s) {
+  const dim3 grid(a.nsplit, a.Hkv, a.B);
+  if (a.C <= 8) {
+    if (bits == 2) decode_scores_kernel<D, 2, score_ring(2), score_slab_keys(2), true><<<grid, 256, 0, s>>>(a);
+    else if (bits == 3) decode_scores_kernel<D, 3, score_ring(3), score_slab_keys(3), true><<<grid, 256, 0, s>>>(a);
+    else decode_scores_kernel<D, 4, score_ring(4), score_slab_keys(4), true><<<grid, 256, 0, s>>>(a);
+  } else {
+    if (bits == 2) decode_scores_kernel<D, 2, score_ring(2), score_slab_keys(2), false><<<grid, 256, 0, s>>>(a);
+    else if (bits == 3) decode_scores_kernel<D, 3, score_ring(3), score_slab_keys(3), false><<<grid, 256, 0, s>>>(a);
+    else decode_scores_kernel<D, 4, score_ring(4), score_slab_keys(4), false><<<grid, 256, 0, s>>>(a);
+  }
+}
+
 static DecodePlan plan_scores(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) {
   if (!decode_shape(Hq, Hkv, Sq, Sk, d, bits)) return DecodePlan{false, 0, 0, 0};
   const int slab = 4 * score_slab_keys(bits);
@@ -226,20 +233,12 @@ int decode_scores(int64_t ldk, const uint16_t* q_rot, const float* q_proj, const
   a.coeff = coeff;
   a.scale = 1.f;
   a.scores = out;
-  dim3 grid(a.nsplit, a.Hkv, a.B);
   if (bits <= 3 && a.C <= 8) {
     launch_scores_planes(a, bits, d, s);  // tq_decode.hip
     return launch_status("tq_attention_scores (decode, bit planes)");
   }
-  if (a.C <= 8) {
-    if (bits == 2) decode_scores_kernel<128, 2, score_ring(2), score_slab_keys(2), true><<<grid, 256, 0, s>>>(a);
-    else if (bits == 3) decode_scores_kernel<128, 3, score_ring(3), score_slab_keys(3), true><<<grid, 256, 0, s>>>(a);
-    else decode_scores_kernel<128, 4, score_ring(4), score_slab_keys(4), true><<<grid, 256, 0, s>>>(a);
-  } else {
-    if (bits == 2) decode_scores_kernel<128, 2, score_ring(2), score_slab_keys(2), false><<<grid, 256, 0, s>>>(a);
-    else if (bits == 3) decode_scores_kernel<128, 3, score_ring(3), score_slab_keys(3), false><<<grid, 256, 0, s>>>(a);
-    else decode_scores_kernel<128, 4, score_ring(4), score_slab_keys(4), false><<<grid, 256, 0, s>>>(a);
-  }
+  if (d == 64) launch_scores_tables<64>(a, bits, s);
+  else launch_scores_tables<128>(a, bits, s);
   return launch_status("tq_attention_scores (decode)");
 }
 
