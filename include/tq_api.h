@@ -249,9 +249,8 @@ int tq_cache_append(const void* k, const void* v, int32_t dtype, int32_t B,
                     uint16_t* q_rot, float* q_proj, void* stream);
 
 /* Bytes of caller-provided device workspace tq_attention_fwd uses to split the keys of a
- * few-query shape: the split-K decode kernels (head_dim 128 with bits 2-4 and at most 16
- * (query row, query head) pairs per kv head, or head_dim 64 with bits 2-3 and at most 8;
- * value bits == key bits) or, for other
+ * few-query shape: the split-K decode kernels (head_dim 64 or 128, bits 2-4, at most 16
+ * (query row, query head) pairs per kv head, value bits == key bits) or, for other
  * few-query shapes whose kv head's columns fit one block (any head dim, other value
  * bits, larger groups) with at least 512 keys, the fused kernels split over keys plus a
  * merge; the larger of the two, 0 when neither applies.  With a smaller or NULL

@@ -1,6 +1,5 @@
-"""GPU parity of the split-K decode kernels (head_dim 128 with at most 16 query
-(row, head) columns per kv head; head_dim 64 with bits 2-3 and at most 8) against
-the CPU oracle and the tiled kernel.
+"""GPU parity of the split-K decode kernels (head_dim 64 / 128, at most 16 query
+(row, head) columns per kv head) against the CPU oracle and the tiled kernel.
 
 Same bars as the other kernel tests: scores and attention outputs within
 rel-err 1e-3 and cosine >= 0.9999 of the float64 oracle estimator evaluated on

@@ -1,5 +1,5 @@
-// Decode-shaped materialised scores (split-K over keys) through lookup tables, for bits 4
-// and 9-16 columns (the bit-plane kernel for bits 2-3 and at most 8 columns is in
+// Decode-shaped materialised scores (split-K over keys) through lookup tables, head_dim 64
+// and 128, for bits 4 and 9-16 columns (the bit-plane kernel for bits 2-3 and at most 8 columns is in
 // tq_decode.hip); the shared argument block, lookup tables and split planning are in
 // tq_decode.h.  Built without -amdgpu-mfma-vgpr-form: with MFMA accumulators in VGPRs the
 // compiler gave wrong scores from the second ring slot on when part of an accumulator is
