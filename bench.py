@@ -643,7 +643,8 @@ def head_dim64_leg(steps: int, warmup: int) -> dict:
     """The head_dim-64 path (GPT-2's attention, BASELINE.json configs[0]'s shape: 12 heads, bits 3)
     through the prefill kernel at head_dim 64: one layer's compress K / V + query prep + fused attention per step,
     at configs[0]'s 512 tokens and at 8192 tokens (causal), HIP events around the attention call
-    and around the whole step."""
+    and around the whole step; and one decode step's attention (one query row over 4k / 32k
+    cached keys) through the split-K decode kernel at head_dim 64."""
     import torch
 
     from turboquant_pytorch.compressors import TurboQuantCompressorMSE, TurboQuantCompressorV2
@@ -686,7 +687,7 @@ def head_dim64_leg(steps: int, warmup: int) -> dict:
         out[f"S{S_}"] = {"step_ms": step_ms, "attention_ms": attn_ms, "attention_tflops": tflops,
                          "mfma_frac": tflops / MFMA_F16_PEAK_TFLOPS}
     # one decode step's attention over a compressed cache at this head dim (one query row per
-    # sequence): the prefill kernel split over keys + merge
+    # sequence): the split-K decode kernel (bit planes) + merge
     for b_, sk in ((1, 4096), (1, 32768)):
         g = torch.Generator(device="cuda").manual_seed(sk)
         ck = kc.compress(torch.randn(b_, h, sk, d, device="cuda", generator=g).to(torch.bfloat16))
@@ -706,7 +707,8 @@ def head_dim64_leg(steps: int, warmup: int) -> dict:
         out[f"decode_B{b_}_S{sk}"] = {"attention_us": e0.elapsed_time(e1) / steps * 1e3}
     return {"workload": f"GPT-2 attention shape: B1 x {h} heads x d{d}, bits {BITS}, causal; "
                         "tq::prefill_kernel<64, 3, false> (q_proj as f16 hi + lo); decode steps (one query "
-                        "row over 4k / 32k cached keys) through the same kernel split over keys + merge",
+                        "row over 4k / 32k cached keys) through tq::decode_attn_i8_kernel<2, 3, false, 1, 64> "
+                        "+ merge",
             **out}
 
 
