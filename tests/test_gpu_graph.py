@@ -19,10 +19,10 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-@pytest.mark.parametrize("sk", [700, 5000])
-def test_decode_step_graph_replays_match_eager(sk):
-    print("case: graph decode step sk", sk, flush=True)
-    d, B, Hkv, G, bits = 128, 2, 8, 4, 3
+@pytest.mark.parametrize("sk,d,bits", [(700, 128, 3), (5000, 128, 3), (5000, 64, 3), (20000, 64, 4)])
+def test_decode_step_graph_replays_match_eager(sk, d, bits):
+    print("case: graph decode step sk", sk, "d", d, "bits", bits, flush=True)
+    B, Hkv, G = 2, 8, 4
     kc = TurboQuantCompressorV2(d, bits, seed=42, device=DEV)
     vc = TurboQuantCompressorMSE(d, bits, seed=10042, device=DEV)
     g = torch.Generator(device=DEV).manual_seed(9)

@@ -19,8 +19,7 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def _setup(B, hq, hkv, sk, bits, seed):
-    d = 128
+def _setup(B, hq, hkv, sk, bits, seed, d=128):
     g = torch.Generator(device=DEV).manual_seed(seed)
     q = torch.randn(B, hq, 1, d, device=DEV, generator=g).to(torch.bfloat16)
     k = torch.randn(B, hkv, sk, d, device=DEV, generator=g).to(torch.bfloat16)
@@ -72,6 +71,18 @@ def test_noalloc_matches_workspace_entry_point_twice():
     assert torch.isfinite(a2).all() and torch.equal(a2, b2)
     # and back to the first shape, causal, after the smaller call's partials
     assert torch.equal(_call(True, *big, causal=1), _call(False, *big, causal=1))
+
+
+def test_noalloc_head_dim64_matches_workspace_entry_point():
+    """Head_dim 64 on the decode kernels: few splits (the split merge of any head dim), many
+    splits (the per-column merge) and the table kernel (bits 4), each against the workspace
+    entry point, in a row on the one scratch array."""
+    print("case: noalloc head_dim 64 (16 x 32768 bits 3, 1 x 20000 MHA bits 3, 2 x 5000 bits 4)", flush=True)
+    for shape in ((16, 32, 8, 32768, 3, 5), (1, 12, 12, 20000, 3, 6), (2, 8, 2, 5000, 4, 7)):
+        case = _setup(*shape, d=64)
+        a = _call(True, *case)
+        b = _call(False, *case)
+        assert torch.isfinite(a).all() and torch.equal(a, b), shape
 
 
 def test_noalloc_refuses_shapes_beyond_the_scratch_array():
