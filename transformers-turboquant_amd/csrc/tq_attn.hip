@@ -1,7 +1,7 @@
 // Compressed-domain attention on gfx950: asymmetric scores from packed keys,
 // online softmax, and P.V over packed values, in one kernel.  This tiled kernel
 // serves every head dim that is a multiple of 8 up to 256 (the prefill and
-// split-K decode kernels cover head_dim 128 at their shapes).
+// split-K decode kernels cover head_dim 64 and 128 at their shapes).
 //
 // Scores follow the reference estimator (kernels/attention.py:380-461,
 // compressors.py:178-200):
@@ -1026,8 +1026,8 @@ int tq_attention_fwd_kv(const uint16_t* q_rot, const float* q_proj, const uint8_
                             scale, causal, mask, smb, smh, smq, smk, out, out_dtype, sob, soh, sos,
                             workspace, as_stream(stream));
   // few query rows per kv head over a long key range: the tiled kernel split over keys, then a
-  // merge (the decode kernels above take head_dim 128, and head_dim 64 at bits 2-3 with at most 8
-  // columns, with key bits = value bits)
+  // merge (the decode kernels above take head_dim 64 / 128 with at most 16 columns and key
+  // bits = value bits)
   const SplitPlan sp = tiled_split_plan(B, Hq, Hkv, Sq, Sk, d);
   const bool split = sp.nsplit > 0 && workspace && workspace_bytes >= sp.bytes &&
                      reinterpret_cast<uintptr_t>(workspace) % 16 == 0;
