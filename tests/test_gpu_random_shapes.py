@@ -6,8 +6,9 @@ sweep draws shapes the kernels' tiling does not line up with: GQA groups 1-8 (in
 16/32/64-key blocks, 1-48 query rows (decode, split-K and prefill paths), causal or not,
 bits 2-4, head_dim 64 and 128.  Same bar as the rest of the suite: rel-err 1e-3 and
 cosine 0.9999 against the float64 oracle evaluated on the device's own packed planes.
-A second set draws decode-shaped cases (1-2 query rows, head_dim 128) with 600-20000 keys,
-so the split-K decode kernels run with many splits and their merge combines them.
+A second set draws decode-shaped cases (1-2 query rows, head_dim 128, and a third head_dim
+64) with 600-20000 keys, so the split-K decode kernels run with many splits and their merge
+combines them.
 """
 
 import numpy as np
@@ -57,7 +58,22 @@ def _long_shapes(n, seed=4242):
     return out
 
 
-@pytest.mark.parametrize("d,bits,B,hq,hkv,sq,sk,causal", _shapes(24) + _long_shapes(6))
+def _long_shapes_d64(n, seed=6464):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        bits = int(rng.integers(2, 5))
+        hkv = int(rng.choice([1, 2, 4, 12]))
+        g = int(rng.choice([1, 2, 3, 4, 8, 16]))
+        sq = int(rng.choice([1, 1, 2, 4]))
+        sk = int(rng.integers(600, 20000))
+        causal = bool(rng.random() < 0.6)
+        b = int(rng.integers(1, 3))
+        out.append((64, bits, b, hkv * g, hkv, sq if g * sq <= 16 else 1, sk, causal))
+    return out
+
+
+@pytest.mark.parametrize("d,bits,B,hq,hkv,sq,sk,causal", _shapes(24) + _long_shapes(6) + _long_shapes_d64(6))
 def test_random_shape_scores_and_attention(d, bits, B, hq, hkv, sq, sk, causal):
     print("case:", dict(d=d, bits=bits, B=B, hq=hq, hkv=hkv, sq=sq, sk=sk, causal=causal), flush=True)
     torch.manual_seed(d * 7 + bits * 131 + hq * 17 + sq * 5 + sk)
