@@ -584,12 +584,14 @@ def compress_leg(kc, vc, steps: int, warmup: int) -> dict:
             "tokens_per_s": 4 * 32768 / (both * 1e-6), **out}
 
 
-def decode_step_leg(kc, vc, steps: int = 200) -> dict:
+def decode_step_leg(kc, vc, steps: int = 200, hq: int = HQ, hkv: int = HKV, d: int = D,
+                    shapes=((1, 4096), (1, 32768), (16, 4096), (16, 32768)), label: str = "decode_step") -> dict:
     """One attention layer's decode step on the cached serving path (TurboQuantCache, as a patched
-    layer runs it under generate): tq::cache_append compresses the new token's K and V (8 kv heads)
-    straight into the cache planes and prepares the 32 query heads' query in one launch, then the
-    split-K attention over every cached position (attention + merge).  bits 3, B = 1 and 16, with
-    4096 and 32768 cached tokens; the cache is sized beforehand so that no step grows it.  Host time
+    layer runs it under generate): tq::cache_append compresses the new token's K and V (hkv kv heads,
+    8 by default) straight into the cache planes and prepares the hq query heads' query (32) in one
+    launch, then the split-K attention over every cached position (attention + merge).  bits 3, B
+    and cached tokens from `shapes` (1 and 16 x 4096 and 32768 by default); the cache is sized
+    beforehand so that no step grows it.  Host time
     per step (wall clock over `steps` back-to-back steps, synchronised at the end) and device time
     (HIP events around the same steps)."""
     import torch
@@ -600,18 +602,18 @@ def decode_step_leg(kc, vc, steps: int = 200) -> dict:
     dev = "cuda"
     out = {}
     warm = 20
-    for b_, cached in ((1, 4096), (1, 32768), (16, 4096), (16, 32768)):
+    for b_, cached in shapes:
         g = torch.Generator(device=dev).manual_seed(5 + b_ + cached)
         cache = TurboQuantCache()
         total = cached + warm + steps
         for lo in range(0, total, 8192):  # prefill in chunks; then keep `cached` positions
             n = min(8192, total - lo)
-            cache.append(0, kc, vc, torch.randn(b_, HKV, n, D, device=dev, generator=g).to(torch.bfloat16),
-                         torch.randn(b_, HKV, n, D, device=dev, generator=g).to(torch.bfloat16))
+            cache.append(0, kc, vc, torch.randn(b_, hkv, n, d, device=dev, generator=g).to(torch.bfloat16),
+                         torch.randn(b_, hkv, n, d, device=dev, generator=g).to(torch.bfloat16))
         cache.layer(0).crop(cached)
-        k1 = torch.randn(b_, HKV, 1, D, device=dev, generator=g).to(torch.bfloat16)
-        v1 = torch.randn(b_, HKV, 1, D, device=dev, generator=g).to(torch.bfloat16)
-        q1 = torch.randn(b_, HQ, 1, D, device=dev, generator=g).to(torch.bfloat16)
+        k1 = torch.randn(b_, hkv, 1, d, device=dev, generator=g).to(torch.bfloat16)
+        v1 = torch.randn(b_, hkv, 1, d, device=dev, generator=g).to(torch.bfloat16)
+        q1 = torch.randn(b_, hq, 1, d, device=dev, generator=g).to(torch.bfloat16)
 
         def step():
             ck, cv, q_rot, q_proj = cache.append_prepare(0, kc, vc, k1, v1, q1)
@@ -621,7 +623,7 @@ def decode_step_leg(kc, vc, steps: int = 200) -> dict:
             step()
         cache.layer(0).crop(cached)
         torch.cuda.synchronize()
-        RANGES.push(f"decode_step_B{b_}_S{cached}", steps)
+        RANGES.push(f"{label}_B{b_}_S{cached}", steps)
         e0, e1 = _events(2)
         t0 = time.perf_counter()
         e0.record()
@@ -634,7 +636,7 @@ def decode_step_leg(kc, vc, steps: int = 200) -> dict:
         out[f"B{b_}_S{cached}"] = {"host_us_per_step": host_us, "device_us_per_step": e0.elapsed_time(e1) / steps * 1e3}
         del cache
         torch.cuda.empty_cache()
-    return {"workload": (f"Hq{HQ} Hkv{HKV} d{D} bits{BITS}: one new token per step appended to a TurboQuantCache "
+    return {"workload": (f"Hq{hq} Hkv{hkv} d{d} bits{BITS}: one new token per step appended to a TurboQuantCache "
                          "(one launch: K, V and query preparation) + split-K attention over every cached position"),
             **out}
 
@@ -705,6 +707,9 @@ def head_dim64_leg(steps: int, warmup: int) -> dict:
         torch.cuda.synchronize()
         RANGES.pop()
         out[f"decode_B{b_}_S{sk}"] = {"attention_us": e0.elapsed_time(e1) / steps * 1e3}
+    # the cached serving step at this shape (append + attention over every cached position)
+    out["decode_step"] = decode_step_leg(kc, vc, steps=max(steps, 50), hq=h, hkv=h, d=d,
+                                         shapes=((1, 4096), (1, 32768)), label="head_dim64_decode_step")
     return {"workload": f"GPT-2 attention shape: B1 x {h} heads x d{d}, bits {BITS}, causal; "
                         "tq::prefill_kernel<64, 3, false> (q_proj as f16 hi + lo); decode steps (one query "
                         "row over 4k / 32k cached keys) through tq::decode_attn_i8_kernel<2, 3, false, 1, 64> "
