@@ -587,9 +587,10 @@ def compress_leg(kc, vc, steps: int, warmup: int) -> dict:
 def decode_step_leg(kc, vc, steps: int = 200, hq: int = HQ, hkv: int = HKV, d: int = D,
                     shapes=((1, 4096), (1, 32768), (16, 4096), (16, 32768)), label: str = "decode_step") -> dict:
     """One attention layer's decode step on the cached serving path (TurboQuantCache, as a patched
-    layer runs it under generate): tq::cache_append compresses the new token's K and V (hkv kv heads,
-    8 by default) straight into the cache planes and prepares the hq query heads' query (32) in one
-    launch, then the split-K attention over every cached position (attention + merge).  bits 3, B
+    layer runs it under generate, TurboQuantCache.append_attend: one tq::cache_attend operator call):
+    tq::cache_append compresses the new token's K and V (hkv kv heads, 8 by default) straight into
+    the cache planes and prepares the hq query heads' query (32) in one launch, then the split-K
+    attention over every cached position (attention + merge).  bits 3, B
     and cached tokens from `shapes` (1 and 16 x 4096 and 32768 by default); the cache is sized
     beforehand so that no step grows it.  Host time
     per step (wall clock over `steps` back-to-back steps, synchronised at the end) and device time
@@ -597,7 +598,6 @@ def decode_step_leg(kc, vc, steps: int = 200, hq: int = HQ, hkv: int = HKV, d: i
     import torch
 
     from transformers_turboquant import TurboQuantCache
-    from turboquant_pytorch.fused import attention_from_prepared
 
     dev = "cuda"
     out = {}
@@ -616,8 +616,7 @@ def decode_step_leg(kc, vc, steps: int = 200, hq: int = HQ, hkv: int = HKV, d: i
         q1 = torch.randn(b_, hq, 1, d, device=dev, generator=g).to(torch.bfloat16)
 
         def step():
-            ck, cv, q_rot, q_proj = cache.append_prepare(0, kc, vc, k1, v1, q1)
-            return attention_from_prepared(q_rot, q_proj, kc, vc, ck, cv, out_dtype=torch.bfloat16)
+            return cache.append_attend(0, kc, vc, k1, v1, q1, out_dtype=torch.bfloat16)
 
         for _ in range(warm):
             step()

@@ -221,3 +221,42 @@ def test_cached_decode_step_uses_one_append_launch():
     ref = compressed_attention(q, kc, vc, fk, fv, out_dtype=torch.float32)
     torch.cuda.synchronize()
     assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("d,bits,Hkv,G", [(128, 3, 8, 4), (64, 3, 12, 1), (64, 4, 2, 8), (128, 2, 2, 8)])
+def test_append_attend_matches_append_prepare_then_attention(d, bits, Hkv, G):
+    """TurboQuantCache.append_attend (one tq::cache_attend call) against append_prepare followed
+    by attention_from_prepared on a copy of the same cache: the same output and cache planes, bit
+    for bit, over several decode steps (causal, with a padding mask on the last one)."""
+    print("case: append_attend", dict(d=d, bits=bits, Hkv=Hkv, G=G), flush=True)
+    from turboquant_pytorch.fused import attention_from_prepared
+
+    dev, B = "cuda", 2
+    kc = TurboQuantCompressorV2(d, bits, seed=42, device=dev)
+    vc = TurboQuantCompressorMSE(d, bits, seed=10042, device=dev)
+    g = torch.Generator(device=dev).manual_seed(d + bits)
+    total = 1500
+    k = torch.randn(B, Hkv, total, d, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, total, d, device=dev, generator=g).to(torch.bfloat16)
+    a, b = TurboQuantCache(), TurboQuantCache()
+    for c in (a, b):
+        c.append(0, kc, vc, k[:, :, :1496], v[:, :, :1496])
+    for pos in range(1496, total):
+        q = torch.randn(B, Hkv * G, 1, d, device=dev, generator=g).to(torch.bfloat16)
+        mask = None
+        if pos == total - 1:
+            mask = torch.zeros(B, 1, 1, pos + 1, device=dev)
+            mask[0, 0, 0, :100] = torch.finfo(torch.float32).min
+        got = a.append_attend(0, kc, vc, k[:, :, pos:pos + 1], v[:, :, pos:pos + 1], q, attention_mask=mask,
+                              causal=True, out_dtype=torch.bfloat16)
+        ck, cv, q_rot, q_proj = b.append_prepare(0, kc, vc, k[:, :, pos:pos + 1], v[:, :, pos:pos + 1], q)
+        want = attention_from_prepared(q_rot, q_proj, kc, vc, ck, cv, attention_mask=mask, causal=True,
+                                       out_dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        assert torch.isfinite(got.float()).all() and torch.equal(got, want), pos
+    la, lb = a.layer(0), b.layer(0)
+    assert la.length == lb.length == total
+    for name in la.kp:
+        assert torch.equal(la.kp[name], lb.kp[name]), name
+    for name in la.vp:
+        assert torch.equal(la.vp[name], lb.vp[name]), name

@@ -427,8 +427,9 @@ std::tuple<Tensor, Tensor> cache_append(const Tensor& k_in, const Tensor& v_in, 
                                         const Tensor& vbounds, int64_t val_bits, const Tensor& kseff16,
                                         const Tensor& kcodes, const Tensor& ksigns, const Tensor& krn,
                                         const Tensor& kvn, const Tensor& vcodes, const Tensor& vvn, int64_t pos) {
-  cache_append_meta(k_in, v_in, q_in, kpi, kseff, kcent, kbounds, key_code_bits, vpi, vbounds, val_bits, kseff16,
-                    kcodes, ksigns, krn, kvn, vcodes, vvn, pos);
+  // the checks, and the q_rot / q_proj outputs they return (allocated on k's device)
+  auto outs = cache_append_meta(k_in, v_in, q_in, kpi, kseff, kcent, kbounds, key_code_bits, vpi, vbounds, val_bits,
+                                kseff16, kcodes, ksigns, krn, kvn, vcodes, vvn, pos);
   const c10::DeviceGuard g(k_in.device());
   Tensor k = activation(k_in);
   Tensor v = v_in.scalar_type() == k.scalar_type() && v_in.stride(-1) == 1 ? v_in : v_in.to(k.scalar_type()).contiguous();
@@ -438,8 +439,7 @@ std::tuple<Tensor, Tensor> cache_append(const Tensor& k_in, const Tensor& v_in, 
                    : Tensor();
   const int64_t B = k.size(0), H = k.size(1), S = k.size(2), D = k.size(3), cap = kcodes.size(2);
   const int64_t Hq = has_q ? q.size(1) : 0;
-  Tensor q_rot = at::empty({has_q ? B : 0, Hq, S, D}, k.options().dtype(at::kHalf));
-  Tensor q_proj = at::empty({has_q ? B : 0, Hq, S, D}, k.options().dtype(at::kFloat));
+  Tensor q_rot = std::get<0>(outs), q_proj = std::get<1>(outs);
   check_status(tq_cache_append(k.data_ptr(), v.data_ptr(), dtype_code(k.scalar_type()), static_cast<int32_t>(B),
                                static_cast<int32_t>(H), static_cast<int32_t>(S), static_cast<int32_t>(D), k.stride(0),
                                k.stride(1), k.stride(2), v.stride(0), v.stride(1), v.stride(2), ptr<uint16_t>(kpi),
@@ -502,12 +502,12 @@ Tensor attention(const Tensor& q_rot, const Tensor& q_proj, const Tensor& kcodes
                  const Tensor& vvn, const Tensor& vcent32, int64_t val_bits, const Tensor& vpit, int64_t hkv,
                  int64_t sk, int64_t kv_stride, double coeff, double scale, bool causal,
                  const c10::optional<Tensor>& mask_in, at::ScalarType out_dtype, int64_t workspace) {
-  attention_meta(q_rot, q_proj, kcodes, ksigns, krn, kvn, kcent16, bits, vcodes, vvn, vcent32, val_bits, vpit, hkv, sk,
-                 kv_stride, coeff, scale, causal, mask_in, out_dtype, workspace);
+  // the checks, and the [B, Sq, Hq, D] output they return (allocated on q_rot's device)
+  Tensor out = attention_meta(q_rot, q_proj, kcodes, ksigns, krn, kvn, kcent16, bits, vcodes, vvn, vcent32, val_bits,
+                              vpit, hkv, sk, kv_stride, coeff, scale, causal, mask_in, out_dtype, workspace);
   const Checker c{"tq::attention", q_rot.device()};
   const c10::DeviceGuard g(q_rot.device());
   const int64_t B = q_rot.size(0), Hq = q_rot.size(1), Sq = q_rot.size(2), D = q_rot.size(3);
-  Tensor out = at::empty({B, Sq, Hq, D}, q_rot.options().dtype(out_dtype));
   Tensor mask = attention_mask(c, mask_in, q_rot, sk);
   int64_t ms[4] = {0, 0, 0, 0};
   if (mask.defined())
@@ -546,6 +546,39 @@ Tensor attention(const Tensor& q_rot, const Tensor& q_proj, const Tensor& kcodes
   return out;
 }
 
+// A cached decode step in one call: cache_append (the new keys / values into the capacity
+// planes at row pos, the new queries prepared in the same launch), then attention over the
+// planes' first pos + S rows.  The same two operators back to back, without the second
+// crossing of the dispatcher and the Python between them (a one-token step is bound by that
+// host time, not by its kernels).
+Tensor cache_attend(const Tensor& k, const Tensor& v, const Tensor& q, const Tensor& kpi, const Tensor& kseff,
+                    const Tensor& kcent, const Tensor& kbounds, int64_t key_code_bits, const Tensor& vpi,
+                    const Tensor& vbounds, int64_t val_bits, const Tensor& kseff16, const Tensor& kcodes,
+                    const Tensor& ksigns, const Tensor& krn, const Tensor& kvn, const Tensor& vcodes,
+                    const Tensor& vvn, int64_t pos, const Tensor& kcent16, const Tensor& vcent32, const Tensor& vpit,
+                    double coeff, double scale, bool causal, const c10::optional<Tensor>& mask,
+                    at::ScalarType out_dtype, int64_t workspace) {
+  auto qp = cache_append(k, v, q, kpi, kseff, kcent, kbounds, key_code_bits, vpi, vbounds, val_bits, kseff16, kcodes,
+                         ksigns, krn, kvn, vcodes, vvn, pos);
+  return attention(std::get<0>(qp), std::get<1>(qp), kcodes, ksigns, krn, kvn, kcent16, key_code_bits + 1, vcodes, vvn,
+                   vcent32, val_bits, vpit, k.size(1), pos + k.size(2), kvn.size(-1), coeff, scale, causal, mask,
+                   out_dtype, workspace);
+}
+
+Tensor cache_attend_meta(const Tensor& k, const Tensor& v, const Tensor& q, const Tensor& kpi, const Tensor& kseff,
+                         const Tensor& kcent, const Tensor& kbounds, int64_t key_code_bits, const Tensor& vpi,
+                         const Tensor& vbounds, int64_t val_bits, const Tensor& kseff16, const Tensor& kcodes,
+                         const Tensor& ksigns, const Tensor& krn, const Tensor& kvn, const Tensor& vcodes,
+                         const Tensor& vvn, int64_t pos, const Tensor& kcent16, const Tensor& vcent32,
+                         const Tensor& vpit, double coeff, double scale, bool causal,
+                         const c10::optional<Tensor>& mask, at::ScalarType out_dtype, int64_t workspace) {
+  auto qp = cache_append_meta(k, v, q, kpi, kseff, kcent, kbounds, key_code_bits, vpi, vbounds, val_bits, kseff16,
+                              kcodes, ksigns, krn, kvn, vcodes, vvn, pos);
+  return attention_meta(std::get<0>(qp), std::get<1>(qp), kcodes, ksigns, krn, kvn, kcent16, key_code_bits + 1, vcodes,
+                        vvn, vcent32, val_bits, vpit, k.size(1), pos + k.size(2), kvn.size(-1), coeff, scale, causal,
+                        mask, out_dtype, workspace);
+}
+
 int64_t workspace_size(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t d, int64_t bits) {
   return tq_attention_workspace_size(static_cast<int32_t>(B), static_cast<int32_t>(Hq), static_cast<int32_t>(Hkv),
                                      static_cast<int32_t>(Sq), static_cast<int32_t>(Sk), static_cast<int32_t>(d),
@@ -576,6 +609,11 @@ TORCH_LIBRARY(tq, m) {
         "Tensor kcent, int bits, Tensor vcodes, Tensor vvn, Tensor vcent, int val_bits, Tensor vpit, int hkv, "
         "int sk, int kv_stride, float coeff, float scale, bool causal, Tensor? mask, ScalarType out_dtype, "
         "int workspace) -> Tensor");
+  m.def("cache_attend(Tensor k, Tensor v, Tensor q, Tensor kpi, Tensor kseff, Tensor kcent, Tensor kbounds, "
+        "int key_code_bits, Tensor vpi, Tensor vbounds, int val_bits, Tensor kseff16, Tensor(a!) kcodes, "
+        "Tensor(b!) ksigns, Tensor(c!) krn, Tensor(d!) kvn, Tensor(e!) vcodes, Tensor(f!) vvn, int pos, "
+        "Tensor kcent16, Tensor vcent, Tensor vpit, float coeff, float scale, bool causal, Tensor? mask, "
+        "ScalarType out_dtype, int workspace) -> Tensor");
   m.def("workspace_size(int B, int Hq, int Hkv, int Sq, int Sk, int d, int bits) -> int", &workspace_size);
 }
 
@@ -591,6 +629,7 @@ TORCH_LIBRARY_IMPL(tq, CUDA, m) {
   m.impl("cache_append", &cache_append);
   m.impl("scores", &scores);
   m.impl("attention", &attention);
+  m.impl("cache_attend", &cache_attend);
 }
 
 // the same checks on tensor metadata, returning empty outputs of the right shapes
@@ -606,4 +645,5 @@ TORCH_LIBRARY_IMPL(tq, Meta, m) {
   m.impl("cache_append", &cache_append_meta);
   m.impl("scores", &scores_meta);
   m.impl("attention", &attention_meta);
+  m.impl("cache_attend", &cache_attend_meta);
 }

@@ -21,6 +21,8 @@ use_cache=True)`` on a model patched by ``apply_turboquant``.
 
 from __future__ import annotations
 
+import math
+
 import torch
 from transformers.cache_utils import Cache, CacheLayerMixin
 
@@ -121,15 +123,8 @@ class TurboQuantCacheLayer(CacheLayerMixin):
         if k.device.type != "cuda":
             return (*self._append_cpu(key_compressor, val_compressor, k, v), None, None)
         from turboquant_pytorch._ops import ops
-        from turboquant_pytorch.compressors import _tables
 
-        need = self.length + S
-        widths = (_cols(D, key_compressor.mse_bits), _cols(D, 1), _cols(D, val_compressor.bits))
-        if self.kp is None or need > self.capacity or self.kp["vec_norms"].shape[:2] != (B, H) or \
-                self._widths() != widths:
-            self._grow(need, B, H, widths, k.device)
-        tk = _tables(key_compressor, k.device, with_qjl=True)
-        tv = _tables(val_compressor, k.device, with_qjl=False)
+        tk, tv, need = self._gpu_room(key_compressor, val_compressor, k)
         q_rot, q_proj = ops().cache_append(
             k, v, q, tk.pi_split, tk.seff_split, tk.cent32, tk.bounds32, key_compressor.mse_bits, tv.pi_split,
             tv.bounds32, val_compressor.bits, tk.s_eff16, self.kp["packed_key_indices"], self.kp["packed_qjl_signs"],
@@ -138,6 +133,60 @@ class TurboQuantCacheLayer(CacheLayerMixin):
         self.length = need
         ck, cv = self.strided()
         return (ck, cv, q_rot, q_proj) if q is not None else (ck, cv, None, None)
+
+    def _gpu_room(self, key_compressor, val_compressor, k: torch.Tensor):
+        """Device tables of both compressors, and capacity planes that hold S more rows (grown,
+        or re-laid out for other shapes or bit widths); returns (tk, tv, length after the append)."""
+        from turboquant_pytorch.compressors import _tables
+
+        B, H, S, D = k.shape
+        need = self.length + S
+        widths = (_cols(D, key_compressor.mse_bits), _cols(D, 1), _cols(D, val_compressor.bits))
+        if self.kp is None or need > self.capacity or self.kp["vec_norms"].shape[:2] != (B, H) or \
+                self._widths() != widths:
+            self._grow(need, B, H, widths, k.device)
+        tk = _tables(key_compressor, k.device, with_qjl=True)
+        tv = _tables(val_compressor, k.device, with_qjl=False)
+        return tk, tv, need
+
+    def append_attend(self, key_compressor, val_compressor, k: torch.Tensor, v: torch.Tensor, q: torch.Tensor,
+                      attention_mask: torch.Tensor | None = None, causal: bool = False, scale: float | None = None,
+                      out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+        """GPU: append_prepare() followed by attention over every cached position
+        (turboquant_pytorch.fused.attention_from_prepared), in one operator call
+        (tq::cache_attend): the same kernels and results, without the second operator's host
+        cost, which bounds a one-token decode step.  Returns the attention output [B, S_q, Hq, D]."""
+        if k.device.type != "cuda":
+            raise ValueError("append_attend runs on the GPU; use append_prepare on the CPU")
+        B, H, S, D = k.shape
+        if self.shape is not None and self.length > 0 and self.shape != (B, H, D):
+            raise ValueError(f"cache holds [B, Hkv, D] = {self.shape}, got {(B, H, D)}")
+        codec = {"key_bits": key_compressor.bits, "value_bits": val_compressor.bits,
+                 "key_seed": getattr(key_compressor, "seed", None),
+                 "value_seed": getattr(val_compressor, "seed", None)}
+        if self.length > 0 and self.codec and codec != self.codec:
+            stale = {k_: (self.codec.get(k_), v_) for k_, v_ in codec.items()
+                     if self.codec.get(k_) is not None and v_ is not None and self.codec.get(k_) != v_}
+            if stale:
+                raise ValueError(f"cache layer holds {self.length} positions compressed with other "
+                                 f"settings (cached, new): {stale}")
+        self.shape = (B, H, D)
+        self.codec = codec
+        from turboquant_pytorch._ops import ops
+
+        tk, tv, need = self._gpu_room(key_compressor, val_compressor, k)
+        if out_dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            out_dtype = torch.float32
+        mask = attention_mask.to(k.device, torch.float32) if attention_mask is not None else None
+        out = ops().cache_attend(
+            k, v, q, tk.pi_split, tk.seff_split, tk.cent32, tk.bounds32, key_compressor.mse_bits, tv.pi_split,
+            tv.bounds32, val_compressor.bits, tk.s_eff16, self.kp["packed_key_indices"], self.kp["packed_qjl_signs"],
+            self.kp["residual_norm"], self.kp["vec_norms"], self.vp["packed_indices"], self.vp["vec_norms"],
+            self.length, tk.cent16, tv.cent32, tv.pit_split,
+            float(math.sqrt(math.pi / 2) / key_compressor.S.shape[0]),
+            float(scale if scale is not None else 1.0 / math.sqrt(D)), bool(causal), mask, out_dtype, 1)
+        self.length = need
+        return out
 
     def _widths(self) -> tuple | None:
         if self.kp is None:
@@ -318,6 +367,16 @@ class TurboQuantCache(Cache):
         if layer_idx is None:
             raise ValueError("TurboQuantCache needs attention modules with a layer_idx")
         return self.layer(layer_idx).append(key_compressor, val_compressor, k, v)
+
+    def append_attend(self, layer_idx: int, key_compressor, val_compressor, k: torch.Tensor, v: torch.Tensor,
+                      q: torch.Tensor, attention_mask: torch.Tensor | None = None, causal: bool = False,
+                      scale: float | None = None, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+        """append_prepare() and the attention over every cached position in one operator call
+        on the GPU (see TurboQuantCacheLayer.append_attend)."""
+        if layer_idx is None:
+            raise ValueError("TurboQuantCache needs attention modules with a layer_idx")
+        return self.layer(layer_idx).append_attend(key_compressor, val_compressor, k, v, q, attention_mask, causal,
+                                                   scale, out_dtype)
 
     def append_prepare(self, layer_idx: int, key_compressor, val_compressor, k: torch.Tensor, v: torch.Tensor,
                        q: torch.Tensor | None = None):

@@ -23,7 +23,7 @@ import math
 import torch
 import torch.nn.functional as F
 
-from turboquant_pytorch.fused import attention_from_prepared, compressed_attention
+from turboquant_pytorch.fused import compressed_attention
 
 from ..cache import TurboQuantCache
 
@@ -66,10 +66,10 @@ def attention_tail(module, q, k, v, attention_mask, output_attentions: bool = Fa
     cached = None  # (compressed keys, compressed values) of every cached position
     if isinstance(cache, TurboQuantCache):
         if fused:
-            # one launch compresses the new keys / values into the cache and prepares the queries
-            ck, cv, q_rot, q_proj = cache.append_prepare(module.layer_idx, kc, vc, k, v, q)
-            out = attention_from_prepared(q_rot, q_proj, kc, vc, ck, cv, attention_mask=mask, causal=causal,
-                                          scale=1.0 / math.sqrt(D), out_dtype=q.dtype)
+            # one operator call: one launch compresses the new keys / values into the cache and
+            # prepares the queries, then the attention over every cached position
+            out = cache.append_attend(module.layer_idx, kc, vc, k, v, q, attention_mask=mask, causal=causal,
+                                      scale=1.0 / math.sqrt(D), out_dtype=q.dtype)
             return out.reshape(B, T, Hq * D), None
         cached = cache.append(module.layer_idx, kc, vc, k, v)
         lay = cache.layer(module.layer_idx)
