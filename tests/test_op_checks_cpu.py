@@ -167,3 +167,26 @@ def test_kernel_function_ops():
     _raises("expected 3 boundaries", ops().quantize_pack, _e(10, 128), _e(4), 2)
     assert ops().dequantize(_e(10, 32, dtype=U8), _e(4), 2, 128).dtype == F16
     _raises("centroids for 2-bit", ops().dequantize, _e(10, 32, dtype=U8), _e(3), 2, 128)
+
+
+def test_cache_ops():
+    """tq::cache_append and tq::cache_attend (a cached decode step in one call) on meta tensors:
+    output shapes, and the capacity, plane and query checks."""
+    H, S, CAP, POS = HKV, 1, 64, 40
+    k, v, q = _e(B, H, S, D), _e(B, H, S, D), _e(B, HQ, S, D)
+    pi, seff, s16 = _e(2, D, D, dtype=F16), _e(2, D, D, dtype=F16), _e(D, D, dtype=F16)
+    kcent, kbnd, vbnd = _e(1 << (BITS - 1)), _e((1 << (BITS - 1)) - 1), _e((1 << BITS) - 1)
+    planes = [_e(B, H, CAP, D * (BITS - 1) // 8, dtype=U8), _e(B, H, CAP, D // 8, dtype=U8),
+              _e(B, H, CAP, dtype=F16), _e(B, H, CAP, dtype=F16), _e(B, H, CAP, D * BITS // 8, dtype=U8),
+              _e(B, H, CAP, dtype=F16)]
+    head = (k, v, q, pi, seff, kcent, kbnd, BITS - 1, pi, vbnd, BITS, s16)
+    qr, qp = ops().cache_append(*head, *planes, POS)
+    assert qr.shape == (B, HQ, S, D) and qr.dtype == F16 and qp.dtype == F32
+    tail = (_e(1 << (BITS - 1), dtype=F16), _e(1 << BITS), pi, 0.01, 0.1, True, None, torch.bfloat16, 1)
+    out = ops().cache_attend(*head, *planes, POS, *tail)
+    assert out.shape == (B, S, HQ, D) and out.dtype == torch.bfloat16
+    _raises("exceed the capacity", ops().cache_attend, *head, *planes, CAP, *tail)
+    _raises("q must be", ops().cache_attend, k, v, _e(B, HQ, S + 1, D), *head[3:], *planes, POS, *tail)
+    bad = list(planes)
+    bad[4] = _e(B, H, CAP, D * BITS // 8 - 1, dtype=U8)
+    _raises("value codes", ops().cache_attend, *head, *bad, POS, *tail)
